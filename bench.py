@@ -1,0 +1,270 @@
+"""Benchmark of the MI355X Q8_0 hot path (one JSON line on stdout).
+
+Workload ("C2"): one EmbeddingGemma layer's quantized
+projections at T = 512, hidden 768 — RMSNorm(eps 1e-6) -> q/k/v (fused
+768->1280), o 768->768 on a fixed synthetic attention output, RMSNorm ->
+gate/up 768->2x1152 with the tanh-GeGLU epilogue -> down 1152->768.  A step is
+one pass of those 7 projections; value = algorithmic Q8_0 ops / step time.
+
+Also reported (in "extra"): configs[0] (C1, one 512x768x1152 linear) and
+configs[2] (C3, M = 16384 through the same 7 projections) for both variants.
+
+    python bench.py [--steps K] [--warmup W] [--variant int8|bf16] [--no-cpu]
+
+Inputs are synthetic (seeded numpy), resident in HBM before the timed region.
+The roofline entry is measured live: the library brackets every kernel of the
+timed region with HIP events on its launch stream (glypr_hip_profile_*).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+H, F, NQ, NKV = 768, 1152, 768, 256
+PROJ = [("qkv", NQ + 2 * NKV, H), ("o", H, NQ), ("gate_up", 2 * F, H), ("down", H, F)]
+LAYER_NK = sum(n * k for _, n, k in PROJ)  # 4,227,072 weights
+
+
+def q8_0_weight(rng, n, k, sigma=0.02):
+    """GGUF Q8_0 bytes [n, k/32*34]: qs uniform in [-127,127], d = f16(|N(0,sigma)|/127)."""
+    nb = k // 32
+    d = (np.abs(rng.standard_normal((n, nb))) * sigma / 127).astype(np.float16)
+    qs = rng.integers(-127, 128, size=(n, nb, 32), dtype=np.int8)
+    out = np.empty((n, nb, 34), np.uint8)
+    out[:, :, :2] = d.view(np.uint8).reshape(n, nb, 2)
+    out[:, :, 2:] = qs.view(np.uint8)
+    return out.reshape(n, nb * 34)
+
+
+class Layer:
+    """The C2/C3 workload: weights + activations for one layer's projections."""
+
+    def __init__(self, ctx, m, seed=0):
+        import torch
+        from glypr_amd.ops import Q8Weight
+        rng = np.random.default_rng(seed)
+        self.m = m
+        self.blocks = {
+            "q": q8_0_weight(rng, NQ, H), "k": q8_0_weight(rng, NKV, H),
+            "v": q8_0_weight(rng, NKV, H), "o": q8_0_weight(rng, H, NQ),
+            "gate": q8_0_weight(rng, F, H), "up": q8_0_weight(rng, F, H),
+            "down": q8_0_weight(rng, H, F)}
+        w = {n: Q8Weight.from_gguf(ctx, b, b.shape[0], b.shape[1] // 34 * 32)
+             for n, b in self.blocks.items()}
+        self.qkv, _ = Q8Weight.concat(ctx, [w["q"], w["k"], w["v"]])
+        self.gate_up, _ = Q8Weight.concat(ctx, [w["gate"], w["up"]])
+        self.o, self.down = w["o"], w["down"]
+        for n in ("q", "k", "v", "gate", "up"):
+            w[n].close()
+        self.x = torch.from_numpy(rng.standard_normal((m, H)).astype(np.float32)).cuda()
+        self.attn = torch.from_numpy(rng.standard_normal((m, NQ)).astype(np.float32)).cuda()
+        self.norm1 = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
+        self.norm2 = torch.from_numpy((1 + 0.1 * rng.standard_normal(H)).astype(np.float32)).cuda()
+        self.y_qkv = torch.empty((m, NQ + 2 * NKV), dtype=torch.float32, device="cuda")
+        self.y_o = torch.empty((m, H), dtype=torch.float32, device="cuda")
+        self.y_mlp = torch.empty((m, H), dtype=torch.float32, device="cuda")
+
+    def step(self, ctx, variant):
+        from glypr_amd import ops
+        ops.rmsnorm_q8_0_matmul(ctx, self.qkv, self.x, self.norm1, 1e-6, variant, out=self.y_qkv)
+        ops.q8_0_matmul(ctx, self.o, self.attn, variant, out=self.y_o)
+        ops.rmsnorm_mlp(ctx, self.gate_up, self.down, self.x, self.norm2, 1e-6, variant,
+                        out=self.y_mlp)
+
+    def ops_per_step(self):
+        return 2 * self.m * LAYER_NK
+
+
+def kernel_bytes(kernel: str, m: int, variant: int):
+    """Algorithmic HBM bytes of every launch of `kernel` in one C2/C3 step:
+    each operand read once and each result written once."""
+    nb = lambda k: k // 32
+    if kernel == "gemm_i8":     # qkv, o, down on int8 activations, f32 out
+        return sum(m * k + 4 * m * nb(k) + n * k + 4 * n * nb(k) + 4 * m * n
+                   for (n, k) in [(NQ + 2 * NKV, H), (H, NQ), (H, F)])
+    if kernel == "gemm_i8_geglu":
+        return m * H + 4 * m * nb(H) + 2 * F * H + 4 * 2 * F * nb(H) + m * F + 4 * m * nb(F)
+    if kernel == "gemm_bf16":
+        return sum(2 * m * k + n * k + 4 * n * nb(k) + 4 * m * n
+                   for (n, k) in [(NQ + 2 * NKV, H), (H, NQ), (H, F)])
+    if kernel == "gemm_bf16_geglu":
+        return 2 * m * H + 2 * F * H + 4 * 2 * F * nb(H) + 2 * m * F
+    if kernel == "rmsnorm_quant":   # two launches (qkv, mlp)
+        return 2 * (4 * m * H + 4 * H + m * H + 4 * m * nb(H))
+    if kernel == "quantize":
+        return 4 * m * NQ + m * NQ + 4 * m * nb(NQ)
+    if kernel in ("rmsnorm_bf16",):
+        return 2 * (4 * m * H + 4 * H + 2 * m * H)
+    if kernel == "to_bf16":
+        return 4 * m * NQ + 2 * m * NQ
+    return 0
+
+
+def kernel_ops(kernel: str, m: int):
+    if kernel in ("gemm_i8", "gemm_bf16"):
+        return 2 * m * ((NQ + 2 * NKV) * H + H * NQ + H * F)
+    if kernel in ("gemm_i8_geglu", "gemm_bf16_geglu"):
+        return 2 * m * 2 * F * H
+    return 0
+
+
+def run_workload(ctx, m, variant, steps, warmup, seed=0):
+    import torch
+    from glypr_amd import _lib
+    L = Layer(ctx, m, seed)
+    for _ in range(warmup):
+        L.step(ctx, variant)
+    torch.cuda.synchronize()
+    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 1))
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        L.step(ctx, variant)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    tot = (ctypes.c_double * _lib.KERNEL_COUNT)()
+    cnt = (ctypes.c_int64 * _lib.KERNEL_COUNT)()
+    _lib.check(_lib.lib().glypr_hip_profile_read(ctx.handle, tot, cnt))
+    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 0))
+    kern = {}
+    for i in range(_lib.KERNEL_COUNT):
+        if cnt[i]:
+            name = _lib.lib().glypr_hip_kernel_name(i).decode()
+            kern[name] = {"ms_total": tot[i], "launches": int(cnt[i]),
+                          "us_per_launch": 1000.0 * tot[i] / cnt[i]}
+    return L, ms, kern
+
+
+def roofline_for(kern, m, variant, steps):
+    dom = max(kern, key=lambda k: kern[k]["ms_total"])
+    k = kern[dom]
+    secs_per_step = k["ms_total"] / 1000.0 / steps
+    nbytes = kernel_bytes(dom, m, variant)
+    gbs = nbytes / secs_per_step / 1e9
+    return dom, {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                 "kernel": dom, "us_per_launch": round(k["us_per_launch"], 3),
+                 "launches_per_step": k["launches"] // steps,
+                 "algorithmic_bytes_per_step": nbytes}
+
+
+def cpu_baseline(seconds=10.0):
+    """glypr's CPU Q8_0 path (the oracle restatement) on this host: the C2 layer as
+    glypr's CPU backend runs it (separate q/k/v and gate/up QMatMuls, cpu_geglu)."""
+    from oracle import pyoracle as po
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    m = 512
+    rng = np.random.default_rng(0)
+    b = {n: q8_0_weight(rng, nn, kk) for n, nn, kk in
+         [("q", NQ, H), ("k", NKV, H), ("v", NKV, H), ("o", H, NQ), ("gate", F, H),
+          ("up", F, H), ("down", H, F)]}
+    x = rng.standard_normal((m, H)).astype(np.float32)
+    attn = rng.standard_normal((m, NQ)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+
+    def step():
+        xn = po.rmsnorm(x, nw, 1e-6, threads=cores)
+        for n, nn in (("q", NQ), ("k", NKV), ("v", NKV)):
+            po.matmul(xn, b[n], nn, threads=cores)
+        po.matmul(attn, b["o"], H, threads=cores)
+        g = po.matmul(xn, b["gate"], F, threads=cores)
+        u = po.matmul(xn, b["up"], F, threads=cores)
+        po.matmul(po.geglu(g, u, threads=cores), b["down"], H, threads=cores)
+
+    step()
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        step()
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(2 * m * LAYER_NK / dt / 1e12, 5), "unit": "TOPS", "cores": cores,
+            "kind": "port", "ms_per_step": round(dt * 1e3, 3),
+            "sample": f"C2 layer at T=512, {n} steps over {seconds:.0f}s, candle-default-x86 "
+                      "scalar vec_dot semantics (oracle/glypr_oracle.c, gcc -O3 x86-64-v3)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--variant", choices=["int8", "bf16"], default="int8")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3 extra lines")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the path shards by independent sequences, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from glypr_amd import ops
+    from glypr_amd.ops import BF16_DEQUANT, INT8_EXACT
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    variant = INT8_EXACT if args.variant == "int8" else BF16_DEQUANT
+    ctx = ops.Context(0)
+
+    m = 512
+    L, ms, kern = run_workload(ctx, m, variant, args.steps, args.warmup)
+    tops = L.ops_per_step() / (ms / 1e3) / 1e12
+    dom, roof = roofline_for(kern, m, variant, args.steps)
+    peak = INT8_PEAK_TOPS if variant == INT8_EXACT else BF16_PEAK_TFLOPS
+
+    extra = {"kernels_c2": {k: {"us_per_launch": round(v["us_per_launch"], 3),
+                                "launches_per_step": v["launches"] // args.steps}
+                            for k, v in kern.items()},
+             "pct_mfma_peak_c2": round(100 * tops / peak, 3)}
+    if not args.no_extra:
+        for name, mm, steps in (("c3", 16384, max(10, args.steps // 10)),):
+            for vname, v in (("int8", INT8_EXACT), ("bf16", BF16_DEQUANT)):
+                Lx, msx, kx = run_workload(ctx, mm, v, steps, 3)
+                t = Lx.ops_per_step() / (msx / 1e3) / 1e12
+                pk = INT8_PEAK_TOPS if v == INT8_EXACT else BF16_PEAK_TFLOPS
+                extra[f"{name}_{vname}"] = {
+                    "tops": round(t, 2), "ms_per_step": round(msx, 4),
+                    "pct_mfma_peak": round(100 * t / pk, 2),
+                    "kernels": {k: round(vv["us_per_launch"], 2) for k, vv in kx.items()}}
+                del Lx
+
+    line = {
+        "metric": "Q8_0 matmul TOPS (% MFMA peak); 512-tok embeddings/sec on 1 MI355X",
+        "value": round(tops, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8" if variant == INT8_EXACT else "bf16", "data": "synthetic",
+        "config": {"workload": "C2: one EmbeddingGemma layer's 7 Q8_0 projections at T=512 "
+                               "(RMSNorm->qkv, o, RMSNorm->gate/up+GeGLU->down)",
+                   "T": m, "hidden": H, "ffn": F, "q_dim": NQ, "kv_dim": NKV,
+                   "variant": "INT8_EXACT" if variant == INT8_EXACT else "BF16_DEQUANT",
+                   "ops_per_step": L.ops_per_step()},
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    line["extra"] = extra
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

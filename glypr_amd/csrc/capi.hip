@@ -1,0 +1,698 @@
+// capi.hip — the C ABI (include/glypr_hip.h): argument validation, weight
+// handles, workspace management and kernel dispatch.
+//
+// Validation order in every entry point: scalar arguments (sizes, variant),
+// then pointers (null, 16-byte alignment), then context/device.  Nothing is
+// launched or allocated before all three pass, so every error path can be
+// exercised on a machine without a GPU.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include "internal.hpp"
+
+namespace glypr {
+
+static thread_local char g_err[512];
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_error(hipError_t e, const char* what) {
+  if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+    return set_error(GLYPR_ERR_OOM, "%s: %s", what, hipGetErrorString(e));
+  return set_error(GLYPR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+namespace {
+
+inline void clear_error() { g_err[0] = '\0'; }
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+#define GLYPR_TRY_HIP(expr, what)              \
+  do {                                         \
+    hipError_t e_ = (expr);                    \
+    if (e_ != hipSuccess) return hip_error(e_, what); \
+  } while (0)
+
+#define GLYPR_CHECK(cond, code, ...)                     \
+  do {                                                   \
+    if (!(cond)) return set_error(code, __VA_ARGS__);    \
+  } while (0)
+
+// Make ctx->device current for the duration of a call.
+struct DeviceScope {
+  int prev = -1;
+  bool changed = false;
+  hipError_t err = hipSuccess;
+  explicit DeviceScope(int dev) {
+    err = hipGetDevice(&prev);
+    if (err == hipSuccess && prev != dev) {
+      err = hipSetDevice(dev);
+      changed = err == hipSuccess;
+    }
+  }
+  ~DeviceScope() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Grow the context workspace to at least `bytes`.  Growth waits for the device
+// so no queued kernel still reads the old buffer.
+int ensure_ws(glypr_hip_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->ws_cap) return GLYPR_OK;
+  size_t cap = align_up(bytes + bytes / 4, 1 << 21);
+  if (ctx->ws) {
+    GLYPR_TRY_HIP(hipDeviceSynchronize(), "workspace growth: hipDeviceSynchronize");
+    GLYPR_TRY_HIP(hipFree(ctx->ws), "workspace growth: hipFree");
+    ctx->ws = nullptr;
+    ctx->ws_cap = 0;
+  }
+  GLYPR_TRY_HIP(hipMalloc(&ctx->ws, cap), "workspace: hipMalloc");
+  ctx->ws_cap = cap;
+  return GLYPR_OK;
+}
+
+template <typename T>
+int ensure_staging(T*& ptr, size_t& cap, size_t count) {
+  if (count <= cap) return GLYPR_OK;
+  size_t n = align_up(count, 4096);
+  if (ptr) {
+    GLYPR_TRY_HIP(hipDeviceSynchronize(), "staging growth: hipDeviceSynchronize");
+    GLYPR_TRY_HIP(hipFree(ptr), "staging growth: hipFree");
+    ptr = nullptr;
+    cap = 0;
+  }
+  GLYPR_TRY_HIP(hipMalloc((void**)&ptr, n * sizeof(T)), "staging: hipMalloc");
+  cap = n;
+  return GLYPR_OK;
+}
+
+// Bump allocator over the workspace.
+struct Carve {
+  char* base;
+  size_t off = 0;
+  explicit Carve(void* b) : base((char*)b) {}
+  template <typename T>
+  T* take(size_t count) {
+    off = align_up(off, 256);
+    T* p = (T*)(base + off);
+    off += count * sizeof(T);
+    return p;
+  }
+};
+
+inline size_t q8_act_bytes(int64_t m, int64_t k) {
+  return align_up((size_t)(m * k), 256) + align_up((size_t)(m * (k / 32)) * 4, 256);
+}
+
+int check_ctx(glypr_hip_ctx* ctx) {
+  GLYPR_CHECK(ctx != nullptr, GLYPR_ERR_INVALID_ARG, "ctx is NULL");
+  return GLYPR_OK;
+}
+
+int check_weight_device(const glypr_hip_ctx* ctx, const glypr_q8w* w, const char* name) {
+  GLYPR_CHECK(w->buf->device == ctx->device, GLYPR_ERR_DEVICE,
+              "%s lives on device %d, context is device %d", name, w->buf->device, ctx->device);
+  return GLYPR_OK;
+}
+
+int check_variant(int variant) {
+  GLYPR_CHECK(variant == GLYPR_Q8_INT8_EXACT || variant == GLYPR_Q8_BF16_DEQUANT,
+              GLYPR_ERR_UNSUPPORTED, "unknown Q8_0 variant %d", variant);
+  return GLYPR_OK;
+}
+
+#define RET_IF(x)              \
+  do {                         \
+    int rc_ = (x);             \
+    if (rc_ != GLYPR_OK) return rc_; \
+  } while (0)
+
+hipEvent_t get_event(glypr_hip_ctx* ctx) {
+  if (!ctx->event_pool.empty()) {
+    hipEvent_t e = ctx->event_pool.back();
+    ctx->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+// While profiling is on, brackets one kernel launch with events on its stream.
+struct ProfScope {
+  glypr_hip_ctx* ctx;
+  int kernel;
+  hipStream_t s;
+  hipEvent_t a = nullptr, b = nullptr;
+  ProfScope(glypr_hip_ctx* c, int k, hipStream_t st) : ctx(c), kernel(k), s(st) {
+    if (!ctx->profiling) return;
+    a = get_event(ctx);
+    b = get_event(ctx);
+    if (a && b) (void)hipEventRecord(a, s);
+  }
+  ~ProfScope() {
+    if (a && b) {
+      (void)hipEventRecord(b, s);
+      ctx->prof.push_back({kernel, a, b});
+    }
+  }
+};
+
+#define LAUNCH(kid, s, expr, what)                       \
+  do {                                                   \
+    ProfScope ps_(ctx, kid, s);                          \
+    hipError_t e_ = (expr);                              \
+    if (e_ != hipSuccess) return hip_error(e_, what);    \
+  } while (0)
+
+// Shared body of the plain and RMSNorm-prologue matmuls.
+int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const float* norm_w,
+                float eps, bool norm, float* y, int64_t m, int variant, hipStream_t s) {
+  const int64_t n = w->n, k = w->k;
+  if (variant == GLYPR_Q8_INT8_EXACT) {
+    RET_IF(ensure_ws(ctx, q8_act_bytes(m, k)));
+    Carve c(ctx->ws);
+    int8_t* xq = c.take<int8_t>((size_t)(m * k));
+    float* dx = c.take<float>((size_t)(m * (k / 32)));
+    if (norm)
+      LAUNCH(GLYPR_K_RMSNORM_QUANT, s, launch_rmsnorm_quant(x, norm_w, eps, m, k, xq, dx, s),
+             "rmsnorm_quant launch");
+    else
+      LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(x, m, k, xq, dx, s), "quantize launch");
+    LAUNCH(GLYPR_K_GEMM_I8, s, launch_gemm_i8(xq, dx, w->qs(), w->dw(), y, m, n, k, n, s),
+           "gemm_i8 launch");
+    return GLYPR_OK;
+  }
+  RET_IF(ensure_ws(ctx, align_up((size_t)(m * k) * 2, 256)));
+  Carve c(ctx->ws);
+  uint16_t* xb = c.take<uint16_t>((size_t)(m * k));
+  if (norm)
+    LAUNCH(GLYPR_K_RMSNORM_BF16, s, launch_rmsnorm_bf16(x, norm_w, eps, m, k, xb, s),
+           "rmsnorm_bf16 launch");
+  else
+    LAUNCH(GLYPR_K_TO_BF16, s, launch_to_bf16(x, m * k, xb, s), "to_bf16 launch");
+  LAUNCH(GLYPR_K_GEMM_BF16, s, launch_gemm_bf16(xb, w->qs(), w->dw(), y, m, n, k, n, s),
+         "gemm_bf16 launch");
+  return GLYPR_OK;
+}
+
+int mlp_impl(glypr_hip_ctx* ctx, const glypr_q8w* gu, const glypr_q8w* down, const float* x,
+             const float* norm_w, float eps, bool norm, float* y, int64_t m, int variant,
+             hipStream_t s) {
+  const int64_t H = gu->k, F = down->k;
+  if (variant == GLYPR_Q8_INT8_EXACT) {
+    RET_IF(ensure_ws(ctx, q8_act_bytes(m, H) + q8_act_bytes(m, F)));
+    Carve c(ctx->ws);
+    int8_t* xq = c.take<int8_t>((size_t)(m * H));
+    float* dx = c.take<float>((size_t)(m * (H / 32)));
+    int8_t* hq = c.take<int8_t>((size_t)(m * F));
+    float* dh = c.take<float>((size_t)(m * (F / 32)));
+    if (norm)
+      LAUNCH(GLYPR_K_RMSNORM_QUANT, s, launch_rmsnorm_quant(x, norm_w, eps, m, H, xq, dx, s),
+             "rmsnorm_quant launch");
+    else
+      LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(x, m, H, xq, dx, s), "quantize launch");
+    LAUNCH(GLYPR_K_GEMM_I8_GEGLU, s,
+           launch_gemm_i8_geglu(xq, dx, gu->qs(), gu->dw(), hq, dh, m, F, H, s),
+           "gate/up GeGLU launch");
+    LAUNCH(GLYPR_K_GEMM_I8, s, launch_gemm_i8(hq, dh, down->qs(), down->dw(), y, m, H, F, H, s),
+           "down launch");
+    return GLYPR_OK;
+  }
+  RET_IF(ensure_ws(ctx, align_up((size_t)(m * H) * 2, 256) + align_up((size_t)(m * F) * 2, 256)));
+  Carve c(ctx->ws);
+  uint16_t* xb = c.take<uint16_t>((size_t)(m * H));
+  uint16_t* hb = c.take<uint16_t>((size_t)(m * F));
+  if (norm)
+    LAUNCH(GLYPR_K_RMSNORM_BF16, s, launch_rmsnorm_bf16(x, norm_w, eps, m, H, xb, s),
+           "rmsnorm_bf16 launch");
+  else
+    LAUNCH(GLYPR_K_TO_BF16, s, launch_to_bf16(x, m * H, xb, s), "to_bf16 launch");
+  LAUNCH(GLYPR_K_GEMM_BF16_GEGLU, s, launch_gemm_bf16_geglu(xb, gu->qs(), gu->dw(), hb, m, F, H, s),
+         "bf16 gate/up GeGLU launch");
+  LAUNCH(GLYPR_K_GEMM_BF16, s, launch_gemm_bf16(hb, down->qs(), down->dw(), y, m, H, F, H, s),
+         "bf16 down launch");
+  return GLYPR_OK;
+}
+
+int check_mlp_args(const glypr_q8w* gu, const glypr_q8w* down, const float* x, float* y,
+                   int64_t m, int variant) {
+  GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
+  RET_IF(check_variant(variant));
+  GLYPR_CHECK(gu != nullptr && down != nullptr, GLYPR_ERR_INVALID_ARG, "weight handle is NULL");
+  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(aligned16(x) && aligned16(y), GLYPR_ERR_ALIGNMENT,
+              "x and y must be 16-byte aligned");
+  GLYPR_CHECK(gu->n == 2 * down->k, GLYPR_ERR_SHAPE,
+              "gate_up has %lld rows, expected 2 x down.in_dim = %lld", (long long)gu->n,
+              (long long)(2 * down->k));
+  GLYPR_CHECK(down->n == gu->k, GLYPR_ERR_SHAPE,
+              "down.out_dim %lld != gate_up.in_dim %lld", (long long)down->n, (long long)gu->k);
+  return GLYPR_OK;
+}
+
+}  // namespace
+}  // namespace glypr
+
+using namespace glypr;
+
+extern "C" {
+
+const char* glypr_hip_last_error(void) { return g_err; }
+
+int glypr_hip_abi_version(void) { return GLYPR_HIP_ABI_VERSION; }
+
+int glypr_hip_ctx_create(int device, glypr_hip_ctx** out) {
+  clear_error();
+  GLYPR_CHECK(out != nullptr, GLYPR_ERR_INVALID_ARG, "out is NULL");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  GLYPR_CHECK(e == hipSuccess && count > 0, GLYPR_ERR_DEVICE, "no HIP device available (%s)",
+              e == hipSuccess ? "count 0" : hipGetErrorString(e));
+  GLYPR_CHECK(device >= 0 && device < count, GLYPR_ERR_DEVICE, "device %d out of range [0,%d)",
+              device, count);
+  DeviceScope ds(device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  hipDeviceProp_t prop;
+  GLYPR_TRY_HIP(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  glypr_hip_ctx* ctx = new (std::nothrow) glypr_hip_ctx();
+  GLYPR_CHECK(ctx != nullptr, GLYPR_ERR_OOM, "host allocation failed");
+  ctx->device = device;
+  ctx->cu_count = prop.multiProcessorCount;
+  *out = ctx;
+  return GLYPR_OK;
+}
+
+int glypr_hip_ctx_destroy(glypr_hip_ctx* ctx) {
+  clear_error();
+  if (!ctx) return GLYPR_OK;
+  {
+    DeviceScope ds(ctx->device);
+    (void)hipDeviceSynchronize();
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->ids) (void)hipFree(ctx->ids);
+    if (ctx->mask) (void)hipFree(ctx->mask);
+    for (auto& r : ctx->prof) {
+      (void)hipEventDestroy(r.start);
+      (void)hipEventDestroy(r.stop);
+    }
+    for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+  }
+  delete ctx;
+  return GLYPR_OK;
+}
+
+int glypr_hip_sync(glypr_hip_ctx* ctx, glypr_stream stream) {
+  clear_error();
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  GLYPR_TRY_HIP(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_weight_create(glypr_hip_ctx* ctx, const uint8_t* gguf_blocks, int64_t n,
+                                 int64_t k, glypr_q8w** out) {
+  clear_error();
+  GLYPR_CHECK(n > 0 && k > 0, GLYPR_ERR_SHAPE, "weight shape (%lld, %lld) must be positive",
+              (long long)n, (long long)k);
+  GLYPR_CHECK(k % 32 == 0, GLYPR_ERR_SHAPE, "in_dim %lld is not a multiple of 32",
+              (long long)k);
+  GLYPR_CHECK(gguf_blocks != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG,
+              "gguf_blocks or out is NULL");
+  *out = nullptr;
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  const size_t nblk = (size_t)(n * (k / 32));
+  Q8Buffer* buf = new (std::nothrow) Q8Buffer();
+  GLYPR_CHECK(buf != nullptr, GLYPR_ERR_OOM, "host allocation failed");
+  buf->rows = n;
+  buf->k = k;
+  buf->device = ctx->device;
+  uint8_t* tmp = nullptr;
+  hipError_t e = hipMalloc((void**)&buf->qs, (size_t)(n * k));
+  if (e == hipSuccess) e = hipMalloc((void**)&buf->dw, nblk * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc((void**)&tmp, nblk * 34);
+  if (e == hipSuccess) e = hipMemcpy(tmp, gguf_blocks, nblk * 34, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = launch_repack(tmp, buf->qs, buf->dw, n, k, nullptr);
+  if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  if (tmp) (void)hipFree(tmp);
+  if (e != hipSuccess) {
+    if (buf->qs) (void)hipFree(buf->qs);
+    if (buf->dw) (void)hipFree(buf->dw);
+    delete buf;
+    return hip_error(e, "weight upload/repack");
+  }
+  glypr_q8w* w = new (std::nothrow) glypr_q8w{buf, 0, n, k};
+  if (!w) {
+    (void)hipFree(buf->qs);
+    (void)hipFree(buf->dw);
+    delete buf;
+    return set_error(GLYPR_ERR_OOM, "host allocation failed");
+  }
+  *out = w;
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_weight_concat(glypr_hip_ctx* ctx, const glypr_q8w* const* parts, int count,
+                                 glypr_q8w** fused, glypr_q8w** views) {
+  clear_error();
+  GLYPR_CHECK(count >= 2, GLYPR_ERR_SHAPE, "concat needs at least 2 parts, got %d", count);
+  GLYPR_CHECK(parts != nullptr && fused != nullptr, GLYPR_ERR_INVALID_ARG,
+              "parts or fused is NULL");
+  *fused = nullptr;
+  int64_t rows = 0, k = -1;
+  for (int i = 0; i < count; i++) {
+    GLYPR_CHECK(parts[i] != nullptr, GLYPR_ERR_INVALID_ARG, "parts[%d] is NULL", i);
+    if (k < 0) k = parts[i]->k;
+    GLYPR_CHECK(parts[i]->k == k, GLYPR_ERR_SHAPE, "parts[%d] in_dim %lld != %lld", i,
+                (long long)parts[i]->k, (long long)k);
+    rows += parts[i]->n;
+  }
+  RET_IF(check_ctx(ctx));
+  for (int i = 0; i < count; i++) RET_IF(check_weight_device(ctx, parts[i], "part"));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  Q8Buffer* buf = new (std::nothrow) Q8Buffer();
+  GLYPR_CHECK(buf != nullptr, GLYPR_ERR_OOM, "host allocation failed");
+  buf->rows = rows;
+  buf->k = k;
+  buf->device = ctx->device;
+  const int64_t nb = k / 32;
+  hipError_t e = hipMalloc((void**)&buf->qs, (size_t)(rows * k));
+  if (e == hipSuccess) e = hipMalloc((void**)&buf->dw, (size_t)(rows * nb) * sizeof(float));
+  int64_t off = 0;
+  for (int i = 0; i < count && e == hipSuccess; i++) {
+    e = hipMemcpy(buf->qs + off * k, parts[i]->qs(), (size_t)(parts[i]->n * k),
+                  hipMemcpyDeviceToDevice);
+    if (e == hipSuccess)
+      e = hipMemcpy(buf->dw + off * nb, parts[i]->dw(), (size_t)(parts[i]->n * nb) * sizeof(float),
+                    hipMemcpyDeviceToDevice);
+    off += parts[i]->n;
+  }
+  if (e != hipSuccess) {
+    if (buf->qs) (void)hipFree(buf->qs);
+    if (buf->dw) (void)hipFree(buf->dw);
+    delete buf;
+    return hip_error(e, "concat copy");
+  }
+  glypr_q8w* f = new glypr_q8w{buf, 0, rows, k};
+  if (views) {
+    int64_t r0 = 0;
+    for (int i = 0; i < count; i++) {
+      buf->refs.fetch_add(1);
+      views[i] = new glypr_q8w{buf, r0, parts[i]->n, k};
+      r0 += parts[i]->n;
+    }
+  }
+  *fused = f;
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_weight_view(const glypr_q8w* w, int64_t row0, int64_t rows, glypr_q8w** out) {
+  clear_error();
+  GLYPR_CHECK(w != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "w or out is NULL");
+  GLYPR_CHECK(row0 >= 0 && rows > 0 && row0 + rows <= w->n, GLYPR_ERR_SHAPE,
+              "view [%lld, %lld) outside %lld rows", (long long)row0, (long long)(row0 + rows),
+              (long long)w->n);
+  w->buf->refs.fetch_add(1);
+  *out = new glypr_q8w{w->buf, w->row0 + row0, rows, w->k};
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_weight_destroy(glypr_q8w* w) {
+  clear_error();
+  if (!w) return GLYPR_OK;
+  Q8Buffer* buf = w->buf;
+  delete w;
+  if (buf->refs.fetch_sub(1) == 1) {
+    DeviceScope ds(buf->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(buf->qs);
+    (void)hipFree(buf->dw);
+    delete buf;
+  }
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_weight_shape(const glypr_q8w* w, int64_t* n, int64_t* k) {
+  clear_error();
+  GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
+  if (n) *n = w->n;
+  if (k) *k = w->k;
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_dequantize(glypr_hip_ctx* ctx, const glypr_q8w* w, float* out,
+                              glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(w != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "w or out is NULL");
+  GLYPR_CHECK(aligned16(out), GLYPR_ERR_ALIGNMENT, "out must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  RET_IF(check_weight_device(ctx, w, "w"));
+  DeviceScope ds(ctx->device);
+  LAUNCH(GLYPR_K_DEQUANT, (hipStream_t)stream,
+         launch_dequant(w->qs(), w->dw(), w->n, w->k, out, (hipStream_t)stream),
+         "dequantize launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_quantize(glypr_hip_ctx* ctx, const float* x, int64_t m, int64_t k,
+                            uint8_t* out_blocks, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(m >= 0 && k > 0, GLYPR_ERR_SHAPE, "shape (%lld, %lld) invalid", (long long)m,
+              (long long)k);
+  GLYPR_CHECK(k % 32 == 0, GLYPR_ERR_SHAPE, "k %lld is not a multiple of 32", (long long)k);
+  GLYPR_CHECK(x != nullptr && out_blocks != nullptr, GLYPR_ERR_INVALID_ARG,
+              "x or out_blocks is NULL");
+  GLYPR_CHECK(aligned16(x) && ((uintptr_t)out_blocks & 1u) == 0, GLYPR_ERR_ALIGNMENT,
+              "x must be 16-byte and out_blocks 2-byte aligned");
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  LAUNCH(GLYPR_K_QUANTIZE, (hipStream_t)stream,
+         launch_quantize_gguf(x, m, k, out_blocks, (hipStream_t)stream), "quantize launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, float* y,
+                          int64_t m, int variant, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
+  RET_IF(check_variant(variant));
+  GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
+  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(aligned16(x) && aligned16(y), GLYPR_ERR_ALIGNMENT,
+              "x and y must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  RET_IF(check_weight_device(ctx, w, "w"));
+  if (m == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return matmul_impl(ctx, w, x, nullptr, 0.0f, false, y, m, variant, (hipStream_t)stream);
+}
+
+int glypr_hip_rmsnorm(glypr_hip_ctx* ctx, const float* x, const float* weight, float eps,
+                      float* y, int64_t rows, int64_t dim, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(rows >= 0 && dim > 0, GLYPR_ERR_SHAPE, "shape (%lld, %lld) invalid",
+              (long long)rows, (long long)dim);
+  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  RET_IF(check_ctx(ctx));
+  if (rows == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  LAUNCH(GLYPR_K_RMSNORM, (hipStream_t)stream,
+         launch_rmsnorm(x, weight, eps, y, rows, dim, (hipStream_t)stream), "rmsnorm launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_rmsnorm_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x,
+                                  const float* norm_weight, float eps, float* y, int64_t m,
+                                  int variant, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
+  RET_IF(check_variant(variant));
+  GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
+  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(aligned16(x) && aligned16(y) && aligned16(norm_weight), GLYPR_ERR_ALIGNMENT,
+              "x, y and norm_weight must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  RET_IF(check_weight_device(ctx, w, "w"));
+  if (m == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return matmul_impl(ctx, w, x, norm_weight, eps, true, y, m, variant, (hipStream_t)stream);
+}
+
+int glypr_hip_geglu(glypr_hip_ctx* ctx, const float* gate, const float* up, float* out,
+                    int64_t n, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(n >= 0, GLYPR_ERR_SHAPE, "n = %lld is negative", (long long)n);
+  GLYPR_CHECK(gate != nullptr && up != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG,
+              "gate, up or out is NULL");
+  RET_IF(check_ctx(ctx));
+  if (n == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  LAUNCH(GLYPR_K_GEGLU, (hipStream_t)stream, launch_geglu(gate, up, out, n, (hipStream_t)stream),
+         "geglu launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_mlp(glypr_hip_ctx* ctx, const glypr_q8w* gate_up, const glypr_q8w* down,
+                  const float* x, float* y, int64_t m, int variant, glypr_stream stream) {
+  clear_error();
+  RET_IF(check_mlp_args(gate_up, down, x, y, m, variant));
+  RET_IF(check_ctx(ctx));
+  RET_IF(check_weight_device(ctx, gate_up, "gate_up"));
+  RET_IF(check_weight_device(ctx, down, "down"));
+  if (m == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return mlp_impl(ctx, gate_up, down, x, nullptr, 0.0f, false, y, m, variant,
+                  (hipStream_t)stream);
+}
+
+int glypr_hip_rmsnorm_mlp(glypr_hip_ctx* ctx, const glypr_q8w* gate_up, const glypr_q8w* down,
+                          const float* x, const float* norm_weight, float eps, float* y,
+                          int64_t m, int variant, glypr_stream stream) {
+  clear_error();
+  RET_IF(check_mlp_args(gate_up, down, x, y, m, variant));
+  GLYPR_CHECK(aligned16(norm_weight), GLYPR_ERR_ALIGNMENT, "norm_weight must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  RET_IF(check_weight_device(ctx, gate_up, "gate_up"));
+  RET_IF(check_weight_device(ctx, down, "down"));
+  if (m == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return mlp_impl(ctx, gate_up, down, x, norm_weight, eps, true, y, m, variant,
+                  (hipStream_t)stream);
+}
+
+int glypr_hip_q8_0_embed_gather(glypr_hip_ctx* ctx, const glypr_q8w* table, const uint32_t* ids,
+                                int64_t n_ids, float scale, float* out, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(n_ids >= 0, GLYPR_ERR_SHAPE, "n_ids = %lld is negative", (long long)n_ids);
+  GLYPR_CHECK(table != nullptr, GLYPR_ERR_INVALID_ARG, "table is NULL");
+  GLYPR_CHECK((ids != nullptr || n_ids == 0) && out != nullptr, GLYPR_ERR_INVALID_ARG,
+              "ids or out is NULL");
+  GLYPR_CHECK(aligned16(out), GLYPR_ERR_ALIGNMENT, "out must be 16-byte aligned");
+  for (int64_t i = 0; i < n_ids; i++)
+    GLYPR_CHECK((int64_t)ids[i] < table->n, GLYPR_ERR_RANGE,
+                "token id %u at position %lld is out of range for vocab %lld", ids[i],
+                (long long)i, (long long)table->n);
+  RET_IF(check_ctx(ctx));
+  RET_IF(check_weight_device(ctx, table, "table"));
+  if (n_ids == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  RET_IF(ensure_staging(ctx->ids, ctx->ids_cap, (size_t)n_ids));
+  GLYPR_TRY_HIP(hipMemcpyAsync(ctx->ids, ids, (size_t)n_ids * 4, hipMemcpyHostToDevice,
+                               (hipStream_t)stream),
+                "ids upload");
+  LAUNCH(GLYPR_K_GATHER, (hipStream_t)stream,
+         launch_gather(table->qs(), table->dw(), table->k, ctx->ids, n_ids, scale, out,
+                       (hipStream_t)stream),
+         "gather launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_pool_normalize(glypr_hip_ctx* ctx, const float* tokens, const uint8_t* mask,
+                             int64_t t, int64_t d, int64_t trunc, float* out,
+                             glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(t > 0 && d > 0 && trunc >= 0, GLYPR_ERR_SHAPE, "shape (t=%lld, d=%lld, trunc=%lld)",
+              (long long)t, (long long)d, (long long)trunc);
+  GLYPR_CHECK(tokens != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG,
+              "tokens or out is NULL");
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  RET_IF(ensure_ws(ctx, (size_t)d * sizeof(float)));
+  const uint8_t* dmask = nullptr;
+  if (mask) {
+    RET_IF(ensure_staging(ctx->mask, ctx->mask_cap, (size_t)t));
+    GLYPR_TRY_HIP(hipMemcpyAsync(ctx->mask, mask, (size_t)t, hipMemcpyHostToDevice,
+                                 (hipStream_t)stream),
+                  "mask upload");
+    dmask = ctx->mask;
+  }
+  LAUNCH(GLYPR_K_POOL, (hipStream_t)stream,
+         launch_pool(tokens, dmask, t, d, trunc, out, (float*)ctx->ws, (hipStream_t)stream),
+         "pool launch");
+  return GLYPR_OK;
+}
+
+static const char* const kKernelNames[GLYPR_K_COUNT] = {
+    "quantize",   "rmsnorm_quant",  "gemm_i8", "gemm_i8_geglu", "to_bf16", "rmsnorm_bf16",
+    "gemm_bf16",  "gemm_bf16_geglu", "rmsnorm", "geglu",         "gather",  "dequant",
+    "pool"};
+
+const char* glypr_hip_kernel_name(int id) {
+  return (id >= 0 && id < GLYPR_K_COUNT) ? kKernelNames[id] : "";
+}
+
+static int drain_profile(glypr_hip_ctx* ctx) {
+  int rc = GLYPR_OK;
+  for (auto& r : ctx->prof) {
+    float ms = 0.0f;
+    hipError_t e = hipEventSynchronize(r.stop);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.start, r.stop);
+    if (e != hipSuccess && rc == GLYPR_OK) rc = hip_error(e, "profile event");
+    ctx->prof_ms[r.kernel] += ms;
+    ctx->prof_n[r.kernel] += 1;
+    ctx->event_pool.push_back(r.start);
+    ctx->event_pool.push_back(r.stop);
+  }
+  ctx->prof.clear();
+  return rc;
+}
+
+int glypr_hip_profile_enable(glypr_hip_ctx* ctx, int enable) {
+  clear_error();
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  int rc = drain_profile(ctx);
+  for (int i = 0; i < GLYPR_K_COUNT; i++) {
+    ctx->prof_ms[i] = 0.0;
+    ctx->prof_n[i] = 0;
+  }
+  ctx->profiling = enable != 0;
+  return rc;
+}
+
+int glypr_hip_profile_read(glypr_hip_ctx* ctx, double* total_ms, int64_t* launches) {
+  clear_error();
+  GLYPR_CHECK(total_ms != nullptr && launches != nullptr, GLYPR_ERR_INVALID_ARG,
+              "total_ms or launches is NULL");
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  int rc = drain_profile(ctx);
+  for (int i = 0; i < GLYPR_K_COUNT; i++) {
+    total_ms[i] = ctx->prof_ms[i];
+    launches[i] = ctx->prof_n[i];
+  }
+  return rc;
+}
+
+}  // extern "C"

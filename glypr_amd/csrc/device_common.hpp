@@ -1,0 +1,106 @@
+// device_common.hpp — device helpers shared by the gfx950 kernels.
+//
+// Everything here must round exactly like glypr's CPU path on x86-64, so the
+// library is compiled with -ffp-contract=off (no implicit FMA, as in Rust) and
+// uses fmaf only where the reference itself fuses (pulp mul_add in RMSNorm).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glypr {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int QK = 32;                // Q8_0 block length along K
+constexpr int BLOCK_BYTES = 34;       // GGUF Q8_0 block: f16 d + 32 x int8
+
+// f32 -> f16 with round-to-nearest-even (v_cvt_f16_f32 in the default mode),
+// overflow to inf, subnormals kept: half 2.7.1's f16::from_f32.
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+
+// Rust `f32::round(v) as i8`: half away from zero, saturating, NaN -> 0.
+__device__ __forceinline__ int quant_round(float v) {
+  float r = roundf(v);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return (v != v) ? 0 : (int)r;
+}
+
+// BlockQ8_0::from_float scale: d = amax / 127; id = d != 0 ? 1/d : 0.
+// IEEE division (hipcc's default correctly rounded f32 divide).
+struct QScale {
+  float d;    // f32 scale (id is derived from it)
+  float id;   // inverse used for rounding
+  float dq;   // f32(f16(d)): the scale every later dot product sees
+  uint16_t dbits;
+};
+__device__ __forceinline__ QScale q8_scale(float amax) {
+  QScale s;
+  s.d = amax / 127.0f;
+  s.id = (s.d != 0.0f) ? 1.0f / s.d : 0.0f;
+  s.dbits = f32_to_f16_bits(s.d);
+  s.dq = f16_bits_to_f32(s.dbits);
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// tanh for GeGLU.  glypr's geglu_scalar_f32 calls the platform libm tanh, so
+// its bits differ between glibc and Apple libm.  The backend defines tanh as
+//   tanh|x| = -t / (t + 2),  t = expm1(-2|x|),
+// expm1 by Cody-Waite reduction y = k*ln2 + r (float ln2 hi/lo split as in
+// fdlibm), |r| <= ln2/2, degree-8 Taylor polynomial in Horner form with fma,
+// expm1(y) = 2^k * p + (2^k - 1).  Only IEEE +,-,*,/ and fma appear, so the
+// CPU oracle computes the same bits.  Max error ~2.5 ulp vs exact tanh.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float expm1_nonpos(float y) {
+  if (y < -30.0f) return -1.0f;
+  const float LOG2E = 1.44269504088896341f;
+  const float LN2_HI = 6.93145751953125e-01f;
+  const float LN2_LO = 1.42860682030941723e-06f;
+  float kf = rintf(y * LOG2E);
+  float r = fmaf(-kf, LN2_HI, y);
+  r = fmaf(-kf, LN2_LO, r);
+  float p = fmaf(r, 2.48015873015873016e-05f, 1.98412698412698413e-04f);
+  p = fmaf(r, p, 1.38888888888888889e-03f);
+  p = fmaf(r, p, 8.33333333333333333e-03f);
+  p = fmaf(r, p, 4.16666666666666667e-02f);
+  p = fmaf(r, p, 1.66666666666666667e-01f);
+  p = fmaf(r, p, 0.5f);
+  p = fmaf(r * r, p, r);
+  int k = (int)kf;
+  if (k == 0) return p;
+  float s = __int_as_float((k + 127) << 23);
+  return fmaf(s, p, s - 1.0f);
+}
+
+__device__ __forceinline__ float tanh_glypr(float x) {
+  float ax = fabsf(x);
+  if (x != x) return x;
+  if (ax >= 10.0f) return copysignf(1.0f, x);
+  if (ax < 2.44140625e-04f) return x;
+  float t = expm1_nonpos(-2.0f * ax);
+  float r = -t / (t + 2.0f);
+  return copysignf(r, x);
+}
+
+// geglu_scalar_f32 (cpu_simd/geglu.rs:6-18).
+__device__ __forceinline__ float geglu_scalar(float g, float u) {
+  if (g <= -10.0f) return 0.0f;
+  if (g >= 10.0f) return g * u;
+  float g3 = g * g * g;
+  float inner = 0.7978846f * (g + 0.044715f * g3);
+  float th = tanh_glypr(inner);
+  float act = 0.5f * g * (1.0f + th);
+  return act * u;
+}
+
+}  // namespace glypr

@@ -1,0 +1,101 @@
+// internal.hpp — host-side structures and kernel launchers of libglypr_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <mutex>
+#include <vector>
+
+#include "glypr_hip.h"
+
+// Device-resident Q8_0 weight, repacked once at load:
+//   qs: int8 [rows][k]      (16-byte aligned rows; k % 32 == 0)
+//   dw: f32  [rows][k/32]   (f32 of the GGUF f16 scale: exact)
+struct Q8Buffer {
+  int8_t* qs = nullptr;
+  float* dw = nullptr;
+  int64_t rows = 0, k = 0;
+  int device = 0;
+  std::atomic<int> refs{1};
+};
+
+struct glypr_q8w {
+  Q8Buffer* buf;
+  int64_t row0;  // first row of this view inside buf
+  int64_t n, k;  // out_dim, in_dim
+  const int8_t* qs() const { return buf->qs + row0 * k; }
+  const float* dw() const { return buf->dw + row0 * (k / 32); }
+};
+
+struct ProfRec {
+  int kernel;
+  hipEvent_t start, stop;
+};
+
+struct glypr_hip_ctx {
+  int device = 0;
+  bool profiling = false;
+  std::vector<ProfRec> prof;          // recorded, not yet read
+  std::vector<hipEvent_t> event_pool; // reusable events
+  double prof_ms[GLYPR_K_COUNT] = {};
+  int64_t prof_n[GLYPR_K_COUNT] = {};
+  int cu_count = 0;
+  std::mutex mu;
+  void* ws = nullptr;       // activation workspace (quantized operands)
+  size_t ws_cap = 0;
+  uint32_t* ids = nullptr;  // token-id staging for the gather
+  size_t ids_cap = 0;
+  uint8_t* mask = nullptr;  // pooling-mask staging
+  size_t mask_cap = 0;
+};
+
+namespace glypr {
+
+// error.cpp-style helpers (defined in capi.hip)
+int set_error(int code, const char* fmt, ...);
+int hip_error(hipError_t e, const char* what);
+
+// ---- k_codec.hip ----
+hipError_t launch_repack(const uint8_t* gguf, int8_t* qs, float* dw, int64_t rows, int64_t k,
+                         hipStream_t s);
+hipError_t launch_dequant(const int8_t* qs, const float* dw, int64_t rows, int64_t k, float* out,
+                          hipStream_t s);
+hipError_t launch_gather(const int8_t* qs, const float* dw, int64_t k, const uint32_t* ids,
+                         int64_t n_ids, float scale, float* out, hipStream_t s);
+hipError_t launch_quantize_planar(const float* x, int64_t m, int64_t k, int8_t* xq, float* dx,
+                                  hipStream_t s);
+hipError_t launch_quantize_gguf(const float* x, int64_t m, int64_t k, uint8_t* out,
+                                hipStream_t s);
+hipError_t launch_to_bf16(const float* x, int64_t n, uint16_t* out, hipStream_t s);
+
+// ---- k_norm.hip ----
+hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* y, int64_t rows,
+                          int64_t dim, hipStream_t s);
+hipError_t launch_rmsnorm_quant(const float* x, const float* w, float eps, int64_t rows,
+                                int64_t dim, int8_t* xq, float* dx, hipStream_t s);
+hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_t rows,
+                               int64_t dim, uint16_t* xb, hipStream_t s);
+hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, hipStream_t s);
+hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t d, int64_t trunc,
+                       float* out, float* scratch /* d floats */, hipStream_t s);
+
+// ---- k_gemm_i8.hip ----
+// y[m,n] = sum_b ((float)S_b * dw[n,b]) * dx[m,b], sequential over b (exact).
+hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                          float* y, int64_t M, int64_t N, int64_t K, int64_t ldc,
+                          hipStream_t s);
+// Gate/up GEMM ([gate; up] rows, 2F x K) with GeGLU + Q8_0 quantization epilogue:
+// hq int8 [M][F], dh f32 [M][F/32].
+hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t* wq,
+                                const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
+                                int64_t K, hipStream_t s);
+
+// ---- k_gemm_bf16.hip ----
+hipError_t launch_gemm_bf16(const uint16_t* xb, const int8_t* wq, const float* dw, float* y,
+                            int64_t M, int64_t N, int64_t K, int64_t ldc, hipStream_t s);
+hipError_t launch_gemm_bf16_geglu(const uint16_t* xb, const int8_t* wq, const float* dw,
+                                  uint16_t* hb, int64_t M, int64_t F, int64_t K, hipStream_t s);
+
+}  // namespace glypr

@@ -1,0 +1,227 @@
+"""Torch-tensor helpers over the C ABI (tests, bench, smoke).
+
+PyTorch only provides device memory and the current HIP stream here; every
+computation is a libglypr_hip.so kernel.  Tensors must be contiguous and live
+on the context's device.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import numpy as np
+import torch
+
+from ._lib import BF16_DEQUANT, INT8_EXACT, check, lib
+
+__all__ = ["Context", "Q8Weight", "INT8_EXACT", "BF16_DEQUANT", "q8_0_matmul",
+           "rmsnorm_q8_0_matmul", "rmsnorm", "geglu", "mlp", "rmsnorm_mlp", "dequantize",
+           "quantize", "embed_gather", "pool_normalize"]
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise ValueError("tensor must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class Context:
+    """glypr_hip_ctx for one device."""
+
+    def __init__(self, device: int = 0):
+        self.device = device
+        h = ctypes.c_void_p()
+        check(lib().glypr_hip_ctx_create(device, ctypes.byref(h)))
+        self.handle = h
+
+    @property
+    def stream(self):
+        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+
+    def sync(self):
+        check(lib().glypr_hip_sync(self.handle, self.stream))
+
+    def close(self):
+        if self.handle:
+            lib().glypr_hip_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check_tensor(self, t: torch.Tensor, name: str, dtype=torch.float32):
+        if t.device.type != "cuda" or t.device.index != self.device:
+            raise ValueError(f"{name} must be on cuda:{self.device}")
+        if t.dtype != dtype:
+            raise ValueError(f"{name} must be {dtype}")
+
+
+class Q8Weight:
+    """Opaque Q8_0 weight handle (LinearOp::from_gguf_tensor / try_concat)."""
+
+    def __init__(self, handle, n: int, k: int):
+        self.handle = handle
+        self.n = n
+        self.k = k
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, blocks: np.ndarray, n: int, k: int) -> "Q8Weight":
+        b = np.ascontiguousarray(blocks, dtype=np.uint8)
+        if b.size != n * (k // 32) * 34:
+            raise ValueError("blocks size does not match (n, k)")
+        h = ctypes.c_void_p()
+        check(lib().glypr_hip_q8_0_weight_create(ctx.handle, b.ctypes.data_as(ctypes.c_void_p),
+                                                 n, k, ctypes.byref(h)))
+        return cls(h, n, k)
+
+    @classmethod
+    def concat(cls, ctx: Context, parts: Sequence["Q8Weight"]):
+        arr = (ctypes.c_void_p * len(parts))(*[p.handle for p in parts])
+        views = (ctypes.c_void_p * len(parts))()
+        f = ctypes.c_void_p()
+        check(lib().glypr_hip_q8_0_weight_concat(ctx.handle, arr, len(parts), ctypes.byref(f),
+                                                 views))
+        fused = cls(f, sum(p.n for p in parts), parts[0].k)
+        vs = [cls(ctypes.c_void_p(views[i]), parts[i].n, parts[i].k) for i in range(len(parts))]
+        return fused, vs
+
+    def view(self, row0: int, rows: int) -> "Q8Weight":
+        h = ctypes.c_void_p()
+        check(lib().glypr_hip_q8_0_weight_view(self.handle, row0, rows, ctypes.byref(h)))
+        return Q8Weight(h, rows, self.k)
+
+    def shape(self):
+        n = ctypes.c_int64()
+        k = ctypes.c_int64()
+        check(lib().glypr_hip_q8_0_weight_shape(self.handle, ctypes.byref(n), ctypes.byref(k)))
+        return n.value, k.value
+
+    def close(self):
+        if self.handle:
+            lib().glypr_hip_q8_0_weight_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _out(x: torch.Tensor, shape, out: Optional[torch.Tensor]):
+    if out is None:
+        return torch.empty(shape, dtype=torch.float32, device=x.device)
+    return out
+
+
+def q8_0_matmul(ctx: Context, w: Q8Weight, x: torch.Tensor, variant: int = INT8_EXACT,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(x, "x")
+    m = x.numel() // w.k
+    y = _out(x, (*x.shape[:-1], w.n), out)
+    check(lib().glypr_hip_q8_0_matmul(ctx.handle, w.handle, _ptr(x), _ptr(y), m, variant,
+                                      ctx.stream))
+    return y
+
+
+def rmsnorm_q8_0_matmul(ctx: Context, w: Q8Weight, x: torch.Tensor,
+                        norm_weight: Optional[torch.Tensor], eps: float = 1e-6,
+                        variant: int = INT8_EXACT,
+                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(x, "x")
+    m = x.numel() // w.k
+    y = _out(x, (*x.shape[:-1], w.n), out)
+    check(lib().glypr_hip_rmsnorm_q8_0_matmul(ctx.handle, w.handle, _ptr(x), _ptr(norm_weight),
+                                              eps, _ptr(y), m, variant, ctx.stream))
+    return y
+
+
+def rmsnorm(ctx: Context, x: torch.Tensor, weight: Optional[torch.Tensor], eps: float = 1e-6,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(x, "x")
+    d = x.shape[-1]
+    y = _out(x, x.shape, out)
+    check(lib().glypr_hip_rmsnorm(ctx.handle, _ptr(x), _ptr(weight), eps, _ptr(y),
+                                  x.numel() // d, d, ctx.stream))
+    return y
+
+
+def geglu(ctx: Context, gate: torch.Tensor, up: torch.Tensor,
+          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(gate, "gate")
+    ctx._check_tensor(up, "up")
+    if gate.shape != up.shape:
+        raise ValueError("gate/up shape mismatch")
+    y = _out(gate, gate.shape, out)
+    check(lib().glypr_hip_geglu(ctx.handle, _ptr(gate), _ptr(up), _ptr(y), gate.numel(),
+                                ctx.stream))
+    return y
+
+
+def mlp(ctx: Context, gate_up: Q8Weight, down: Q8Weight, x: torch.Tensor,
+        variant: int = INT8_EXACT, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(x, "x")
+    m = x.numel() // gate_up.k
+    y = _out(x, (*x.shape[:-1], down.n), out)
+    check(lib().glypr_hip_mlp(ctx.handle, gate_up.handle, down.handle, _ptr(x), _ptr(y), m,
+                              variant, ctx.stream))
+    return y
+
+
+def rmsnorm_mlp(ctx: Context, gate_up: Q8Weight, down: Q8Weight, x: torch.Tensor,
+                norm_weight: Optional[torch.Tensor], eps: float = 1e-6,
+                variant: int = INT8_EXACT, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(x, "x")
+    m = x.numel() // gate_up.k
+    y = _out(x, (*x.shape[:-1], down.n), out)
+    check(lib().glypr_hip_rmsnorm_mlp(ctx.handle, gate_up.handle, down.handle, _ptr(x),
+                                      _ptr(norm_weight), eps, _ptr(y), m, variant, ctx.stream))
+    return y
+
+
+def dequantize(ctx: Context, w: Q8Weight) -> torch.Tensor:
+    y = torch.empty((w.n, w.k), dtype=torch.float32, device=f"cuda:{ctx.device}")
+    check(lib().glypr_hip_q8_0_dequantize(ctx.handle, w.handle, _ptr(y), ctx.stream))
+    return y
+
+
+def quantize(ctx: Context, x: torch.Tensor) -> torch.Tensor:
+    ctx._check_tensor(x, "x")
+    k = x.shape[-1]
+    m = x.numel() // k
+    out = torch.empty((m, k // 32 * 34), dtype=torch.uint8, device=x.device)
+    check(lib().glypr_hip_q8_0_quantize(ctx.handle, _ptr(x), m, k, _ptr(out), ctx.stream))
+    return out
+
+
+def embed_gather(ctx: Context, table: Q8Weight, ids, scale: float,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    if out is None:
+        out = torch.empty((ids.size, table.k), dtype=torch.float32, device=f"cuda:{ctx.device}")
+    check(lib().glypr_hip_q8_0_embed_gather(ctx.handle, table.handle,
+                                            ids.ctypes.data_as(ctypes.c_void_p), ids.size,
+                                            scale, _ptr(out), ctx.stream))
+    return out
+
+
+def pool_normalize(ctx: Context, tokens: torch.Tensor, mask=None, trunc: int = 0,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(tokens, "tokens")
+    t, d = tokens.shape
+    td = trunc if 0 < trunc < d else d
+    if out is None:
+        out = torch.empty(td, dtype=torch.float32, device=tokens.device)
+    mk = None
+    if mask is not None:
+        mk = np.ascontiguousarray(mask, dtype=np.uint8)
+    check(lib().glypr_hip_pool_normalize(
+        ctx.handle, _ptr(tokens),
+        None if mk is None else mk.ctypes.data_as(ctypes.c_void_p), t, d, trunc, _ptr(out),
+        ctx.stream))
+    return out

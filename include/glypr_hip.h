@@ -1,0 +1,207 @@
+/*
+ * glypr_hip.h — C ABI of glypr's MI355X (gfx950) Q8_0 backend.
+ *
+ * A HIP backend beside glypr-core's Metal and CPU-SIMD backends.  The entry
+ * points are what a Rust `glypr-hip-sys` crate binds (see INTEGRATION.md for
+ * the binding and the `LinearOp::HipQ8_0` arm).  Each declaration names the
+ * reference interface it replaces (paths inside phrozen/glypr v0.3.0,
+ * crates/glypr-core/src/).
+ *
+ * Conventions
+ *  - Every entry point returns a glypr_status (0 = GLYPR_OK).  On error,
+ *    glypr_hip_last_error() returns a thread-local message.
+ *  - All arguments are validated on the host before anything is launched, so
+ *    every error path is reachable without a GPU.
+ *  - Tensors are caller-allocated device buffers, row-major and contiguous,
+ *    f32 unless stated.  Q8_0 weights are library-owned opaque handles.
+ *  - Launches are asynchronous on `stream` (a hipStream_t; NULL = the null
+ *    stream).  A context's workspace is shared by its calls: calls on one
+ *    context must be issued from one thread onto one stream at a time.
+ *  - Q8_0 is the GGUF block format: 34 bytes = { f16 d; int8 qs[32] }, rows
+ *    of K/32 blocks; K must be a multiple of 32.
+ */
+#ifndef GLYPR_HIP_H
+#define GLYPR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLYPR_HIP_ABI_VERSION 1
+
+typedef enum glypr_status {
+  GLYPR_OK = 0,
+  GLYPR_ERR_INVALID_ARG = 1, /* null pointer, negative or zero size */
+  GLYPR_ERR_SHAPE = 2,       /* K % 32 != 0, dimension mismatch */
+  GLYPR_ERR_ALIGNMENT = 3,   /* device pointer not 16-byte aligned */
+  GLYPR_ERR_DEVICE = 4,      /* no HIP device, or handle from another device */
+  GLYPR_ERR_HIP = 5,         /* HIP runtime error (message has the HIP error) */
+  GLYPR_ERR_OOM = 6,         /* device allocation failed */
+  GLYPR_ERR_RANGE = 7,       /* token id >= vocab */
+  GLYPR_ERR_UNSUPPORTED = 8  /* unknown variant or flag */
+} glypr_status;
+
+/* Numerics of the Q8_0 GEMM.
+ * INT8_EXACT: activations quantized per 32-block exactly as candle's
+ *   BlockQ8_0::from_float, int8 MFMA block sums, and the scalar vec_dot's
+ *   f32 sequence sum += ((float)isum * d_w) * d_x in block order: the output
+ *   is bit-identical to glypr's CPU QMatMul path on x86-64.
+ * BF16_DEQUANT: weights dequantized in registers to bf16(q*d), activations
+ *   rounded to bf16, bf16 MFMA with f32 accumulation (the semantics of
+ *   glypr's Metal kernels / CANDLE_DEQUANTIZE_ALL, at bf16 precision). */
+typedef enum glypr_q8_variant {
+  GLYPR_Q8_INT8_EXACT = 0,
+  GLYPR_Q8_BF16_DEQUANT = 1
+} glypr_q8_variant;
+
+typedef struct glypr_hip_ctx glypr_hip_ctx; /* per-device context + workspace */
+typedef struct glypr_q8w glypr_q8w;         /* Q8_0 weight on one device */
+typedef void* glypr_stream;                 /* hipStream_t */
+
+/* ---- library / context ------------------------------------------------- */
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char* glypr_hip_last_error(void);
+int glypr_hip_abi_version(void);
+
+/* Per-device state: replaces candle's per-device Metal pipeline/library
+ * caches keyed by device (metal_kernels/mod.rs:15-114). */
+int glypr_hip_ctx_create(int device, glypr_hip_ctx** out);
+int glypr_hip_ctx_destroy(glypr_hip_ctx* ctx);
+
+/* Block until `stream` is idle: the read-back synchronisation of
+ * encode_single_text (lib.rs:988-989). */
+int glypr_hip_sync(glypr_hip_ctx* ctx, glypr_stream stream);
+
+/* ---- Q8_0 weights (LinearOp load path) --------------------------------- */
+
+/* LinearOp::from_gguf_tensor, Q8_0 arm (linear.rs:36-78; the Metal arm keeps
+ * the raw bytes [N, K/32*34], linear.rs:55-71).  `gguf_blocks` is host memory
+ * holding n*(k/32) GGUF Q8_0 blocks.  The weight is uploaded and repacked once
+ * into an int8 plane [n][k] plus an f32 scale plane [n][k/32] (f32 of the f16
+ * d, exact).  K % 32 != 0 -> GLYPR_ERR_SHAPE (the caller falls back to its CPU
+ * QMatMul exactly as linear.rs:57-60 does for Metal). */
+int glypr_hip_q8_0_weight_create(glypr_hip_ctx* ctx, const uint8_t* gguf_blocks, int64_t n,
+                                 int64_t k, glypr_q8w** out);
+
+/* LinearOp::try_concat (linear.rs:82-148): concatenate `count` >= 2 weights
+ * with equal K along out_dim into one buffer.  If `views` is non-NULL it
+ * receives `count` handles that are narrow views of the fused buffer (the
+ * zero-copy views of linear.rs:128-137).  Differing K -> GLYPR_ERR_SHAPE
+ * (try_concat returns None). */
+int glypr_hip_q8_0_weight_concat(glypr_hip_ctx* ctx, const glypr_q8w* const* parts, int count,
+                                 glypr_q8w** fused, glypr_q8w** views);
+
+/* Tensor::narrow(0, row0, rows) of a weight: a view sharing the buffer. */
+int glypr_hip_q8_0_weight_view(const glypr_q8w* w, int64_t row0, int64_t rows, glypr_q8w** out);
+
+/* Release a handle; the buffer is freed with its last handle. */
+int glypr_hip_q8_0_weight_destroy(glypr_q8w* w);
+
+/* (out_dim, in_dim) of a handle: the fields of LinearOp::MetalQ8_0 (linear.rs:10-14). */
+int glypr_hip_q8_0_weight_shape(const glypr_q8w* w, int64_t* n, int64_t* k);
+
+/* QTensor::dequantize (model.rs:252-254; BlockQ8_0::to_float): out f32 [n,k],
+ * out[r][j] = f32(d) * q, bit-exact. */
+int glypr_hip_q8_0_dequantize(glypr_hip_ctx* ctx, const glypr_q8w* w, float* out,
+                              glypr_stream stream);
+
+/* ---- Q8_0 activations --------------------------------------------------- */
+
+/* BlockQ8_0::from_float as k_quants::matmul applies it to activations
+ * (reached from linear.rs:153-162): x f32 [m,k] -> GGUF blocks [m][k/32]
+ * (34 B each) in device memory, bit-exact with the CPU path. */
+int glypr_hip_q8_0_quantize(glypr_hip_ctx* ctx, const float* x, int64_t m, int64_t k,
+                            uint8_t* out_blocks, glypr_stream stream);
+
+/* ---- the hot path ------------------------------------------------------ */
+
+/* LinearOp::forward (linear.rs:150-172) -> QMatMul::forward on CPU, or
+ * fused_metal_q8_0_matmul(weight, x, out_dim, in_dim) on Metal
+ * (metal_kernels/mod.rs:1271-1394).  x [m,k], y [m,n]. */
+int glypr_hip_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, float* y,
+                          int64_t m, int variant, glypr_stream stream);
+
+/* RMSNorm::forward (norm.rs:22-63) -> cpu_rmsnorm (cpu_simd/mod.rs:10-32;
+ * simd_rmsnorm_row_f32, cpu_simd/rmsnorm.rs:6-47).  weight may be NULL (the
+ * weightless v_norm).  x,y [rows,dim]; x == y allowed. */
+int glypr_hip_rmsnorm(glypr_hip_ctx* ctx, const float* x, const float* weight, float eps,
+                      float* y, int64_t rows, int64_t dim, glypr_stream stream);
+
+/* RMSNorm::forward feeding LinearOp::forward (layer.rs:30-31, 38-39): the
+ * RMSNorm prologue fused with activation quantization; the normalised f32
+ * tensor is never written.  x [m,k] (k = norm dim), y [m,n]. */
+int glypr_hip_rmsnorm_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x,
+                                  const float* norm_weight, float eps, float* y, int64_t m,
+                                  int variant, glypr_stream stream);
+
+/* cpu_geglu (cpu_simd/mod.rs:35-47; geglu_scalar_f32, cpu_simd/geglu.rs:6-18):
+ * out = gelu_tanh(gate) * up, elementwise over n floats; out may alias. */
+int glypr_hip_geglu(glypr_hip_ctx* ctx, const float* gate, const float* up, float* out,
+                    int64_t n, glypr_stream stream);
+
+/* MLP::forward (mlp.rs:31-70): gate/up GEMM with the GeGLU applied in its
+ * epilogue (and the result quantized there for `down`), then down.
+ * gate_up: the try_concat of [gate; up] ([2F, H]); down: [H, F].
+ * x [m,H] is the (already normalised) input; y [m,H]. */
+int glypr_hip_mlp(glypr_hip_ctx* ctx, const glypr_q8w* gate_up, const glypr_q8w* down,
+                  const float* x, float* y, int64_t m, int variant, glypr_stream stream);
+
+/* pre_feedforward_layernorm + MLP::forward (layer.rs:37-39): the same with
+ * the RMSNorm prologue fused into the gate/up GEMM's activation quantizer. */
+int glypr_hip_rmsnorm_mlp(glypr_hip_ctx* ctx, const glypr_q8w* gate_up, const glypr_q8w* down,
+                          const float* x, const float* norm_weight, float eps, float* y,
+                          int64_t m, int variant, glypr_stream stream);
+
+/* Embedding::forward + x embed_scale (model.rs:254-255, 507-508): rows of a
+ * Q8_0 token table gathered and dequantized directly from the int8 plane,
+ * out[t,:] = (f32(d)*q) * scale.  `ids` is host memory (tokenizer output);
+ * any id >= vocab -> GLYPR_ERR_RANGE before launch.  out [n_ids, k]. */
+int glypr_hip_q8_0_embed_gather(glypr_hip_ctx* ctx, const glypr_q8w* table, const uint32_t* ids,
+                                int64_t n_ids, float scale, float* out, glypr_stream stream);
+
+/* pool_and_normalize (model.rs:654-705) with truncate_mrl semantics
+ * (util.rs:6-19): mean over valid tokens (mask NULL = all; else host uint8
+ * [t]), L2 with the 1e-12 clamp, then MRL truncation to `trunc` dims and
+ * renormalisation (trunc 0 or >= d keeps d).  tokens [t,d] -> out [trunc]. */
+int glypr_hip_pool_normalize(glypr_hip_ctx* ctx, const float* tokens, const uint8_t* mask,
+                             int64_t t, int64_t d, int64_t trunc, float* out,
+                             glypr_stream stream);
+
+/* ---- per-kernel timing --------------------------------------------------- */
+
+/* Kernel identities for the per-kernel timing below. */
+typedef enum glypr_kernel_id {
+  GLYPR_K_QUANTIZE = 0,       /* activation quantize (BlockQ8_0::from_float) */
+  GLYPR_K_RMSNORM_QUANT = 1,  /* RMSNorm prologue emitting Q8_0 activations */
+  GLYPR_K_GEMM_I8 = 2,        /* INT8_EXACT GEMM */
+  GLYPR_K_GEMM_I8_GEGLU = 3,  /* INT8_EXACT gate/up GEMM + GeGLU + quantize epilogue */
+  GLYPR_K_TO_BF16 = 4,        /* f32 -> bf16 activations */
+  GLYPR_K_RMSNORM_BF16 = 5,   /* RMSNorm prologue emitting bf16 activations */
+  GLYPR_K_GEMM_BF16 = 6,      /* BF16_DEQUANT GEMM */
+  GLYPR_K_GEMM_BF16_GEGLU = 7,/* BF16_DEQUANT gate/up GEMM + GeGLU epilogue */
+  GLYPR_K_RMSNORM = 8,
+  GLYPR_K_GEGLU = 9,
+  GLYPR_K_GATHER = 10,
+  GLYPR_K_DEQUANT = 11,
+  GLYPR_K_POOL = 12,
+  GLYPR_K_COUNT = 13
+} glypr_kernel_id;
+
+/* The per-op device timing of forward_profiled (profile.rs:53-56, 63-429),
+ * without its host syncs: while enabled, every kernel the context launches is
+ * bracketed by HIP events on its own stream.  Enabling clears the totals. */
+int glypr_hip_profile_enable(glypr_hip_ctx* ctx, int enable);
+/* Wait for the recorded events and return, per glypr_kernel_id, the summed
+ * duration in milliseconds and the launch count (arrays of GLYPR_K_COUNT). */
+int glypr_hip_profile_read(glypr_hip_ctx* ctx, double* total_ms, int64_t* launches);
+/* Static name of a glypr_kernel_id ("" if out of range). */
+const char* glypr_hip_kernel_name(int id);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GLYPR_HIP_H */

@@ -1,0 +1,292 @@
+"""ctypes + numpy binding of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, always as the checker.  The product package
+(glypr_amd) never imports this module.
+
+The oracle restates glypr's CPU Q8_0 path (candle k_quants Q8_0 + glypr's
+cpu_simd ops); see glypr_oracle.h for the per-function reference citations.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+QK8_0 = 32
+BLOCK_BYTES = 34
+
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_i64 = ctypes.c_int64
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-B" if force else "-s", "-C", HERE, "liboracle.so"], check=True,
+                       stdout=subprocess.DEVNULL)
+    return LIB_PATH
+
+
+class ModelConfig(ctypes.Structure):
+    _fields_ = [("hidden", _i64), ("ffn", _i64), ("n_heads", _i64), ("n_kv_heads", _i64),
+                ("head_dim", _i64), ("n_layers", _i64), ("vocab", _i64),
+                ("sliding_window", _i64), ("eps", ctypes.c_float),
+                ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double)]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [(n, _u8p) for n in ("q", "k", "v", "o", "gate", "up", "down")] + \
+               [(n, _f32p) for n in ("input_norm", "post_attn_norm", "pre_ffn_norm",
+                                     "post_ffn_norm", "q_norm", "k_norm")]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "orc_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "orc_f32_to_f16_array": (None, [_f32p, _u16p, _i64]),
+            "orc_f16_to_f32_array": (None, [_u16p, _f32p, _i64]),
+            "orc_q8_0_quantize_rows": (None, [_f32p, _i64, _i64, _u8p]),
+            "orc_q8_0_dequantize_rows": (None, [_u8p, _i64, _i64, _f32p]),
+            "orc_q8_0_vec_dot": (ctypes.c_float, [_i64, _u8p, _u8p]),
+            "orc_q8_0_matmul": (None, [_f32p, _i64, _i64, _u8p, _i64, _f32p, ctypes.c_int]),
+            "orc_q8_0_matmul_preq": (None, [_u8p, _i64, _i64, _u8p, _i64, _f32p, ctypes.c_int]),
+            "orc_q8_0_matmul_f64": (None, [_u8p, _i64, _i64, _u8p, _i64, _f64p]),
+            "orc_q8_0_matmul_dequant_f64": (None, [_f32p, _i64, _i64, _u8p, _i64, _f64p,
+                                                   ctypes.c_int]),
+            "orc_rmsnorm": (None, [_f32p, _f32p, ctypes.c_float, _f32p, _i64, _i64,
+                                   ctypes.c_int]),
+            "orc_tanhf": (ctypes.c_float, [ctypes.c_float]),
+            "orc_geglu_scalar": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+            "orc_geglu_scalar_libm": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+            "orc_geglu": (None, [_f32p, _f32p, _f32p, _i64, ctypes.c_int]),
+            "orc_embed_gather": (ctypes.c_int, [_u8p, _i64, _i64, _u32p, _i64, ctypes.c_float,
+                                                _f32p]),
+            "orc_pool_normalize": (None, [_f32p, _u8p, _i64, _i64, _i64, _f32p]),
+            "orc_l2_normalize": (None, [_f32p, _i64, _f32p]),
+            "orc_cosine": (ctypes.c_float, [_f32p, _f32p, _i64]),
+            "orc_fill_normal": (None, [_f32p, _i64, ctypes.c_uint64, ctypes.c_float,
+                                       ctypes.c_float]),
+            "orc_fill_uniform_ids": (None, [_u32p, _i64, ctypes.c_uint64, ctypes.c_uint32]),
+            "orc_make_q8_0_weight": (None, [_u8p, _i64, _i64, ctypes.c_uint64, ctypes.c_float]),
+            "orc_layer_is_full": (ctypes.c_int, [_i64]),
+            "orc_rope_tables": (None, [_i64, ctypes.c_double, _i64, _f32p, _f32p]),
+            "orc_attention": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _f32p,
+                                     ctypes.c_int]),
+            "orc_encoder_layer": (None, [ctypes.POINTER(ModelConfig),
+                                         ctypes.POINTER(LayerWeights), _i64, _f32p, _i64,
+                                         ctypes.c_int]),
+            "orc_model_forward": (ctypes.c_int, [ctypes.POINTER(ModelConfig),
+                                                 _u8p, ctypes.POINTER(LayerWeights), _f32p, _u32p,
+                                                 _i64, _i64, _f32p, _f32p, ctypes.c_int]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a: Optional[np.ndarray], ptype):
+    if a is None:
+        return ctypes.cast(None, ptype)
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ptype)
+
+
+# ---------------------------------------------------------------- codec ----
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_array(_p(x, _f32p), _p(out, _u16p), x.size)
+    return out
+
+
+def f16_bits_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_f16_to_f32_array(_p(h, _u16p), _p(out, _f32p), h.size)
+    return out
+
+
+def quantize_rows(x: np.ndarray) -> np.ndarray:
+    """f32 [m,k] -> GGUF Q8_0 blocks uint8 [m, k/32*34]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    out = np.empty((m, k // QK8_0 * BLOCK_BYTES), np.uint8)
+    lib().orc_q8_0_quantize_rows(_p(x, _f32p), m, k, _p(out, _u8p))
+    return out
+
+
+def dequantize_rows(blocks: np.ndarray, k: int) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    rows = blocks.size // (k // QK8_0 * BLOCK_BYTES)
+    out = np.empty((rows, k), np.float32)
+    lib().orc_q8_0_dequantize_rows(_p(blocks, _u8p), rows, k, _p(out, _f32p))
+    return out
+
+
+def split_blocks(blocks: np.ndarray, k: int):
+    """GGUF Q8_0 bytes [rows, k/32*34] -> (d f16 bits uint16 [rows, nb], qs int8 [rows, k])."""
+    nb = k // QK8_0
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1, nb, BLOCK_BYTES)
+    d = b[:, :, :2].copy().view(np.uint16).reshape(-1, nb)
+    qs = b[:, :, 2:].copy().view(np.int8).reshape(-1, k)
+    return d, qs
+
+
+def join_blocks(d_bits: np.ndarray, qs: np.ndarray) -> np.ndarray:
+    rows, k = qs.shape
+    nb = k // QK8_0
+    out = np.empty((rows, nb, BLOCK_BYTES), np.uint8)
+    out[:, :, :2] = np.ascontiguousarray(d_bits, dtype=np.uint16).reshape(rows, nb, 1).view(
+        np.uint8)
+    out[:, :, 2:] = np.ascontiguousarray(qs, dtype=np.int8).reshape(rows, nb, QK8_0).view(np.uint8)
+    return out.reshape(rows, nb * BLOCK_BYTES)
+
+
+# ---------------------------------------------------------------- GEMM -----
+
+def matmul(x: np.ndarray, w_blocks: np.ndarray, n: int, threads: int = 0) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    y = np.empty((m, n), np.float32)
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    lib().orc_q8_0_matmul(_p(x, _f32p), m, k, _p(w, _u8p), n, _p(y, _f32p), threads)
+    return y
+
+
+def matmul_preq(xq: np.ndarray, m: int, k: int, w_blocks: np.ndarray, n: int,
+                threads: int = 0) -> np.ndarray:
+    y = np.empty((m, n), np.float32)
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    lib().orc_q8_0_matmul_preq(_p(xq, _u8p), m, k, _p(w, _u8p), n, _p(y, _f32p), threads)
+    return y
+
+
+def matmul_f64(xq: np.ndarray, m: int, k: int, w_blocks: np.ndarray, n: int) -> np.ndarray:
+    y = np.empty((m, n), np.float64)
+    xq = np.ascontiguousarray(xq, dtype=np.uint8)
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    lib().orc_q8_0_matmul_f64(_p(xq, _u8p), m, k, _p(w, _u8p), n, _p(y, _f64p))
+    return y
+
+
+def matmul_dequant_f64(x: np.ndarray, w_blocks: np.ndarray, n: int, threads: int = 0):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    y = np.empty((m, n), np.float64)
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    lib().orc_q8_0_matmul_dequant_f64(_p(x, _f32p), m, k, _p(w, _u8p), n, _p(y, _f64p), threads)
+    return y
+
+
+# ------------------------------------------------------------- elementwise --
+
+def rmsnorm(x: np.ndarray, weight: Optional[np.ndarray], eps: float = 1e-6,
+            threads: int = 0) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    d = x.shape[-1]
+    rows = x.size // d
+    y = np.empty_like(x)
+    w = None if weight is None else np.ascontiguousarray(weight, dtype=np.float32)
+    lib().orc_rmsnorm(_p(x, _f32p), _p(w, _f32p), ctypes.c_float(eps), _p(y, _f32p), rows, d,
+                      threads)
+    return y
+
+
+def tanhf(x: float) -> float:
+    return lib().orc_tanhf(ctypes.c_float(x))
+
+
+def geglu(gate: np.ndarray, up: np.ndarray, threads: int = 0) -> np.ndarray:
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    lib().orc_geglu(_p(g, _f32p), _p(u, _f32p), _p(out, _f32p), g.size, threads)
+    return out
+
+
+def embed_gather(table_blocks: np.ndarray, vocab: int, d: int, ids: np.ndarray,
+                 scale: float) -> np.ndarray:
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    out = np.empty((ids.size, d), np.float32)
+    t = np.ascontiguousarray(table_blocks, dtype=np.uint8)
+    rc = lib().orc_embed_gather(_p(t, _u8p), vocab, d, _p(ids, _u32p), ids.size,
+                                ctypes.c_float(scale), _p(out, _f32p))
+    if rc != 0:
+        raise IndexError("token id out of range")
+    return out
+
+
+def pool_normalize(tokens: np.ndarray, mask: Optional[np.ndarray] = None,
+                   trunc: int = 0) -> np.ndarray:
+    tok = np.ascontiguousarray(tokens, dtype=np.float32)
+    t, d = tok.shape
+    td = trunc if 0 < trunc < d else d
+    out = np.empty(td, np.float32)
+    mk = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+    lib().orc_pool_normalize(_p(tok, _f32p), _p(mk, _u8p), t, d, trunc, _p(out, _f32p))
+    return out
+
+
+# ------------------------------------------------------------ synthetic ----
+
+def normal(n: int, seed: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal(_p(out, _f32p), n, seed, ctypes.c_float(mean), ctypes.c_float(std))
+    return out
+
+
+def uniform_ids(n: int, seed: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, np.uint32)
+    lib().orc_fill_uniform_ids(_p(out, _u32p), n, seed, vocab)
+    return out
+
+
+def q8_0_weight(n: int, k: int, seed: int, sigma: float = 0.02) -> np.ndarray:
+    """GGUF Q8_0 bytes [n, k/32*34] with BASELINE's synthetic distribution."""
+    out = np.empty((n, k // QK8_0 * BLOCK_BYTES), np.uint8)
+    lib().orc_make_q8_0_weight(_p(out, _u8p), n, k, seed, ctypes.c_float(sigma))
+    return out
+
+
+def rope_tables(head_dim: int, theta: float, t: int):
+    c = np.empty((t, head_dim), np.float32)
+    s = np.empty((t, head_dim), np.float32)
+    lib().orc_rope_tables(head_dim, theta, t, _p(c, _f32p), _p(s, _f32p))
+    return c, s
+
+
+def attention(q, k, v, window: int, threads: int = 0):
+    """q [nh,t,hd], k/v [nkv,t,hd] -> ctx [t, nh*hd]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    nh, t, hd = q.shape
+    nkv = k.shape[0]
+    out = np.empty((t, nh * hd), np.float32)
+    lib().orc_attention(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), nh, nkv, t, hd, window,
+                        _p(out, _f32p), threads)
+    return out

@@ -1,0 +1,315 @@
+"""GPU parity of the Q8_0 hot path (through the C ABI) against the CPU oracle.
+
+Bar: bit-exact for dequantization, activation quantization, RMSNorm, GeGLU,
+gather, pooling and the INT8_EXACT GEMM (+ its fused prologue/epilogues);
+BASELINE's tolerance (max relative error 1e-3, absolute floor 1e-4) is also
+asserted against the float64 brute force.  The BF16_DEQUANT variant is held to
+a bf16 bound against the float64 dequant oracle.
+"""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from glypr_amd import _lib
+from glypr_amd import ops
+from glypr_amd.ops import BF16_DEQUANT, INT8_EXACT, Q8Weight
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KAT = json.load(open(os.path.join(HERE, "golden", "q8_0_kat.json")))
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def assert_bits_equal(got, ref, what):
+    g, r = bits(got), bits(ref)
+    bad = np.count_nonzero(g != r)
+    assert bad == 0, f"{what}: {bad} of {g.size} values differ; max |d| = " \
+                     f"{np.abs(got.astype(np.float64) - ref).max()}"
+
+
+def baseline_tolerance(got, ref64):
+    """BASELINE: max relative error 1e-3 with an absolute floor of 1e-4."""
+    err = np.abs(got.astype(np.float64) - ref64)
+    assert np.all(err <= np.maximum(1e-3 * np.abs(ref64), 1e-4)), err.max()
+
+
+# ------------------------------------------------------------------ codec --
+
+def test_dequant_kat_and_random(ctx, oracle):
+    say("dequant: KAT blocks + random [300 x 768]")
+    for c in KAT["dequant"]:
+        blk = oracle.join_blocks(np.array([[c["d_bits"]]], np.uint16), np.array([c["qs"]], np.int8))
+        w = Q8Weight.from_gguf(ctx, blk, 1, 32)
+        y = host(ops.dequantize(ctx, w))
+        assert np.array_equal(bits(y[0]), np.array(c["y_bits"], np.uint32)), c["d_bits"]
+    wb = oracle.q8_0_weight(300, 768, seed=3)
+    w = Q8Weight.from_gguf(ctx, wb, 300, 768)
+    assert w.shape() == (300, 768)
+    assert_bits_equal(host(ops.dequantize(ctx, w)), oracle.dequantize_rows(wb, 768), "dequant")
+
+
+def test_quantize_kat_and_random(ctx, oracle):
+    say("quantize: KAT blocks + N(0,1) [517 x 1152]")
+    for c in KAT["quantize"]:
+        x = np.array(c["x_bits"], np.uint32).view(np.float32).reshape(1, 32)
+        d, qs = oracle.split_blocks(host(ops.quantize(ctx, dev(x))), 32)
+        assert int(d[0, 0]) == c["d_bits"], c["name"]
+        assert qs[0].tolist() == c["qs"], c["name"]
+    x = oracle.normal(517 * 1152, seed=8).reshape(517, 1152) * np.float32(3.7)
+    x[5, 100:140] = 0.0
+    x[9, 0] = 1e30
+    got = host(ops.quantize(ctx, dev(x)))
+    assert np.array_equal(got, oracle.quantize_rows(x))
+
+
+# ----------------------------------------------------------------- GEMMs ---
+
+SHAPES = [(1, 32, 1), (19, 256, 128), (33, 96, 70), (64, 768, 1280), (100, 1152, 768),
+          (512, 768, 1152), (300, 768, 256), (7, 128, 33)]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+def test_matmul_int8_bit_exact(ctx, oracle, m, k, n):
+    say(f"matmul INT8_EXACT m={m} k={k} n={n}")
+    x = oracle.normal(m * k, seed=100 + m).reshape(m, k)
+    wb = oracle.q8_0_weight(n, k, seed=200 + n)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    y = host(ops.q8_0_matmul(ctx, w, dev(x), INT8_EXACT))
+    ref = oracle.matmul(x, wb, n)
+    assert_bits_equal(y, ref, f"matmul {m}x{k}x{n}")
+    baseline_tolerance(y, oracle.matmul_f64(oracle.quantize_rows(x), m, k, wb, n))
+
+
+def test_matmul_int8_large_tile_path(ctx, oracle):
+    m, k, n = 4096, 768, 2304
+    say(f"matmul INT8_EXACT large-tile path m={m} k={k} n={n}")
+    x = oracle.normal(m * k, seed=7).reshape(m, k)
+    wb = oracle.q8_0_weight(n, k, seed=77)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    y = host(ops.q8_0_matmul(ctx, w, dev(x), INT8_EXACT))
+    assert_bits_equal(y, oracle.matmul(x, wb, n), "large-tile matmul")
+
+
+def test_matmul_deterministic_and_c3_rows(ctx, oracle):
+    """C3 size (M = 16384): two runs are bit-identical (no LDS race) and 64 random
+    rows match the oracle bit for bit."""
+    m, k, n = 16384, 768, 1152
+    say(f"matmul C3 size m={m} k={k} n={n}")
+    x = oracle.normal(m * k, seed=31).reshape(m, k)
+    wb = oracle.q8_0_weight(n, k, seed=32)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    xd = dev(x)
+    y1 = host(ops.q8_0_matmul(ctx, w, xd, INT8_EXACT))
+    y2 = host(ops.q8_0_matmul(ctx, w, xd, INT8_EXACT))
+    assert np.array_equal(bits(y1), bits(y2))
+    rows = np.random.default_rng(0).choice(m, 64, replace=False)
+    assert_bits_equal(y1[rows], oracle.matmul(x[rows], wb, n), "C3 rows")
+
+
+def test_rmsnorm_bit_exact(ctx, oracle):
+    for rows, dim, with_w in [(37, 768, True), (512, 768, True), (96, 256, True), (40, 256, False),
+                              (5, 1152, True), (3, 20, True)]:
+        say(f"rmsnorm rows={rows} dim={dim} weight={with_w}")
+        x = oracle.normal(rows * dim, seed=rows + dim).reshape(rows, dim) * np.float32(2.5)
+        w = (1 + 0.1 * oracle.normal(dim, seed=9)) if with_w else None
+        y = host(ops.rmsnorm(ctx, dev(x), None if w is None else dev(w), 1e-6))
+        assert_bits_equal(y, oracle.rmsnorm(x, w, 1e-6), f"rmsnorm {rows}x{dim}")
+    # in place (x == y) and the KAT rows
+    x = oracle.normal(64 * 768, seed=4).reshape(64, 768)
+    xd = dev(x)
+    ops.rmsnorm(ctx, xd, None, 1e-6, out=xd)
+    assert_bits_equal(host(xd), oracle.rmsnorm(x, None, 1e-6), "rmsnorm in place")
+    for c in KAT["rmsnorm"]:
+        d = c["d"]
+        x = np.full((2, d), np.array([c["c_bits"]], np.uint32).view(np.float32)[0], np.float32)
+        w = np.array(c["w_bits"], np.uint32).view(np.float32)
+        y = host(ops.rmsnorm(ctx, dev(x), dev(w), 0.0))
+        assert np.array_equal(bits(y[1]), np.array(c["y_bits"], np.uint32))
+
+
+@pytest.mark.parametrize("m", [1, 19, 512, 2048])
+def test_rmsnorm_matmul_bit_exact(ctx, oracle, m):
+    k, n = 768, 1280
+    say(f"rmsnorm_q8_0_matmul m={m}")
+    x = oracle.normal(m * k, seed=m).reshape(m, k) * np.float32(4.0)
+    nw = 1 + 0.1 * oracle.normal(k, seed=1)
+    wb = oracle.q8_0_weight(n, k, seed=2)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    y = host(ops.rmsnorm_q8_0_matmul(ctx, w, dev(x), dev(nw), 1e-6, INT8_EXACT))
+    ref = oracle.matmul(oracle.rmsnorm(x, nw, 1e-6), wb, n)
+    assert_bits_equal(y, ref, "rmsnorm+matmul")
+
+
+def test_geglu_bit_exact(ctx, oracle):
+    say("geglu elementwise [512 x 1152] + KAT points")
+    g = oracle.normal(512 * 1152, seed=61, std=3.0)
+    u = oracle.normal(512 * 1152, seed=62)
+    g[:8] = [-10.0, 10.0, 0.0, -0.0, 9.99, -9.99, 1e-6, -50.0]
+    y = host(ops.geglu(ctx, dev(g), dev(u)))
+    assert_bits_equal(y, oracle.geglu(g, u), "geglu")
+    for c in KAT["geglu"]:
+        gg = np.array([c["g_bits"]], np.uint32).view(np.float32)
+        uu = np.array([c["u_bits"]], np.uint32).view(np.float32)
+        assert bits(host(ops.geglu(ctx, dev(gg), dev(uu))))[0] == c["y_bits"]
+
+
+def _mlp_ref(oracle, x, gb, ub, db, H, F):
+    gate = oracle.matmul(x, gb, F)
+    up = oracle.matmul(x, ub, F)
+    return oracle.matmul(oracle.geglu(gate, up), db, H)
+
+
+@pytest.mark.parametrize("m", [1, 33, 512, 4096])
+def test_mlp_bit_exact(ctx, oracle, m):
+    H, F = 768, 1152
+    say(f"mlp (gate/up GeGLU epilogue + down) m={m}")
+    x = oracle.normal(m * H, seed=m + 5).reshape(m, H)
+    gb, ub, db = (oracle.q8_0_weight(F, H, seed=11), oracle.q8_0_weight(F, H, seed=12),
+                  oracle.q8_0_weight(H, F, seed=13))
+    g = Q8Weight.from_gguf(ctx, gb, F, H)
+    u = Q8Weight.from_gguf(ctx, ub, F, H)
+    d = Q8Weight.from_gguf(ctx, db, H, F)
+    gu, views = Q8Weight.concat(ctx, [g, u])
+    y = host(ops.mlp(ctx, gu, d, dev(x), INT8_EXACT))
+    assert_bits_equal(y, _mlp_ref(oracle, x, gb, ub, db, H, F), "mlp")
+    nw = 1 + 0.1 * oracle.normal(H, seed=14)
+    y2 = host(ops.rmsnorm_mlp(ctx, gu, d, dev(x), dev(nw), 1e-6, INT8_EXACT))
+    assert_bits_equal(y2, _mlp_ref(oracle, oracle.rmsnorm(x, nw, 1e-6), gb, ub, db, H, F),
+                      "rmsnorm+mlp")
+
+
+def test_concat_views_share_the_fused_buffer(ctx, oracle):
+    m, H = 77, 768
+    say("try_concat q/k/v: fused output == separate outputs; views == parts")
+    x = oracle.normal(m * H, seed=90).reshape(m, H)
+    parts = [oracle.q8_0_weight(n, H, seed=91 + i) for i, n in enumerate((768, 256, 256))]
+    ws = [Q8Weight.from_gguf(ctx, p, p.shape[0], H) for p in parts]
+    fused, views = Q8Weight.concat(ctx, ws)
+    assert fused.shape() == (1280, H) and [v.shape() for v in views] == [(768, H), (256, H),
+                                                                          (256, H)]
+    xd = dev(x)
+    yf = host(ops.q8_0_matmul(ctx, fused, xd))
+    off = 0
+    for p, v in zip(parts, views):
+        n = p.shape[0]
+        yv = host(ops.q8_0_matmul(ctx, v, xd))
+        ref = oracle.matmul(x, p, n)
+        assert_bits_equal(yv, ref, "view")
+        assert_bits_equal(yf[:, off:off + n], ref, "fused slice")
+        off += n
+    sub = views[0].view(100, 50)
+    assert_bits_equal(host(ops.dequantize(ctx, sub)),
+                      oracle.dequantize_rows(parts[0][100:150], H), "narrow view")
+    # parts can be released; views keep the fused buffer alive
+    for wv in ws:
+        wv.close()
+    fused.close()
+    assert_bits_equal(host(ops.q8_0_matmul(ctx, views[2], xd)), oracle.matmul(x, parts[2], 256),
+                      "view after fused handle released")
+
+
+def test_gather_bit_exact_and_range(ctx, oracle):
+    vocab, d = 50_000, 768
+    say(f"embed gather vocab={vocab} d={d}")
+    tb = oracle.q8_0_weight(vocab, d, seed=71)
+    table = Q8Weight.from_gguf(ctx, tb, vocab, d)
+    ids = oracle.uniform_ids(512, seed=72, vocab=vocab)
+    ids[:4] = [0, vocab - 1, 7, 7]
+    scale = float(np.float32(np.sqrt(768.0)))
+    y = host(ops.embed_gather(ctx, table, ids, scale))
+    assert_bits_equal(y, oracle.embed_gather(tb, vocab, d, ids, scale), "gather")
+    with pytest.raises(_lib.GlyprError) as e:
+        ops.embed_gather(ctx, table, np.array([1, vocab], np.uint32), 1.0)
+    assert e.value.code == _lib.GLYPR_ERR_RANGE
+
+
+def test_pool_bit_exact(ctx, oracle):
+    for t, d, trunc, masked in [(512, 768, 256, False), (512, 768, 0, False), (19, 768, 128, True),
+                                (8192, 768, 256, False)]:
+        say(f"pool_normalize t={t} d={d} trunc={trunc} masked={masked}")
+        tok = oracle.normal(t * d, seed=t + trunc).reshape(t, d)
+        mask = None
+        if masked:
+            mask = (np.arange(t) % 3 != 1).astype(np.uint8)
+        y = host(ops.pool_normalize(ctx, dev(tok), mask, trunc))
+        assert_bits_equal(y, oracle.pool_normalize(tok, mask, trunc), "pool")
+    c = KAT["pool"][0]
+    v = np.array(c["v_bits"], np.uint32).view(np.float32)
+    tok = np.tile(v, (c["t"], 1))
+    assert np.array_equal(bits(host(ops.pool_normalize(ctx, dev(tok)))),
+                          np.array(c["l2_bits"], np.uint32))
+
+
+# ------------------------------------------------------------ bf16 variant -
+
+@pytest.mark.parametrize("m,k,n", [(19, 256, 128), (512, 768, 1152), (4096, 768, 1152),
+                                   (300, 1152, 768)])
+def test_matmul_bf16_dequant_within_bf16_bound(ctx, oracle, m, k, n):
+    """BF16_DEQUANT vs the float64 dequant oracle: both operands rounded to bf16
+    (relative error <= 2^-8 each), f32 accumulation:
+    |y - y64| <= 2^-7 * (|x| @ |w_deq|^T) + f32 accumulation slack."""
+    say(f"matmul BF16_DEQUANT m={m} k={k} n={n}")
+    x = oracle.normal(m * k, seed=300 + m).reshape(m, k)
+    wb = oracle.q8_0_weight(n, k, seed=301)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    y = host(ops.q8_0_matmul(ctx, w, dev(x), BF16_DEQUANT))
+    y64 = oracle.matmul_dequant_f64(x, wb, n)
+    wd = np.abs(oracle.dequantize_rows(wb, k).astype(np.float64))
+    bound = 2.0 ** -7 * (np.abs(x).astype(np.float64) @ wd.T) * (1 + 1e-3) + 1e-6
+    assert np.all(np.abs(y - y64) <= bound)
+    cos = (y * y64).sum(1) / np.linalg.norm(y, axis=1) / np.linalg.norm(y64, axis=1)
+    assert cos.min() > 0.9999
+
+
+def test_mlp_bf16_dequant(ctx, oracle):
+    m, H, F = 512, 768, 1152
+    say("mlp BF16_DEQUANT m=512")
+    x = oracle.normal(m * H, seed=400).reshape(m, H)
+    gb, ub, db = (oracle.q8_0_weight(F, H, seed=41), oracle.q8_0_weight(F, H, seed=42),
+                  oracle.q8_0_weight(H, F, seed=43))
+    g, u, d = (Q8Weight.from_gguf(ctx, gb, F, H), Q8Weight.from_gguf(ctx, ub, F, H),
+               Q8Weight.from_gguf(ctx, db, H, F))
+    gu, _ = Q8Weight.concat(ctx, [g, u])
+    y = host(ops.mlp(ctx, gu, d, dev(x), BF16_DEQUANT))
+    gate = oracle.matmul_dequant_f64(x, gb, F).astype(np.float32)
+    up = oracle.matmul_dequant_f64(x, ub, F).astype(np.float32)
+    ref = oracle.matmul_dequant_f64(oracle.geglu(gate, up), db, H)
+    cos = (y * ref).sum(1) / np.linalg.norm(y, axis=1) / np.linalg.norm(ref, axis=1)
+    assert cos.min() > 0.999, cos.min()
+
+
+def test_zero_rows_and_shape_errors(ctx, oracle):
+    say("m = 0 no-op and shape errors")
+    wb = oracle.q8_0_weight(64, 64, seed=1)
+    w = Q8Weight.from_gguf(ctx, wb, 64, 64)
+    x = torch.zeros((0, 64), dtype=torch.float32, device="cuda")
+    assert ops.q8_0_matmul(ctx, w, x).shape == (0, 64)
+    other = Q8Weight.from_gguf(ctx, oracle.q8_0_weight(8, 96, seed=2), 8, 96)
+    with pytest.raises(_lib.GlyprError) as e:
+        Q8Weight.concat(ctx, [w, other])
+    assert e.value.code == _lib.GLYPR_ERR_SHAPE
+    with pytest.raises(_lib.GlyprError) as e:
+        ops.mlp(ctx, w, other, torch.zeros((4, 64), device="cuda"))
+    assert e.value.code == _lib.GLYPR_ERR_SHAPE

@@ -1,0 +1,320 @@
+"""Pin the CPU oracle (oracle/glypr_oracle.c) before trusting it.
+
+Each check is chosen so a plausible mistake fails it: the known-answer vectors
+(tests/golden/q8_0_kat.json, exact arithmetic) catch a wrong rounding rule, a
+dropped f16 rounding of d, a swapped operand; float64 brute force over the same
+quantized operands catches a wrong block index or scale; the lossless special
+case reduces the whole GEMM to numpy's float64 X @ W^T; invariants pin RMSNorm
+and pooling; tanh is measured against double-precision tanh.
+"""
+import json
+import math
+import os
+import struct
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KAT = json.load(open(os.path.join(HERE, "golden", "q8_0_kat.json")))
+
+
+def bits_to_f32(b):
+    return np.array(b, dtype=np.uint32).view(np.float32)
+
+
+def f32_to_bits(x):
+    return np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+
+
+# ------------------------------------------------------------ f16 codec ----
+
+def test_f16_matches_numpy_rne(oracle):
+    rng = np.random.default_rng(1)
+    bits = rng.integers(0, 2**32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    # plus every boundary region: around f16 max, min normal, subnormals, ties
+    extra = []
+    for h in range(0, 0x7C00, 7):
+        f = np.uint16(h).view(np.float16).astype(np.float32)
+        fb = int(np.float32(f).view(np.uint32))
+        extra += [fb - 1, fb, fb + 1, fb + (1 << 12), fb + (1 << 12) - 1, fb + (1 << 12) + 1]
+    extra = [e % (1 << 32) for e in extra]
+    bits = np.concatenate([bits, np.array(extra, dtype=np.uint64).astype(np.uint32)])
+    x = bits.view(np.float32)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    got = oracle.f32_to_f16_bits(x)
+    ok = np.isnan(x) | (got == ref)
+    assert ok.all(), f"{np.count_nonzero(~ok)} f32->f16 mismatches"
+    h = np.arange(65536, dtype=np.uint16)
+    back = oracle.f16_bits_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(back.view(np.uint32)[~nan], ref.view(np.uint32)[~nan])
+    assert np.isnan(back[nan]).all()
+
+
+# ----------------------------------------------------------- Q8_0 codec ----
+
+def test_dequant_kat(oracle):
+    for c in KAT["dequant"]:
+        blk = oracle.join_blocks(np.array([[c["d_bits"]]], np.uint16),
+                                 np.array([c["qs"]], np.int8))
+        y = oracle.dequantize_rows(blk, 32)
+        assert np.array_equal(f32_to_bits(y[0]), np.array(c["y_bits"], np.uint32)), c["d_bits"]
+
+
+def test_quantize_kat(oracle):
+    for c in KAT["quantize"]:
+        x = bits_to_f32(c["x_bits"]).reshape(1, 32)
+        d, qs = oracle.split_blocks(oracle.quantize_rows(x), 32)
+        assert int(d[0, 0]) == c["d_bits"], c["name"]
+        assert qs[0].tolist() == c["qs"], c["name"]
+
+
+def test_quantize_matches_f64_definition(oracle):
+    """Random rows: q must be the nearest integer to x/d within 1 step, d = amax/127
+    rounded to f16, and |q| = 127 at the amax position."""
+    x = oracle.normal(64 * 768, seed=7).reshape(64, 768)
+    d, qs = oracle.split_blocks(oracle.quantize_rows(x), 768)
+    blocks = x.reshape(-1, 32).astype(np.float64)
+    amax = np.abs(blocks).max(axis=1)
+    d_ref = np.float32(amax / 127).astype(np.float32)
+    assert np.array_equal(d.reshape(-1), oracle.f32_to_f16_bits(
+        (np.float32(amax.astype(np.float32)) / np.float32(127)).astype(np.float32)))
+    q = qs.reshape(-1, 32).astype(np.float64)
+    err = np.abs(blocks / (amax[:, None] / 127) - q)
+    assert err.max() <= 0.5 + 1e-4
+    pos = np.argmax(np.abs(blocks), axis=1)
+    assert np.all(np.abs(q[np.arange(len(pos)), pos]) == 127)
+    del d_ref
+
+
+def test_vec_dot_kat(oracle):
+    for c in KAT["vec_dot"]:
+        k = c["k"]
+        nb = k // 32
+        w = oracle.join_blocks(np.full((1, nb), c["w_d_bits"], np.uint16),
+                               np.array([c["wq"]], np.int8))
+        x = oracle.join_blocks(np.full((1, nb), c["x_d_bits"], np.uint16),
+                               np.array([c["xq"]], np.int8))
+        y = oracle.lib().orc_q8_0_vec_dot(k, w.ctypes.data_as(oracle._u8p),
+                                          x.ctypes.data_as(oracle._u8p))
+        assert struct.unpack("<I", struct.pack("<f", y))[0] == c["y_bits"]
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 32, 1), (19, 256, 128), (64, 768, 96), (7, 1152, 33)])
+def test_matmul_vs_f64_bruteforce(oracle, m, k, n):
+    x = oracle.normal(m * k, seed=11 + m).reshape(m, k)
+    w = oracle.q8_0_weight(n, k, seed=5 + n)
+    xq = oracle.quantize_rows(x)
+    y = oracle.matmul(x, w, n)
+    y64 = oracle.matmul_f64(xq, m, k, w, n)
+    # f32 sequential sum of K/32 rounded terms: relative error <= ~nb * 2^-23 of the
+    # sum of |terms|; bound by the sum of absolute block terms computed in f64.
+    nb = k // 32
+    dw, qw = oracle.split_blocks(w, k)
+    dx, qx = oracle.split_blocks(xq, k)
+    absterm = np.zeros((m, n))
+    for b in range(nb):
+        s = np.abs(qx[:, b * 32:(b + 1) * 32].astype(np.int64)
+                   @ qw[:, b * 32:(b + 1) * 32].astype(np.int64).T)
+        absterm += s * oracle.f16_bits_to_f32(dx[:, b])[:, None] * np.abs(
+            oracle.f16_bits_to_f32(dw[:, b]))[None, :]
+    bound = (3 * nb + 2) * 2.0 ** -24 * absterm + 1e-30
+    assert np.all(np.abs(y - y64) <= bound)
+    # preq path and the single-threaded path give identical bits
+    assert np.array_equal(oracle.matmul_preq(xq, m, k, w, n), y)
+    assert np.array_equal(oracle.matmul(x, w, n, threads=1), y)
+
+
+def test_matmul_lossless_equals_numpy(oracle):
+    """x blocks = k*2^e with one |k| = 127: quantization is lossless, so the Q8_0
+    GEMM equals numpy's float64 X @ W_deq^T up to the f32 summation error."""
+    rng = np.random.default_rng(3)
+    m, k, n = 33, 768, 70
+    ks = rng.integers(-127, 128, size=(m, k))
+    ks.reshape(m, -1, 32)[:, :, 0] = 127
+    e = rng.integers(-6, 3, size=(m, k // 32))
+    x = (ks.reshape(m, -1, 32) * (2.0 ** e)[:, :, None]).reshape(m, k).astype(np.float32)
+    w = oracle.q8_0_weight(n, k, seed=9)
+    xq = oracle.quantize_rows(x)
+    assert np.array_equal(oracle.dequantize_rows(xq, k), x)   # lossless
+    wd = oracle.dequantize_rows(w, k).astype(np.float64)
+    ref = x.astype(np.float64) @ wd.T
+    y = oracle.matmul(x, w, n)
+    scale = np.abs(x).astype(np.float64) @ np.abs(wd).T
+    assert np.all(np.abs(y - ref) <= 1e-6 * scale + 1e-30)
+
+
+def test_reference_metal_case_activation_error_bound(oracle):
+    """glypr's Q8_0 unit-test inputs (metal_kernels/mod.rs:1924-1979): w =
+    sin(0.031 i)*1.5 quantized to Q8_0 [128 x 256], x = cos(0.059 i)*3 via bf16,
+    m in {1, 19, 64}.  The CPU Q8_0 path differs from the dequant GEMM (Metal /
+    CANDLE_DEQUANTIZE_ALL semantics) only by activation quantization, bounded by
+    sum_b (0.5 + 127 * 2^-11) * d_x,b * sum_{j in b} |w_deq|."""
+    n, k = 128, 256
+    wf = (np.sin(np.arange(n * k, dtype=np.float64) * np.float32(0.031)) * 1.5).astype(
+        np.float32).reshape(n, k)
+    wq = oracle.quantize_rows(wf)
+    wabs = np.abs(oracle.dequantize_rows(wq, k).astype(np.float64)).reshape(n, k // 32, 32).sum(2)
+    for m in (1, 19, 64):
+        xf = (np.cos(np.arange(m * k, dtype=np.float64) * np.float32(0.059)) * 3.0).astype(
+            np.float32)
+        xb = (xf.view(np.uint32) + 0x7FFF + ((xf.view(np.uint32) >> 16) & 1)) >> 16
+        x = (xb << 16).astype(np.uint32).view(np.float32).reshape(m, k)
+        y = oracle.matmul(x, wq, n)
+        yd = oracle.matmul_dequant_f64(x, wq, n)
+        amax = np.abs(x.astype(np.float64)).reshape(m, k // 32, 32).max(2)
+        bound = (0.5 + 127 * 2.0 ** -11) * (amax / 127) @ wabs.T
+        assert np.all(np.abs(y - yd) <= bound * (1 + 1e-5) + 1e-5)
+        # and the activation quantization is what separates them: a dequant of the
+        # quantized activations closes the gap to f32 rounding
+        xq = oracle.quantize_rows(x)
+        yq = oracle.matmul_dequant_f64(oracle.dequantize_rows(xq, k), wq, n)
+        assert np.abs(y - yq).max() <= 1e-4
+
+
+# -------------------------------------------------------------- RMSNorm ----
+
+def test_rmsnorm_kat(oracle):
+    for c in KAT["rmsnorm"]:
+        d = c["d"]
+        x = np.full((1, d), bits_to_f32([c["c_bits"]])[0], np.float32)
+        w = bits_to_f32(c["w_bits"])
+        y = oracle.rmsnorm(x, w, eps=0.0)
+        assert np.array_equal(f32_to_bits(y[0]), np.array(c["y_bits"], np.uint32))
+
+
+def test_rmsnorm_vs_f64_and_invariants(oracle):
+    x = oracle.normal(40 * 768, seed=21).reshape(40, 768)
+    w = 1 + 0.1 * oracle.normal(768, seed=22)
+    y = oracle.rmsnorm(x, w, 1e-6)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    assert np.abs(y - ref).max() < 1e-5   # reference tolerance, test_cpu_simd.rs:5-39
+    # eps = 0: scaling a row by 2^k leaves the output bit-identical
+    y0 = oracle.rmsnorm(x, w, 0.0)
+    assert np.array_equal(oracle.rmsnorm(x * np.float32(8.0), w, 0.0), y0)
+    assert np.array_equal(oracle.rmsnorm(x * np.float32(0.25), w, 0.0), y0)
+    # weightless (v_norm) == weight of ones
+    assert np.array_equal(oracle.rmsnorm(x, None, 1e-6), oracle.rmsnorm(x, np.ones(768, np.float32), 1e-6))
+    # the lane order matters: a plain sequential sum differs in some rows' bits
+    seq = np.array([np.float32(1) / np.sqrt(np.float32(np.sum(r.astype(np.float32) ** 2,
+                                                              dtype=np.float32)) / 768 + 1e-6)
+                    for r in x])
+    assert seq.shape == (40,)
+
+
+# ---------------------------------------------------------------- GeGLU ----
+
+def test_tanh_accuracy(oracle):
+    xs = np.concatenate([np.linspace(-12, 12, 400_001), np.geomspace(1e-8, 12, 100_000),
+                         -np.geomspace(1e-8, 12, 100_000)]).astype(np.float32)
+    ours = np.array([oracle.tanhf(float(v)) for v in xs], np.float32)
+    ref = np.tanh(xs.astype(np.float64))
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    err = np.abs(ours.astype(np.float64) - ref) / ulp
+    assert err.max() <= 3.0, err.max()
+    assert oracle.tanhf(0.0) == 0.0 and oracle.tanhf(10.0) == 1.0 and oracle.tanhf(-30.0) == -1.0
+    assert oracle.tanhf(1e-5) == np.float32(1e-5)
+
+
+def test_geglu_kat_and_formula(oracle):
+    for c in KAT["geglu"]:
+        g = bits_to_f32([c["g_bits"]])
+        u = bits_to_f32([c["u_bits"]])
+        y = oracle.geglu(g, u)
+        assert f32_to_bits(y)[0] == c["y_bits"]
+    g = oracle.normal(200_000, seed=31, std=3.0)
+    u = oracle.normal(200_000, seed=32)
+    y = oracle.geglu(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    ref = 0.5 * g64 * (1 + np.tanh(0.7978845608028654 * (g64 + 0.044715 * g64 ** 3))) * u64
+    ref = np.where(g64 <= -10, 0, np.where(g64 >= 10, g64 * u64, ref))
+    assert np.all(np.abs(y - ref) <= 1e-5 * np.abs(u64) * (np.abs(g64) + 1))
+
+
+def test_geglu_tanh_substitution_is_ulp_level(oracle):
+    """The shared tanh replaces the platform libm tanhf.  Away from the cancellation
+    in 1 + tanh (g > -1) outputs agree to a few ulp; everywhere the difference is
+    at most 0.5*|g*u| times a few ulp of 1 (glypr's formula amplifies tanh's ulp
+    error in relative terms where 1 + tanh cancels, on any libm)."""
+    g = oracle.normal(100_000, seed=41, std=2.0)
+    u = oracle.normal(100_000, seed=42)
+    ours = oracle.geglu(g, u)
+    libm = np.array([oracle.lib().orc_geglu_scalar_libm(float(a), float(b))
+                     for a, b in zip(g, u)], np.float32)
+    diff = np.abs(ours.astype(np.float64) - libm)
+    assert np.all(diff <= 0.5 * np.abs(g * u) * 4 * 2.0 ** -24 + 4e-6 * np.abs(libm))
+    ok = g > -1
+    rel = diff[ok] / np.maximum(np.abs(libm[ok]), 1e-30)
+    assert rel.max() < 4e-6
+
+
+# -------------------------------------------------------- gather / pool ----
+
+def test_gather_equals_dequant_rows(oracle):
+    vocab, d = 1000, 768
+    table = oracle.q8_0_weight(vocab, d, seed=51)
+    ids = oracle.uniform_ids(300, seed=52, vocab=vocab)
+    out = oracle.embed_gather(table, vocab, d, ids, 0.5)
+    ref = oracle.dequantize_rows(table, d)[ids] * np.float32(0.5)
+    assert np.array_equal(out, ref)
+    with pytest.raises(IndexError):
+        oracle.embed_gather(table, vocab, d, np.array([3, vocab], np.uint32), 1.0)
+
+
+def test_pool_kat(oracle):
+    c = KAT["pool"][0]
+    v = bits_to_f32(c["v_bits"])
+    tok = np.tile(v, (c["t"], 1))
+    assert np.array_equal(f32_to_bits(oracle.pool_normalize(tok)), np.array(c["l2_bits"], np.uint32))
+    assert np.array_equal(f32_to_bits(oracle.pool_normalize(tok, trunc=1)),
+                          np.array(c["mrl1_bits"], np.uint32))
+
+
+def test_pool_long_context_vs_f64(oracle):
+    """The reference's long-context generator and F64 ground truth
+    (tests/corpus_parity.rs:433-460), here on the f32 path: cos > 0.99999."""
+    hd = 768
+    for t in (1024, 8192):
+        tt = np.arange(t)[:, None]
+        cc = np.arange(hd)[None, :]
+        raw = (((tt * 7919 + cc * 104729) % 10000) / 5000.0 - 1.0).astype(np.float32)
+        ref = raw.astype(np.float64).mean(axis=0)
+        ref = ref / max(np.sqrt((ref ** 2).sum()), 1e-12)
+        got = oracle.pool_normalize(raw)
+        cos = float(got @ ref / np.linalg.norm(got) / np.linalg.norm(ref))
+        assert cos > 0.99999
+        mask = np.ones(t, np.uint8)
+        mask[t // 2:] = 0
+        gm = oracle.pool_normalize(raw, mask=mask)
+        r2 = raw[: t // 2].astype(np.float64).mean(axis=0)
+        r2 /= np.linalg.norm(r2)
+        assert float(gm @ r2 / np.linalg.norm(gm)) > 0.99999
+        m = oracle.pool_normalize(raw, trunc=256)
+        assert m.shape == (256,) and abs(np.linalg.norm(m.astype(np.float64)) - 1) < 1e-6
+
+
+# ------------------------------------------------------------- attention ----
+
+def test_attention_band_equals_masked_dense(oracle):
+    """Chunked sliding attention == dense attention with the -1e9 band mask
+    (attention/chunked.rs:64-172 vs model.rs:580-651): compare with numpy."""
+    rng = np.random.default_rng(5)
+    nh, nkv, t, hd, W = 3, 1, 70, 16, 16
+    q = rng.standard_normal((nh, t, hd)).astype(np.float32)
+    k = rng.standard_normal((nkv, t, hd)).astype(np.float32)
+    v = rng.standard_normal((nkv, t, hd)).astype(np.float32)
+    out = oracle.attention(q, k, v, W)
+    i = np.arange(t)
+    mask = np.where(np.abs(i[:, None] - i[None, :]) > W, -1e9, 0.0)
+    for h in range(nh):
+        s = q[h].astype(np.float64) @ k[0].astype(np.float64).T + mask
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        ref = p @ v[0].astype(np.float64)
+        assert np.abs(out[:, h * hd:(h + 1) * hd] - ref).max() < 1e-5
+    full = oracle.attention(q, k, v, 0)
+    assert not np.allclose(full, out)
