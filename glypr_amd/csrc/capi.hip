@@ -253,7 +253,7 @@ int check_mlp_args(const glypr_q8w* gu, const glypr_q8w* down, const float* x, f
   GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
   RET_IF(check_variant(variant));
   GLYPR_CHECK(gu != nullptr && down != nullptr, GLYPR_ERR_INVALID_ARG, "weight handle is NULL");
-  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(m == 0 || (x != nullptr && y != nullptr), GLYPR_ERR_INVALID_ARG, "x or y is NULL");
   GLYPR_CHECK(aligned16(x) && aligned16(y), GLYPR_ERR_ALIGNMENT,
               "x and y must be 16-byte aligned");
   GLYPR_CHECK(gu->n == 2 * down->k, GLYPR_ERR_SHAPE,
@@ -494,7 +494,7 @@ int glypr_hip_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x
   GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
   RET_IF(check_variant(variant));
   GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
-  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(m == 0 || (x != nullptr && y != nullptr), GLYPR_ERR_INVALID_ARG, "x or y is NULL");
   GLYPR_CHECK(aligned16(x) && aligned16(y), GLYPR_ERR_ALIGNMENT,
               "x and y must be 16-byte aligned");
   RET_IF(check_ctx(ctx));
@@ -511,7 +511,7 @@ int glypr_hip_rmsnorm(glypr_hip_ctx* ctx, const float* x, const float* weight, f
   clear_error();
   GLYPR_CHECK(rows >= 0 && dim > 0, GLYPR_ERR_SHAPE, "shape (%lld, %lld) invalid",
               (long long)rows, (long long)dim);
-  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(rows == 0 || (x != nullptr && y != nullptr), GLYPR_ERR_INVALID_ARG, "x or y is NULL");
   RET_IF(check_ctx(ctx));
   if (rows == 0) return GLYPR_OK;
   DeviceScope ds(ctx->device);
@@ -527,7 +527,7 @@ int glypr_hip_rmsnorm_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const 
   GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
   RET_IF(check_variant(variant));
   GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
-  GLYPR_CHECK(x != nullptr && y != nullptr, GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(m == 0 || (x != nullptr && y != nullptr), GLYPR_ERR_INVALID_ARG, "x or y is NULL");
   GLYPR_CHECK(aligned16(x) && aligned16(y) && aligned16(norm_weight), GLYPR_ERR_ALIGNMENT,
               "x, y and norm_weight must be 16-byte aligned");
   RET_IF(check_ctx(ctx));

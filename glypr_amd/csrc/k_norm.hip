@@ -13,107 +13,46 @@
 
 namespace glypr {
 
-// Sum of squares of one row in the reference's order, returned to all 8 lanes
-// of the row's group.  j = lane & 7.
-__device__ __forceinline__ float row_sumsq(const float* xr, int dim, int j,
-                                           bool valid) {
+// Fallback for dims that are not a multiple of 4 or exceed 2048: eight lanes
+// per row run the chains straight from global memory.
+__global__ void __launch_bounds__(256) rmsnorm_generic_kernel(const float* x, const float* w,
+                                                              float eps, float* y, int64_t rows,
+                                                              int dim) {
+  int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  int j = threadIdx.x & 7;
+  bool valid = row < rows;
+  const float* xr = x + row * dim;
   float acc = 0.0f;
   const int head = dim & ~7;
-  if (valid) {
-#pragma unroll 8
-    for (int c = j; c < head; c += 8) {
-      float v = xr[c];
-      acc = fmaf(v, v, acc);
-    }
-  }
-  float s = acc + __shfl_down(acc, 4, 8);  // j<4: l_j + l_{j+4}
-  float t = s + __shfl_down(s, 2, 8);      // j<2: s_j + s_{j+2}
-  float sum = t + __shfl_down(t, 1, 8);    // j=0: t_0 + t_1
-  sum = __shfl(sum, 0, 8);
   if (valid)
-    for (int c = head; c < dim; c++) sum += xr[c] * xr[c];
-  return sum;
-}
-
-__device__ __forceinline__ float rms_inv(float sum, int dim, float eps) {
-  return 1.0f / sqrtf(sum / (float)dim + eps);
-}
-
-// Plain RMSNorm, f32 out.  256 threads = 4 waves = 32 rows per block.
-__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* x, const float* w, float eps,
-                                                      float* y, int64_t rows, int dim) {
-  int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
-  int j = threadIdx.x & 7;
-  bool valid = row < rows;
-  const float* xr = x + row * dim;
-  float sum = row_sumsq(xr, dim, j, valid);
+    for (int c = j; c < head; c += 8) acc = fmaf(xr[c], xr[c], acc);
+  float s = acc + __shfl_down(acc, 4, 8);
+  float t = s + __shfl_down(s, 2, 8);
+  float sum = t + __shfl_down(t, 1, 8);
+  sum = __shfl(sum, 0, 8);
   if (!valid) return;
-  float inv = rms_inv(sum, dim, eps);
+  for (int c = head; c < dim; c++) sum += xr[c] * xr[c];
+  float inv = 1.0f / sqrtf(sum / (float)dim + eps);
   float* yr = y + row * dim;
-  // x may alias y: every lane finished reading x in row_sumsq's loop before the
-  // shuffles that follow it, and each lane only rewrites its own elements here.
-  if (w) {
-    for (int c = j; c < dim; c += 8) yr[c] = (xr[c] * inv) * w[c];
-  } else {
-    for (int c = j; c < dim; c += 8) yr[c] = xr[c] * inv;
-  }
+  for (int c = j; c < dim; c += 8) yr[c] = w ? (xr[c] * inv) * w[c] : xr[c] * inv;
 }
 
-hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* y, int64_t rows,
-                          int64_t dim, hipStream_t s) {
+static hipError_t launch_rmsnorm_generic(const float* x, const float* w, float eps, float* y,
+                                         int64_t rows, int64_t dim, hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  rmsnorm_kernel<<<(unsigned)((rows + 31) / 32), 256, 0, s>>>(x, w, eps, y, rows, (int)dim);
+  rmsnorm_generic_kernel<<<(unsigned)((rows + 31) / 32), 256, 0, s>>>(x, w, eps, y, rows,
+                                                                      (int)dim);
   return hipGetLastError();
 }
 
-// RMSNorm prologue emitting Q8_0 activations (int8 [rows][dim] + f32 f16-rounded
-// scales [rows][dim/32]) exactly as k_quants::matmul would quantize the
-// normalised rows.  After the sum, the row's 8 lanes re-read it in the
-// quantizer's layout: per 32-block, lane j owns values 4j..4j+3.
-__global__ void __launch_bounds__(256) rmsnorm_quant_kernel(const float* __restrict__ x,
-                                                            const float* __restrict__ w,
-                                                            float eps, int64_t rows, int dim,
-                                                            int8_t* __restrict__ xq,
-                                                            float* __restrict__ dx) {
-  int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
-  int j = threadIdx.x & 7;
-  bool valid = row < rows;
-  const float* xr = x + row * dim;
-  float sum = row_sumsq(xr, dim, j, valid);
-  float inv = rms_inv(sum, dim, eps);
-  const int nb = dim / QK;
-  for (int b = 0; b < nb; b++) {
-    v4f v = valid ? *reinterpret_cast<const v4f*>(xr + b * QK + 4 * j) : v4f{0, 0, 0, 0};
-    v4f wv = w ? *reinterpret_cast<const v4f*>(w + b * QK + 4 * j) : v4f{1, 1, 1, 1};
-    v4f yv;
-    float a = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      yv[e] = w ? (v[e] * inv) * wv[e] : v[e] * inv;
-      a = fmaxf(a, fabsf(yv[e]));
-    }
-    a = fmaxf(a, __shfl_xor(a, 1, 8));
-    a = fmaxf(a, __shfl_xor(a, 2, 8));
-    a = fmaxf(a, __shfl_xor(a, 4, 8));
-    QScale sc = q8_scale(a);
-    uint32_t packed = 0;
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-      packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
-    if (valid) {
-      *reinterpret_cast<uint32_t*>(xq + row * dim + b * QK + 4 * j) = packed;
-      if (j == 0) dx[row * nb + b] = sc.dq;
-    }
-  }
-}
+// One row per wave.  The row is read once, coalesced (lane l holds float4 #l,
+// #l+64, ... : with 8 lanes per 32-block that is exactly the quantizer's
+// layout), and also written to LDS so that lanes 0..7 can run the reference's
+// eight sequential FMA chains (lane j: elements j, j+8, j+16, ...) from LDS.
+// The chains are the only serial part; quantization then uses all 64 lanes.
+constexpr int NORM_WAVES = 4;  // rows per 256-thread block
 
-hipError_t launch_rmsnorm_quant(const float* x, const float* w, float eps, int64_t rows,
-                                int64_t dim, int8_t* xq, float* dx, hipStream_t s) {
-  if (rows == 0) return hipSuccess;
-  rmsnorm_quant_kernel<<<(unsigned)((rows + 31) / 32), 256, 0, s>>>(x, w, eps, rows, (int)dim, xq,
-                                                                    dx);
-  return hipGetLastError();
-}
+enum NormOut { OUT_F32 = 0, OUT_Q8 = 1, OUT_BF16 = 2 };
 
 __device__ __forceinline__ uint32_t bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
@@ -122,35 +61,136 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
   return r;
 }
 
-// RMSNorm prologue for the bf16-dequant GEMM: normalised rows rounded to bf16.
-__global__ void __launch_bounds__(256) rmsnorm_bf16_kernel(const float* __restrict__ x,
-                                                           const float* __restrict__ w,
-                                                           float eps, int64_t rows, int dim,
-                                                           uint16_t* __restrict__ xb) {
-  int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
-  int j = threadIdx.x & 7;
-  bool valid = row < rows;
+// NV = float4s per lane = ceil(dim / 256).  dim % 4 == 0 (dim % 32 == 0 for Q8).
+template <int NV, int MODE>
+__global__ void __launch_bounds__(64 * NORM_WAVES)
+rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64_t rows, int dim,
+                   float* y, int8_t* __restrict__ xq, float* __restrict__ dx,
+                   uint16_t* __restrict__ xb) {
+  extern __shared__ float lds_rows[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * NORM_WAVES + wave;
+  if (row >= rows) return;  // whole wave exits together
+  float* lrow = lds_rows + wave * dim;
   const float* xr = x + row * dim;
-  float sum = row_sumsq(xr, dim, j, valid);
-  if (!valid) return;
-  float inv = rms_inv(sum, dim, eps);
-  for (int c = 4 * j; c < dim; c += 32) {
-    v4f v = *reinterpret_cast<const v4f*>(xr + c);
-    v4f wv = w ? *reinterpret_cast<const v4f*>(w + c) : v4f{1, 1, 1, 1};
-    uint32_t o[4];
+  const int n4 = dim >> 2;
+
+  v4f v[NV];
 #pragma unroll
-    for (int e = 0; e < 4; e++) o[e] = bf16_rne(w ? (v[e] * inv) * wv[e] : v[e] * inv);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + c);
-    dst[0] = o[0] | (o[1] << 16);
-    dst[1] = o[2] | (o[3] << 16);
+  for (int i = 0; i < NV; i++) {
+    int c4 = lane + 64 * i;
+    v[i] = c4 < n4 ? *reinterpret_cast<const v4f*>(xr + 4 * c4) : v4f{0, 0, 0, 0};
   }
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    int c4 = lane + 64 * i;
+    if (c4 < n4) *reinterpret_cast<v4f*>(lrow + 4 * c4) = v[i];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+
+  // Reference-order sum of squares on lanes 0..7.
+  float sum = 0.0f;
+  const int head = dim & ~7;
+  if (lane < 8) {
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int c = lane; c < head; c += 8) {
+      float e = lrow[c];
+      acc = fmaf(e, e, acc);
+    }
+    float s = acc + __shfl_down(acc, 4, 8);
+    float t = s + __shfl_down(s, 2, 8);
+    sum = t + __shfl_down(t, 1, 8);
+    for (int c = head; c < dim; c++) sum += lrow[c] * lrow[c];
+  }
+  sum = __shfl(sum, 0);
+  const float inv = 1.0f / sqrtf(sum / (float)dim + eps);
+
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int c4 = lane + 64 * i;
+    const bool ok = c4 < n4;
+    v4f wv = (w && ok) ? *reinterpret_cast<const v4f*>(w + 4 * c4) : v4f{1, 1, 1, 1};
+    v4f yv;
+#pragma unroll
+    for (int e = 0; e < 4; e++) yv[e] = w ? (v[i][e] * inv) * wv[e] : v[i][e] * inv;
+    if constexpr (MODE == OUT_F32) {
+      if (ok) *reinterpret_cast<v4f*>(y + row * dim + 4 * c4) = yv;
+    } else if constexpr (MODE == OUT_BF16) {
+      if (ok) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
+        dst[0] = bf16_rne(yv[0]) | (bf16_rne(yv[1]) << 16);
+        dst[1] = bf16_rne(yv[2]) | (bf16_rne(yv[3]) << 16);
+      }
+    } else {
+      // 8 consecutive lanes hold one 32-block (dim % 32 == 0 keeps blocks whole).
+      float a = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(yv[e]));
+      a = fmaxf(a, __shfl_xor(a, 1, 8));
+      a = fmaxf(a, __shfl_xor(a, 2, 8));
+      a = fmaxf(a, __shfl_xor(a, 4, 8));
+      QScale sc = q8_scale(a);
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
+      if (ok) {
+        *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed;
+        if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc.dq;
+      }
+    }
+  }
+}
+
+template <int MODE>
+static hipError_t launch_norm(const float* x, const float* w, float eps, int64_t rows, int64_t dim,
+                              float* y, int8_t* xq, float* dx, uint16_t* xb, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
+  const size_t lds = (size_t)NORM_WAVES * dim * sizeof(float);
+  const int nv = (int)((dim + 255) / 256);
+  switch (nv) {
+#define NORM_CASE(N)                                                                        \
+  case N:                                                                                   \
+    rmsnorm_row_kernel<N, MODE><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w, eps, rows, (int)dim, \
+                                                                   y, xq, dx, xb);          \
+    break;
+    NORM_CASE(1)
+    NORM_CASE(2)
+    NORM_CASE(3)
+    NORM_CASE(4)
+    NORM_CASE(5)
+    NORM_CASE(6)
+    NORM_CASE(8)
+#undef NORM_CASE
+    default:
+      if (nv == 7) {
+        rmsnorm_row_kernel<8, MODE><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w, eps, rows, (int)dim,
+                                                                       y, xq, dx, xb);
+        break;
+      }
+      return hipErrorInvalidValue;  // dim > 2048: callers validate this
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* y, int64_t rows,
+                          int64_t dim, hipStream_t s) {
+  if (dim % 4 != 0 || dim > 2048) return launch_rmsnorm_generic(x, w, eps, y, rows, dim, s);
+  return launch_norm<OUT_F32>(x, w, eps, rows, dim, y, nullptr, nullptr, nullptr, s);
+}
+
+hipError_t launch_rmsnorm_quant(const float* x, const float* w, float eps, int64_t rows,
+                                int64_t dim, int8_t* xq, float* dx, hipStream_t s) {
+  return launch_norm<OUT_Q8>(x, w, eps, rows, dim, nullptr, xq, dx, nullptr, s);
 }
 
 hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_t rows,
                                int64_t dim, uint16_t* xb, hipStream_t s) {
-  if (rows == 0) return hipSuccess;
-  rmsnorm_bf16_kernel<<<(unsigned)((rows + 31) / 32), 256, 0, s>>>(x, w, eps, rows, (int)dim, xb);
-  return hipGetLastError();
+  return launch_norm<OUT_BF16>(x, w, eps, rows, dim, nullptr, nullptr, nullptr, xb, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -130,7 +130,7 @@ def test_matmul_deterministic_and_c3_rows(ctx, oracle):
 
 def test_rmsnorm_bit_exact(ctx, oracle):
     for rows, dim, with_w in [(37, 768, True), (512, 768, True), (96, 256, True), (40, 256, False),
-                              (5, 1152, True), (3, 20, True)]:
+                              (5, 1152, True), (3, 20, True), (6, 21, True), (4, 3000, False)]:
         say(f"rmsnorm rows={rows} dim={dim} weight={with_w}")
         x = oracle.normal(rows * dim, seed=rows + dim).reshape(rows, dim) * np.float32(2.5)
         w = (1 + 0.1 * oracle.normal(dim, seed=9)) if with_w else None
