@@ -52,13 +52,20 @@ SIGNATURES = {
     "glypr_hip_rmsnorm_mlp": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _int, _vp]),
     "glypr_hip_q8_0_embed_gather": (_int, [_vp, _vp, _vp, _i64, _f32, _vp, _vp]),
     "glypr_hip_pool_normalize": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "glypr_hip_attention": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _i64, _i64, _i64, _i64,
+                                   _i64, _vp, _vp]),
+    "glypr_hip_model_create": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
+    "glypr_hip_model_set_tensor": (_int, [_vp, ctypes.c_char_p, _vp, _i64, _i64, _int]),
+    "glypr_hip_model_finalize": (_int, [_vp]),
+    "glypr_hip_model_embed": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "glypr_hip_model_destroy": (_int, [_vp]),
     "glypr_hip_profile_enable": (_int, [_vp, _int]),
     "glypr_hip_profile_read": (_int, [_vp, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(_i64)]),
     "glypr_hip_kernel_name": (ctypes.c_char_p, [_int]),
 }
 
-KERNEL_COUNT = 13
+KERNEL_COUNT = 16
 
 
 class GlyprError(RuntimeError):

@@ -81,6 +81,22 @@ hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, h
 hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t d, int64_t trunc,
                        float* out, float* scratch /* d floats */, hipStream_t s);
 
+// h = h + rmsnorm(x; w_post); if xq: (xq, dx) = Q8_0(rmsnorm(h; w_next)).  dim % 32 == 0.
+hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
+                                float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
+                                hipStream_t s);
+
+// ---- k_attn.hip ----
+hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
+                           int64_t hd, const float* qnw, const float* knw, float eps,
+                           const float* cos_t, const float* sin_t, uint16_t* q_hi, uint16_t* q_lo,
+                           uint16_t* k_hi, uint16_t* k_lo, uint16_t* vt_hi, uint16_t* vt_lo,
+                           hipStream_t s);
+hipError_t launch_attention(const uint16_t* q_hi, const uint16_t* q_lo, const uint16_t* k_hi,
+                            const uint16_t* k_lo, const uint16_t* vt_hi, const uint16_t* vt_lo,
+                            float* ctx, int64_t T, int64_t Tp, int64_t nq, int64_t nkv, int64_t hd,
+                            int64_t window, hipStream_t s);
+
 // ---- k_gemm_i8.hip ----
 // y[m,n] = sum_b ((float)S_b * dw[n,b]) * dx[m,b], sequential over b (exact).
 hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,

@@ -194,6 +194,130 @@ hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_
 }
 
 // ---------------------------------------------------------------------------
+// Layer boundary: RMSNorm::forward_residual_add (norm.rs:65-95),
+//   h = h + rmsnorm(x; w_post),
+// optionally followed by the next sublayer's RMSNorm prologue on the new h,
+// emitting Q8_0 activations (xq, dx) for the next GEMM.  Both norms use the
+// reference reduction order, so h and the quantized activations are
+// bit-identical to the CPU path.  One row per wave.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_row_inv(const float* lrow, int dim, int lane, float eps) {
+  float sum = 0.0f;
+  const int head = dim & ~7;
+  if (lane < 8) {
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int c = lane; c < head; c += 8) {
+      float e = lrow[c];
+      acc = fmaf(e, e, acc);
+    }
+    float s = acc + __shfl_down(acc, 4, 8);
+    float t = s + __shfl_down(s, 2, 8);
+    sum = t + __shfl_down(t, 1, 8);
+    for (int c = head; c < dim; c++) sum += lrow[c] * lrow[c];
+  }
+  sum = __shfl(sum, 0);
+  return 1.0f / sqrtf(sum / (float)dim + eps);
+}
+
+template <int NV, bool QNEXT>
+__global__ void __launch_bounds__(64 * NORM_WAVES)
+residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_post,
+                     float* __restrict__ h, const float* __restrict__ w_next, float eps,
+                     int64_t rows, int dim, int8_t* __restrict__ xq, float* __restrict__ dx) {
+  extern __shared__ float lds_rows[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * NORM_WAVES + wave;
+  if (row >= rows) return;
+  float* lrow = lds_rows + wave * dim;
+  const int n4 = dim >> 2;
+  v4f v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    int c4 = lane + 64 * i;
+    v[i] = c4 < n4 ? *reinterpret_cast<const v4f*>(x + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
+    if (c4 < n4) *reinterpret_cast<v4f*>(lrow + 4 * c4) = v[i];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  const float inv = wave_row_inv(lrow, dim, lane, eps);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    int c4 = lane + 64 * i;
+    if (c4 < n4) {
+      v4f wv = *reinterpret_cast<const v4f*>(w_post + 4 * c4);
+      v4f hv = *reinterpret_cast<const v4f*>(h + row * dim + 4 * c4);
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[i][e] = hv[e] + (v[i][e] * inv) * wv[e];
+      *reinterpret_cast<v4f*>(h + row * dim + 4 * c4) = v[i];
+      if (QNEXT) *reinterpret_cast<v4f*>(lrow + 4 * c4) = v[i];
+    }
+  }
+  if constexpr (QNEXT) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const float inv2 = wave_row_inv(lrow, dim, lane, eps);
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int c4 = lane + 64 * i;
+      const bool ok = c4 < n4;
+      v4f wv = (w_next && ok) ? *reinterpret_cast<const v4f*>(w_next + 4 * c4) : v4f{1, 1, 1, 1};
+      v4f yv;
+      float a = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        yv[e] = w_next ? (v[i][e] * inv2) * wv[e] : v[i][e] * inv2;
+        a = fmaxf(a, fabsf(yv[e]));
+      }
+      a = fmaxf(a, __shfl_xor(a, 1, 8));
+      a = fmaxf(a, __shfl_xor(a, 2, 8));
+      a = fmaxf(a, __shfl_xor(a, 4, 8));
+      QScale sc = q8_scale(a);
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
+      if (ok) {
+        *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed;
+        if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc.dq;
+      }
+    }
+  }
+}
+
+hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
+                                float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
+                                hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
+  const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
+  const size_t lds = (size_t)NORM_WAVES * dim * sizeof(float);
+  const int nv = (int)((dim + 255) / 256);
+  const bool q = xq != nullptr;
+#define RES_CASE(N)                                                                              \
+  case N:                                                                                        \
+    if (q)                                                                                       \
+      residual_norm_kernel<N, true><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w_post, h, w_next, eps,  \
+                                                                       rows, (int)dim, xq, dx);  \
+    else                                                                                         \
+      residual_norm_kernel<N, false><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w_post, h, w_next, eps, \
+                                                                        rows, (int)dim, xq, dx); \
+    break;
+  switch (nv) {
+    RES_CASE(1)
+    RES_CASE(2)
+    RES_CASE(3)
+    RES_CASE(4)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef RES_CASE
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // GeGLU elementwise (cpu_geglu).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) geglu_kernel(const float* g, const float* u, float* out,

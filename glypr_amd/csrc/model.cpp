@@ -1,0 +1,496 @@
+// model.cpp — host-side mirror of glypr's text backbone over the HIP kernels.
+//
+// Class names follow the reference modules they replace:
+//   LinearOp            linear.rs:5-172        (a Q8_0 weight handle + forward)
+//   RMSNorm             norm.rs:4-95           (device f32 weight + eps)
+//   SelfAttention       attention/mod.rs:33-277
+//   MLP                 mlp.rs:6-70
+//   EncoderLayer        layer.rs:8-50          (PLE block and layer scalar omitted)
+//   EmbeddingGemma2Model model.rs:244-705      (gather, layers, final norm, pooling)
+// The forward pass runs every projection as an INT8_EXACT Q8_0 GEMM and fuses
+// what the reference computes in separate ops:
+//   - each RMSNorm that feeds a projection is the GEMM's quantizing prologue;
+//   - forward_residual_add of one sublayer and the next sublayer's input
+//     RMSNorm are one kernel (residual_norm);
+//   - q/k/v and gate/up are single fused GEMMs (try_concat, linear.rs:82-148);
+//   - GeGLU is the gate/up GEMM's epilogue.
+// All of these are bit-exact with the CPU path; attention differs from it
+// only by f32 rounding (see k_attn.hip).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "host_common.hpp"
+#include "internal.hpp"
+
+using namespace glypr;
+
+namespace glypr {
+namespace host {
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  int ensure(size_t bytes) {
+    if (bytes <= cap) return GLYPR_OK;
+    if (p) {
+      GLYPR_TRY_HIP(hipDeviceSynchronize(), "buffer growth: hipDeviceSynchronize");
+      GLYPR_TRY_HIP(hipFree(p), "buffer growth: hipFree");
+      p = nullptr;
+      cap = 0;
+    }
+    size_t c = align_up(bytes, 1 << 16);
+    GLYPR_TRY_HIP(hipMalloc(&p, c), "buffer: hipMalloc");
+    cap = c;
+    return GLYPR_OK;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+  }
+  template <typename T>
+  T* as() const { return reinterpret_cast<T*>(p); }
+};
+
+struct LinearOp {
+  glypr_q8w* w = nullptr;
+};
+
+struct RMSNorm {
+  float* weight = nullptr;  // device, nullptr = weightless
+};
+
+struct SelfAttention {
+  LinearOp q, k, v, o;
+  LinearOp fused_qkv;  // try_concat([q, k, v])
+  RMSNorm q_norm, k_norm;
+};
+
+struct MLP {
+  LinearOp gate, up, down;
+  LinearOp fused_gate_up;  // try_concat([gate, up])
+};
+
+struct EncoderLayer {
+  SelfAttention self_attn;
+  MLP mlp;
+  RMSNorm input_layernorm, post_attention_layernorm, pre_feedforward_layernorm,
+      post_feedforward_layernorm;
+  bool full_attention = false;
+};
+
+}  // namespace host
+}  // namespace glypr
+
+using namespace glypr::host;
+
+struct glypr_model {
+  glypr_hip_ctx* ctx = nullptr;
+  glypr_model_config cfg{};
+  LinearOp token_embd;
+  std::vector<EncoderLayer> layers;
+  RMSNorm norm;  // output_norm
+  bool finalized = false;
+  // RoPE tables [rope_cap][head_dim] for the sliding and full layer types.
+  DevBuf cos_s, sin_s, cos_f, sin_f;
+  int64_t rope_cap = 0;
+  // activations
+  DevBuf h, xq, dx, qkv, attn_q_hi, attn_q_lo, attn_k_hi, attn_k_lo, attn_vt_hi, attn_vt_lo, ctx_out,
+      cq, dc, proj, hq, dh, normed, pooled, ids;
+  int64_t cap_t = 0;
+};
+
+namespace {
+
+inline float* dev_f32(const DevBuf& b) { return b.as<float>(); }
+
+// RotaryEmbedding::new + get_cos_sin (rope.rs:14-87): inv_freq computed in f64
+// and cast to f32; positions as f32; freqs = pos * inv_freq in f32;
+// emb = cat(freqs, freqs); cos/sin in f32.
+void rope_table(int64_t hd, double theta, int64_t t, std::vector<float>& c, std::vector<float>& s) {
+  const int64_t half = hd / 2;
+  std::vector<float> inv(half);
+  for (int64_t i = 0; i < half; i++)
+    inv[i] = (float)(1.0 / pow(theta, (double)(2 * i) / (double)hd));
+  c.resize(t * hd);
+  s.resize(t * hd);
+  for (int64_t p = 0; p < t; p++)
+    for (int64_t i = 0; i < hd; i++) {
+      float f = (float)p * inv[i % half];
+      c[p * hd + i] = cosf(f);
+      s[p * hd + i] = sinf(f);
+    }
+}
+
+int upload_f32(const float* host, int64_t n, float** dev) {
+  GLYPR_TRY_HIP(hipMalloc((void**)dev, (size_t)n * sizeof(float)), "norm weight: hipMalloc");
+  GLYPR_TRY_HIP(hipMemcpy(*dev, host, (size_t)n * sizeof(float), hipMemcpyHostToDevice),
+                "norm weight: upload");
+  return GLYPR_OK;
+}
+
+int ensure_rope(glypr_model* m, int64_t t) {
+  if (t <= m->rope_cap) return GLYPR_OK;
+  const int64_t cap = t > 8320 ? t : 8320;  // DEFAULT_MAX_SEQ_LEN, lib.rs:47
+  const int64_t hd = m->cfg.head_dim;
+  std::vector<float> c, s;
+  const size_t bytes = (size_t)(cap * hd) * sizeof(float);
+  RET_IF(m->cos_s.ensure(bytes));
+  RET_IF(m->sin_s.ensure(bytes));
+  RET_IF(m->cos_f.ensure(bytes));
+  RET_IF(m->sin_f.ensure(bytes));
+  rope_table(hd, m->cfg.rope_theta_sliding, cap, c, s);
+  GLYPR_TRY_HIP(hipMemcpy(m->cos_s.p, c.data(), bytes, hipMemcpyHostToDevice), "rope upload");
+  GLYPR_TRY_HIP(hipMemcpy(m->sin_s.p, s.data(), bytes, hipMemcpyHostToDevice), "rope upload");
+  rope_table(hd, m->cfg.rope_theta_full, cap, c, s);
+  GLYPR_TRY_HIP(hipMemcpy(m->cos_f.p, c.data(), bytes, hipMemcpyHostToDevice), "rope upload");
+  GLYPR_TRY_HIP(hipMemcpy(m->sin_f.p, s.data(), bytes, hipMemcpyHostToDevice), "rope upload");
+  m->rope_cap = cap;
+  return GLYPR_OK;
+}
+
+int ensure_activations(glypr_model* m, int64_t t) {
+  if (t <= m->cap_t) return GLYPR_OK;
+  const glypr_model_config& c = m->cfg;
+  const int64_t tp = (t + 31) / 32 * 32;
+  const int64_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+  const int64_t wide = c.hidden > qd ? c.hidden : qd;
+  RET_IF(m->h.ensure((size_t)(t * c.hidden) * 4));
+  RET_IF(m->xq.ensure((size_t)(t * wide)));
+  RET_IF(m->dx.ensure((size_t)(t * (wide / 32)) * 4));
+  RET_IF(m->qkv.ensure((size_t)(t * (qd + 2 * kvd)) * 4));
+  RET_IF(m->attn_q_hi.ensure((size_t)(tp * qd) * 2));
+  RET_IF(m->attn_q_lo.ensure((size_t)(tp * qd) * 2));
+  RET_IF(m->attn_k_hi.ensure((size_t)(tp * kvd) * 2));
+  RET_IF(m->attn_k_lo.ensure((size_t)(tp * kvd) * 2));
+  RET_IF(m->attn_vt_hi.ensure((size_t)(tp * kvd) * 2));
+  RET_IF(m->attn_vt_lo.ensure((size_t)(tp * kvd) * 2));
+  RET_IF(m->ctx_out.ensure((size_t)(t * qd) * 4));
+  RET_IF(m->cq.ensure((size_t)(t * qd)));
+  RET_IF(m->dc.ensure((size_t)(t * (qd / 32)) * 4));
+  RET_IF(m->proj.ensure((size_t)(t * c.hidden) * 4));
+  RET_IF(m->hq.ensure((size_t)(t * c.ffn)));
+  RET_IF(m->dh.ensure((size_t)(t * (c.ffn / 32)) * 4));
+  RET_IF(m->normed.ensure((size_t)(t * c.hidden) * 4));
+  RET_IF(m->pooled.ensure((size_t)c.hidden * 4));
+  RET_IF(m->ids.ensure((size_t)t * 4));
+  m->cap_t = t;
+  return GLYPR_OK;
+}
+
+void free_model(glypr_model* m) {
+  auto drop = [](LinearOp& l) {
+    if (l.w) glypr_hip_q8_0_weight_destroy(l.w);
+    l.w = nullptr;
+  };
+  auto dropn = [](RMSNorm& n) {
+    if (n.weight) (void)hipFree(n.weight);
+    n.weight = nullptr;
+  };
+  drop(m->token_embd);
+  dropn(m->norm);
+  for (auto& L : m->layers) {
+    drop(L.self_attn.q);
+    drop(L.self_attn.k);
+    drop(L.self_attn.v);
+    drop(L.self_attn.o);
+    drop(L.self_attn.fused_qkv);
+    dropn(L.self_attn.q_norm);
+    dropn(L.self_attn.k_norm);
+    drop(L.mlp.gate);
+    drop(L.mlp.up);
+    drop(L.mlp.down);
+    drop(L.mlp.fused_gate_up);
+    dropn(L.input_layernorm);
+    dropn(L.post_attention_layernorm);
+    dropn(L.pre_feedforward_layernorm);
+    dropn(L.post_feedforward_layernorm);
+  }
+  for (DevBuf* b : {&m->cos_s, &m->sin_s, &m->cos_f, &m->sin_f, &m->h, &m->xq, &m->dx, &m->qkv,
+                    &m->attn_q_hi, &m->attn_q_lo, &m->attn_k_hi, &m->attn_k_lo, &m->attn_vt_hi,
+                    &m->attn_vt_lo, &m->ctx_out, &m->cq, &m->dc, &m->proj, &m->hq, &m->dh,
+                    &m->normed, &m->pooled, &m->ids})
+    b->release();
+}
+
+// The attention core shared by glypr_hip_attention and the model forward.
+int attention_core(glypr_hip_ctx* ctx, const float* qkv, const float* qnw, const float* knw,
+                   float eps, const float* cos_t, const float* sin_t, int64_t t, int64_t nq,
+                   int64_t nkv, int64_t hd, int64_t window, uint16_t* q_hi, uint16_t* q_lo,
+                   uint16_t* k_hi, uint16_t* k_lo, uint16_t* vt_hi, uint16_t* vt_lo, float* out,
+                   hipStream_t s) {
+  const int64_t tp = (t + 31) / 32 * 32;
+  LAUNCH(GLYPR_K_QKV_POST, s,
+         launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q_hi, q_lo, k_hi,
+                         k_lo, vt_hi, vt_lo, s),
+         "qkv_post launch");
+  LAUNCH(GLYPR_K_ATTENTION, s,
+         launch_attention(q_hi, q_lo, k_hi, k_lo, vt_hi, vt_lo, out, t, tp, nq, nkv, hd, window, s),
+         "attention launch");
+  return GLYPR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_norm_weight,
+                        const float* k_norm_weight, float eps, const float* cos_table,
+                        const float* sin_table, int64_t t, int64_t n_heads, int64_t n_kv_heads,
+                        int64_t head_dim, int64_t window, float* ctx_out, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(t >= 0 && n_heads > 0 && n_kv_heads > 0 && window >= 0, GLYPR_ERR_SHAPE,
+              "invalid attention shape");
+  GLYPR_CHECK(head_dim == 256, GLYPR_ERR_UNSUPPORTED, "head_dim %lld (only 256 is supported)",
+              (long long)head_dim);
+  GLYPR_CHECK(n_heads % n_kv_heads == 0, GLYPR_ERR_SHAPE,
+              "n_heads %lld not a multiple of n_kv_heads %lld", (long long)n_heads,
+              (long long)n_kv_heads);
+  GLYPR_CHECK(t == 0 || (qkv && cos_table && sin_table && ctx_out), GLYPR_ERR_INVALID_ARG,
+              "qkv, cos/sin tables or ctx_out is NULL");
+  GLYPR_CHECK(aligned16(qkv) && aligned16(ctx_out) && aligned16(cos_table) &&
+                  aligned16(sin_table) && aligned16(q_norm_weight) && aligned16(k_norm_weight),
+              GLYPR_ERR_ALIGNMENT, "attention buffers must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  if (t == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const int64_t tp = (t + 31) / 32 * 32;
+  const size_t qb = align_up((size_t)(tp * n_heads * head_dim) * 2, 256);
+  const size_t kb = align_up((size_t)(tp * n_kv_heads * head_dim) * 2, 256);
+  RET_IF(ensure_ws(ctx, 2 * qb + 4 * kb));
+  char* base = (char*)ctx->ws;
+  uint16_t* q_hi = (uint16_t*)base;
+  uint16_t* q_lo = (uint16_t*)(base + qb);
+  uint16_t* k_hi = (uint16_t*)(base + 2 * qb);
+  uint16_t* k_lo = (uint16_t*)(base + 2 * qb + kb);
+  uint16_t* v_hi = (uint16_t*)(base + 2 * qb + 2 * kb);
+  uint16_t* v_lo = (uint16_t*)(base + 2 * qb + 3 * kb);
+  return attention_core(ctx, qkv, q_norm_weight, k_norm_weight, eps, cos_table, sin_table, t,
+                        n_heads, n_kv_heads, head_dim, window, q_hi, q_lo, k_hi, k_lo, v_hi,
+                        v_lo, ctx_out, (hipStream_t)stream);
+}
+
+int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
+                           glypr_model** out) {
+  clear_error();
+  GLYPR_CHECK(cfg != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "cfg or out is NULL");
+  *out = nullptr;
+  GLYPR_CHECK(cfg->hidden > 0 && cfg->ffn > 0 && cfg->n_layers > 0 && cfg->vocab > 0,
+              GLYPR_ERR_SHAPE, "model dimensions must be positive");
+  GLYPR_CHECK(cfg->hidden % 32 == 0 && cfg->ffn % 32 == 0 && cfg->hidden <= 1024, GLYPR_ERR_SHAPE,
+              "hidden (<= 1024) and ffn must be multiples of 32");
+  GLYPR_CHECK(cfg->head_dim == 256, GLYPR_ERR_UNSUPPORTED, "head_dim %lld (only 256)",
+              (long long)cfg->head_dim);
+  GLYPR_CHECK(cfg->n_heads > 0 && cfg->n_kv_heads > 0 && cfg->n_heads % cfg->n_kv_heads == 0,
+              GLYPR_ERR_SHAPE, "n_heads must be a positive multiple of n_kv_heads");
+  RET_IF(check_ctx(ctx));
+  glypr_model* m = new (std::nothrow) glypr_model();
+  GLYPR_CHECK(m != nullptr, GLYPR_ERR_OOM, "host allocation failed");
+  m->ctx = ctx;
+  m->cfg = *cfg;
+  m->layers.resize((size_t)cfg->n_layers);
+  for (int64_t i = 0; i < cfg->n_layers; i++)
+    m->layers[(size_t)i].full_attention = ((i + 1) % 6) == 0;  // config.rs:131-140
+  *out = m;
+  return GLYPR_OK;
+}
+
+int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* data, int64_t rows,
+                               int64_t cols, int dtype) {
+  clear_error();
+  GLYPR_CHECK(m != nullptr && name != nullptr && data != nullptr, GLYPR_ERR_INVALID_ARG,
+              "model, name or data is NULL");
+  GLYPR_CHECK(dtype == 0 || dtype == 1, GLYPR_ERR_UNSUPPORTED, "dtype %d (0 = f32, 1 = Q8_0)",
+              dtype);
+  GLYPR_CHECK(!m->finalized, GLYPR_ERR_INVALID_ARG, "model already finalized");
+  const glypr_model_config& c = m->cfg;
+  DeviceScope ds(m->ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  const std::string n(name);
+  const int64_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+
+  auto set_q8 = [&](LinearOp& op, int64_t er, int64_t ec) -> int {
+    GLYPR_CHECK(dtype == 1, GLYPR_ERR_UNSUPPORTED, "%s must be Q8_0", name);
+    GLYPR_CHECK(rows == er && cols == ec, GLYPR_ERR_SHAPE,
+                "%s has shape (%lld, %lld), expected (%lld, %lld)", name, (long long)rows,
+                (long long)cols, (long long)er, (long long)ec);
+    if (op.w) glypr_hip_q8_0_weight_destroy(op.w);
+    op.w = nullptr;
+    return glypr_hip_q8_0_weight_create(m->ctx, (const uint8_t*)data, rows, cols, &op.w);
+  };
+  auto set_norm = [&](RMSNorm& nm, int64_t len) -> int {
+    GLYPR_CHECK(dtype == 0, GLYPR_ERR_UNSUPPORTED, "%s must be f32", name);
+    GLYPR_CHECK(rows * cols == len, GLYPR_ERR_SHAPE, "%s has %lld values, expected %lld", name,
+                (long long)(rows * cols), (long long)len);
+    if (nm.weight) (void)hipFree(nm.weight);
+    nm.weight = nullptr;
+    return upload_f32((const float*)data, len, &nm.weight);
+  };
+
+  if (n == "token_embd.weight") return set_q8(m->token_embd, c.vocab, c.hidden);
+  if (n == "output_norm.weight") return set_norm(m->norm, c.hidden);
+  int layer = -1, consumed = 0;
+  char field[64] = {0};
+  if (sscanf(name, "blk.%d.%63[^.].weight%n", &layer, field, &consumed) == 2 &&
+      name[consumed] == '\0' && layer >= 0 && layer < c.n_layers) {
+    EncoderLayer& L = m->layers[(size_t)layer];
+    const std::string f(field);
+    if (f == "attn_norm") return set_norm(L.input_layernorm, c.hidden);
+    if (f == "post_attention_norm") return set_norm(L.post_attention_layernorm, c.hidden);
+    if (f == "ffn_norm") return set_norm(L.pre_feedforward_layernorm, c.hidden);
+    if (f == "post_ffw_norm") return set_norm(L.post_feedforward_layernorm, c.hidden);
+    if (f == "attn_q_norm") return set_norm(L.self_attn.q_norm, c.head_dim);
+    if (f == "attn_k_norm") return set_norm(L.self_attn.k_norm, c.head_dim);
+    if (f == "attn_q") return set_q8(L.self_attn.q, qd, c.hidden);
+    if (f == "attn_k") return set_q8(L.self_attn.k, kvd, c.hidden);
+    if (f == "attn_v") return set_q8(L.self_attn.v, kvd, c.hidden);
+    if (f == "attn_output") return set_q8(L.self_attn.o, c.hidden, qd);
+    if (f == "ffn_gate") return set_q8(L.mlp.gate, c.ffn, c.hidden);
+    if (f == "ffn_up") return set_q8(L.mlp.up, c.ffn, c.hidden);
+    if (f == "ffn_down") return set_q8(L.mlp.down, c.hidden, c.ffn);
+  }
+  return set_error(GLYPR_ERR_INVALID_ARG, "unknown tensor name '%s'", name);
+}
+
+int glypr_hip_model_finalize(glypr_model* m) {
+  clear_error();
+  GLYPR_CHECK(m != nullptr, GLYPR_ERR_INVALID_ARG, "model is NULL");
+  if (m->finalized) return GLYPR_OK;
+  GLYPR_CHECK(m->token_embd.w && m->norm.weight, GLYPR_ERR_INVALID_ARG,
+              "token_embd.weight or output_norm.weight missing");
+  for (size_t i = 0; i < m->layers.size(); i++) {
+    EncoderLayer& L = m->layers[i];
+    GLYPR_CHECK(L.self_attn.q.w && L.self_attn.k.w && L.self_attn.v.w && L.self_attn.o.w &&
+                    L.mlp.gate.w && L.mlp.up.w && L.mlp.down.w && L.self_attn.q_norm.weight &&
+                    L.self_attn.k_norm.weight && L.input_layernorm.weight &&
+                    L.post_attention_layernorm.weight && L.pre_feedforward_layernorm.weight &&
+                    L.post_feedforward_layernorm.weight,
+                GLYPR_ERR_INVALID_ARG, "layer %zu is missing tensors", i);
+    const glypr_q8w* qkv[3] = {L.self_attn.q.w, L.self_attn.k.w, L.self_attn.v.w};
+    RET_IF(glypr_hip_q8_0_weight_concat(m->ctx, qkv, 3, &L.self_attn.fused_qkv.w, nullptr));
+    const glypr_q8w* gu[2] = {L.mlp.gate.w, L.mlp.up.w};
+    RET_IF(glypr_hip_q8_0_weight_concat(m->ctx, gu, 2, &L.mlp.fused_gate_up.w, nullptr));
+  }
+  m->finalized = true;
+  return GLYPR_OK;
+}
+
+int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_t trunc,
+                          float* out, float* hidden, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(m != nullptr, GLYPR_ERR_INVALID_ARG, "model is NULL");
+  GLYPR_CHECK(m->finalized, GLYPR_ERR_INVALID_ARG, "call glypr_hip_model_finalize first");
+  GLYPR_CHECK(t > 0 && trunc >= 0, GLYPR_ERR_SHAPE, "t = %lld, trunc = %lld", (long long)t,
+              (long long)trunc);
+  GLYPR_CHECK(ids != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "ids or out is NULL");
+  GLYPR_CHECK(aligned16(out) && aligned16(hidden), GLYPR_ERR_ALIGNMENT,
+              "out and hidden must be 16-byte aligned");
+  const glypr_model_config& c = m->cfg;
+  for (int64_t i = 0; i < t; i++)
+    GLYPR_CHECK((int64_t)ids[i] < c.vocab, GLYPR_ERR_RANGE,
+                "token id %u at position %lld is out of range for vocab %lld", ids[i],
+                (long long)i, (long long)c.vocab);
+  glypr_hip_ctx* ctx = m->ctx;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  RET_IF(ensure_rope(m, t));
+  RET_IF(ensure_activations(m, t));
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
+  const int64_t qd = nq * hd;
+  float* h = dev_f32(m->h);
+  int8_t* xq = m->xq.as<int8_t>();
+  float* dx = dev_f32(m->dx);
+
+  // model.rs:507-508: Embedding::forward, then * embed_scale (f64 sqrt(hidden) as f32)
+  GLYPR_TRY_HIP(hipMemcpyAsync(m->ids.p, ids, (size_t)t * 4, hipMemcpyHostToDevice, s),
+                "ids upload");
+  const float embed_scale = (float)sqrt((double)H);
+  LAUNCH(GLYPR_K_GATHER, s,
+         launch_gather(m->token_embd.w->qs(), m->token_embd.w->dw(), H, m->ids.as<uint32_t>(), t,
+                       embed_scale, h, s),
+         "gather launch");
+  // layer 0 input_layernorm as the qkv GEMM's prologue
+  LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
+         launch_rmsnorm_quant(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xq, dx, s),
+         "rmsnorm_quant launch");
+
+  for (size_t li = 0; li < m->layers.size(); li++) {
+    EncoderLayer& L = m->layers[li];
+    const bool last = li + 1 == m->layers.size();
+    // ---- attention block (layer.rs:27-34)
+    const glypr_q8w* wqkv = L.self_attn.fused_qkv.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, wqkv->qs(), wqkv->dw(), dev_f32(m->qkv), t, wqkv->n, H, wqkv->n,
+                          s),
+           "qkv gemm launch");
+    const float* cos_t = dev_f32(L.full_attention ? m->cos_f : m->cos_s);
+    const float* sin_t = dev_f32(L.full_attention ? m->sin_f : m->sin_s);
+    RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
+                          L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
+                          L.full_attention ? 0 : c.sliding_window, m->attn_q_hi.as<uint16_t>(),
+                          m->attn_q_lo.as<uint16_t>(), m->attn_k_hi.as<uint16_t>(),
+                          m->attn_k_lo.as<uint16_t>(), m->attn_vt_hi.as<uint16_t>(),
+                          m->attn_vt_lo.as<uint16_t>(), dev_f32(m->ctx_out), s));
+    LAUNCH(GLYPR_K_QUANTIZE, s,
+           launch_quantize_planar(dev_f32(m->ctx_out), t, qd, m->cq.as<int8_t>(), dev_f32(m->dc),
+                                  s),
+           "ctx quantize launch");
+    const glypr_q8w* wo = L.self_attn.o.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(m->cq.as<int8_t>(), dev_f32(m->dc), wo->qs(), wo->dw(),
+                          dev_f32(m->proj), t, H, qd, H, s),
+           "o gemm launch");
+    // post_attention_layernorm.forward_residual_add + pre_feedforward_layernorm prologue
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.post_attention_layernorm.weight, h,
+                                L.pre_feedforward_layernorm.weight, c.eps, t, H, xq, dx, s),
+           "residual_norm launch");
+    // ---- feed-forward block (layer.rs:36-42): gate/up + GeGLU epilogue, down
+    const glypr_q8w* wgu = L.mlp.fused_gate_up.w;
+    LAUNCH(GLYPR_K_GEMM_I8_GEGLU, s,
+           launch_gemm_i8_geglu(xq, dx, wgu->qs(), wgu->dw(), m->hq.as<int8_t>(), dev_f32(m->dh),
+                                t, F, H, s),
+           "gate/up GeGLU launch");
+    const glypr_q8w* wd = L.mlp.down.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wd->qs(), wd->dw(),
+                          dev_f32(m->proj), t, H, F, H, s),
+           "down gemm launch");
+    // post_feedforward_layernorm.forward_residual_add + next layer's input norm
+    const float* w_next = last ? nullptr : m->layers[li + 1].input_layernorm.weight;
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h, w_next,
+                                c.eps, t, H, last ? nullptr : xq, last ? nullptr : dx, s),
+           "residual_norm launch");
+  }
+  // model.rs:576: final norm (the embedding projection is not part of this backbone)
+  float* normed = hidden ? hidden : dev_f32(m->normed);
+  LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, normed, t, H, s),
+         "final rmsnorm launch");
+  LAUNCH(GLYPR_K_POOL, s, launch_pool(normed, nullptr, t, H, trunc, out, dev_f32(m->pooled), s),
+         "pool launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_model_destroy(glypr_model* m) {
+  clear_error();
+  if (!m) return GLYPR_OK;
+  {
+    DeviceScope ds(m->ctx->device);
+    (void)hipDeviceSynchronize();
+    free_model(m);
+  }
+  delete m;
+  return GLYPR_OK;
+}
+
+}  // extern "C"

@@ -225,3 +225,74 @@ def pool_normalize(ctx: Context, tokens: torch.Tensor, mask=None, trunc: int = 0
         None if mk is None else mk.ctypes.data_as(ctypes.c_void_p), t, d, trunc, _ptr(out),
         ctx.stream))
     return out
+
+
+def attention(ctx: Context, qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor,
+              eps: float, cos_t: torch.Tensor, sin_t: torch.Tensor, n_heads: int, n_kv_heads: int,
+              head_dim: int = 256, window: int = 0,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """SelfAttention core: per-head norms, RoPE, GQA attention -> ctx [t, n_heads*head_dim]."""
+    ctx._check_tensor(qkv, "qkv")
+    t = qkv.shape[0]
+    y = _out(qkv, (t, n_heads * head_dim), out)
+    check(lib().glypr_hip_attention(ctx.handle, _ptr(qkv), _ptr(q_norm), _ptr(k_norm), eps,
+                                    _ptr(cos_t), _ptr(sin_t), t, n_heads, n_kv_heads, head_dim,
+                                    window, _ptr(y), ctx.stream))
+    return y
+
+
+class ModelConfig(ctypes.Structure):
+    """glypr_model_config (include/glypr_hip.h)."""
+    _fields_ = [("hidden", ctypes.c_int64), ("ffn", ctypes.c_int64), ("n_heads", ctypes.c_int64),
+                ("n_kv_heads", ctypes.c_int64), ("head_dim", ctypes.c_int64),
+                ("n_layers", ctypes.c_int64), ("vocab", ctypes.c_int64),
+                ("sliding_window", ctypes.c_int64), ("eps", ctypes.c_float),
+                ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double)]
+
+
+class Model:
+    """The text backbone (glypr_hip_model_*): tensors by their GGUF names."""
+
+    def __init__(self, ctx: Context, **cfg):
+        defaults = dict(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256, n_layers=24,
+                        vocab=262144, sliding_window=512, eps=1e-6, rope_theta_sliding=10000.0,
+                        rope_theta_full=1e6)
+        defaults.update(cfg)
+        self.cfg = defaults
+        self.ctx = ctx
+        c = ModelConfig(**defaults)
+        h = ctypes.c_void_p()
+        check(lib().glypr_hip_model_create(ctx.handle, ctypes.byref(c), ctypes.byref(h)))
+        self.handle = h
+
+    def set_tensor(self, name: str, data: np.ndarray, rows: int, cols: int, q8_0: bool):
+        a = np.ascontiguousarray(data)
+        check(lib().glypr_hip_model_set_tensor(self.handle, name.encode(),
+                                               a.ctypes.data_as(ctypes.c_void_p), rows, cols,
+                                               1 if q8_0 else 0))
+
+    def finalize(self):
+        check(lib().glypr_hip_model_finalize(self.handle))
+
+    def embed(self, ids, trunc: int = 0, hidden: Optional[torch.Tensor] = None,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        H = self.cfg["hidden"]
+        td = trunc if 0 < trunc < H else H
+        if out is None:
+            out = torch.empty(td, dtype=torch.float32, device=f"cuda:{self.ctx.device}")
+        check(lib().glypr_hip_model_embed(self.handle, ids.ctypes.data_as(ctypes.c_void_p),
+                                          ids.size, trunc, _ptr(out), _ptr(hidden),
+                                          self.ctx.stream))
+        return out
+
+    def close(self):
+        if self.handle:
+            lib().glypr_hip_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

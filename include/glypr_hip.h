@@ -171,6 +171,71 @@ int glypr_hip_pool_normalize(glypr_hip_ctx* ctx, const float* tokens, const uint
                              int64_t t, int64_t d, int64_t trunc, float* out,
                              glypr_stream stream);
 
+/* ---- attention core ------------------------------------------------------ */
+
+/* SelfAttention::forward between the projections and o_proj
+ * (attention/mod.rs:166-273): per-head q_norm / k_norm / weightless v_norm
+ * (RMSNorm over head_dim, bit-exact with the CPU path), RoPE with the caller's
+ * cos/sin tables (rope.rs:99-106; [t][head_dim] f32 device arrays as
+ * RotaryEmbedding::get_cos_sin returns them), repeat_kv, and attention with
+ * scale 1.0 and f32 softmax (attention/standard.rs:10-83); window > 0 and
+ * t > window applies the sliding band |i - j| <= window (attention/chunked.rs).
+ * qkv [t][(n_heads + 2*n_kv_heads) * head_dim] (q | k | v columns, the fused
+ * projection's output) -> ctx [t][n_heads * head_dim].  head_dim must be 256. */
+int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_norm_weight,
+                        const float* k_norm_weight, float eps, const float* cos_table,
+                        const float* sin_table, int64_t t, int64_t n_heads, int64_t n_kv_heads,
+                        int64_t head_dim, int64_t window, float* ctx_out, glypr_stream stream);
+
+/* ---- text backbone (configs 4-5) ---------------------------------------- */
+
+/* EmbeddingGemma layer geometry (TextConfig, config.rs:76-213; BASELINE uses
+ * hidden 768, ffn 1152, 3 q heads / 1 kv head, head_dim 256, 24 layers). */
+typedef struct glypr_model_config {
+  int64_t hidden;
+  int64_t ffn;
+  int64_t n_heads;
+  int64_t n_kv_heads;
+  int64_t head_dim;
+  int64_t n_layers;
+  int64_t vocab;
+  int64_t sliding_window;      /* 512 (config.rs:191) */
+  float eps;                   /* rms_norm_eps, 1e-6 */
+  double rope_theta_sliding;   /* 10000 (config.rs:171-172) */
+  double rope_theta_full;      /* 1e6 (config.rs:173-174) */
+} glypr_model_config;
+
+typedef struct glypr_model glypr_model;
+
+/* EmbeddingGemma2Model::from_gguf_content (model.rs:244-488), minus the
+ * Per-Layer-Embedding block: an empty model whose tensors arrive through
+ * glypr_hip_model_set_tensor.  Layer i is full attention iff (i+1) % 6 == 0
+ * (config.rs:131-140), sliding otherwise. */
+int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
+                           glypr_model** out);
+
+/* One GGUF tensor by its glypr name (model.rs:252-470): "token_embd.weight",
+ * "output_norm.weight", "blk.{i}.{attn_norm, post_attention_norm, ffn_norm,
+ * post_ffw_norm, attn_q_norm, attn_k_norm}.weight" (f32, dtype 0) and
+ * "blk.{i}.{attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up,
+ * ffn_down}.weight" (Q8_0 GGUF blocks, dtype 1).  Host memory; rows x cols
+ * is the GGUF (out_dim, in_dim). */
+int glypr_hip_model_set_tensor(glypr_model* model, const char* name, const void* data,
+                               int64_t rows, int64_t cols, int dtype);
+
+/* Check every tensor is present and build the fused q|k|v and gate|up
+ * weights (SelfAttention::new / MLP::new via try_concat). */
+int glypr_hip_model_finalize(glypr_model* model);
+
+/* forward (model.rs:498-578) + pool_and_normalize (model.rs:654-705) for one
+ * sequence: ids (host, tokenizer output) -> out [trunc] on the device.
+ * hidden (nullable, device [t][hidden]) receives the final-normed token
+ * states.  Only GLYPR_Q8_INT8_EXACT is supported here. */
+int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, int64_t trunc,
+                          float* out, float* hidden, glypr_stream stream);
+
+int glypr_hip_model_destroy(glypr_model* model);
+
 /* ---- per-kernel timing --------------------------------------------------- */
 
 /* Kernel identities for the per-kernel timing below. */
@@ -188,7 +253,10 @@ typedef enum glypr_kernel_id {
   GLYPR_K_GATHER = 10,
   GLYPR_K_DEQUANT = 11,
   GLYPR_K_POOL = 12,
-  GLYPR_K_COUNT = 13
+  GLYPR_K_QKV_POST = 13,      /* q/k/v norms + RoPE + f16 split */
+  GLYPR_K_ATTENTION = 14,     /* flash attention */
+  GLYPR_K_RESIDUAL_NORM = 15, /* residual + RMSNorm (+ next prologue) */
+  GLYPR_K_COUNT = 16
 } glypr_kernel_id;
 
 /* The per-op device timing of forward_profiled (profile.rs:53-56, 63-429),
