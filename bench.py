@@ -156,6 +156,33 @@ def run_workload(ctx, m, variant, steps, warmup, seed=0):
     return L, ms, kern
 
 
+def c1_linear(ctx, steps):
+    """one Q8_0 linear, X f32 [512, 768] -> Y f32 [512, 1152]."""
+    import torch
+    from glypr_amd import ops
+    from glypr_amd.ops import INT8_EXACT, Q8Weight
+    rng = np.random.default_rng(3)
+    w = Q8Weight.from_gguf(ctx, q8_0_weight(rng, 1152, 768), 1152, 768)
+    x = torch.from_numpy(rng.standard_normal((512, 768)).astype(np.float32)).cuda()
+    y = torch.empty((512, 1152), dtype=torch.float32, device="cuda")
+    for _ in range(10):
+        ops.q8_0_matmul(ctx, w, x, INT8_EXACT, out=y)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ops.q8_0_matmul(ctx, w, x, INT8_EXACT, out=y)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ops_ = 2 * 512 * 768 * 1152
+    nbytes = 4 * 512 * 768 + 1152 * 24 * 34 + 4 * 512 * 1152
+    w.close()
+    return {"us_per_call": round(ms * 1e3, 3), "tops": round(ops_ / (ms / 1e3) / 1e12, 2),
+            "hbm_frac_algorithmic": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "note": "quantize + GEMM, two kernels"}
+
+
 def roofline_for(kern, m, variant, steps):
     dom = max(kern, key=lambda k: kern[k]["ms_total"])
     k = kern[dom]
@@ -167,6 +194,116 @@ def roofline_for(kern, m, variant, steps):
                  "kernel": dom, "us_per_launch": round(k["us_per_launch"], 3),
                  "launches_per_step": k["launches"] // steps,
                  "algorithmic_bytes_per_step": nbytes}
+
+
+QK_NORM_SCALE = 0.25  # 1/sqrt(head_dim) folded into q/k norms
+
+
+def model_tensors(rng, n_layers, vocab, hidden=H, ffn=F, nq=3, nkv=1, hd=256):
+    """Synthetic EmbeddingGemma backbone tensors by GGUF name: Q8_0 projections with
+    BASELINE's distribution, norm weights 1 + 0.1 N(0,1) (q/k norms x 0.25)."""
+    t = {"token_embd.weight": (q8_0_weight(rng, vocab, hidden), vocab, hidden, True),
+         "output_norm.weight": ((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32), 1,
+                                hidden, False)}
+    for i in range(n_layers):
+        for name, n, k in [("attn_q", nq * hd, hidden), ("attn_k", nkv * hd, hidden),
+                           ("attn_v", nkv * hd, hidden), ("attn_output", hidden, nq * hd),
+                           ("ffn_gate", ffn, hidden), ("ffn_up", ffn, hidden),
+                           ("ffn_down", hidden, ffn)]:
+            t[f"blk.{i}.{name}.weight"] = (q8_0_weight(rng, n, k), n, k, True)
+        for name, n in [("attn_norm", hidden), ("post_attention_norm", hidden),
+                        ("ffn_norm", hidden), ("post_ffw_norm", hidden), ("attn_q_norm", hd),
+                        ("attn_k_norm", hd)]:
+            w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+            if name in ("attn_q_norm", "attn_k_norm"):
+                w = (w * QK_NORM_SCALE).astype(np.float32)
+            t[f"blk.{i}.{name}.weight"] = (w, 1, n, False)
+    return t
+
+
+def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1):
+    """Embeddings/s of the full backbone for one t-token sequence (config 4/5), plus
+    the per-op split from a second, profiled pass."""
+    import torch
+    from glypr_amd import _lib
+    from glypr_amd.ops import Model
+    m = Model(ctx, n_layers=n_layers, vocab=vocab)
+    for name, (data, r, c, q8) in tensors.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    ids = np.random.default_rng(seed).integers(0, vocab, size=t).astype(np.uint32)
+    out = torch.empty(256, dtype=torch.float32, device="cuda")
+    for _ in range(warmup):
+        m.embed(ids, trunc=256, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        m.embed(ids, trunc=256, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 1))
+    for _ in range(steps):
+        m.embed(ids, trunc=256, out=out)
+    tot = (ctypes.c_double * _lib.KERNEL_COUNT)()
+    cnt = (ctypes.c_int64 * _lib.KERNEL_COUNT)()
+    _lib.check(_lib.lib().glypr_hip_profile_read(ctx.handle, tot, cnt))
+    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 0))
+    split = {}
+    for i in range(_lib.KERNEL_COUNT):
+        if cnt[i]:
+            split[_lib.lib().glypr_hip_kernel_name(i).decode()] = round(tot[i] / steps, 4)
+    gemm = sum(v for k, v in split.items() if k.startswith("gemm"))
+    att = split.get("attention", 0.0) + split.get("qkv_post", 0.0)
+    m.close()
+    return {"ms_per_embedding": round(ms, 4), "embeddings_per_s": round(1000.0 / ms, 2),
+            "tokens_per_s": round(t * 1000.0 / ms, 1),
+            "gemm_ops_per_embedding": 2 * t * n_layers * LAYER_NK,
+            "q8_gemm_tops": round(2 * t * n_layers * LAYER_NK / (ms / 1e3) / 1e12, 2),
+            "split_ms_profiled": split, "gemm_ms": round(gemm, 4), "attention_ms": round(att, 4)}
+
+
+def cpu_backbone_baseline(tensors, n_layers, vocab, t, seconds=10.0):
+    """The oracle's full forward (glypr's CPU path restated) on this host."""
+    from oracle import pyoracle as po
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    cfg = po.ModelConfig(hidden=H, ffn=F, n_heads=3, n_kv_heads=1, head_dim=256,
+                         n_layers=n_layers, vocab=vocab, sliding_window=512, eps=1e-6,
+                         rope_theta_sliding=10000.0, rope_theta_full=1e6)
+    keep = []
+
+    def u8(name):
+        a = np.ascontiguousarray(tensors[name][0], dtype=np.uint8)
+        keep.append(a)
+        return a.ctypes.data_as(po._u8p)
+
+    def f32(name):
+        a = np.ascontiguousarray(tensors[name][0], dtype=np.float32)
+        keep.append(a)
+        return a.ctypes.data_as(po._f32p)
+
+    layers = (po.LayerWeights * n_layers)()
+    for i in range(n_layers):
+        p = f"blk.{i}."
+        layers[i] = po.LayerWeights(*[u8(p + n + ".weight") for n in (
+            "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")],
+            *[f32(p + n + ".weight") for n in ("attn_norm", "post_attention_norm", "ffn_norm",
+                                                "post_ffw_norm", "attn_q_norm", "attn_k_norm")])
+    ids = np.ascontiguousarray(np.random.default_rng(1).integers(0, vocab, size=t), np.uint32)
+    out = np.empty(256, np.float32)
+    t0 = time.perf_counter()
+    n = 0
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        rc = po.lib().orc_model_forward(ctypes.byref(cfg), u8("token_embd.weight"), layers,
+                                        f32("output_norm.weight"), ids.ctypes.data_as(po._u32p),
+                                        t, 256, out.ctypes.data_as(po._f32p), None, cores)
+        assert rc == 0
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(1.0 / dt, 4), "unit": "embeddings/s", "cores": cores, "kind": "port",
+            "sample": f"config 4 full forward (24 layers, T={t}), {n} embeddings"}
 
 
 def cpu_baseline(seconds=10.0):
@@ -239,16 +376,23 @@ def main():
                             for k, v in kern.items()},
              "pct_mfma_peak_c2": round(100 * tops / peak, 3)}
     if not args.no_extra:
-        for name, mm, steps in (("c3", 16384, max(10, args.steps // 10)),):
-            for vname, v in (("int8", INT8_EXACT), ("bf16", BF16_DEQUANT)):
-                Lx, msx, kx = run_workload(ctx, mm, v, steps, 3)
-                t = Lx.ops_per_step() / (msx / 1e3) / 1e12
-                pk = INT8_PEAK_TOPS if v == INT8_EXACT else BF16_PEAK_TFLOPS
-                extra[f"{name}_{vname}"] = {
-                    "tops": round(t, 2), "ms_per_step": round(msx, 4),
-                    "pct_mfma_peak": round(100 * t / pk, 2),
-                    "kernels": {k: round(vv["us_per_launch"], 2) for k, vv in kx.items()}}
-                del Lx
+        for vname, v in (("int8", INT8_EXACT), ("bf16", BF16_DEQUANT)):
+            Lx, msx, kx = run_workload(ctx, 16384, v, max(10, args.steps // 10), 3)
+            t = Lx.ops_per_step() / (msx / 1e3) / 1e12
+            pk = INT8_PEAK_TOPS if v == INT8_EXACT else BF16_PEAK_TFLOPS
+            extra[f"c3_{vname}"] = {
+                "tops": round(t, 2), "ms_per_step": round(msx, 4),
+                "pct_mfma_peak": round(100 * t / pk, 2),
+                "kernels_us": {k: round(vv["us_per_launch"], 2) for k, vv in kx.items()}}
+            del Lx
+        extra["c1_int8"] = c1_linear(ctx, args.steps)
+        rng = np.random.default_rng(7)
+        tensors = model_tensors(rng, 24, 262144)
+        extra["c4"] = run_backbone(ctx, tensors, 24, 262144, 512, max(10, args.steps // 10), 3)
+        extra["c5"] = run_backbone(ctx, tensors, 24, 262144, 8192, 3, 1)
+        if not args.no_cpu:
+            extra["c4"]["cpu_baseline"] = cpu_backbone_baseline(tensors, 24, 262144, 512)
+        del tensors
 
     line = {
         "metric": "Q8_0 matmul TOPS (% MFMA peak); 512-tok embeddings/sec on 1 MI355X",

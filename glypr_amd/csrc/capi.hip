@@ -485,7 +485,7 @@ int glypr_hip_pool_normalize(glypr_hip_ctx* ctx, const float* tokens, const uint
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  RET_IF(ensure_ws(ctx, (size_t)d * sizeof(float)));
+  RET_IF(ensure_ws(ctx, pool_scratch_floats(t, d) * sizeof(float)));
   const uint8_t* dmask = nullptr;
   if (mask) {
     RET_IF(ensure_staging(ctx->mask, ctx->mask_cap, (size_t)t));

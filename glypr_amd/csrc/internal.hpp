@@ -78,8 +78,10 @@ hipError_t launch_rmsnorm_quant(const float* x, const float* w, float eps, int64
 hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_t rows,
                                int64_t dim, uint16_t* xb, hipStream_t s);
 hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, hipStream_t s);
+// scratch: pool_scratch_floats(t, d) floats
+size_t pool_scratch_floats(int64_t t, int64_t d);
 hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t d, int64_t trunc,
-                       float* out, float* scratch /* d floats */, hipStream_t s);
+                       float* out, float* scratch, hipStream_t s);
 
 // h = h + rmsnorm(x; w_post); if xq: (xq, dx) = Q8_0(rmsnorm(h; w_next)).  dim % 32 == 0.
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
@@ -87,14 +89,16 @@ hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, c
                                 hipStream_t s);
 
 // ---- k_attn.hip ----
+// q split hi/lo [nq][Tp][hd]; k f16 [nkv][Tp][hd]; vt f16 [nkv][hd][Tp].  hd == 256.
 hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
                            int64_t hd, const float* qnw, const float* knw, float eps,
                            const float* cos_t, const float* sin_t, uint16_t* q_hi, uint16_t* q_lo,
-                           uint16_t* k_hi, uint16_t* k_lo, uint16_t* vt_hi, uint16_t* vt_lo,
-                           hipStream_t s);
-hipError_t launch_attention(const uint16_t* q_hi, const uint16_t* q_lo, const uint16_t* k_hi,
-                            const uint16_t* k_lo, const uint16_t* vt_hi, const uint16_t* vt_lo,
-                            float* ctx, int64_t T, int64_t Tp, int64_t nq, int64_t nkv, int64_t hd,
+                           uint16_t* k16, uint16_t* vt16, hipStream_t s);
+size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t window);
+// ctx (f32 [T][nq*hd]) and/or (cq, dc) (Q8_0 planar) may be null.
+hipError_t launch_attention(const uint16_t* q_hi, const uint16_t* q_lo, const uint16_t* k16,
+                            const uint16_t* vt16, float* scratch, float* ctx, int8_t* cq,
+                            float* dc, int64_t T, int64_t Tp, int64_t nq, int64_t nkv, int64_t hd,
                             int64_t window, hipStream_t s);
 
 // ---- k_gemm_i8.hip ----

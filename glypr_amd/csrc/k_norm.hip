@@ -336,32 +336,58 @@ hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, h
 }
 
 // ---------------------------------------------------------------------------
-// pool_and_normalize (model.rs:654-705).  candle sums over the token axis in
-// token order per column and L2-reduces the last axis sequentially; each
-// column's sum is one thread's sequential loop, the norms are one lane's loop,
-// so the result is bit-identical to the CPU path.  One 256-thread block.
+// pool_and_normalize (model.rs:654-705): f32 mean over the valid tokens, L2
+// with the 1e-12 clamp, MRL narrow + renormalise.  candle sums the token axis
+// sequentially; a sequential sum is one dependent chain of t loads per column
+// (latency-bound: milliseconds at t = 8192), so the sum here is chunked:
+// pool_partial sums POOL_CHUNK-token chunks per column (sequentially inside a
+// chunk), pool_finalize adds the chunk sums in chunk order, divides, and runs
+// the norms.  Deterministic (fixed order) and within a few f32 ulps of the
+// sequential sum; tested against a float64 mean.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) pool_kernel(const float* __restrict__ tok,
-                                                   const uint8_t* __restrict__ mask, int64_t t,
-                                                   int64_t d, int64_t trunc,
-                                                   float* __restrict__ out,
-                                                   float* __restrict__ pooled) {
-  __shared__ float s_norm;
-  float cnt = 0.0f;
+constexpr int POOL_CHUNK = 64;
+
+__global__ void __launch_bounds__(256) pool_partial_kernel(const float* __restrict__ tok,
+                                                           const uint8_t* __restrict__ mask,
+                                                           int64_t t, int64_t d,
+                                                           float* __restrict__ partial) {
+  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t chunk = blockIdx.y;
+  if (col >= d) return;
+  const int64_t r0 = chunk * POOL_CHUNK;
+  const int64_t r1 = r0 + POOL_CHUNK < t ? r0 + POOL_CHUNK : t;
+  float s = 0.0f;
   if (mask) {
-    for (int64_t j = 0; j < t; j++) cnt += mask[j] ? 1.0f : 0.0f;
-    if (cnt < 1e-9f) cnt = 1e-9f;
+    for (int64_t j = r0; j < r1; j++) s += tok[j * d + col] * (mask[j] ? 1.0f : 0.0f);
+  } else {
+#pragma unroll 16
+    for (int64_t j = r0; j < r1; j++) s += tok[j * d + col];
   }
+  partial[chunk * d + col] = s;
+}
+
+__global__ void __launch_bounds__(1024) pool_finalize_kernel(const float* __restrict__ partial,
+                                                             const uint8_t* __restrict__ mask,
+                                                             int64_t t, int64_t d, int64_t trunc,
+                                                             float* __restrict__ out,
+                                                             float* __restrict__ pooled) {
+  __shared__ float s_norm;
+  __shared__ float s_cnt;
+  const int64_t nchunk = (t + POOL_CHUNK - 1) / POOL_CHUNK;
+  if (threadIdx.x == 0) {
+    float cnt = 0.0f;
+    if (mask) {
+      for (int64_t j = 0; j < t; j++) cnt += mask[j] ? 1.0f : 0.0f;
+      if (cnt < 1e-9f) cnt = 1e-9f;
+    }
+    s_cnt = cnt;
+  }
+  __syncthreads();
   const float inv_t = (float)(1.0 / (double)t);
   for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
     float s = 0.0f;
-    if (mask) {
-      for (int64_t j = 0; j < t; j++) s += tok[j * d + i] * (mask[j] ? 1.0f : 0.0f);
-      pooled[i] = s / cnt;
-    } else {
-      for (int64_t j = 0; j < t; j++) s += tok[j * d + i];
-      pooled[i] = s * inv_t + 0.0f;
-    }
+    for (int64_t c = 0; c < nchunk; c++) s += partial[c * d + i];
+    pooled[i] = mask ? s / s_cnt : s * inv_t + 0.0f;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -390,9 +416,18 @@ __global__ void __launch_bounds__(256) pool_kernel(const float* __restrict__ tok
   for (int64_t i = threadIdx.x; i < td; i += blockDim.x) out[i] = pooled[i] / nrm;
 }
 
+size_t pool_scratch_floats(int64_t t, int64_t d) {
+  return (size_t)(((t + POOL_CHUNK - 1) / POOL_CHUNK) * d + d);
+}
+
 hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t d, int64_t trunc,
                        float* out, float* scratch, hipStream_t s) {
-  pool_kernel<<<1, 256, 0, s>>>(tok, mask, t, d, trunc, out, scratch);
+  const int64_t nchunk = (t + POOL_CHUNK - 1) / POOL_CHUNK;
+  float* partial = scratch;
+  float* pooled = scratch + nchunk * d;
+  dim3 g1((unsigned)((d + 255) / 256), (unsigned)nchunk);
+  pool_partial_kernel<<<g1, 256, 0, s>>>(tok, mask, t, d, partial);
+  pool_finalize_kernel<<<1, 1024, 0, s>>>(partial, mask, t, d, trunc, out, pooled);
   return hipGetLastError();
 }
 

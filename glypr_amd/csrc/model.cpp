@@ -14,8 +14,9 @@
 //     RMSNorm are one kernel (residual_norm);
 //   - q/k/v and gate/up are single fused GEMMs (try_concat, linear.rs:82-148);
 //   - GeGLU is the gate/up GEMM's epilogue.
-// All of these are bit-exact with the CPU path; attention differs from it
-// only by f32 rounding (see k_attn.hip).
+// The GEMMs, norms, GeGLU and residual adds are bit-exact with the CPU path;
+// attention (f16 MFMA with split operands, see k_attn.hip) and the chunked
+// pooling sum differ from it at f32-rounding level.
 #include <math.h>
 #include <stdio.h>
 #include <string.h>
@@ -100,8 +101,8 @@ struct glypr_model {
   DevBuf cos_s, sin_s, cos_f, sin_f;
   int64_t rope_cap = 0;
   // activations
-  DevBuf h, xq, dx, qkv, attn_q_hi, attn_q_lo, attn_k_hi, attn_k_lo, attn_vt_hi, attn_vt_lo, ctx_out,
-      cq, dc, proj, hq, dh, normed, pooled, ids;
+  DevBuf h, xq, dx, qkv, attn_q_hi, attn_q_lo, attn_k, attn_vt, attn_scratch, cq, dc, proj, hq,
+      dh, normed, pooled, ids;
   int64_t cap_t = 0;
 };
 
@@ -166,18 +167,19 @@ int ensure_activations(glypr_model* m, int64_t t) {
   RET_IF(m->qkv.ensure((size_t)(t * (qd + 2 * kvd)) * 4));
   RET_IF(m->attn_q_hi.ensure((size_t)(tp * qd) * 2));
   RET_IF(m->attn_q_lo.ensure((size_t)(tp * qd) * 2));
-  RET_IF(m->attn_k_hi.ensure((size_t)(tp * kvd) * 2));
-  RET_IF(m->attn_k_lo.ensure((size_t)(tp * kvd) * 2));
-  RET_IF(m->attn_vt_hi.ensure((size_t)(tp * kvd) * 2));
-  RET_IF(m->attn_vt_lo.ensure((size_t)(tp * kvd) * 2));
-  RET_IF(m->ctx_out.ensure((size_t)(t * qd) * 4));
+  RET_IF(m->attn_k.ensure((size_t)(tp * kvd) * 2));
+  RET_IF(m->attn_vt.ensure((size_t)(tp * kvd) * 2));
+  size_t sc = attention_scratch_floats(t, c.n_heads, c.n_kv_heads, 0);
+  const size_t sc2 = attention_scratch_floats(t, c.n_heads, c.n_kv_heads, c.sliding_window);
+  if (sc2 > sc) sc = sc2;
+  RET_IF(m->attn_scratch.ensure(sc * 4));
   RET_IF(m->cq.ensure((size_t)(t * qd)));
   RET_IF(m->dc.ensure((size_t)(t * (qd / 32)) * 4));
   RET_IF(m->proj.ensure((size_t)(t * c.hidden) * 4));
   RET_IF(m->hq.ensure((size_t)(t * c.ffn)));
   RET_IF(m->dh.ensure((size_t)(t * (c.ffn / 32)) * 4));
   RET_IF(m->normed.ensure((size_t)(t * c.hidden) * 4));
-  RET_IF(m->pooled.ensure((size_t)c.hidden * 4));
+  RET_IF(m->pooled.ensure(pool_scratch_floats(t, c.hidden) * 4));
   RET_IF(m->ids.ensure((size_t)t * 4));
   m->cap_t = t;
   return GLYPR_OK;
@@ -212,25 +214,27 @@ void free_model(glypr_model* m) {
     dropn(L.post_feedforward_layernorm);
   }
   for (DevBuf* b : {&m->cos_s, &m->sin_s, &m->cos_f, &m->sin_f, &m->h, &m->xq, &m->dx, &m->qkv,
-                    &m->attn_q_hi, &m->attn_q_lo, &m->attn_k_hi, &m->attn_k_lo, &m->attn_vt_hi,
-                    &m->attn_vt_lo, &m->ctx_out, &m->cq, &m->dc, &m->proj, &m->hq, &m->dh,
-                    &m->normed, &m->pooled, &m->ids})
+                    &m->attn_q_hi, &m->attn_q_lo, &m->attn_k, &m->attn_vt, &m->attn_scratch,
+                    &m->cq, &m->dc, &m->proj, &m->hq, &m->dh, &m->normed, &m->pooled, &m->ids})
     b->release();
 }
 
-// The attention core shared by glypr_hip_attention and the model forward.
+// The attention core shared by glypr_hip_attention and the model forward:
+// per-head norms + RoPE, then flash attention writing ctx (f32) and/or the
+// o projection's Q8_0 operand (cq, dc).
 int attention_core(glypr_hip_ctx* ctx, const float* qkv, const float* qnw, const float* knw,
                    float eps, const float* cos_t, const float* sin_t, int64_t t, int64_t nq,
                    int64_t nkv, int64_t hd, int64_t window, uint16_t* q_hi, uint16_t* q_lo,
-                   uint16_t* k_hi, uint16_t* k_lo, uint16_t* vt_hi, uint16_t* vt_lo, float* out,
-                   hipStream_t s) {
+                   uint16_t* k16, uint16_t* vt16, float* scratch, float* out, int8_t* cq,
+                   float* dc, hipStream_t s) {
   const int64_t tp = (t + 31) / 32 * 32;
   LAUNCH(GLYPR_K_QKV_POST, s,
-         launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q_hi, q_lo, k_hi,
-                         k_lo, vt_hi, vt_lo, s),
+         launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q_hi, q_lo, k16,
+                         vt16, s),
          "qkv_post launch");
   LAUNCH(GLYPR_K_ATTENTION, s,
-         launch_attention(q_hi, q_lo, k_hi, k_lo, vt_hi, vt_lo, out, t, tp, nq, nkv, hd, window, s),
+         launch_attention(q_hi, q_lo, k16, vt16, scratch, out, cq, dc, t, tp, nq, nkv, hd, window,
+                          s),
          "attention launch");
   return GLYPR_OK;
 }
@@ -264,17 +268,17 @@ int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_nor
   const int64_t tp = (t + 31) / 32 * 32;
   const size_t qb = align_up((size_t)(tp * n_heads * head_dim) * 2, 256);
   const size_t kb = align_up((size_t)(tp * n_kv_heads * head_dim) * 2, 256);
-  RET_IF(ensure_ws(ctx, 2 * qb + 4 * kb));
+  const size_t sb = attention_scratch_floats(t, n_heads, n_kv_heads, window) * 4;
+  RET_IF(ensure_ws(ctx, 2 * qb + 2 * kb + sb));
   char* base = (char*)ctx->ws;
   uint16_t* q_hi = (uint16_t*)base;
   uint16_t* q_lo = (uint16_t*)(base + qb);
-  uint16_t* k_hi = (uint16_t*)(base + 2 * qb);
-  uint16_t* k_lo = (uint16_t*)(base + 2 * qb + kb);
-  uint16_t* v_hi = (uint16_t*)(base + 2 * qb + 2 * kb);
-  uint16_t* v_lo = (uint16_t*)(base + 2 * qb + 3 * kb);
+  uint16_t* k16 = (uint16_t*)(base + 2 * qb);
+  uint16_t* vt16 = (uint16_t*)(base + 2 * qb + kb);
+  float* scratch = (float*)(base + 2 * qb + 2 * kb);
   return attention_core(ctx, qkv, q_norm_weight, k_norm_weight, eps, cos_table, sin_table, t,
-                        n_heads, n_kv_heads, head_dim, window, q_hi, q_lo, k_hi, k_lo, v_hi,
-                        v_lo, ctx_out, (hipStream_t)stream);
+                        n_heads, n_kv_heads, head_dim, window, q_hi, q_lo, k16, vt16, scratch,
+                        ctx_out, nullptr, nullptr, (hipStream_t)stream);
 }
 
 int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
@@ -437,13 +441,9 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
     RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
                           L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
                           L.full_attention ? 0 : c.sliding_window, m->attn_q_hi.as<uint16_t>(),
-                          m->attn_q_lo.as<uint16_t>(), m->attn_k_hi.as<uint16_t>(),
-                          m->attn_k_lo.as<uint16_t>(), m->attn_vt_hi.as<uint16_t>(),
-                          m->attn_vt_lo.as<uint16_t>(), dev_f32(m->ctx_out), s));
-    LAUNCH(GLYPR_K_QUANTIZE, s,
-           launch_quantize_planar(dev_f32(m->ctx_out), t, qd, m->cq.as<int8_t>(), dev_f32(m->dc),
-                                  s),
-           "ctx quantize launch");
+                          m->attn_q_lo.as<uint16_t>(), m->attn_k.as<uint16_t>(),
+                          m->attn_vt.as<uint16_t>(), dev_f32(m->attn_scratch), nullptr,
+                          m->cq.as<int8_t>(), dev_f32(m->dc), s));
     const glypr_q8w* wo = L.self_attn.o.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
            launch_gemm_i8(m->cq.as<int8_t>(), dev_f32(m->dc), wo->qs(), wo->dw(),

@@ -1,9 +1,10 @@
 """GPU parity of the backbone pieces (configs 4-5): the attention core and the
 multi-layer forward through the C ABI, against the CPU oracle.
 
-Attention is not bit-exact (split-f16 MFMA products, f32 online softmax vs the
-oracle's double accumulation), so its bar is f32-level agreement; the final
-pooled embedding must reach BASELINE's cosine >= 0.9999 vs the oracle.
+Attention is not bit-exact: it rounds K and V to f16 (Q and P are split), so it
+is held to f32-level agreement with the oracle fed the same f16 K/V, and to an
+f16-level bound against the unrounded oracle; the final pooled embedding must
+reach BASELINE's cosine >= 0.9999 vs the oracle.
 """
 import sys
 
@@ -37,7 +38,9 @@ def rope_np(x, c, s):
     return (x * c).astype(np.float32) + (rot * s).astype(np.float32)
 
 
-def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window):
+def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window, f16_kv=False):
+    """Oracle attention core.  f16_kv rounds K and V (after norm + RoPE) to f16,
+    the one rounding the GPU kernel makes by design (Q and P are split hi/lo)."""
     t = qkv.shape[0]
     c, s = oracle.rope_tables(hd, theta, t)
     q = qkv[:, :nq * hd].reshape(t, nq, hd)
@@ -48,22 +51,32 @@ def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window):
     vn = oracle.rmsnorm(v.reshape(-1, hd), None, eps).reshape(t, nkv, hd)
     qr = rope_np(qn, c[:, None, :], s[:, None, :]).transpose(1, 0, 2)
     kr = rope_np(kn, c[:, None, :], s[:, None, :]).transpose(1, 0, 2)
-    return oracle.attention(qr, kr, vn.transpose(1, 0, 2), window), c, s
+    vr = vn.transpose(1, 0, 2)
+    if f16_kv:
+        kr = kr.astype(np.float16).astype(np.float32)
+        vr = vr.astype(np.float16).astype(np.float32)
+    return oracle.attention(qr, kr, vr, window), c, s
 
 
-@pytest.mark.parametrize("t,window", [(70, 0), (512, 0), (600, 512), (1100, 256)])
-def test_attention_core_vs_oracle(ctx, oracle, t, window):
+@pytest.mark.parametrize("t,window,qk_scale", [(70, 0, 1.0), (512, 0, 0.25), (600, 512, 0.25),
+                                               (1100, 256, 1.0), (2048, 512, 0.25)])
+def test_attention_core_vs_oracle(ctx, oracle, t, window, qk_scale):
     nq, nkv, hd, eps = 3, 1, 256, 1e-6
-    say(f"attention core t={t} window={window}")
+    say(f"attention core t={t} window={window} qk_norm_scale={qk_scale}")
     qkv = oracle.normal(t * (nq + 2 * nkv) * hd, seed=t).reshape(t, -1) * np.float32(0.7)
-    qnw = 1 + 0.1 * oracle.normal(hd, seed=1)
-    knw = 1 + 0.1 * oracle.normal(hd, seed=2)
-    ref, c, s = attention_ref(oracle, qkv, qnw, knw, eps, 10000.0, nq, nkv, hd, window)
+    qnw = (1 + 0.1 * oracle.normal(hd, seed=1)) * np.float32(qk_scale)
+    knw = (1 + 0.1 * oracle.normal(hd, seed=2)) * np.float32(qk_scale)
+    ref16, c, s = attention_ref(oracle, qkv, qnw, knw, eps, 10000.0, nq, nkv, hd, window, True)
+    ref, _, _ = attention_ref(oracle, qkv, qnw, knw, eps, 10000.0, nq, nkv, hd, window)
     got = host(ops.attention(ctx, dev(qkv), dev(qnw), dev(knw), eps, dev(c), dev(s), nq, nkv, hd,
-                             window))
-    err = np.abs(got.astype(np.float64) - ref)
+                             window)).astype(np.float64)
     scale = np.abs(ref).max()
-    assert err.max() <= 2e-5 * scale, (err.max(), scale)
+    # same input roundings as the kernel: f32-level agreement
+    assert np.abs(got - ref16).max() <= 2e-5 * scale, np.abs(got - ref16).max() / scale
+    # against the unrounded oracle: the f16 rounding of K/V, amplified by the
+    # logit scale (std ~16 with unit q/k norms, ~1 with the folded 1/sqrt(d))
+    bound = 5e-3 if qk_scale == 1.0 else 1e-3
+    assert np.abs(got - ref).max() <= bound * scale, np.abs(got - ref).max() / scale
 
 
 # q_norm / k_norm weights are 0.25 * (1 + 0.1 N(0,1)): glypr's attention has no

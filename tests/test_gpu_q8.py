@@ -245,16 +245,27 @@ def test_gather_bit_exact_and_range(ctx, oracle):
     assert e.value.code == _lib.GLYPR_ERR_RANGE
 
 
-def test_pool_bit_exact(ctx, oracle):
+def test_pool_vs_f64_and_oracle(ctx, oracle):
+    """pool_and_normalize: the GPU sums tokens in 64-token chunks (fixed order), so
+    it is held to the float64 mean (|err| <= 1e-6 of the largest component) and
+    to the sequential-sum oracle at cosine > 1 - 1e-10, not bit-exactness."""
     for t, d, trunc, masked in [(512, 768, 256, False), (512, 768, 0, False), (19, 768, 128, True),
-                                (8192, 768, 256, False)]:
+                                (8192, 768, 256, False), (1000, 768, 0, True)]:
         say(f"pool_normalize t={t} d={d} trunc={trunc} masked={masked}")
-        tok = oracle.normal(t * d, seed=t + trunc).reshape(t, d)
+        tok = oracle.normal(t * d, seed=t + trunc).reshape(t, d) + np.float32(0.05)
         mask = None
         if masked:
             mask = (np.arange(t) % 3 != 1).astype(np.uint8)
         y = host(ops.pool_normalize(ctx, dev(tok), mask, trunc))
-        assert_bits_equal(y, oracle.pool_normalize(tok, mask, trunc), "pool")
+        sel = tok.astype(np.float64) if mask is None else tok[mask.astype(bool)].astype(np.float64)
+        ref = sel.mean(0)
+        ref = ref / np.linalg.norm(ref)
+        if 0 < trunc < d:
+            ref = ref[:trunc] / np.linalg.norm(ref[:trunc])
+        assert np.abs(y - ref).max() <= 1e-6 * np.abs(ref).max()
+        orc = oracle.pool_normalize(tok, mask, trunc)
+        cos = float(y.astype(np.float64) @ orc / np.linalg.norm(y) / np.linalg.norm(orc))
+        assert cos > 1 - 1e-10
     c = KAT["pool"][0]
     v = np.array(c["v_bits"], np.uint32).view(np.float32)
     tok = np.tile(v, (c["t"], 1))
