@@ -350,7 +350,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--variant", choices=["int8", "bf16"], default="int8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3 extra lines")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run one plain device copy of MIB MiB (calibrates rocprof "
+                         "FETCH_SIZE / WRITE_SIZE against known bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -364,6 +367,13 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     variant = INT8_EXACT if args.variant == "int8" else BF16_DEQUANT
     ctx = ops.Context(0)
+    if args.copy_probe:
+        n = args.copy_probe * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     m = 512
     L, ms, kern = run_workload(ctx, m, variant, args.steps, args.warmup)
