@@ -120,8 +120,10 @@ inline hipEvent_t get_event(glypr_hip_ctx* ctx) {
     ctx->event_pool.pop_back();
     return e;
   }
+  // No system-scope release: a timing marker must not add an L2 write-back
+  // between the kernels it brackets.
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 

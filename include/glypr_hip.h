@@ -2,8 +2,8 @@
  * glypr_hip.h — C ABI of glypr's MI355X (gfx950) Q8_0 backend.
  *
  * A HIP backend beside glypr-core's Metal and CPU-SIMD backends.  The entry
- * points are what a Rust `glypr-hip-sys` crate binds (see INTEGRATION.md for
- * the binding and the `LinearOp::HipQ8_0` arm).  Each declaration names the
+ * points are what a Rust `glypr-hip-sys` crate binds from a `LinearOp::HipQ8_0`
+ * arm of linear.rs.  Each declaration names the
  * reference interface it replaces (paths inside phrozen/glypr v0.3.0,
  * crates/glypr-core/src/).
  *
