@@ -16,6 +16,26 @@
  *
  * Block format (GGUF Q8_0): 34 bytes = { uint16 f16 scale d; int8 qs[32] },
  * rows of K/32 blocks, row-major [N][K/32].
+ *
+ * How each function is pinned (tests/test_oracle.py):
+ *  - f16 codec: every finite f16 and RNE ties against numpy's float16.
+ *  - quantize / dequantize / vec_dot: exact known-answer blocks
+ *    (tests/golden/q8_0_kat.json), float64 restatement of the definition,
+ *    lossless case (GEMM == numpy float64 X @ W^T exactly).
+ *  - matmul / matmul_preq: float64 brute force over the same quantized operands.
+ *  - rmsnorm: constant-row KAT, float64 formula, 2^k scale invariance.
+ *  - tanhf / geglu: double-precision tanh (<= 3 ulp), exact special points.
+ *  - embed_gather, pool_normalize: dequantized rows; closed-form KAT and the
+ *    reference's long-context generator against float64.
+ *  - attention: chunked band == dense masked attention in float64.
+ *  - rope_tables: closed form (f32 product, float64 cos/sin).
+ *  - encoder_layer / model_forward: an independent float64 statement of the
+ *    whole forward at small dimensions, both layer types.
+ * Parity unpinned (no runnable reference vector exists offline): the exact f32
+ * bit pattern of candle's vec_dot accumulation (scalar vec_dot_unopt order is
+ * restated; AVX/NEON builds differ in the last bits), pulp's RMSNorm lane order
+ * (the AVX2 8-lane order is restated), and the platform tanhf (this file's own
+ * tanh replaces it; the substitution is bounded by a test).
  */
 #ifndef GLYPR_ORACLE_H
 #define GLYPR_ORACLE_H

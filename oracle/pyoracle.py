@@ -290,3 +290,43 @@ def attention(q, k, v, window: int, threads: int = 0):
     lib().orc_attention(_p(q, _f32p), _p(k, _f32p), _p(v, _f32p), nh, nkv, t, hd, window,
                         _p(out, _f32p), threads)
     return out
+
+
+def model_forward(tensors: dict, ids: np.ndarray, trunc: int, *, hidden: int, ffn: int,
+                  n_heads: int, n_kv_heads: int, head_dim: int, n_layers: int, vocab: int,
+                  sliding_window: int = 512, eps: float = 1e-6, theta_sliding: float = 1e4,
+                  theta_full: float = 1e6, threads: int = 0):
+    """orc_model_forward over GGUF-named tensors {name: array} (Q8_0 tensors as
+    block bytes, norms as f32).  Returns (pooled [trunc or hidden], final-normed
+    token states [t, hidden])."""
+    cfg = ModelConfig(hidden=hidden, ffn=ffn, n_heads=n_heads, n_kv_heads=n_kv_heads,
+                      head_dim=head_dim, n_layers=n_layers, vocab=vocab,
+                      sliding_window=sliding_window, eps=eps, rope_theta_sliding=theta_sliding,
+                      rope_theta_full=theta_full)
+    keep = []
+
+    def arr(name, dt, ptype):
+        a = np.ascontiguousarray(tensors[name], dtype=dt)
+        keep.append(a)
+        return _p(a, ptype)
+
+    layers = (LayerWeights * n_layers)()
+    for i in range(n_layers):
+        p = f"blk.{i}."
+        layers[i] = LayerWeights(
+            *[arr(p + n + ".weight", np.uint8, _u8p) for n in
+              ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")],
+            *[arr(p + n + ".weight", np.float32, _f32p) for n in
+              ("attn_norm", "post_attention_norm", "ffn_norm", "post_ffw_norm", "attn_q_norm",
+               "attn_k_norm")])
+    ids = np.ascontiguousarray(ids, np.uint32)
+    t = ids.size
+    out = np.empty(trunc if 0 < trunc < hidden else hidden, np.float32)
+    states = np.empty((t, hidden), np.float32)
+    rc = lib().orc_model_forward(ctypes.byref(cfg), arr("token_embd.weight", np.uint8, _u8p),
+                                 layers, arr("output_norm.weight", np.float32, _f32p),
+                                 _p(ids, _u32p), t, trunc, _p(out, _f32p), _p(states, _f32p),
+                                 threads)
+    if rc != 0:
+        raise ValueError("orc_model_forward: token id out of range")
+    return out, states

@@ -318,3 +318,125 @@ def test_attention_band_equals_masked_dense(oracle):
         assert np.abs(out[:, h * hd:(h + 1) * hd] - ref).max() < 1e-5
     full = oracle.attention(q, k, v, 0)
     assert not np.allclose(full, out)
+
+
+# ------------------------------------------------------------------ RoPE ----
+
+@pytest.mark.parametrize("hd,theta", [(256, 1e4), (256, 1e6), (64, 1e4)])
+def test_rope_tables_closed_form(oracle, hd, theta):
+    """rope.rs:14-87: inv_freq[i] = f32(1 / theta^(2i/hd)), freqs = f32(pos) * inv_freq
+    in f32, emb = [freqs, freqs], tables = cos/sin(emb).  numpy reproduces the f32
+    product exactly; the cos/sin of it are checked against float64."""
+    t = 8192
+    c, s = oracle.rope_tables(hd, theta, t)
+    inv = (1.0 / np.power(theta, 2.0 * np.arange(hd // 2) / hd)).astype(np.float32)
+    freqs = np.arange(t, dtype=np.float32)[:, None] * inv[None, :]     # f32 product
+    emb = np.concatenate([freqs, freqs], axis=1).astype(np.float64)
+    assert np.abs(c - np.cos(emb)).max() < 2e-7
+    assert np.abs(s - np.sin(emb)).max() < 2e-7
+    assert np.all(c[0] == 1) and np.all(s[0] == 0)
+    assert np.array_equal(c[:, :hd // 2], c[:, hd // 2:])
+
+
+# -------------------------------------------------------- whole forward ----
+
+def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, window, eps=1e-6):
+    """Independent float64 statement of forward_embeds (model.rs:498-578) over the
+    layer order of layer.rs:20-50 (no PLE): the same Q8_0 quantization of every
+    GEMM input (oracle quantizer, pinned above), everything else in float64."""
+    def deq(name, n, k):
+        return oracle.dequantize_rows(tensors[name], k).reshape(n, k).astype(np.float64)
+
+    def lin(x, name, n, k):
+        xq = oracle.dequantize_rows(oracle.quantize_rows(x.astype(np.float32)), k)
+        return xq.reshape(x.shape[0], k).astype(np.float64) @ deq(name, n, k).T
+
+    def rms(x, w):
+        y = x / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+        return y if w is None else y * w.astype(np.float64)
+
+    def rope(x, theta):     # x [t, hd]
+        t = x.shape[0]
+        inv = (1.0 / np.power(theta, 2.0 * np.arange(hd // 2) / hd)).astype(np.float32)
+        f = np.arange(t, dtype=np.float32)[:, None] * inv[None, :]
+        e = np.concatenate([f, f], 1).astype(np.float64)
+        rot = np.concatenate([-x[:, hd // 2:], x[:, :hd // 2]], 1)
+        return x * np.cos(e) + rot * np.sin(e)
+
+    t = ids.size
+    table = oracle.dequantize_rows(tensors["token_embd.weight"], H).reshape(-1, H)
+    h = (table[ids] * np.float32(np.sqrt(H))).astype(np.float64)
+    idx = np.arange(t)
+    for l in range(n_layers):
+        p = f"blk.{l}."
+        full = (l + 1) % 6 == 0
+        theta = 1e6 if full else 1e4
+        mask = np.zeros((t, t)) if full else \
+            np.where(np.abs(idx[:, None] - idx[None, :]) > window, -np.inf, 0.0)
+        x = rms(h, tensors[p + "attn_norm.weight"])
+        q = lin(x, p + "attn_q.weight", nh * hd, H).reshape(t, nh, hd)
+        k = lin(x, p + "attn_k.weight", nkv * hd, H).reshape(t, nkv, hd)
+        v = lin(x, p + "attn_v.weight", nkv * hd, H).reshape(t, nkv, hd)
+        ctx = np.empty((t, nh * hd))
+        for j in range(nh):
+            g = j // (nh // nkv)
+            qj = rope(rms(q[:, j], tensors[p + "attn_q_norm.weight"]), theta)
+            kg = rope(rms(k[:, g], tensors[p + "attn_k_norm.weight"]), theta)
+            vg = rms(v[:, g], None)
+            s = qj @ kg.T + mask                     # scale 1.0
+            pr = np.exp(s - s.max(1, keepdims=True))
+            ctx[:, j * hd:(j + 1) * hd] = (pr / pr.sum(1, keepdims=True)) @ vg
+        h = h + rms(lin(ctx, p + "attn_output.weight", H, nh * hd),
+                    tensors[p + "post_attention_norm.weight"])
+        x = rms(h, tensors[p + "ffn_norm.weight"])
+        gt = lin(x, p + "ffn_gate.weight", F, H)
+        up = lin(x, p + "ffn_up.weight", F, H)
+        act = 0.5 * gt * (1 + np.tanh(np.sqrt(2 / np.pi) * (gt + 0.044715 * gt ** 3))) * up
+        h = h + rms(lin(act, p + "ffn_down.weight", H, F), tensors[p + "post_ffw_norm.weight"])
+    states = rms(h, tensors["output_norm.weight"])
+    pooled = states.mean(0)
+    pooled /= max(np.linalg.norm(pooled), 1e-12)
+    m = pooled[:trunc]
+    return m / max(np.linalg.norm(m), 1e-12), states
+
+
+def test_model_forward_vs_float64_statement(oracle):
+    """The oracle's composition (gather x sqrt(H), q/k/v norms, RoPE, GQA attention
+    with scale 1.0 and the 5:1 sliding/full pattern, post-norm residuals, GeGLU MLP,
+    final norm, pool, L2, MRL) against an independent float64 statement at small
+    dimensions: 6 layers so both layer types run, window 8 < t so the band binds."""
+    H, F, nh, nkv, hd, L, vocab, t, W = 128, 192, 2, 1, 64, 6, 1000, 40, 8
+    rng = np.random.default_rng(11)
+    tensors = {"token_embd.weight": oracle.q8_0_weight(vocab, H, 100, 0.02),
+               "output_norm.weight": (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)}
+    seed = 200
+    for l in range(L):
+        for name, n, k in [("attn_q", nh * hd, H), ("attn_k", nkv * hd, H),
+                           ("attn_v", nkv * hd, H), ("attn_output", H, nh * hd),
+                           ("ffn_gate", F, H), ("ffn_up", F, H), ("ffn_down", H, F)]:
+            tensors[f"blk.{l}.{name}.weight"] = oracle.q8_0_weight(n, k, seed, 0.02)
+            seed += 1
+        for name, n in [("attn_norm", H), ("post_attention_norm", H), ("ffn_norm", H),
+                        ("post_ffw_norm", H), ("attn_q_norm", hd), ("attn_k_norm", hd)]:
+            w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+            if name in ("attn_q_norm", "attn_k_norm"):
+                w = (w * 0.25).astype(np.float32)
+            tensors[f"blk.{l}.{name}.weight"] = w
+    ids = rng.integers(0, vocab, t).astype(np.uint32)
+    out, states = oracle.model_forward(tensors, ids, 32, hidden=H, ffn=F, n_heads=nh,
+                                       n_kv_heads=nkv, head_dim=hd, n_layers=L, vocab=vocab,
+                                       sliding_window=W)
+    ref_out, ref_states = _forward_f64(oracle, tensors, ids, 32, H, F, nh, nkv, hd, L, W)
+    row_cos = (states * ref_states).sum(1) / np.linalg.norm(states, axis=1) / \
+        np.linalg.norm(ref_states, axis=1)
+    assert row_cos.min() > 0.9999, row_cos.min()
+    assert float(out @ ref_out) > 0.99999
+    assert out.shape == (32,) and abs(np.linalg.norm(out.astype(np.float64)) - 1) < 1e-6
+    # a wrong window (full attention everywhere) must be visible at this size
+    bad_out, _ = oracle.model_forward(tensors, ids, 32, hidden=H, ffn=F, n_heads=nh,
+                                      n_kv_heads=nkv, head_dim=hd, n_layers=L, vocab=vocab,
+                                      sliding_window=t)
+    assert float(bad_out @ ref_out) < float(out @ ref_out)
+    with pytest.raises(ValueError):
+        oracle.model_forward(tensors, np.array([vocab], np.uint32), 32, hidden=H, ffn=F,
+                             n_heads=nh, n_kv_heads=nkv, head_dim=hd, n_layers=L, vocab=vocab)
