@@ -190,6 +190,7 @@ TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
 def measured_traffic(workload, kernel, variant):
     """HBM bytes per launch of `kernel` from the rocprof FETCH_SIZE / WRITE_SIZE
     passes recorded in profiles/traffic.json (copy-calibrated), or None."""
+    from glypr_amd.ops import INT8_EXACT
     try:
         with open(TRAFFIC_FILE) as f:
             table = json.load(f)

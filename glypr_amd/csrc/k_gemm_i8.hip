@@ -257,99 +257,119 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 
 // ---------------------------------------------------------------------------
 // Small-M variant (T <= ~2K tokens: one sequence through a layer).  There the
-// big-tile grid has fewer waves than the chip has SIMDs and every K stage
-// exposes a full HBM/L2 latency.  This kernel instead:
+// big-tile grid has fewer waves than the chip has SIMDs, and the exact
+// epilogue (3 VALU ops per output and block) is the bound.  This kernel:
 //  - uses v_mfma_i32_16x16x32_i8 (still one Q8_0 block per MFMA) so each wave
-//    owns a 16x16 (or 16 x 4*16) tile: 4x more waves for the same problem;
-//  - stages the whole K range of its A and B tiles in LDS at once with
-//    global_load_lds_dwordx4 (asynchronous, no register staging), so the
-//    kernel pays one memory latency instead of one per K stage.
-// LDS layout per operand: [stage][row][128 B], 16-byte chunk c of row r stored
-// at chunk c ^ (r & 7).  A wave's global_load_lds writes 1 KB linearly (lane i
-// -> bytes 16i..16i+15 = row i/8, physical chunk i%8), so lane i loads global
+//    owns a 16 x 16*TNW tile: many small waves spread over all SIMDs;
+//  - streams K in 128-byte stages through a RING-slot LDS ring filled by
+//    global_load_lds_dwordx4 (LDS DMA, no register staging).  The DMAs are
+//    issued from inline asm: the compiler then does not see them and adds no
+//    vmcnt(0) before the ds_reads of earlier stages.  Every loop iteration
+//    issues exactly UPW DMAs per wave (past the last stage it reloads the last
+//    stage into the slot just freed), so "stage s has landed" is the single
+//    constant wait vmcnt((RING-2)*UPW) followed by a barrier;
+//  - stages the per-block scales once, coalesced, in their natural [row][b]
+//    layout (dA rows of the tile, then dB rows).
+// LDS layout of a ring slot: A rows then B rows, each [row][128 B] with the
+// 16-byte chunk c of row r stored at chunk c ^ (r & 7).  One DMA writes 1 KB
+// linearly (lane i -> row i/8, physical chunk i%8), so lane i reads global
 // chunk (i%8) ^ (row & 7).  Rows past M/N are clamped to a valid row (their
-// outputs are never stored); stage bytes past K are never read.
+// outputs are never stored).
 // ---------------------------------------------------------------------------
 typedef long v1l;
 
-// WM x WN waves; each wave owns a 16-row slab and TNW 16-column tiles.
-// GEGLU: TNW == 2 (gate tile, up tile of the same 16 h columns); the 32-wide
-// Q8_0 block of h spans the two waves wn = 0, 1, which exchange their amax
-// through LDS.  Requires K % 128 == 0 (whole 4-block stages, no tail guard).
-template <int WM, int WN, int TNW, bool GEGLU>
+// 16 bytes per lane, global -> LDS (lane i -> lds_base + 16 i).
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(lds_base) : "memory", "m0");
+}
+// 4 bytes per lane, global -> LDS (lane i -> lds_base + 4 i).
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(g), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+
+constexpr int SMALL_NB_MAX = 36;   // K <= 1152
+
+// WM x WN waves; wave (wm, wn) owns rows 16 wm.. and TNW 16-row B tiles.
+// GEGLU: TNW == 2 (gate tile, up tile of the same 16 h columns) and WN == 2:
+// the 32-wide Q8_0 block of h spans waves wn = 0, 1, which exchange their
+// amax through LDS.  Requires K % 128 == 0 and K <= 32 * SMALL_NB_MAX.
+template <int WM, int WN, int TNW, bool GEGLU, int RING>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
                      const int8_t* __restrict__ B, const float* __restrict__ dB,
                      float* __restrict__ C, int8_t* __restrict__ Hq, float* __restrict__ dH,
                      int M, int N, int K, int ldc, int F) {
-  constexpr int NT = WM * WN * 64;
   constexpr int NW = WM * WN;
   constexpr int BM = WM * 16;
-  constexpr int BN = WN * 16 * TNW;  // B rows per block tile
+  constexpr int BN = WN * 16 * TNW;         // B rows per tile
+  constexpr int UA = BM / 8, UB = BN / 8;   // 1 KB DMA units per stage
+  constexpr int UPW = (UA + UB) / NW;
+  static_assert((UA + UB) % NW == 0, "stage units must split evenly over the waves");
+  static_assert(RING >= 3, "ring needs >= 3 slots");
   static_assert(!GEGLU || (TNW == 2 && WN == 2), "GeGLU tile: 2 waves x (gate, up)");
-
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int SLOT = (BM + BN) * BK;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
+  __shared__ __attribute__((aligned(16))) float sc[(BM + BN) * SMALL_NB_MAX + 64];
   __shared__ float amax_x[GEGLU ? WN * BM : 1];
-  const int nb = K / QK;
-  const int nst = K / BK;
-  uint8_t* As = smem;
-  uint8_t* Bs = As + nst * BM * BK;
-  float* dAs = reinterpret_cast<float*>(Bs + nst * BN * BK);  // [BM][nb]
-  float* dBs = dAs + ((nb * BM + 63) & ~63);                    // [BN][nb]
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int NB = K / QK, NST = K / BK;
+  const int SA = NB * BM, SB = NB * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;   // GEGLU: virtual column index (2 per h column)
   const int hc0 = n0 >> 1;
 
-  // GEGLU B rows: [gate hc0..+15, up hc0..+15, gate hc0+16..+31, up hc0+16..+31]
-  auto b_src = [&](int nl, bool& ok) -> int {
-    if (!GEGLU) {
-      ok = n0 + nl < N;
-      return ok ? n0 + nl : N - 1;
-    }
+  // B row of tile-local row nl.  GEGLU: [gate hc0..+15, up hc0..+15,
+  // gate hc0+16..+31, up hc0+16..+31].
+  auto b_row = [&](int nl) -> int {
+    if (!GEGLU) return n0 + nl < N ? n0 + nl : N - 1;
     int t = nl >> 4;
     int c = hc0 + (t >> 1) * 16 + (nl & 15);
-    ok = c < F;
-    if (!ok) c = F - 1;
+    if (c >= F) c = F - 1;
     return (t & 1) ? F + c : c;
   };
 
-  // ---- asynchronous operand loads: units of 8 rows x 128 B = 1 KB per instruction
+  // ---- scales: dA rows [BM][NB] then dB rows [BN][NB], coalesced
+  for (int e0 = wave * 64; e0 < SA + SB; e0 += NW * 64) {
+    int e = e0 + lane;
+    const float* src;
+    if (e < SA) {
+      int r = e / NB, b = e - r * NB;
+      int gm = m0 + r < M ? m0 + r : M - 1;
+      src = dA + (int64_t)gm * NB + b;
+    } else {
+      int f = e - SA < SB ? e - SA : SB - 1;
+      int c = f / NB, b = f - c * NB;
+      src = dB + (int64_t)b_row(c) * NB + b;
+    }
+    dma4(src, lds_u32(sc + e0));
+  }
+  // ---- this wave's DMA units: row pointers (stage 0) and slot offsets
   const int rsub = lane >> 3, pch = lane & 7;
-  const int a_units = nst * (BM / 8), b_units = nst * (BN / 8);
-  for (int u = wave; u < a_units; u += NW) {
-    int st = u / (BM / 8), row = (u % (BM / 8)) * 8 + rsub;
-    int gm = m0 + row < M ? m0 + row : M - 1;
-    int gk = st * BK + ((pch ^ (row & 7)) << 4);
-    __builtin_amdgcn_global_load_lds(A + (int64_t)gm * K + gk, As + u * 1024, 16, 0, 0);
+  const int8_t* usrc[UPW];
+  int uoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; j++) {
+    int u = j * NW + wave;
+    int row = (u < UA ? u : u - UA) * 8 + rsub;
+    const int8_t* base = u < UA ? A + (int64_t)(m0 + row < M ? m0 + row : M - 1) * K
+                                : B + (int64_t)b_row(row) * K;
+    usrc[j] = base + ((pch ^ (row & 7)) << 4);
+    uoff[j] = u * 1024;
   }
-  for (int u = wave; u < b_units; u += NW) {
-    int st = u / (BN / 8), row = (u % (BN / 8)) * 8 + rsub;
-    bool ok;
-    int gn = b_src(row, ok);
-    int gk = st * BK + ((pch ^ (row & 7)) << 4);
-    __builtin_amdgcn_global_load_lds(B + (int64_t)gn * K + gk, Bs + u * 1024, 16, 0, 0);
-  }
-  // ---- scales: row-major [row][nb] copies (4 B per lane)
-  for (int e0 = wave * 64; e0 < BM * nb; e0 += NW * 64) {
-    int e = e0 + lane < BM * nb ? e0 + lane : BM * nb - 1;
-    int r = e / nb, b = e - r * nb;
-    int gm = m0 + r < M ? m0 + r : M - 1;
-    __builtin_amdgcn_global_load_lds(dA + (int64_t)gm * nb + b, dAs + e0, 4, 0, 0);
-  }
-  for (int e0 = wave * 64; e0 < BN * nb; e0 += NW * 64) {
-    int e = e0 + lane < BN * nb ? e0 + lane : BN * nb - 1;
-    int r = e / nb, b = e - r * nb;
-    bool ok;
-    int gn = b_src(r, ok);
-    __builtin_amdgcn_global_load_lds(dB + (int64_t)gn * nb + b, dBs + e0, 4, 0, 0);
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  auto issue = [&](int st) {
+    const int s = st < NST ? st : NST - 1;
+    uint8_t* slot = ring + (st % RING) * SLOT;
+#pragma unroll
+    for (int j = 0; j < UPW; j++) dma16(usrc[j] + s * BK, lds_u32(slot + uoff[j]));
+  };
+  for (int st = 0; st < RING - 1; st++) issue(st);
 
   const int l16 = lane & 15, lq = lane >> 4;   // lq: 8-byte K slice (operands) / row quad (out)
   const int arow = wm * 16 + l16;
@@ -360,39 +380,48 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   for (int t = 0; t < TNW; t++)
 #pragma unroll
     for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
+  const float* xs = sc + (wm * 16 + 4 * lq) * NB;   // this lane's 4 output rows
 
-  const float* xs = dAs + (wm * 16 + 4 * lq) * nb;  // this lane's 4 output rows
-  for (int st = 0; st < nst; st++) {
-    const uint8_t* Ast = As + st * BM * BK + arow * BK;
-    const uint8_t* Bst = Bs + st * BN * BK;
+#pragma unroll 1
+  for (int st = 0; st < NST; st++) {
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"((RING - 2) * UPW) : "memory");
+    __syncthreads();
+    issue(st + RING - 1);
+    const uint8_t* As = ring + (st % RING) * SLOT;
+    const uint8_t* Bs = As + BM * BK;
+    v4i d[KB][TNW];
 #pragma unroll
     for (int kb = 0; kb < KB; kb++) {
-      const int b = st * KB + kb;
       const int ch = 2 * kb + (lq >> 1);
-      v1l af = *reinterpret_cast<const v1l*>(Ast + ((ch ^ (arow & 7)) << 4) + hoff);
-      v4i d[TNW];
+      v1l af = *reinterpret_cast<const v1l*>(As + arow * BK + ((ch ^ (arow & 7)) << 4) + hoff);
 #pragma unroll
       for (int t = 0; t < TNW; t++) {
         const int brow = wn * 16 * TNW + t * 16 + l16;
-        v1l bf = *reinterpret_cast<const v1l*>(Bst + brow * BK + ((ch ^ (brow & 7)) << 4) + hoff);
-        d[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, magic, 0, 0, 0);
+        v1l bf = *reinterpret_cast<const v1l*>(Bs + brow * BK + ((ch ^ (brow & 7)) << 4) + hoff);
+        d[kb][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, magic, 0, 0, 0);
       }
+    }
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+      const int b = st * KB + kb;
       float xd[4];
 #pragma unroll
-      for (int r = 0; r < 4; r++) xd[r] = xs[r * nb + b];
+      for (int r = 0; r < 4; r++) xd[r] = xs[r * NB + b];
 #pragma unroll
       for (int t = 0; t < TNW; t++) {
-        const float wd = dBs[(wn * 16 * TNW + t * 16 + l16) * nb + b];
+        const float wd = sc[SA + (wn * 16 * TNW + t * 16 + l16) * NB + b];
         const float wc = wd * NEG_MAGIC;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          float tt = fmaf(__int_as_float(d[t][r]), wd, wc);  // round(S * d_w)
-          float u = tt * xd[r];                               // round(. * d_x)
-          acc[t][r] = acc[t][r] + u;                          // round(acc + .)
+          float tt = fmaf(__int_as_float(d[kb][t][r]), wd, wc);  // round(S * d_w)
+          float u = tt * xd[r];                                   // round(. * d_x)
+          acc[t][r] = acc[t][r] + u;                              // round(acc + .)
         }
       }
     }
   }
+  // the reloads issued past the last stage must land before the LDS is released
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   const int grow0 = m0 + wm * 16 + 4 * lq;
   if constexpr (!GEGLU) {
@@ -424,40 +453,31 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const float other = amax_x[(wn ^ 1) * BM + wm * 16 + 4 * lq + r];
-      QScale sc = q8_scale(fmaxf(a[r], other));
+      QScale sc8 = q8_scale(fmaxf(a[r], other));
       const int gm = grow0 + r;
       if (gm < M && hc < F) {
-        Hq[(int64_t)gm * F + hc] = (int8_t)quant_round(h[r] * sc.id);
-        if (wn == 0 && l16 == 0) dH[(int64_t)gm * nbh + (hc >> 5)] = sc.dq;
+        Hq[(int64_t)gm * F + hc] = (int8_t)quant_round(h[r] * sc8.id);
+        if (wn == 0 && l16 == 0) dH[(int64_t)gm * nbh + (hc >> 5)] = sc8.dq;
       }
     }
   }
 }
 
-template <int WM, int WN, int TNW, bool GEGLU>
+template <int WM, int WN, int TNW, bool GEGLU, int RING>
 hipError_t run_small(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                      float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K,
                      int64_t ldc, int64_t F, hipStream_t s) {
   constexpr int BM = WM * 16, BN = WN * 16 * TNW;
-  const int64_t nst = K / BK, nb = K / QK;
-  const size_t lds = (size_t)(nst * (BM + BN) * BK + (((nb * BM + 63) & ~63) + nb * BN + 64) * 4);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_i8_small_kernel<WM, WN, TNW, GEGLU>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
   dim3 grid((unsigned)((Nrows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  gemm_i8_small_kernel<WM, WN, TNW, GEGLU><<<grid, WM * WN * 64, lds, s>>>(
+  gemm_i8_small_kernel<WM, WN, TNW, GEGLU, RING><<<grid, WM * WN * 64, 0, s>>>(
       xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F);
   return hipGetLastError();
 }
 
-// Small-M kernels stage the whole K range: (BM + BN) * K bytes + scales of LDS.
+// Small-M kernels stream K through an LDS ring; the scales of the whole K
+// range stay in LDS ((BM + BN) * K/32 floats).
 constexpr int64_t SMALL_M_MAX = 2048;
-constexpr int64_t SMALL_K_MAX = 1152;
+constexpr int64_t SMALL_K_MAX = 32 * SMALL_NB_MAX;
 inline bool small_ok(int64_t M, int64_t K) {
   return M <= SMALL_M_MAX && K <= SMALL_K_MAX && K % BK == 0;
 }
@@ -479,7 +499,7 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
                           hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
   if (small_ok(M, K))
-    return run_small<4, 2, 1, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+    return run_small<2, 2, 1, false, 4>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
   int64_t big_tiles = ((M + 127) / 128) * ((N + 127) / 128);
   if (big_tiles >= 512)
     return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
@@ -491,7 +511,7 @@ hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t*
                                 int64_t K, hipStream_t s) {
   if (M == 0 || F == 0) return hipSuccess;
   if (small_ok(M, K))
-    return run_small<4, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+    return run_small<2, 2, 2, true, 3>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
   int64_t big_tiles = ((M + 127) / 128) * ((2 * F + 127) / 128);
   if (big_tiles >= 512)
     return run<128, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
