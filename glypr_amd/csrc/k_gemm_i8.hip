@@ -278,10 +278,11 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 // ---------------------------------------------------------------------------
 typedef long v1l;
 
-// 16 bytes per lane, global -> LDS (lane i -> lds_base + 16 i).
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(lds_base) : "memory", "m0");
+// 16 bytes per lane, global -> LDS (lane i -> lds_base + 16 i); the address
+// is the uniform base plus the lane's 32-bit offset.
+__device__ __forceinline__ void dma16(const int8_t* base, int voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
 }
 // 4 bytes per lane, global -> LDS (lane i -> lds_base + 4 i).
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
@@ -297,29 +298,36 @@ constexpr int SMALL_NB_MAX = 36;   // K <= 1152
 // WM x WN waves; wave (wm, wn) owns rows 16 wm.. and TNW 16-row B tiles.
 // GEGLU: TNW == 2 (gate tile, up tile of the same 16 h columns) and WN == 2:
 // the 32-wide Q8_0 block of h spans waves wn = 0, 1, which exchange their
-// amax through LDS.  Requires K % 128 == 0 and K <= 32 * SMALL_NB_MAX.
-template <int WM, int WN, int TNW, bool GEGLU, int RING>
+// amax through LDS.  NB = K / 32 blocks, NB % 4 == 0.
+//
+// Scales stay in their natural [row][b] layout in LDS, so the four blocks of
+// a stage are 16 contiguous bytes of a row: per stage a lane reads its four
+// row scales and its TNW column scales with 4 + TNW ds_read_b128.  The stage
+// loop is unrolled by RING so ring slots are compile-time LDS offsets.
+template <int WM, int WN, int TNW, bool GEGLU, int RING, int NB>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
                      const int8_t* __restrict__ B, const float* __restrict__ dB,
                      float* __restrict__ C, int8_t* __restrict__ Hq, float* __restrict__ dH,
-                     int M, int N, int K, int ldc, int F) {
+                     int M, int N, int ldc, int F) {
+  constexpr int K = NB * QK, NST = NB / KB;
   constexpr int NW = WM * WN;
   constexpr int BM = WM * 16;
   constexpr int BN = WN * 16 * TNW;         // B rows per tile
   constexpr int UA = BM / 8, UB = BN / 8;   // 1 KB DMA units per stage
   constexpr int UPW = (UA + UB) / NW;
+  constexpr int SA = NB * BM, SB = NB * BN;
+  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 1152");
   static_assert((UA + UB) % NW == 0, "stage units must split evenly over the waves");
   static_assert(RING >= 3, "ring needs >= 3 slots");
   static_assert(!GEGLU || (TNW == 2 && WN == 2), "GeGLU tile: 2 waves x (gate, up)");
   constexpr int SLOT = (BM + BN) * BK;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
-  __shared__ __attribute__((aligned(16))) float sc[(BM + BN) * SMALL_NB_MAX + 64];
+  __shared__ __attribute__((aligned(16))) float sc[SA + SB + 64];
   __shared__ float amax_x[GEGLU ? WN * BM : 1];
 
-  const int NB = K / QK, NST = K / BK;
-  const int SA = NB * BM, SB = NB * BN;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;   // GEGLU: virtual column index (2 per h column)
@@ -335,7 +343,7 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     return (t & 1) ? F + c : c;
   };
 
-  // ---- scales: dA rows [BM][NB] then dB rows [BN][NB], coalesced
+  // ---- scales: dA rows [BM][NB] then dB rows [BN][NB], coalesced DMA
   for (int e0 = wave * 64; e0 < SA + SB; e0 += NW * 64) {
     int e = e0 + lane;
     const float* src;
@@ -350,73 +358,90 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     }
     dma4(src, lds_u32(sc + e0));
   }
-  // ---- this wave's DMA units: row pointers (stage 0) and slot offsets
+  // ---- this wave's DMA units: uniform base (A or B) + per-lane row offset
   const int rsub = lane >> 3, pch = lane & 7;
-  const int8_t* usrc[UPW];
-  int uoff[UPW];
+  const int8_t* ubase[UPW];
+  int uvoff[UPW];
 #pragma unroll
   for (int j = 0; j < UPW; j++) {
-    int u = j * NW + wave;
-    int row = (u < UA ? u : u - UA) * 8 + rsub;
-    const int8_t* base = u < UA ? A + (int64_t)(m0 + row < M ? m0 + row : M - 1) * K
-                                : B + (int64_t)b_row(row) * K;
-    usrc[j] = base + ((pch ^ (row & 7)) << 4);
-    uoff[j] = u * 1024;
+    const int u = j * NW + wave;
+    const int row = (u < UA ? u : u - UA) * 8 + rsub;
+    const int grow = u < UA ? (m0 + row < M ? m0 + row : M - 1) : b_row(row);
+    ubase[j] = u < UA ? A : B;
+    uvoff[j] = grow * K + ((pch ^ (row & 7)) << 4);
   }
-  auto issue = [&](int st) {
-    const int s = st < NST ? st : NST - 1;
-    uint8_t* slot = ring + (st % RING) * SLOT;
+  // stage st (clamped to the last one) into ring slot `slot`
+  auto issue = [&](int st, int slot) {
+    const int sc8 = (st < NST ? st : NST - 1) * BK;
 #pragma unroll
-    for (int j = 0; j < UPW; j++) dma16(usrc[j] + s * BK, lds_u32(slot + uoff[j]));
+    for (int j = 0; j < UPW; j++)
+      dma16(ubase[j] + sc8, uvoff[j], lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
   };
-  for (int st = 0; st < RING - 1; st++) issue(st);
+#pragma unroll
+  for (int st = 0; st < RING - 1; st++) issue(st, st);
 
   const int l16 = lane & 15, lq = lane >> 4;   // lq: 8-byte K slice (operands) / row quad (out)
   const int arow = wm * 16 + l16;
-  const int hoff = (lq & 1) << 3;
+  int offA[KB], offB[TNW][KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    const int ch = 2 * kb + (lq >> 1);
+    offA[kb] = arow * BK + ((ch ^ (arow & 7)) << 4) + ((lq & 1) << 3);
+#pragma unroll
+    for (int t = 0; t < TNW; t++) {
+      const int brow = wn * 16 * TNW + t * 16 + l16;
+      offB[t][kb] = (BM + brow) * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+    }
+  }
+  const float* xrow = sc + (wm * 16 + 4 * lq) * NB;   // row 4 lq + r at xrow + r * NB
+  const float* wrow = sc + SA + (wn * 16 * TNW + l16) * NB;  // tile t at wrow + 16 t NB
   const v4i magic = {MAGIC, MAGIC, MAGIC, MAGIC};
   float acc[TNW][4];
 #pragma unroll
   for (int t = 0; t < TNW; t++)
 #pragma unroll
     for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
-  const float* xs = sc + (wm * 16 + 4 * lq) * NB;   // this lane's 4 output rows
 
 #pragma unroll 1
-  for (int st = 0; st < NST; st++) {
-    asm volatile("s_waitcnt vmcnt(%0)" :: "n"((RING - 2) * UPW) : "memory");
-    __syncthreads();
-    issue(st + RING - 1);
-    const uint8_t* As = ring + (st % RING) * SLOT;
-    const uint8_t* Bs = As + BM * BK;
-    v4i d[KB][TNW];
+  for (int g = 0; g < NST; g += RING) {
 #pragma unroll
-    for (int kb = 0; kb < KB; kb++) {
-      const int ch = 2 * kb + (lq >> 1);
-      v1l af = *reinterpret_cast<const v1l*>(As + arow * BK + ((ch ^ (arow & 7)) << 4) + hoff);
+    for (int r = 0; r < RING; r++) {
+      const int st = g + r;
+      if (st < NST) {
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"((RING - 2) * UPW) : "memory");
+        __syncthreads();
+        issue(st + RING - 1, (r + RING - 1) % RING);
+        const uint8_t* slot = ring + r * SLOT;
+        v4i d[KB][TNW];
 #pragma unroll
-      for (int t = 0; t < TNW; t++) {
-        const int brow = wn * 16 * TNW + t * 16 + l16;
-        v1l bf = *reinterpret_cast<const v1l*>(Bs + brow * BK + ((ch ^ (brow & 7)) << 4) + hoff);
-        d[kb][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, magic, 0, 0, 0);
-      }
-    }
+        for (int kb = 0; kb < KB; kb++) {
+          const v1l af = *reinterpret_cast<const v1l*>(slot + offA[kb]);
 #pragma unroll
-    for (int kb = 0; kb < KB; kb++) {
-      const int b = st * KB + kb;
-      float xd[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) xd[r] = xs[r * NB + b];
-#pragma unroll
-      for (int t = 0; t < TNW; t++) {
-        const float wd = sc[SA + (wn * 16 * TNW + t * 16 + l16) * NB + b];
-        const float wc = wd * NEG_MAGIC;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          float tt = fmaf(__int_as_float(d[kb][t][r]), wd, wc);  // round(S * d_w)
-          float u = tt * xd[r];                                   // round(. * d_x)
-          acc[t][r] = acc[t][r] + u;                              // round(acc + .)
+          for (int t = 0; t < TNW; t++) {
+            const v1l bf = *reinterpret_cast<const v1l*>(slot + offB[t][kb]);
+            d[kb][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, magic, 0, 0, 0);
+          }
         }
+        v4f xq[4], wq[TNW];
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++)
+          xq[rr] = *reinterpret_cast<const v4f*>(xrow + rr * NB + st * KB);
+#pragma unroll
+        for (int t = 0; t < TNW; t++)
+          wq[t] = *reinterpret_cast<const v4f*>(wrow + t * 16 * NB + st * KB);
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+          for (int t = 0; t < TNW; t++) {
+            const float wd = wq[t][kb];
+            const float wc = wd * NEG_MAGIC;
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+              float tt = fmaf(__int_as_float(d[kb][t][rr]), wd, wc);  // round(S * d_w)
+              float u = tt * xq[rr][kb];                              // round(. * d_x)
+              acc[t][rr] = acc[t][rr] + u;                            // round(acc + .)
+            }
+          }
       }
     }
   }
@@ -463,15 +488,40 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   }
 }
 
+template <int WM, int WN, int TNW, bool GEGLU, int RING, int NB>
+hipError_t run_small_nb(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                        float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t ldc,
+                        int64_t F, hipStream_t s) {
+  constexpr int BM = WM * 16, BN = WN * 16 * TNW;
+  dim3 grid((unsigned)((Nrows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
+  gemm_i8_small_kernel<WM, WN, TNW, GEGLU, RING, NB><<<grid, WM * WN * 64, 0, s>>>(
+      xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)ldc, (int)F);
+  return hipGetLastError();
+}
+
+// K is a multiple of 128 and <= 1152 (small_ok).
 template <int WM, int WN, int TNW, bool GEGLU, int RING>
 hipError_t run_small(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                      float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K,
                      int64_t ldc, int64_t F, hipStream_t s) {
-  constexpr int BM = WM * 16, BN = WN * 16 * TNW;
-  dim3 grid((unsigned)((Nrows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  gemm_i8_small_kernel<WM, WN, TNW, GEGLU, RING><<<grid, WM * WN * 64, 0, s>>>(
-      xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F);
-  return hipGetLastError();
+#define GLYPR_SMALL_NB(nb)                                                                 \
+  case nb:                                                                                 \
+    return run_small_nb<WM, WN, TNW, GEGLU, RING, nb>(xq, dx, wq, dw, y, hq, dh, M, Nrows, \
+                                                      ldc, F, s);
+  switch (K / QK) {
+    GLYPR_SMALL_NB(4)
+    GLYPR_SMALL_NB(8)
+    GLYPR_SMALL_NB(12)
+    GLYPR_SMALL_NB(16)
+    GLYPR_SMALL_NB(20)
+    GLYPR_SMALL_NB(24)
+    GLYPR_SMALL_NB(28)
+    GLYPR_SMALL_NB(32)
+    GLYPR_SMALL_NB(36)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef GLYPR_SMALL_NB
 }
 
 // Small-M kernels stream K through an LDS ring; the scales of the whole K
