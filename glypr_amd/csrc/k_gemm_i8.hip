@@ -284,9 +284,9 @@ __device__ __forceinline__ void dma16(const int8_t* base, int voff, uint32_t lds
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
 }
-// 4 bytes per lane, global -> LDS (lane i -> lds_base + 4 i).
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+// 16 bytes per lane from a per-lane 64-bit address (lane i -> lds_base + 16 i).
+__device__ __forceinline__ void dma16_flat(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :: "v"(g), "s"(lds_base) : "memory", "m0");
 }
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
@@ -323,7 +323,7 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   static_assert(!GEGLU || (TNW == 2 && WN == 2), "GeGLU tile: 2 waves x (gate, up)");
   constexpr int SLOT = (BM + BN) * BK;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
-  __shared__ __attribute__((aligned(16))) float sc[SA + SB + 64];
+  __shared__ __attribute__((aligned(16))) float sc[SA + SB + 256];
   __shared__ float amax_x[GEGLU ? WN * BM : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -343,20 +343,22 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     return (t & 1) ? F + c : c;
   };
 
-  // ---- scales: dA rows [BM][NB] then dB rows [BN][NB], coalesced DMA
-  for (int e0 = wave * 64; e0 < SA + SB; e0 += NW * 64) {
-    int e = e0 + lane;
+  // ---- scales: dA rows [BM][NB] then dB rows [BN][NB], 16 B (four blocks)
+  // per lane; the last unit's spare lanes repeat the last chunk into the slack
+  constexpr int NQ = NB / 4;                    // 16-byte chunks per row
+  constexpr int SCH = (SA + SB) / 4;            // chunks in all
+  for (int c0 = wave * 64; c0 < SCH; c0 += NW * 64) {
+    const int c = c0 + lane < SCH ? c0 + lane : SCH - 1;
     const float* src;
-    if (e < SA) {
-      int r = e / NB, b = e - r * NB;
-      int gm = m0 + r < M ? m0 + r : M - 1;
-      src = dA + (int64_t)gm * NB + b;
+    if (c < SA / 4) {
+      const int r = c / NQ, q = c - r * NQ;
+      const int gm = m0 + r < M ? m0 + r : M - 1;
+      src = dA + (int64_t)gm * NB + 4 * q;
     } else {
-      int f = e - SA < SB ? e - SA : SB - 1;
-      int c = f / NB, b = f - c * NB;
-      src = dB + (int64_t)b_row(c) * NB + b;
+      const int f = c - SA / 4, r = f / NQ, q = f - r * NQ;
+      src = dB + (int64_t)b_row(r) * NB + 4 * q;
     }
-    dma4(src, lds_u32(sc + e0));
+    dma16_flat(src, lds_u32(sc + 4 * c0));
   }
   // ---- this wave's DMA units: uniform base (A or B) + per-lane row offset
   const int rsub = lane >> 3, pch = lane & 7;
@@ -458,9 +460,12 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
         if (grow0 + r < M && gn < N) C[(int64_t)(grow0 + r) * ldc + gn] = acc[t][r];
     }
   } else {
+    // h = geglu(gate, up); a row's 32-wide block spans waves wn = 0, 1: each
+    // wave reduces its 16 columns, then one lane per row derives the scale.
+    __shared__ float s_id[BM], s_dq[BM];
     const int nbh = F / QK;
     const int hc = hc0 + wn * 16 + l16;
-    float h[4], a[4];
+    float h[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       h[r] = geglu_scalar(acc[0][r], acc[1][r]);
@@ -469,20 +474,22 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
       v = fmaxf(v, __shfl_xor(v, 2));
       v = fmaxf(v, __shfl_xor(v, 4));
       v = fmaxf(v, __shfl_xor(v, 8));
-      a[r] = v;
+      if (l16 == 0) amax_x[wn * BM + wm * 16 + 4 * lq + r] = v;
     }
-    if (l16 == 0)
-#pragma unroll
-      for (int r = 0; r < 4; r++) amax_x[wn * BM + wm * 16 + 4 * lq + r] = a[r];
+    __syncthreads();
+    if (tid < BM) {
+      const QScale q = q8_scale(fmaxf(amax_x[tid], amax_x[BM + tid]));
+      s_id[tid] = q.id;
+      s_dq[tid] = q.dq;
+    }
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const float other = amax_x[(wn ^ 1) * BM + wm * 16 + 4 * lq + r];
-      QScale sc8 = q8_scale(fmaxf(a[r], other));
+      const int lr = wm * 16 + 4 * lq + r;
       const int gm = grow0 + r;
       if (gm < M && hc < F) {
-        Hq[(int64_t)gm * F + hc] = (int8_t)quant_round(h[r] * sc8.id);
-        if (wn == 0 && l16 == 0) dH[(int64_t)gm * nbh + (hc >> 5)] = sc8.dq;
+        Hq[(int64_t)gm * F + hc] = (int8_t)quant_round(h[r] * s_id[lr]);
+        if (wn == 0 && l16 == 0) dH[(int64_t)gm * nbh + (hc >> 5)] = s_dq[lr];
       }
     }
   }
