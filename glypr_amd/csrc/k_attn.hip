@@ -127,195 +127,234 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 
 // ---------------------------------------------------------------------------
 // Flash attention, split over keys.
-// attn_partial: block = (16-query block, key partition, kv group); one wave per
-//   q head of the group, so the K/V tiles staged in LDS serve all of them
-//   (GQA).  Per 32-key tile: S = Q K^T with v_mfma_f32_16x16x32_f16 (8 k-steps
-//   x 2 key tiles x {q_hi, q_lo}), band/length mask, online softmax in f32,
-//   P (split hi/lo) through LDS into the A-operand layout, O += P V (16 dim
-//   tiles x {p_hi, p_lo}).  The next K/V tile is loaded into registers while the
-//   current one is consumed (double buffering through registers, single LDS
-//   buffer).  Each partition writes its running max m, sum l and unnormalised
-//   O for its 16 queries.
+// attn_partial: block = (32-query block, key partition, kv group) with
+//   QS x G waves: wave (qs, hh) owns queries q0 + 16 qs .. +15 of q head
+//   g G + hh, so every K/V tile staged in LDS serves 16 QS queries of all G
+//   heads of the group (GQA).  K/V tiles (32 keys) stream through a two-slot
+//   LDS ring filled by LDS DMA (global_load_lds_dwordx4 from inline asm, so
+//   the compiler adds no vmcnt waits of its own): tile kb+1 is in flight while
+//   tile kb is consumed.  Per tile: S = Q K^T with v_mfma_f32_16x16x32_f16
+//   (8 k-steps x 2 key tiles x {q_hi, q_lo}), band/length mask, online softmax
+//   in f32, P (split hi/lo) through LDS into the A-operand layout, O += P V
+//   (16 dim tiles x {p_hi, p_lo}).  Each partition writes its running max m,
+//   sum l and unnormalised O for its queries.
+// LDS layouts (16-byte chunks, conflict-free fragment reads):
+//   K slot  [32 keys][256 dims]: chunk c of key row r at c ^ (r & 7);
+//   V^T slot [256 dims][32 keys]: chunk c of dim row r at c ^ ((r >> 1) & 3).
 // attn_combine: one wave per token merges the partitions per head,
 //   ctx = sum_p e^{m_p - M} O_p / sum_p e^{m_p - M} l_p, and writes ctx as f32
 //   and/or directly as the o projection's Q8_0 operand (BlockQ8_0::from_float).
 // MFMA 16x16x32 layouts: A (16 x 32): lane l holds row l%16, k = 8(l/16)..+7;
 // B (32 x 16): column l%16, same k; D (16 x 16): column l%16, rows 4(l/16)+r.
 // ---------------------------------------------------------------------------
-constexpr int AQ = 16;            // queries per block
 constexpr int AK = 32;            // keys per tile
-constexpr int KROW = QKV_HD + 8;  // padded K row in LDS (halves): 132 words, conflict-free
-constexpr int VROW = AK + 8;      // padded V^T row in LDS (halves): 20 words
-constexpr int PROW = AK + 8;
+constexpr int AQB = 32;           // queries per block (QS * 16 with QS <= 2; Tp % 32 == 0)
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
 
-template <int G>
-__global__ void __launch_bounds__(G * 64) attn_partial_kernel(
+// 16 bytes per lane, global (uniform base + lane byte offset) -> LDS (lane i -> lds_base + 16 i).
+__device__ __forceinline__ void attn_dma16(const void* base, int voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
+}
+
+template <int G, int QS>
+__global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
     const f16* __restrict__ q_hi, const f16* __restrict__ q_lo, const f16* __restrict__ kk,
     const f16* __restrict__ vt, float* __restrict__ part_o, float* __restrict__ part_ml, int T,
-    int Tp, int nq, int window, int kb_per_part) {
-  __shared__ __attribute__((aligned(16))) f16 Ks[AK][KROW];
-  __shared__ __attribute__((aligned(16))) f16 Vs[QKV_HD][VROW];
-  __shared__ __attribute__((aligned(16))) f16 Ph[G][AQ][PROW];
-  __shared__ __attribute__((aligned(16))) f16 Pl[G][AQ][PROW];
+    int Tp, int nq, int nkv, int window, int kb_per_part, int kparts) {
+  constexpr int NWV = G * QS;
+  constexpr int TILE_H = AK * QKV_HD;   // halves per K (or V^T) tile: 16 KB
+  __shared__ __attribute__((aligned(16))) f16 Ks[2][TILE_H];
+  __shared__ __attribute__((aligned(16))) f16 Vs[2][TILE_H];
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lq = lane >> 4;
-  const int q0 = blockIdx.x * AQ;
-  const int kp = blockIdx.y;
-  const int g = blockIdx.z;
-  const int h = g * G + w;
+  const int hh = w % G, qs = w / G;
+  // Blocks are dealt round-robin to the 8 XCDs (block id % 8).  Give each XCD
+  // a contiguous run of work items W = (group, partition, query block), so the
+  // K/V range one XCD streams (one partition, or the band of neighbouring
+  // query blocks) stays in its L2.
+  const int nqb = Tp / (16 * QS);
+  const int W = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+  if (W >= nkv * kparts * nqb) return;   // grid padding (whole block)
+  const int g = W / (kparts * nqb);
+  const int kp = (W / nqb) % kparts;
+  const int q0 = (W % nqb) * (16 * QS);
+  const int h = g * G + hh;
+  const int qw = q0 + 16 * qs;   // this wave's first query
   const bool banded = window > 0 && T > window;
 
   int kb_lo = 0, kb_hi = (T + AK - 1) / AK;
   if (banded) {
-    int lo_key = q0 - window, hi_key = q0 + AQ - 1 + window;
+    int lo_key = q0 - window, hi_key = q0 + 16 * QS - 1 + window;
     kb_lo = lo_key > 0 ? lo_key / AK : 0;
     kb_hi = (hi_key < T - 1 ? hi_key : T - 1) / AK + 1;
   }
   const int kb0 = kb_lo + kp * kb_per_part;
   const int kb1 = kb0 + kb_per_part < kb_hi ? kb0 + kb_per_part : kb_hi;
 
-  // Q fragments (A operand): row q0 + l16, dims 32s + 8 lq .. +7
+  const f16* kbase = kk + (int64_t)g * Tp * QKV_HD;
+  const f16* vbase = vt + (int64_t)g * QKV_HD * Tp;
+  // A tile is 16 K units (2 key rows each) + 16 V^T units (16 dim rows each),
+  // 1 KB per unit; wave w issues units w, w + NWV, ...  Per-lane byte offsets
+  // are fixed; the tile moves the (uniform) base.
+  constexpr int UPWA = (32 + NWV - 1) / NWV;
+  int uoff[UPWA];
+#pragma unroll
+  for (int j = 0; j < UPWA; j++) {
+    const int u = w + NWV * j;
+    if (u < 16) {
+      const int row = 2 * u + (lane >> 5), pc = lane & 31;
+      uoff[j] = (row * QKV_HD + ((pc ^ (row & 7)) << 3)) * 2;
+    } else {
+      const int row = 16 * (u - 16) + (lane >> 2), pc = lane & 3;
+      uoff[j] = (row * Tp + ((pc ^ ((row >> 1) & 3)) << 3)) * 2;
+    }
+  }
+  auto issue = [&](int kb, int sl) {
+    const int k0 = kb * AK;
+    const f16* kb_base = kbase + (int64_t)k0 * QKV_HD;
+    const f16* vb_base = vbase + k0;
+#pragma unroll
+    for (int j = 0; j < UPWA; j++) {
+      const int u = w + NWV * j;
+      if (u < 32) {
+        const f16* dst = u < 16 ? &Ks[sl][u * 512] : &Vs[sl][(u - 16) * 512];
+        attn_dma16(u < 16 ? kb_base : vb_base, uoff[j],
+                   __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst));
+      }
+    }
+  };
+  if (kb0 < kb1) issue(kb0, 0);
+
+  // Q fragments: query qw + l16, dims 32s + 8 lq .. +7 (the B operand of
+  // S^T = K Q^T)
   v8h qh[QKV_HD / 32], ql[QKV_HD / 32];
   {
-    const int64_t off = ((int64_t)h * Tp + q0 + l16) * QKV_HD + 8 * lq;
+    const int64_t off = ((int64_t)h * Tp + qw + l16) * QKV_HD + 8 * lq;
 #pragma unroll
     for (int s = 0; s < QKV_HD / 32; s++) {
       qh[s] = *reinterpret_cast<const v8h*>(q_hi + off + 32 * s);
       ql[s] = *reinterpret_cast<const v8h*>(q_lo + off + 32 * s);
     }
   }
-  float m_run[4], l_run[4];
-  v4f_ o[QKV_HD / 16];
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    m_run[r] = -INFINITY;
-    l_run[r] = 0.0f;
-  }
+  // Transposed formulation: S^T = K Q^T and O^T = V^T P^T, so a lane owns ONE
+  // query (qw + l16) in S, P and O: its running max / sum are scalars, the
+  // row reductions need two shuffles (lanes l16 + 16 lq'), and P^T goes from
+  // the S^T accumulator straight into the B operand (no LDS round trip).  The
+  // lane's 8 probabilities are keys 4 lq + r and 16 + 4 lq + r (r < 4); the
+  // V^T operand is read in that same key order.
+  const int qi = qw + l16;
+  float m_run = -INFINITY, l_run = 0.0f;
+  v4f_ o[QKV_HD / 16];   // O^T: dims 16 t + 4 lq + r of query qi
 #pragma unroll
   for (int t = 0; t < QKV_HD / 16; t++) o[t] = v4f_{0, 0, 0, 0};
 
-  // K tile: 32 rows x 512 B = 1024 chunks; V^T tile: 256 rows x 64 B = 1024 chunks.
-  constexpr int NCH = 2048;
-  constexpr int PER = (NCH + G * 64 - 1) / (G * 64);
-  const f16* kbase = kk + (int64_t)g * Tp * QKV_HD;
-  const f16* vbase = vt + (int64_t)g * QKV_HD * Tp;
-  v4i stage[PER];
-  auto load_tile = [&](int kb) {
-    const int k0 = kb * AK;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int c = tid + i * G * 64;
-      if (c < 1024) {
-        stage[i] = *reinterpret_cast<const v4i*>(kbase + (int64_t)(k0 + (c >> 5)) * QKV_HD +
-                                                 ((c & 31) << 3));
-      } else if (c < NCH) {
-        const int cc = c - 1024;
-        stage[i] = *reinterpret_cast<const v4i*>(vbase + (int64_t)(cc >> 2) * Tp + k0 +
-                                                 ((cc & 3) << 3));
-      }
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-      const int c = tid + i * G * 64;
-      if (c < 1024) {
-        *reinterpret_cast<v4i*>(&Ks[c >> 5][(c & 31) << 3]) = stage[i];
-      } else if (c < NCH) {
-        const int cc = c - 1024;
-        *reinterpret_cast<v4i*>(&Vs[cc >> 2][(cc & 3) << 3]) = stage[i];
-      }
-    }
-  };
-
-  if (kb0 < kb1) load_tile(kb0);
   for (int kb = kb0; kb < kb1; kb++) {
-    __syncthreads();  // previous tile fully consumed
-    store_tile();
-    __syncthreads();
-    if (kb + 1 < kb1) load_tile(kb + 1);
+    const int sl = (kb - kb0) & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kb has landed
+    __syncthreads();                                   // ... for every wave; slot sl^1 is free
+    if (kb + 1 < kb1) issue(kb + 1, sl ^ 1);
+    const f16* Kt = Ks[sl];
+    const f16* Vt = Vs[sl];
     const int k0 = kb * AK;
-    // ---- S = Q K^T: two 16-key tiles
+    // ---- S^T = K Q^T: two 16-key tiles; sacc[kt][r] = S[qi][k0 + 16 kt + 4 lq + r]
     v4f_ sacc[2] = {v4f_{0, 0, 0, 0}, v4f_{0, 0, 0, 0}};
 #pragma unroll
     for (int s = 0; s < QKV_HD / 32; s++) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
-        v8h kf = *reinterpret_cast<const v8h*>(&Ks[16 * kt + l16][32 * s + 8 * lq]);
-        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s], kf, sacc[kt], 0, 0, 0);
-        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s], kf, sacc[kt], 0, 0, 0);
+        const int row = 16 * kt + l16;
+        const v8h kf = *reinterpret_cast<const v8h*>(Kt + row * QKV_HD +
+                                                     (((4 * s + lq) ^ (row & 7)) << 3));
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sacc[kt], 0, 0, 0);
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sacc[kt], 0, 0, 0);
       }
     }
-    // ---- mask + online softmax; rows 4 lq + r, key = k0 + 16 kt + l16
-    float alpha[4];
+    // ---- mask (only where a key of the tile can be out of range or band)
+    const bool edge = k0 + AK > T ||
+                      (banded && (k0 < q0 + 16 * QS - 1 - window || k0 + AK - 1 > q0 + window));
+    if (edge) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int qi = q0 + 4 * lq + r;
-      float sv[2];
+      for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++) {
-        const int key = k0 + 16 * kt + l16;
-        bool ok = key < T;
-        if (banded) {
-          int d = qi - key;
-          ok = ok && d <= window && -d <= window;
+        for (int r = 0; r < 4; r++) {
+          const int key = k0 + 16 * kt + 4 * lq + r;
+          bool ok = key < T;
+          if (banded) {
+            const int d = qi - key;
+            ok = ok && d <= window && -d <= window;
+          }
+          if (!ok) sacc[kt][r] = -INFINITY;
         }
-        sv[kt] = ok ? sacc[kt][r] : -INFINITY;
-      }
-      float mx = fmaxf(sv[0], sv[1]);
-      mx = fmaxf(mx, __shfl_xor(mx, 1));
-      mx = fmaxf(mx, __shfl_xor(mx, 2));
-      mx = fmaxf(mx, __shfl_xor(mx, 4));
-      mx = fmaxf(mx, __shfl_xor(mx, 8));
-      const float m_new = fmaxf(m_run[r], mx);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      alpha[r] = __expf(m_run[r] - m_use);
-      const float p0 = __expf(sv[0] - m_use), p1 = __expf(sv[1] - m_use);
-      float ps = p0 + p1;
-      ps += __shfl_xor(ps, 1);
-      ps += __shfl_xor(ps, 2);
-      ps += __shfl_xor(ps, 4);
-      ps += __shfl_xor(ps, 8);
-      l_run[r] = l_run[r] * alpha[r] + ps;
-      m_run[r] = m_new;
-      split_f16(p0, Ph[w][4 * lq + r][l16], Pl[w][4 * lq + r][l16]);
-      split_f16(p1, Ph[w][4 * lq + r][16 + l16], Pl[w][4 * lq + r][16 + l16]);
     }
+    // ---- online softmax for query qi
+    float mx = fmaxf(fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3])),
+                     fmaxf(fmaxf(sacc[1][0], sacc[1][1]), fmaxf(sacc[1][2], sacc[1][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __expf(m_run - m_use);
+    float p[2][4];
+    float ps = 0.0f;
 #pragma unroll
-    for (int t = 0; t < QKV_HD / 16; t++)
+    for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) o[t][r] *= alpha[r];
-    // P was written by other lanes of this wave: LDS executes a wave's
-    // accesses in order, so a compiler fence suffices (no s_waitcnt, which
-    // would also wait for the next tile's prefetch).
-    __builtin_amdgcn_wave_barrier();
-    // ---- O += P V
-    const v8h ah = *reinterpret_cast<const v8h*>(&Ph[w][l16][8 * lq]);
-    const v8h al = *reinterpret_cast<const v8h*>(&Pl[w][l16][8 * lq]);
+      for (int r = 0; r < 4; r++) {
+        p[kt][r] = __expf(sacc[kt][r] - m_use);
+        ps += p[kt][r];
+      }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+    // the running max moves on few tiles once the sequence is under way
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int t = 0; t < QKV_HD / 16; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o[t][r] *= alpha;
+    }
+    // ---- P^T (split hi/lo) as the B operand; k-slots [kt 0: r 0..3, kt 1: r 0..3]
+    v8h ph, pl;
+#pragma unroll
+    for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        f16 hi, lo;
+        split_f16(p[kt][r], hi, lo);
+        ph[4 * kt + r] = hi;
+        pl[4 * kt + r] = lo;
+      }
+    // ---- O^T += V^T P^T: A = V^T[16 t + l16][keys 4 lq..+3, 16 + 4 lq..+3]
 #pragma unroll
     for (int t = 0; t < QKV_HD / 16; t++) {
-      v8h vf = *reinterpret_cast<const v8h*>(&Vs[16 * t + l16][8 * lq]);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, vf, o[t], 0, 0, 0);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, vf, o[t], 0, 0, 0);
+      const int row = 16 * t + l16;
+      const int sw = (row >> 1) & 3;
+      const f16* vr = Vt + row * AK;
+      typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+      const v4h va = *reinterpret_cast<const v4h*>(vr + ((((lq >> 1) ^ sw) << 3) | ((lq & 1) << 2)));
+      const v4h vb = *reinterpret_cast<const v4h*>(vr + (((2 + (lq >> 1)) ^ sw) << 3 | ((lq & 1) << 2)));
+      const v8h vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[t], 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[t], 0, 0, 0);
     }
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- partial results
-  const int64_t row0 = (int64_t)kp * Tp + q0 + 4 * lq;
+  // ---- partial results: query qi, dims 16 t + 4 lq .. +3
+  const int64_t prow = (int64_t)kp * Tp + qi;
 #pragma unroll
   for (int t = 0; t < QKV_HD / 16; t++)
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-      part_o[(row0 + r) * nq * QKV_HD + (int64_t)h * QKV_HD + 16 * t + l16] = o[t][r];
-  if (l16 == 0)
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      part_ml[((row0 + r) * nq + h) * 2] = m_run[r];
-      part_ml[((row0 + r) * nq + h) * 2 + 1] = l_run[r];
-    }
+    *reinterpret_cast<v4f_*>(part_o + prow * nq * QKV_HD + (int64_t)h * QKV_HD + 16 * t + 4 * lq) =
+        o[t];
+  if (lq == 0) {
+    part_ml[(prow * nq + h) * 2] = m_run;
+    part_ml[(prow * nq + h) * 2 + 1] = l_run;
+  }
 }
 
 // One wave per token: merge partitions per head; emit f32 ctx and/or Q8_0.
@@ -364,16 +403,20 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
   }
 }
 
+// Key tiles per partition: enough partitions for ~2 blocks per CU, at least
+// two tiles each, and at most 64 tiles (2 MB of K and V) so one partition's
+// K/V stays in an XCD's L2.
 static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, int* kparts) {
   const int64_t tp = (T + AK - 1) / AK * AK;
-  const int64_t nqb = tp / AQ;
+  const int64_t nqb = tp / AQB;
   int64_t nkb = (T + AK - 1) / AK;
   if (window > 0 && T > window) {
-    int64_t band = (2 * window + AQ + AK - 1) / AK + 1;
+    int64_t band = (2 * window + AQB + AK - 1) / AK + 1;
     if (band < nkb) nkb = band;
   }
-  int64_t want = (640 + nqb * nkv - 1) / (nqb * nkv);  // ~2.5 blocks per CU
-  if (want > (nkb + 1) / 2) want = (nkb + 1) / 2;      // >= 2 key tiles per partition
+  int64_t want = (512 + nqb * nkv - 1) / (nqb * nkv);
+  if (want > (nkb + 1) / 2) want = (nkb + 1) / 2;
+  if (want < (nkb + 63) / 64) want = (nkb + 63) / 64;
   if (want < 1) want = 1;
   const int64_t per = (nkb + want - 1) / want;
   *kparts = (int)((nkb + per - 1) / per);
@@ -391,37 +434,33 @@ hipError_t launch_attention(const uint16_t* q_hi, const uint16_t* q_lo, const ui
                             const uint16_t* vt16, float* scratch, float* ctx, int8_t* cq,
                             float* dc, int64_t T, int64_t Tp, int64_t nq, int64_t nkv, int64_t hd,
                             int64_t window, hipStream_t s) {
-  if (hd != QKV_HD || Tp % AK != 0 || nq % nkv != 0) return hipErrorInvalidValue;
+  if (hd != QKV_HD || Tp % AQB != 0 || nq % nkv != 0) return hipErrorInvalidValue;
   const int64_t G = nq / nkv;
   int kparts;
   const int per = attn_kb_per_part(T, nq, nkv, window, &kparts);
   float* part_o = scratch;
   float* part_ml = scratch + (int64_t)kparts * Tp * nq * QKV_HD;
-  dim3 grid((unsigned)(Tp / AQ), (unsigned)kparts, (unsigned)nkv);
+  const int64_t items = nkv * kparts * (Tp / AQB);
+  const unsigned grid = (unsigned)((items + 7) / 8 * 8);
   const f16* a = reinterpret_cast<const f16*>(q_hi);
   const f16* b = reinterpret_cast<const f16*>(q_lo);
   const f16* c = reinterpret_cast<const f16*>(k16);
   const f16* d = reinterpret_cast<const f16*>(vt16);
+#define GLYPR_ATTN_CASE(GG)                                                                   \
+  case GG:                                                                                    \
+    attn_partial_kernel<GG, 2><<<grid, GG * 2 * 64, 0, s>>>(a, b, c, d, part_o, part_ml, (int)T, \
+                                                           (int)Tp, (int)nq, (int)nkv,          \
+                                                           (int)window, per, kparts);           \
+    break;
   switch (G) {
-    case 1:
-      attn_partial_kernel<1><<<grid, 64, 0, s>>>(a, b, c, d, part_o, part_ml, (int)T, (int)Tp,
-                                                 (int)nq, (int)window, per);
-      break;
-    case 2:
-      attn_partial_kernel<2><<<grid, 128, 0, s>>>(a, b, c, d, part_o, part_ml, (int)T, (int)Tp,
-                                                  (int)nq, (int)window, per);
-      break;
-    case 3:
-      attn_partial_kernel<3><<<grid, 192, 0, s>>>(a, b, c, d, part_o, part_ml, (int)T, (int)Tp,
-                                                  (int)nq, (int)window, per);
-      break;
-    case 4:
-      attn_partial_kernel<4><<<grid, 256, 0, s>>>(a, b, c, d, part_o, part_ml, (int)T, (int)Tp,
-                                                  (int)nq, (int)window, per);
-      break;
+    GLYPR_ATTN_CASE(1)
+    GLYPR_ATTN_CASE(2)
+    GLYPR_ATTN_CASE(3)
+    GLYPR_ATTN_CASE(4)
     default:
       return hipErrorInvalidValue;
   }
+#undef GLYPR_ATTN_CASE
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   attn_combine_kernel<<<(unsigned)((T + 3) / 4), 256, 0, s>>>(part_o, part_ml, (int)T, (int)Tp,
