@@ -139,7 +139,7 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 //   (16 dim tiles x {p_hi, p_lo}).  Each partition writes its running max m,
 //   sum l and unnormalised O for its queries.
 // LDS layouts (16-byte chunks, conflict-free fragment reads):
-//   K slot  [32 keys][256 dims]: chunk c of key row r at c ^ (r & 7);
+//   K slot  [32 keys][256 dims]: chunk c of key row r at c ^ kswz(r);
 //   V^T slot [256 dims][32 keys]: chunk c of dim row r at c ^ ((r >> 1) & 3).
 // attn_combine: one wave per token merges the partitions per head,
 //   ctx = sum_p e^{m_p - M} O_p / sum_p e^{m_p - M} l_p, and writes ctx as f32
@@ -151,6 +151,11 @@ constexpr int AK = 32;            // keys per tile
 constexpr int AQB = 32;           // queries per block (QS * 16 with QS <= 2; Tp % 32 == 0)
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
+
+// K tile swizzle: 16-byte chunk c of key row r sits at chunk c ^ kswz(r).  The
+// S^T tiles read rows 8 (l16 / 4) + 4 kt + l16 % 4, and kswz maps any 8
+// consecutive lanes of those rows to 8 distinct chunk positions.
+__device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 4); }
 
 // 16 bytes per lane, global (uniform base + lane byte offset) -> LDS (lane i -> lds_base + 16 i).
 __device__ __forceinline__ void attn_dma16(const void* base, int voff, uint32_t lds_base) {
@@ -207,7 +212,7 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
     const int u = w + NWV * j;
     if (u < 16) {
       const int row = 2 * u + (lane >> 5), pc = lane & 31;
-      uoff[j] = (row * QKV_HD + ((pc ^ (row & 7)) << 3)) * 2;
+      uoff[j] = (row * QKV_HD + ((pc ^ kswz(row)) << 3)) * 2;
     } else {
       const int row = 16 * (u - 16) + (lane >> 2), pc = lane & 3;
       uoff[j] = (row * Tp + ((pc ^ ((row >> 1) & 3)) << 3)) * 2;
@@ -243,9 +248,10 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
   // Transposed formulation: S^T = K Q^T and O^T = V^T P^T, so a lane owns ONE
   // query (qw + l16) in S, P and O: its running max / sum are scalars, the
   // row reductions need two shuffles (lanes l16 + 16 lq'), and P^T goes from
-  // the S^T accumulator straight into the B operand (no LDS round trip).  The
-  // lane's 8 probabilities are keys 4 lq + r and 16 + 4 lq + r (r < 4); the
-  // V^T operand is read in that same key order.
+  // the S^T accumulator straight into the B operand (no LDS round trip).  Row
+  // m of S^T tile kt is key 8 (m / 4) + 4 kt + m % 4, so the lane's 8
+  // probabilities (tile kt, r) are keys 8 lq + 4 kt + r: one contiguous
+  // 16-byte chunk of a V^T row is the matching A operand.
   const int qi = qw + l16;
   float m_run = -INFINITY, l_run = 0.0f;
   v4f_ o[QKV_HD / 16];   // O^T: dims 16 t + 4 lq + r of query qi
@@ -260,15 +266,15 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
     const f16* Kt = Ks[sl];
     const f16* Vt = Vs[sl];
     const int k0 = kb * AK;
-    // ---- S^T = K Q^T: two 16-key tiles; sacc[kt][r] = S[qi][k0 + 16 kt + 4 lq + r]
+    // ---- S^T = K Q^T: two 16-key tiles; sacc[kt][r] = S[qi][k0 + 8 lq + 4 kt + r]
     v4f_ sacc[2] = {v4f_{0, 0, 0, 0}, v4f_{0, 0, 0, 0}};
 #pragma unroll
     for (int s = 0; s < QKV_HD / 32; s++) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
-        const int row = 16 * kt + l16;
+        const int row = 8 * (l16 >> 2) + 4 * kt + (l16 & 3);
         const v8h kf = *reinterpret_cast<const v8h*>(Kt + row * QKV_HD +
-                                                     (((4 * s + lq) ^ (row & 7)) << 3));
+                                                     (((4 * s + lq) ^ kswz(row)) << 3));
         sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sacc[kt], 0, 0, 0);
         sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sacc[kt], 0, 0, 0);
       }
@@ -281,7 +287,7 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
       for (int kt = 0; kt < 2; kt++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const int key = k0 + 16 * kt + 4 * lq + r;
+          const int key = k0 + 8 * lq + 4 * kt + r;
           bool ok = key < T;
           if (banded) {
             const int d = qi - key;
@@ -318,7 +324,7 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
 #pragma unroll
         for (int r = 0; r < 4; r++) o[t][r] *= alpha;
     }
-    // ---- P^T (split hi/lo) as the B operand; k-slots [kt 0: r 0..3, kt 1: r 0..3]
+    // ---- P^T (split hi/lo) as the B operand; k-slot 4 kt + r = key 8 lq + 4 kt + r
     v8h ph, pl;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
@@ -329,16 +335,11 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
         ph[4 * kt + r] = hi;
         pl[4 * kt + r] = lo;
       }
-    // ---- O^T += V^T P^T: A = V^T[16 t + l16][keys 4 lq..+3, 16 + 4 lq..+3]
+    // ---- O^T += V^T P^T: A = V^T[16 t + l16][keys 8 lq .. +7]
 #pragma unroll
     for (int t = 0; t < QKV_HD / 16; t++) {
       const int row = 16 * t + l16;
-      const int sw = (row >> 1) & 3;
-      const f16* vr = Vt + row * AK;
-      typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-      const v4h va = *reinterpret_cast<const v4h*>(vr + ((((lq >> 1) ^ sw) << 3) | ((lq & 1) << 2)));
-      const v4h vb = *reinterpret_cast<const v4h*>(vr + (((2 + (lq >> 1)) ^ sw) << 3 | ((lq & 1) << 2)));
-      const v8h vf = __builtin_shufflevector(va, vb, 0, 1, 2, 3, 4, 5, 6, 7);
+      const v8h vf = *reinterpret_cast<const v8h*>(Vt + row * AK + ((lq ^ ((row >> 1) & 3)) << 3));
       o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[t], 0, 0, 0);
       o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[t], 0, 0, 0);
     }
