@@ -130,17 +130,17 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 // attn_partial: block = (32-query block, key partition, kv group) with
 //   QS x G waves: wave (qs, hh) owns queries q0 + 16 qs .. +15 of q head
 //   g G + hh, so every K/V tile staged in LDS serves 16 QS queries of all G
-//   heads of the group (GQA).  K/V tiles (32 keys) stream through a two-slot
+//   heads of the group (GQA).  K/V tiles (32 keys) stream through a three-slot
 //   LDS ring filled by LDS DMA (global_load_lds_dwordx4 from inline asm, so
-//   the compiler adds no vmcnt waits of its own): tile kb+1 is in flight while
-//   tile kb is consumed.  Per tile: S = Q K^T with v_mfma_f32_16x16x32_f16
+//   the compiler adds no vmcnt waits of its own): tiles kb+1 and kb+2 are in
+//   flight while tile kb is consumed.  Per tile: S = Q K^T with v_mfma_f32_16x16x32_f16
 //   (8 k-steps x 2 key tiles x {q_hi, q_lo}), band/length mask, online softmax
 //   in f32, P (split hi/lo) through LDS into the A-operand layout, O += P V
 //   (16 dim tiles x {p_hi, p_lo}).  Each partition writes its running max m,
 //   sum l and unnormalised O for its queries.
 // LDS layouts (16-byte chunks, conflict-free fragment reads):
 //   K slot  [32 keys][256 dims]: chunk c of key row r at c ^ kswz(r);
-//   V^T slot [256 dims][32 keys]: chunk c of dim row r at c ^ ((r >> 1) & 3).
+//   V^T slot [256 dims][32 keys]: chunk c of dim row r at c ^ vswz(r).
 // attn_combine: one wave per token merges the partitions per head,
 //   ctx = sum_p e^{m_p - M} O_p / sum_p e^{m_p - M} l_p, and writes ctx as f32
 //   and/or directly as the o projection's Q8_0 operand (BlockQ8_0::from_float).
@@ -152,10 +152,13 @@ constexpr int AQB = 32;           // queries per block (QS * 16 with QS <= 2; Tp
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
 
-// K tile swizzle: 16-byte chunk c of key row r sits at chunk c ^ kswz(r).  The
-// S^T tiles read rows 8 (l16 / 4) + 4 kt + l16 % 4, and kswz maps any 8
-// consecutive lanes of those rows to 8 distinct chunk positions.
-__device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 4); }
+// LDS swizzles (16-byte chunk c of row r is stored at chunk c ^ swz(r)); both
+// keep any 8 consecutive lanes of a fragment read on distinct 16-byte bank
+// groups of a 128-byte line and any 16 on distinct groups of 256 bytes.
+// K rows are 512 B; the S^T tiles read rows 8 (l16 / 4) + 4 kt + l16 % 4.
+__device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
+// V^T rows are 64 B (4 chunks); the O^T tiles read rows 16 t + l16.
+__device__ __forceinline__ int vswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 // 16 bytes per lane, global (uniform base + lane byte offset) -> LDS (lane i -> lds_base + 16 i).
 __device__ __forceinline__ void attn_dma16(const void* base, int voff, uint32_t lds_base) {
@@ -170,8 +173,9 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
     int Tp, int nq, int nkv, int window, int kb_per_part, int kparts) {
   constexpr int NWV = G * QS;
   constexpr int TILE_H = AK * QKV_HD;   // halves per K (or V^T) tile: 16 KB
-  __shared__ __attribute__((aligned(16))) f16 Ks[2][TILE_H];
-  __shared__ __attribute__((aligned(16))) f16 Vs[2][TILE_H];
+  constexpr int RING = 3;
+  __shared__ __attribute__((aligned(16))) f16 Ks[RING][TILE_H];
+  __shared__ __attribute__((aligned(16))) f16 Vs[RING][TILE_H];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -215,7 +219,7 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
       uoff[j] = (row * QKV_HD + ((pc ^ kswz(row)) << 3)) * 2;
     } else {
       const int row = 16 * (u - 16) + (lane >> 2), pc = lane & 3;
-      uoff[j] = (row * Tp + ((pc ^ ((row >> 1) & 3)) << 3)) * 2;
+      uoff[j] = (row * Tp + ((pc ^ vswz(row)) << 3)) * 2;
     }
   }
   auto issue = [&](int kb, int sl) {
@@ -232,7 +236,6 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
       }
     }
   };
-  if (kb0 < kb1) issue(kb0, 0);
 
   // Q fragments: query qw + l16, dims 32s + 8 lq .. +7 (the B operand of
   // S^T = K Q^T)
@@ -245,6 +248,9 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
       ql[s] = *reinterpret_cast<const v8h*>(q_lo + off + 32 * s);
     }
   }
+  if (kb0 < kb1) issue(kb0, 0);
+  if (kb0 + 1 < kb1) issue(kb0 + 1, 1);
+
   // Transposed formulation: S^T = K Q^T and O^T = V^T P^T, so a lane owns ONE
   // query (qw + l16) in S, P and O: its running max / sum are scalars, the
   // row reductions need two shuffles (lanes l16 + 16 lq'), and P^T goes from
@@ -258,16 +264,11 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
 #pragma unroll
   for (int t = 0; t < QKV_HD / 16; t++) o[t] = v4f_{0, 0, 0, 0};
 
-  for (int kb = kb0; kb < kb1; kb++) {
-    const int sl = (kb - kb0) & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kb has landed
-    __syncthreads();                                   // ... for every wave; slot sl^1 is free
-    if (kb + 1 < kb1) issue(kb + 1, sl ^ 1);
+  // S^T of tile kb (needs its K slot): sacc[kt][r] = S[qi][k0 + 8 lq + 4 kt + r]
+  auto scores = [&](int sl, v4f_ (&sacc)[2]) {
     const f16* Kt = Ks[sl];
-    const f16* Vt = Vs[sl];
-    const int k0 = kb * AK;
-    // ---- S^T = K Q^T: two 16-key tiles; sacc[kt][r] = S[qi][k0 + 8 lq + 4 kt + r]
-    v4f_ sacc[2] = {v4f_{0, 0, 0, 0}, v4f_{0, 0, 0, 0}};
+    sacc[0] = v4f_{0, 0, 0, 0};
+    sacc[1] = v4f_{0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < QKV_HD / 32; s++) {
 #pragma unroll
@@ -279,6 +280,35 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
         sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sacc[kt], 0, 0, 0);
       }
     }
+  };
+
+  // Software pipeline over key tiles (ring of three slots, slot = (kb - kb0) % 3):
+  // iteration kb computes S^T of tile kb+1 on the MFMA pipe while the VALU
+  // runs the softmax of tile kb, then O^T += V^T P^T for tile kb.  Tile kb+2
+  // is in flight meanwhile.
+  const int my_units = (32 - w + NWV - 1) / NWV;   // this wave's DMAs per tile
+  v4f_ sacc[2];
+  if (kb0 < kb1) {
+    if (kb0 + 1 >= kb1)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (my_units == (32 + NWV - 1) / NWV)
+      asm volatile("s_waitcnt vmcnt(%0)" :: "n"((32 + NWV - 1) / NWV) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(%0)" :: "n"(32 / NWV) : "memory");
+    __syncthreads();
+    scores(0, sacc);
+  }
+  for (int kb = kb0, sl = 0; kb < kb1; kb++, sl = sl == RING - 1 ? 0 : sl + 1) {
+    const int sl1 = sl == RING - 1 ? 0 : sl + 1;
+    v4f_ snext[2];
+    if (kb + 1 < kb1) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kb+1 has landed
+      __syncthreads();   // ... for every wave; tile kb-1's slot is free
+      if (kb + 2 < kb1) issue(kb + 2, sl == 0 ? RING - 1 : sl - 1);
+      scores(sl1, snext);
+    }
+    const f16* Vt = Vs[sl];
+    const int k0 = kb * AK;
     // ---- mask (only where a key of the tile can be out of range or band)
     const bool edge = k0 + AK > T ||
                       (banded && (k0 < q0 + 16 * QS - 1 - window || k0 + AK - 1 > q0 + window));
@@ -339,10 +369,12 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
 #pragma unroll
     for (int t = 0; t < QKV_HD / 16; t++) {
       const int row = 16 * t + l16;
-      const v8h vf = *reinterpret_cast<const v8h*>(Vt + row * AK + ((lq ^ ((row >> 1) & 3)) << 3));
+      const v8h vf = *reinterpret_cast<const v8h*>(Vt + row * AK + ((lq ^ vswz(row)) << 3));
       o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[t], 0, 0, 0);
       o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[t], 0, 0, 0);
     }
+    sacc[0] = snext[0];
+    sacc[1] = snext[1];
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
