@@ -89,17 +89,20 @@ hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, c
                                 hipStream_t s);
 
 // ---- k_attn.hip ----
-// q split hi/lo [nq][Tp][hd]; k f16 [nkv][Tp][hd]; vt f16 [nkv][hd][Tp].  hd == 256.
+// Attention operands are padded to Tp = attn_padded_len(T) tokens.
+constexpr int64_t ATTN_TP_ALIGN = 64;
+inline int64_t attn_padded_len(int64_t t) { return (t + ATTN_TP_ALIGN - 1) / ATTN_TP_ALIGN * ATTN_TP_ALIGN; }
+// q16 [nq][Tp][hd], k16 [nkv][Tp][hd], vt16 [nkv][hd][Tp] (f16).  hd == 256.
 hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
                            int64_t hd, const float* qnw, const float* knw, float eps,
-                           const float* cos_t, const float* sin_t, uint16_t* q_hi, uint16_t* q_lo,
-                           uint16_t* k16, uint16_t* vt16, hipStream_t s);
+                           const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
+                           uint16_t* vt16, hipStream_t s);
 size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t window);
 // ctx (f32 [T][nq*hd]) and/or (cq, dc) (Q8_0 planar) may be null.
-hipError_t launch_attention(const uint16_t* q_hi, const uint16_t* q_lo, const uint16_t* k16,
-                            const uint16_t* vt16, float* scratch, float* ctx, int8_t* cq,
-                            float* dc, int64_t T, int64_t Tp, int64_t nq, int64_t nkv, int64_t hd,
-                            int64_t window, hipStream_t s);
+hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
+                            float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
+                            int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
+                            hipStream_t s);
 
 // ---- k_gemm_i8.hip ----
 // y[m,n] = sum_b ((float)S_b * dw[n,b]) * dx[m,b], sequential over b (exact).

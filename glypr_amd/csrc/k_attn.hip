@@ -10,10 +10,11 @@
 // repeat_kv -> StandardAttention / ChunkedSlidingAttention (softmax in f32 of
 // q k^T + mask, no 1/sqrt(d) scale) -> context @ o_proj.
 //
-// Precision: f16 MFMA with f32 accumulation.  Q and the probabilities P are
-// split as x = hi + lo (hi = f16(x), lo = f16(x - hi)) and multiplied as
-// hi*y + lo*y, so only K and V carry an f16 rounding (2^-11 relative); the
-// context matches an f32 computation to ~1e-5 relative.
+// Precision: Q, K, V and the probabilities P enter f16 MFMAs (2^-11 relative
+// rounding each) with f32 accumulation; max, exp, sums and the final
+// normalisation are f32.  The K and V roundings dominate: carrying Q and P in
+// two f16 parts as well would cut the context error by only ~20 % at twice the
+// MFMA work.
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -23,10 +24,6 @@ namespace {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 f16;
 
-__device__ __forceinline__ void split_f16(float x, f16& hi, f16& lo) {
-  hi = (f16)x;
-  lo = (f16)(x - (float)hi);
-}
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -37,14 +34,14 @@ __device__ __forceinline__ void split_f16(float x, f16& hi, f16& lo) {
 // path; RoPE is x*cos + rot*sin with both products rounded (no FMA), rot =
 // -x[i+128] for i < 128 and x[i-128] otherwise: lane l's partner is l ^ 32.
 // Outputs (token rows padded to Tp, padding zero-filled):
-//   q_hi/q_lo [nq][Tp][hd] (split), k [nkv][Tp][hd], vt [nkv][hd][Tp] (f16).
+//   q [nq][Tp][hd], k [nkv][Tp][hd], vt [nkv][hd][Tp] (f16).
 // ---------------------------------------------------------------------------
 constexpr int QKV_HD = 256;
 
 __global__ void __launch_bounds__(256) qkv_post_kernel(
     const float* __restrict__ qkv, int T, int Tp, int nq, int nkv, const float* __restrict__ qnw,
     const float* __restrict__ knw, float eps, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, f16* __restrict__ q_hi, f16* __restrict__ q_lo,
+    const float* __restrict__ sin_t, f16* __restrict__ q16,
     f16* __restrict__ k16, f16* __restrict__ vt16) {
   __shared__ float lrows[4][QKV_HD];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -101,7 +98,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
   if (kind == 0) {
     const int64_t off = ((int64_t)head * Tp + t) * QKV_HD + 4 * lane;
 #pragma unroll
-    for (int e = 0; e < 4; e++) split_f16(y[e], q_hi[off + e], q_lo[off + e]);
+    for (int e = 0; e < 4; e++) q16[off + e] = (f16)y[e];
   } else if (kind == 1) {
     const int64_t off = ((int64_t)head * Tp + t) * QKV_HD + 4 * lane;
 #pragma unroll
@@ -114,30 +111,35 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
 
 hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
                            int64_t hd, const float* qnw, const float* knw, float eps,
-                           const float* cos_t, const float* sin_t, uint16_t* q_hi, uint16_t* q_lo,
-                           uint16_t* k16, uint16_t* vt16, hipStream_t s) {
+                           const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
+                           uint16_t* vt16, hipStream_t s) {
   if (hd != QKV_HD) return hipErrorInvalidValue;
   const int64_t tasks = Tp * (nq + 2 * nkv);
   qkv_post_kernel<<<(unsigned)((tasks + 3) / 4), 256, 0, s>>>(
       qkv, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
-      reinterpret_cast<f16*>(q_hi), reinterpret_cast<f16*>(q_lo), reinterpret_cast<f16*>(k16),
+      reinterpret_cast<f16*>(q16), reinterpret_cast<f16*>(k16),
       reinterpret_cast<f16*>(vt16));
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
 // Flash attention, split over keys.
-// attn_partial: block = (32-query block, key partition, kv group) with
-//   QS x G waves: wave (qs, hh) owns queries q0 + 16 qs .. +15 of q head
-//   g G + hh, so every K/V tile staged in LDS serves 16 QS queries of all G
-//   heads of the group (GQA).  K/V tiles (32 keys) stream through a three-slot
-//   LDS ring filled by LDS DMA (global_load_lds_dwordx4 from inline asm, so
-//   the compiler adds no vmcnt waits of its own): tiles kb+1 and kb+2 are in
-//   flight while tile kb is consumed.  Per tile: S = Q K^T with v_mfma_f32_16x16x32_f16
-//   (8 k-steps x 2 key tiles x {q_hi, q_lo}), band/length mask, online softmax
-//   in f32, P (split hi/lo) through LDS into the A-operand layout, O += P V
-//   (16 dim tiles x {p_hi, p_lo}).  Each partition writes its running max m,
-//   sum l and unnormalised O for its queries.
+// attn_partial: block = (64-query block, key partition, kv group) with
+//   4 x G waves: wave (qs, hh) owns queries q0 + 16 qs .. +15 of q head
+//   g G + hh, so every K/V tile staged in LDS serves 64 queries of all G heads
+//   of the group (GQA).  K/V tiles (32 keys) stream through a three-slot LDS
+//   ring filled by LDS DMA (global_load_lds_dwordx4 from inline asm, so the
+//   compiler adds no vmcnt waits of its own).
+//   Transposed formulation: S^T = K Q^T and O^T = V^T P^T with
+//   v_mfma_f32_16x16x32_f16, so a lane owns ONE query (q0 + 16 qs + l16) in S,
+//   P and O: its running max and sum are scalars, the key reductions need two
+//   shuffles (lanes l16 + 16 lq'), and P^T goes from the S^T accumulator
+//   straight into the B operand of the PV product.  Row m of S^T tile kt is
+//   key 8 (m / 4) + 4 kt + m % 4, so the lane's 8 probabilities (tile kt, r)
+//   are keys 8 lq + 4 kt + r: one contiguous 16-byte chunk of a V^T row is the
+//   matching A operand.  The S^T of tile kb+1 is issued before the softmax of
+//   tile kb so the MFMA pipe and the VALU overlap.  Each partition writes its
+//   running max m, sum l and unnormalised O for its queries.
 // LDS layouts (16-byte chunks, conflict-free fragment reads):
 //   K slot  [32 keys][256 dims]: chunk c of key row r at c ^ kswz(r);
 //   V^T slot [256 dims][32 keys]: chunk c of dim row r at c ^ vswz(r).
@@ -148,7 +150,9 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 // B (32 x 16): column l%16, same k; D (16 x 16): column l%16, rows 4(l/16)+r.
 // ---------------------------------------------------------------------------
 constexpr int AK = 32;            // keys per tile
-constexpr int AQB = 32;           // queries per block (QS * 16 with QS <= 2; Tp % 32 == 0)
+constexpr int AQS = 4;            // 16-query wave rows per block
+constexpr int AQB = 16 * AQS;     // queries per block (== ATTN_TP_ALIGN)
+static_assert(AQB == ATTN_TP_ALIGN, "query blocks must tile the padded length");
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
 
@@ -166,14 +170,14 @@ __device__ __forceinline__ void attn_dma16(const void* base, int voff, uint32_t 
                :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
 }
 
-template <int G, int QS>
-__global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
-    const f16* __restrict__ q_hi, const f16* __restrict__ q_lo, const f16* __restrict__ kk,
-    const f16* __restrict__ vt, float* __restrict__ part_o, float* __restrict__ part_ml, int T,
-    int Tp, int nq, int nkv, int window, int kb_per_part, int kparts) {
-  constexpr int NWV = G * QS;
-  constexpr int TILE_H = AK * QKV_HD;   // halves per K (or V^T) tile: 16 KB
+template <int G>
+__global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
+    const f16* __restrict__ q16, const f16* __restrict__ kk, const f16* __restrict__ vt,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int T, int Tp, int nq, int nkv,
+    int window, int kb_per_part, int kparts) {
+  constexpr int NWV = G * AQS;
   constexpr int RING = 3;
+  constexpr int TILE_H = AK * QKV_HD;   // halves per K (or V^T) tile: 16 KB
   __shared__ __attribute__((aligned(16))) f16 Ks[RING][TILE_H];
   __shared__ __attribute__((aligned(16))) f16 Vs[RING][TILE_H];
 
@@ -185,24 +189,33 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
   // a contiguous run of work items W = (group, partition, query block), so the
   // K/V range one XCD streams (one partition, or the band of neighbouring
   // query blocks) stays in its L2.
-  const int nqb = Tp / (16 * QS);
+  const int nqb = Tp / AQB;
   const int W = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
   if (W >= nkv * kparts * nqb) return;   // grid padding (whole block)
   const int g = W / (kparts * nqb);
   const int kp = (W / nqb) % kparts;
-  const int q0 = (W % nqb) * (16 * QS);
+  const int q0 = (W % nqb) * AQB;
   const int h = g * G + hh;
   const int qw = q0 + 16 * qs;   // this wave's first query
+  const int qi = qw + l16;       // this lane's query
   const bool banded = window > 0 && T > window;
 
   int kb_lo = 0, kb_hi = (T + AK - 1) / AK;
   if (banded) {
-    int lo_key = q0 - window, hi_key = q0 + 16 * QS - 1 + window;
+    int lo_key = q0 - window, hi_key = q0 + AQB - 1 + window;
     kb_lo = lo_key > 0 ? lo_key / AK : 0;
     kb_hi = (hi_key < T - 1 ? hi_key : T - 1) / AK + 1;
   }
   const int kb0 = kb_lo + kp * kb_per_part;
   const int kb1 = kb0 + kb_per_part < kb_hi ? kb0 + kb_per_part : kb_hi;
+
+  // Q fragments (B operand of S^T = K Q^T): query qi, dims 32 s + 8 lq .. +7
+  v8h qf[QKV_HD / 32];
+  {
+    const int64_t off = ((int64_t)h * Tp + qi) * QKV_HD + 8 * lq;
+#pragma unroll
+    for (int s = 0; s < QKV_HD / 32; s++) qf[s] = *reinterpret_cast<const v8h*>(q16 + off + 32 * s);
+  }
 
   const f16* kbase = kk + (int64_t)g * Tp * QKV_HD;
   const f16* vbase = vt + (int64_t)g * QKV_HD * Tp;
@@ -236,35 +249,15 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
       }
     }
   };
-
-  // Q fragments: query qw + l16, dims 32s + 8 lq .. +7 (the B operand of
-  // S^T = K Q^T)
-  v8h qh[QKV_HD / 32], ql[QKV_HD / 32];
-  {
-    const int64_t off = ((int64_t)h * Tp + qw + l16) * QKV_HD + 8 * lq;
-#pragma unroll
-    for (int s = 0; s < QKV_HD / 32; s++) {
-      qh[s] = *reinterpret_cast<const v8h*>(q_hi + off + 32 * s);
-      ql[s] = *reinterpret_cast<const v8h*>(q_lo + off + 32 * s);
-    }
-  }
   if (kb0 < kb1) issue(kb0, 0);
   if (kb0 + 1 < kb1) issue(kb0 + 1, 1);
 
-  // Transposed formulation: S^T = K Q^T and O^T = V^T P^T, so a lane owns ONE
-  // query (qw + l16) in S, P and O: its running max / sum are scalars, the
-  // row reductions need two shuffles (lanes l16 + 16 lq'), and P^T goes from
-  // the S^T accumulator straight into the B operand (no LDS round trip).  Row
-  // m of S^T tile kt is key 8 (m / 4) + 4 kt + m % 4, so the lane's 8
-  // probabilities (tile kt, r) are keys 8 lq + 4 kt + r: one contiguous
-  // 16-byte chunk of a V^T row is the matching A operand.
-  const int qi = qw + l16;
   float m_run = -INFINITY, l_run = 0.0f;
   v4f_ o[QKV_HD / 16];   // O^T: dims 16 t + 4 lq + r of query qi
 #pragma unroll
   for (int t = 0; t < QKV_HD / 16; t++) o[t] = v4f_{0, 0, 0, 0};
 
-  // S^T of tile kb (needs its K slot): sacc[kt][r] = S[qi][k0 + 8 lq + 4 kt + r]
+  // S^T of the tile in slot sl: sacc[kt][r] = S[qi][k0 + 8 lq + 4 kt + r]
   auto scores = [&](int sl, v4f_ (&sacc)[2]) {
     const f16* Kt = Ks[sl];
     sacc[0] = v4f_{0, 0, 0, 0};
@@ -276,16 +269,14 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
         const int row = 8 * (l16 >> 2) + 4 * kt + (l16 & 3);
         const v8h kf = *reinterpret_cast<const v8h*>(Kt + row * QKV_HD +
                                                      (((4 * s + lq) ^ kswz(row)) << 3));
-        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], sacc[kt], 0, 0, 0);
-        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], sacc[kt], 0, 0, 0);
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sacc[kt], 0, 0, 0);
       }
     }
   };
 
-  // Software pipeline over key tiles (ring of three slots, slot = (kb - kb0) % 3):
-  // iteration kb computes S^T of tile kb+1 on the MFMA pipe while the VALU
-  // runs the softmax of tile kb, then O^T += V^T P^T for tile kb.  Tile kb+2
-  // is in flight meanwhile.
+  // Software pipeline over key tiles, slot = (kb - kb0) % 3: iteration kb
+  // issues S^T of tile kb+1, runs the softmax of tile kb, then O^T += V^T P^T
+  // for tile kb; tile kb+2 is in flight meanwhile.
   const int my_units = (32 - w + NWV - 1) / NWV;   // this wave's DMAs per tile
   v4f_ sacc[2];
   if (kb0 < kb1) {
@@ -311,7 +302,7 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
     const int k0 = kb * AK;
     // ---- mask (only where a key of the tile can be out of range or band)
     const bool edge = k0 + AK > T ||
-                      (banded && (k0 < q0 + 16 * QS - 1 - window || k0 + AK - 1 > q0 + window));
+                      (banded && (k0 < q0 + AQB - 1 - window || k0 + AK - 1 > q0 + window));
     if (edge) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++)
@@ -334,14 +325,15 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = __expf(m_run - m_use);
-    float p[2][4];
+    v8h pf;   // P^T B operand: k-slot 4 kt + r = key 8 lq + 4 kt + r
     float ps = 0.0f;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        p[kt][r] = __expf(sacc[kt][r] - m_use);
-        ps += p[kt][r];
+        const float pv = __expf(sacc[kt][r] - m_use);
+        ps += pv;
+        pf[4 * kt + r] = (f16)pv;
       }
     ps += __shfl_xor(ps, 16);
     ps += __shfl_xor(ps, 32);
@@ -354,24 +346,12 @@ __global__ void __launch_bounds__(G * QS * 64) attn_partial_kernel(
 #pragma unroll
         for (int r = 0; r < 4; r++) o[t][r] *= alpha;
     }
-    // ---- P^T (split hi/lo) as the B operand; k-slot 4 kt + r = key 8 lq + 4 kt + r
-    v8h ph, pl;
-#pragma unroll
-    for (int kt = 0; kt < 2; kt++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        f16 hi, lo;
-        split_f16(p[kt][r], hi, lo);
-        ph[4 * kt + r] = hi;
-        pl[4 * kt + r] = lo;
-      }
     // ---- O^T += V^T P^T: A = V^T[16 t + l16][keys 8 lq .. +7]
 #pragma unroll
     for (int t = 0; t < QKV_HD / 16; t++) {
       const int row = 16 * t + l16;
       const v8h vf = *reinterpret_cast<const v8h*>(Vt + row * AK + ((lq ^ vswz(row)) << 3));
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[t], 0, 0, 0);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[t], 0, 0, 0);
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[t], 0, 0, 0);
     }
     sacc[0] = snext[0];
     sacc[1] = snext[1];
@@ -440,7 +420,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
 // two tiles each, and at most 64 tiles (2 MB of K and V) so one partition's
 // K/V stays in an XCD's L2.
 static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, int* kparts) {
-  const int64_t tp = (T + AK - 1) / AK * AK;
+  const int64_t tp = attn_padded_len(T);
   const int64_t nqb = tp / AQB;
   int64_t nkb = (T + AK - 1) / AK;
   if (window > 0 && T > window) {
@@ -459,15 +439,15 @@ static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, 
 size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t window) {
   int kp;
   attn_kb_per_part(T, nq, nkv, window, &kp);
-  const int64_t tp = (T + AK - 1) / AK * AK;
+  const int64_t tp = attn_padded_len(T);
   return (size_t)(kp * tp * nq * (QKV_HD + 2));
 }
 
-hipError_t launch_attention(const uint16_t* q_hi, const uint16_t* q_lo, const uint16_t* k16,
-                            const uint16_t* vt16, float* scratch, float* ctx, int8_t* cq,
-                            float* dc, int64_t T, int64_t Tp, int64_t nq, int64_t nkv, int64_t hd,
-                            int64_t window, hipStream_t s) {
-  if (hd != QKV_HD || Tp % AQB != 0 || nq % nkv != 0) return hipErrorInvalidValue;
+hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
+                            float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
+                            int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
+                            hipStream_t s) {
+  if (hd != QKV_HD || Tp % AQB != 0 || Tp < T || nq % nkv != 0) return hipErrorInvalidValue;
   const int64_t G = nq / nkv;
   int kparts;
   const int per = attn_kb_per_part(T, nq, nkv, window, &kparts);
@@ -475,15 +455,14 @@ hipError_t launch_attention(const uint16_t* q_hi, const uint16_t* q_lo, const ui
   float* part_ml = scratch + (int64_t)kparts * Tp * nq * QKV_HD;
   const int64_t items = nkv * kparts * (Tp / AQB);
   const unsigned grid = (unsigned)((items + 7) / 8 * 8);
-  const f16* a = reinterpret_cast<const f16*>(q_hi);
-  const f16* b = reinterpret_cast<const f16*>(q_lo);
-  const f16* c = reinterpret_cast<const f16*>(k16);
-  const f16* d = reinterpret_cast<const f16*>(vt16);
-#define GLYPR_ATTN_CASE(GG)                                                                   \
-  case GG:                                                                                    \
-    attn_partial_kernel<GG, 2><<<grid, GG * 2 * 64, 0, s>>>(a, b, c, d, part_o, part_ml, (int)T, \
-                                                           (int)Tp, (int)nq, (int)nkv,          \
-                                                           (int)window, per, kparts);           \
+  const f16* q = reinterpret_cast<const f16*>(q16);
+  const f16* k = reinterpret_cast<const f16*>(k16);
+  const f16* v = reinterpret_cast<const f16*>(vt16);
+#define GLYPR_ATTN_CASE(GG)                                                                  \
+  case GG:                                                                                   \
+    attn_partial_kernel<GG><<<grid, GG * AQS * 64, 0, s>>>(q, k, v, part_o, part_ml, (int)T, \
+                                                          (int)Tp, (int)nq, (int)nkv,       \
+                                                          (int)window, per, kparts);        \
     break;
   switch (G) {
     GLYPR_ATTN_CASE(1)

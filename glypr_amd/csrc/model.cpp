@@ -101,7 +101,7 @@ struct glypr_model {
   DevBuf cos_s, sin_s, cos_f, sin_f;
   int64_t rope_cap = 0;
   // activations
-  DevBuf h, xq, dx, qkv, attn_q_hi, attn_q_lo, attn_k, attn_vt, attn_scratch, cq, dc, proj, hq,
+  DevBuf h, xq, dx, qkv, attn_q, attn_k, attn_vt, attn_scratch, cq, dc, proj, hq,
       dh, normed, pooled, ids;
   int64_t cap_t = 0;
 };
@@ -158,15 +158,14 @@ int ensure_rope(glypr_model* m, int64_t t) {
 int ensure_activations(glypr_model* m, int64_t t) {
   if (t <= m->cap_t) return GLYPR_OK;
   const glypr_model_config& c = m->cfg;
-  const int64_t tp = (t + 31) / 32 * 32;
+  const int64_t tp = attn_padded_len(t);
   const int64_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
   const int64_t wide = c.hidden > qd ? c.hidden : qd;
   RET_IF(m->h.ensure((size_t)(t * c.hidden) * 4));
   RET_IF(m->xq.ensure((size_t)(t * wide)));
   RET_IF(m->dx.ensure((size_t)(t * (wide / 32)) * 4));
   RET_IF(m->qkv.ensure((size_t)(t * (qd + 2 * kvd)) * 4));
-  RET_IF(m->attn_q_hi.ensure((size_t)(tp * qd) * 2));
-  RET_IF(m->attn_q_lo.ensure((size_t)(tp * qd) * 2));
+  RET_IF(m->attn_q.ensure((size_t)(tp * qd) * 2));
   RET_IF(m->attn_k.ensure((size_t)(tp * kvd) * 2));
   RET_IF(m->attn_vt.ensure((size_t)(tp * kvd) * 2));
   size_t sc = attention_scratch_floats(t, c.n_heads, c.n_kv_heads, 0);
@@ -214,7 +213,7 @@ void free_model(glypr_model* m) {
     dropn(L.post_feedforward_layernorm);
   }
   for (DevBuf* b : {&m->cos_s, &m->sin_s, &m->cos_f, &m->sin_f, &m->h, &m->xq, &m->dx, &m->qkv,
-                    &m->attn_q_hi, &m->attn_q_lo, &m->attn_k, &m->attn_vt, &m->attn_scratch,
+                    &m->attn_q, &m->attn_k, &m->attn_vt, &m->attn_scratch,
                     &m->cq, &m->dc, &m->proj, &m->hq, &m->dh, &m->normed, &m->pooled, &m->ids})
     b->release();
 }
@@ -224,17 +223,15 @@ void free_model(glypr_model* m) {
 // o projection's Q8_0 operand (cq, dc).
 int attention_core(glypr_hip_ctx* ctx, const float* qkv, const float* qnw, const float* knw,
                    float eps, const float* cos_t, const float* sin_t, int64_t t, int64_t nq,
-                   int64_t nkv, int64_t hd, int64_t window, uint16_t* q_hi, uint16_t* q_lo,
-                   uint16_t* k16, uint16_t* vt16, float* scratch, float* out, int8_t* cq,
-                   float* dc, hipStream_t s) {
-  const int64_t tp = (t + 31) / 32 * 32;
+                   int64_t nkv, int64_t hd, int64_t window, uint16_t* q16, uint16_t* k16,
+                   uint16_t* vt16, float* scratch, float* out, int8_t* cq, float* dc,
+                   hipStream_t s) {
+  const int64_t tp = attn_padded_len(t);
   LAUNCH(GLYPR_K_QKV_POST, s,
-         launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q_hi, q_lo, k16,
-                         vt16, s),
+         launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q16, k16, vt16, s),
          "qkv_post launch");
   LAUNCH(GLYPR_K_ATTENTION, s,
-         launch_attention(q_hi, q_lo, k16, vt16, scratch, out, cq, dc, t, tp, nq, nkv, hd, window,
-                          s),
+         launch_attention(q16, k16, vt16, scratch, out, cq, dc, t, tp, nq, nkv, hd, window, s),
          "attention launch");
   return GLYPR_OK;
 }
@@ -265,20 +262,19 @@ int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_nor
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  const int64_t tp = (t + 31) / 32 * 32;
+  const int64_t tp = attn_padded_len(t);
   const size_t qb = align_up((size_t)(tp * n_heads * head_dim) * 2, 256);
   const size_t kb = align_up((size_t)(tp * n_kv_heads * head_dim) * 2, 256);
   const size_t sb = attention_scratch_floats(t, n_heads, n_kv_heads, window) * 4;
-  RET_IF(ensure_ws(ctx, 2 * qb + 2 * kb + sb));
+  RET_IF(ensure_ws(ctx, qb + 2 * kb + sb));
   char* base = (char*)ctx->ws;
-  uint16_t* q_hi = (uint16_t*)base;
-  uint16_t* q_lo = (uint16_t*)(base + qb);
-  uint16_t* k16 = (uint16_t*)(base + 2 * qb);
-  uint16_t* vt16 = (uint16_t*)(base + 2 * qb + kb);
-  float* scratch = (float*)(base + 2 * qb + 2 * kb);
+  uint16_t* q16 = (uint16_t*)base;
+  uint16_t* k16 = (uint16_t*)(base + qb);
+  uint16_t* vt16 = (uint16_t*)(base + qb + kb);
+  float* scratch = (float*)(base + qb + 2 * kb);
   return attention_core(ctx, qkv, q_norm_weight, k_norm_weight, eps, cos_table, sin_table, t,
-                        n_heads, n_kv_heads, head_dim, window, q_hi, q_lo, k16, vt16, scratch,
-                        ctx_out, nullptr, nullptr, (hipStream_t)stream);
+                        n_heads, n_kv_heads, head_dim, window, q16, k16, vt16, scratch, ctx_out,
+                        nullptr, nullptr, (hipStream_t)stream);
 }
 
 int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
@@ -440,9 +436,9 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
     const float* sin_t = dev_f32(L.full_attention ? m->sin_f : m->sin_s);
     RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
                           L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
-                          L.full_attention ? 0 : c.sliding_window, m->attn_q_hi.as<uint16_t>(),
-                          m->attn_q_lo.as<uint16_t>(), m->attn_k.as<uint16_t>(),
-                          m->attn_vt.as<uint16_t>(), dev_f32(m->attn_scratch), nullptr,
+                          L.full_attention ? 0 : c.sliding_window, m->attn_q.as<uint16_t>(),
+                          m->attn_k.as<uint16_t>(), m->attn_vt.as<uint16_t>(),
+                          dev_f32(m->attn_scratch), nullptr,
                           m->cq.as<int8_t>(), dev_f32(m->dc), s));
     const glypr_q8w* wo = L.self_attn.o.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,

@@ -1,10 +1,11 @@
 """GPU parity of the backbone pieces (configs 4-5): the attention core and the
 multi-layer forward through the C ABI, against the CPU oracle.
 
-Attention is not bit-exact: it rounds K and V to f16 (Q and P are split), so it
-is held to f32-level agreement with the oracle fed the same f16 K/V, and to an
-f16-level bound against the unrounded oracle; the final pooled embedding must
-reach BASELINE's cosine >= 0.9999 vs the oracle.
+Attention is not bit-exact: its MFMAs take Q, K, V and the probabilities P in
+f16 (f32 accumulation and softmax), so it is held to the P-rounding level
+against the oracle fed the same f16 Q/K/V, and to an f16-level bound against
+the unrounded oracle; the final pooled embedding must reach BASELINE's cosine
+>= 0.9999 vs the oracle.
 """
 import sys
 
@@ -38,9 +39,9 @@ def rope_np(x, c, s):
     return (x * c).astype(np.float32) + (rot * s).astype(np.float32)
 
 
-def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window, f16_kv=False):
-    """Oracle attention core.  f16_kv rounds K and V (after norm + RoPE) to f16,
-    the one rounding the GPU kernel makes by design (Q and P are split hi/lo)."""
+def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window, f16_qkv=False):
+    """Oracle attention core.  f16_qkv rounds Q, K and V (after norm + RoPE) to
+    f16, the input roundings the GPU kernel makes by design."""
     t = qkv.shape[0]
     c, s = oracle.rope_tables(hd, theta, t)
     q = qkv[:, :nq * hd].reshape(t, nq, hd)
@@ -52,7 +53,8 @@ def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window, f16_kv
     qr = rope_np(qn, c[:, None, :], s[:, None, :]).transpose(1, 0, 2)
     kr = rope_np(kn, c[:, None, :], s[:, None, :]).transpose(1, 0, 2)
     vr = vn.transpose(1, 0, 2)
-    if f16_kv:
+    if f16_qkv:
+        qr = qr.astype(np.float16).astype(np.float32)
         kr = kr.astype(np.float16).astype(np.float32)
         vr = vr.astype(np.float16).astype(np.float32)
     return oracle.attention(qr, kr, vr, window), c, s
@@ -71,11 +73,13 @@ def test_attention_core_vs_oracle(ctx, oracle, t, window, qk_scale):
     got = host(ops.attention(ctx, dev(qkv), dev(qnw), dev(knw), eps, dev(c), dev(s), nq, nkv, hd,
                              window)).astype(np.float64)
     scale = np.abs(ref).max()
-    # same input roundings as the kernel: f32-level agreement
-    assert np.abs(got - ref16).max() <= 2e-5 * scale, np.abs(got - ref16).max() / scale
-    # against the unrounded oracle: the f16 rounding of K/V, amplified by the
-    # logit scale (std ~16 with unit q/k norms, ~1 with the folded 1/sqrt(d))
-    bound = 5e-3 if qk_scale == 1.0 else 1e-3
+    # same input roundings as the kernel: what remains is P in f16 (2^-12
+    # absolute per probability), which moves the context by at most ~2.5e-4
+    # of its scale
+    assert np.abs(got - ref16).max() <= 5e-4 * scale, np.abs(got - ref16).max() / scale
+    # against the unrounded oracle: the f16 rounding of Q/K/V, amplified by
+    # the logit scale (std ~16 with unit q/k norms, ~1 with the folded 1/sqrt(d))
+    bound = 1e-2 if qk_scale == 1.0 else 1e-3
     assert np.abs(got - ref).max() <= bound * scale, np.abs(got - ref).max() / scale
 
 
