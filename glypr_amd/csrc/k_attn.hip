@@ -124,10 +124,10 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 
 // ---------------------------------------------------------------------------
 // Flash attention, split over keys.
-// attn_partial: block = (64-query block, key partition, kv group) with
-//   4 x G waves: wave (qs, hh) owns queries q0 + 16 qs .. +15 of q head
-//   g G + hh, so every K/V tile staged in LDS serves 64 queries of all G heads
-//   of the group (GQA).  K/V tiles (32 keys) stream through a three-slot LDS
+// attn_partial: block = (16 AQS-query block, key partition, kv group) with
+//   AQS x G waves: wave (qs, hh) owns queries q0 + 16 qs .. +15 of q head
+//   g G + hh, so every K/V tile staged in LDS serves 16 AQS queries of all G
+//   heads of the group (GQA).  K/V tiles (32 keys) stream through a three-slot LDS
 //   ring filled by LDS DMA (global_load_lds_dwordx4 from inline asm, so the
 //   compiler adds no vmcnt waits of its own).
 //   Transposed formulation: S^T = K Q^T and O^T = V^T P^T with
@@ -150,9 +150,11 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 // B (32 x 16): column l%16, same k; D (16 x 16): column l%16, rows 4(l/16)+r.
 // ---------------------------------------------------------------------------
 constexpr int AK = 32;            // keys per tile
-constexpr int AQS = 4;            // 16-query wave rows per block
-constexpr int AQB = 16 * AQS;     // queries per block (== ATTN_TP_ALIGN)
-static_assert(AQB == ATTN_TP_ALIGN, "query blocks must tile the padded length");
+static_assert(ATTN_TP_ALIGN % 64 == 0, "query blocks (16 or 64) must tile the padded length");
+// Short sequences use 16-query blocks (more blocks to spread), long ones
+// 64-query blocks (each K/V tile serves 4x the queries).
+constexpr int64_t ATTN_SMALL_T = 1024;
+inline int attn_qs(int64_t T) { return T <= ATTN_SMALL_T ? 1 : 4; }
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
 
@@ -170,12 +172,13 @@ __device__ __forceinline__ void attn_dma16(const void* base, int voff, uint32_t 
                :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
 }
 
-template <int G>
+template <int G, int AQS>
 __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     const f16* __restrict__ q16, const f16* __restrict__ kk, const f16* __restrict__ vt,
     float* __restrict__ part_o, float* __restrict__ part_ml, int T, int Tp, int nq, int nkv,
     int window, int kb_per_part, int kparts) {
   constexpr int NWV = G * AQS;
+  constexpr int AQB = 16 * AQS;
   constexpr int RING = 3;
   constexpr int TILE_H = AK * QKV_HD;   // halves per K (or V^T) tile: 16 KB
   __shared__ __attribute__((aligned(16))) f16 Ks[RING][TILE_H];
@@ -370,49 +373,58 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
   }
 }
 
-// One wave per token: merge partitions per head; emit f32 ctx and/or Q8_0.
+// One wave per (token, head): merge the partitions in order p = 0, 1, ...;
+// emit f32 ctx and/or the head's 256 columns of the Q8_0 operand.  Lane p
+// holds partition p's (m, l); readlane broadcasts them.
 __global__ void __launch_bounds__(256) attn_combine_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml, int T, int Tp, int nq,
     int kparts, float* __restrict__ ctx, int8_t* __restrict__ cq, float* __restrict__ dc) {
   const int lane = threadIdx.x & 63;
-  const int64_t q = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (q >= T) return;
+  const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task >= (int64_t)T * nq) return;
+  const int64_t q = task / nq;
+  const int h = (int)(task % nq);
   const int width = nq * QKV_HD;
-  for (int h = 0; h < nq; h++) {
-    float M = -INFINITY;
-    for (int p = 0; p < kparts; p++) M = fmaxf(M, part_ml[(((int64_t)p * Tp + q) * nq + h) * 2]);
-    float L = 0.0f;
-    v4f acc = {0, 0, 0, 0};
-    for (int p = 0; p < kparts; p++) {
-      const int64_t r = (int64_t)p * Tp + q;
-      const float mp = part_ml[(r * nq + h) * 2];
-      const float wgt = mp == -INFINITY ? 0.0f : __expf(mp - M);
-      L += wgt * part_ml[(r * nq + h) * 2 + 1];
-      v4f v = *reinterpret_cast<const v4f*>(part_o + r * width + h * QKV_HD + 4 * lane);
+  float mp = -INFINITY, lp = 0.0f;
+  if (lane < kparts) {
+    const int64_t r = ((int64_t)lane * Tp + q) * nq + h;
+    mp = part_ml[r * 2];
+    lp = part_ml[r * 2 + 1];
+  }
+  float M = -INFINITY;
+  for (int p = 0; p < kparts; p++)
+    M = fmaxf(M, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mp), p)));
+  const float wl = mp == -INFINITY ? 0.0f : __expf(mp - M);
+  float L = 0.0f;
+  v4f acc = {0, 0, 0, 0};
+  const float* src = part_o + q * width + h * QKV_HD + 4 * lane;
+  for (int p = 0; p < kparts; p++) {
+    const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), p));
+    L += wgt * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lp), p));
+    const v4f v = *reinterpret_cast<const v4f*>(src + (int64_t)p * Tp * width);
 #pragma unroll
-      for (int e = 0; e < 4; e++) acc[e] += wgt * v[e];
-    }
-    const float inv = 1.0f / L;
-    v4f y;
+    for (int e = 0; e < 4; e++) acc[e] += wgt * v[e];
+  }
+  const float inv = 1.0f / L;
+  v4f y;
 #pragma unroll
-    for (int e = 0; e < 4; e++) y[e] = acc[e] * inv;
-    const int64_t col = (int64_t)h * QKV_HD + 4 * lane;
-    if (ctx) *reinterpret_cast<v4f*>(ctx + q * width + col) = y;
-    if (cq) {
-      float a = 0.0f;
+  for (int e = 0; e < 4; e++) y[e] = acc[e] * inv;
+  const int64_t col = (int64_t)h * QKV_HD + 4 * lane;
+  if (ctx) *reinterpret_cast<v4f*>(ctx + q * width + col) = y;
+  if (cq) {
+    float a = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(y[e]));
-      a = fmaxf(a, __shfl_xor(a, 1, 8));
-      a = fmaxf(a, __shfl_xor(a, 2, 8));
-      a = fmaxf(a, __shfl_xor(a, 4, 8));
-      QScale sc = q8_scale(a);
-      uint32_t packed = 0;
+    for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(y[e]));
+    a = fmaxf(a, __shfl_xor(a, 1, 8));
+    a = fmaxf(a, __shfl_xor(a, 2, 8));
+    a = fmaxf(a, __shfl_xor(a, 4, 8));
+    QScale sc = q8_scale(a);
+    uint32_t packed = 0;
 #pragma unroll
-      for (int e = 0; e < 4; e++)
-        packed |= ((uint32_t)(quant_round(y[e] * sc.id) & 0xFF)) << (8 * e);
-      *reinterpret_cast<uint32_t*>(cq + q * width + col) = packed;
-      if ((lane & 7) == 0) dc[q * (width / QK) + (col >> 5)] = sc.dq;
-    }
+    for (int e = 0; e < 4; e++)
+      packed |= ((uint32_t)(quant_round(y[e] * sc.id) & 0xFF)) << (8 * e);
+    *reinterpret_cast<uint32_t*>(cq + q * width + col) = packed;
+    if ((lane & 7) == 0) dc[q * (width / QK) + (col >> 5)] = sc.dq;
   }
 }
 
@@ -420,11 +432,12 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
 // two tiles each, and at most 64 tiles (2 MB of K and V) so one partition's
 // K/V stays in an XCD's L2.
 static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, int* kparts) {
+  const int64_t aqb = 16 * attn_qs(T);
   const int64_t tp = attn_padded_len(T);
-  const int64_t nqb = tp / AQB;
+  const int64_t nqb = tp / aqb;
   int64_t nkb = (T + AK - 1) / AK;
   if (window > 0 && T > window) {
-    int64_t band = (2 * window + AQB + AK - 1) / AK + 1;
+    int64_t band = (2 * window + aqb + AK - 1) / AK + 1;
     if (band < nkb) nkb = band;
   }
   int64_t want = (512 + nqb * nkv - 1) / (nqb * nkv);
@@ -447,36 +460,35 @@ hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint
                             float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
                             int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
                             hipStream_t s) {
-  if (hd != QKV_HD || Tp % AQB != 0 || Tp < T || nq % nkv != 0) return hipErrorInvalidValue;
+  if (hd != QKV_HD || Tp % ATTN_TP_ALIGN != 0 || Tp < T || nq % nkv != 0)
+    return hipErrorInvalidValue;
   const int64_t G = nq / nkv;
+  const int aqs = attn_qs(T);
   int kparts;
   const int per = attn_kb_per_part(T, nq, nkv, window, &kparts);
+  if (kparts > 64) return hipErrorInvalidValue;   // the combine holds one partition per lane
   float* part_o = scratch;
   float* part_ml = scratch + (int64_t)kparts * Tp * nq * QKV_HD;
-  const int64_t items = nkv * kparts * (Tp / AQB);
+  const int64_t items = nkv * kparts * (Tp / (16 * aqs));
   const unsigned grid = (unsigned)((items + 7) / 8 * 8);
   const f16* q = reinterpret_cast<const f16*>(q16);
   const f16* k = reinterpret_cast<const f16*>(k16);
   const f16* v = reinterpret_cast<const f16*>(vt16);
-#define GLYPR_ATTN_CASE(GG)                                                                  \
-  case GG:                                                                                   \
-    attn_partial_kernel<GG><<<grid, GG * AQS * 64, 0, s>>>(q, k, v, part_o, part_ml, (int)T, \
-                                                          (int)Tp, (int)nq, (int)nkv,       \
-                                                          (int)window, per, kparts);        \
-    break;
-  switch (G) {
-    GLYPR_ATTN_CASE(1)
-    GLYPR_ATTN_CASE(2)
-    GLYPR_ATTN_CASE(3)
-    GLYPR_ATTN_CASE(4)
-    default:
-      return hipErrorInvalidValue;
-  }
+#define GLYPR_ATTN_CASE(GG, QS)                                                              \
+  if (G == GG && aqs == QS)                                                                  \
+    attn_partial_kernel<GG, QS><<<grid, GG * QS * 64, 0, s>>>(q, k, v, part_o, part_ml, (int)T, \
+                                                             (int)Tp, (int)nq, (int)nkv,       \
+                                                             (int)window, per, kparts);
+  GLYPR_ATTN_CASE(1, 1) else GLYPR_ATTN_CASE(1, 4)
+  else GLYPR_ATTN_CASE(2, 1) else GLYPR_ATTN_CASE(2, 4)
+  else GLYPR_ATTN_CASE(3, 1) else GLYPR_ATTN_CASE(3, 4)
+  else GLYPR_ATTN_CASE(4, 1) else GLYPR_ATTN_CASE(4, 4)
+  else return hipErrorInvalidValue;
 #undef GLYPR_ATTN_CASE
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  attn_combine_kernel<<<(unsigned)((T + 3) / 4), 256, 0, s>>>(part_o, part_ml, (int)T, (int)Tp,
-                                                              (int)nq, kparts, ctx, cq, dc);
+  attn_combine_kernel<<<(unsigned)((T * nq + 3) / 4), 256, 0, s>>>(
+      part_o, part_ml, (int)T, (int)Tp, (int)nq, kparts, ctx, cq, dc);
   return hipGetLastError();
 }
 
