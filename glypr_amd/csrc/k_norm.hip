@@ -61,8 +61,42 @@ __device__ __forceinline__ uint32_t bf16_rne(float f) {
   return r;
 }
 
+// Chain-major row staging for the reference-order sum of squares (dim % 32
+// == 0): element e of a row is stored at lrow[(e % 8) * S + e / 8] with
+// S = dim / 8 + 4, so chain lane j reads its elements x[j], x[j+8], ... as
+// consecutive ds_read_b128 and runs its FMA chain from registers.  Even and odd
+// lanes of a row write 4 S apart (16 banks), so the staging stores do not
+// conflict either.
+__device__ __forceinline__ int chain_stride(int dim) { return dim / 8 + 4; }
+__device__ __forceinline__ void stage_chains(float* lrow, int S, int c4, const v4f& v) {
+  const int j0 = 4 * (c4 & 1), idx = c4 >> 1;
+#pragma unroll
+  for (int k = 0; k < 4; k++) lrow[(j0 + k) * S + idx] = v[k];
+}
+__device__ __forceinline__ float chain_row_inv(const float* lrow, int dim, int lane, float eps) {
+  float sum = 0.0f;
+  if (lane < 8) {
+    const v4f* src = reinterpret_cast<const v4f*>(lrow + lane * chain_stride(dim));
+    const int n = dim / 32;
+    float acc = 0.0f;
+#pragma unroll 6
+    for (int t = 0; t < n; t++) {
+      const v4f e = src[t];
+      acc = fmaf(e[0], e[0], acc);
+      acc = fmaf(e[1], e[1], acc);
+      acc = fmaf(e[2], e[2], acc);
+      acc = fmaf(e[3], e[3], acc);
+    }
+    float s = acc + __shfl_down(acc, 4, 8);
+    float t = s + __shfl_down(s, 2, 8);
+    sum = t + __shfl_down(t, 1, 8);
+  }
+  sum = __shfl(sum, 0);
+  return 1.0f / sqrtf(sum / (float)dim + eps);
+}
+
 // NV = float4s per lane = ceil(dim / 256).  dim % 4 == 0 (dim % 32 == 0 for Q8).
-template <int NV, int MODE>
+template <int NV, int MODE, bool CHAIN>
 __global__ void __launch_bounds__(64 * NORM_WAVES)
 rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64_t rows, int dim,
                    float* y, int8_t* __restrict__ xq, float* __restrict__ dx,
@@ -72,7 +106,7 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
   const int wave = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * NORM_WAVES + wave;
   if (row >= rows) return;  // whole wave exits together
-  float* lrow = lds_rows + wave * dim;
+  float* lrow = lds_rows + wave * (dim + 32);
   const float* xr = x + row * dim;
   const int n4 = dim >> 2;
 
@@ -82,31 +116,43 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
     int c4 = lane + 64 * i;
     v[i] = c4 < n4 ? *reinterpret_cast<const v4f*>(xr + 4 * c4) : v4f{0, 0, 0, 0};
   }
+  float inv;
+  if constexpr (CHAIN) {
+    const int S = chain_stride(dim);
 #pragma unroll
-  for (int i = 0; i < NV; i++) {
-    int c4 = lane + 64 * i;
-    if (c4 < n4) *reinterpret_cast<v4f*>(lrow + 4 * c4) = v[i];
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-
-  // Reference-order sum of squares on lanes 0..7.
-  float sum = 0.0f;
-  const int head = dim & ~7;
-  if (lane < 8) {
-    float acc = 0.0f;
-#pragma unroll 16
-    for (int c = lane; c < head; c += 8) {
-      float e = lrow[c];
-      acc = fmaf(e, e, acc);
+    for (int i = 0; i < NV; i++) {
+      int c4 = lane + 64 * i;
+      if (c4 < n4) stage_chains(lrow, S, c4, v[i]);
     }
-    float s = acc + __shfl_down(acc, 4, 8);
-    float t = s + __shfl_down(s, 2, 8);
-    sum = t + __shfl_down(t, 1, 8);
-    for (int c = head; c < dim; c++) sum += lrow[c] * lrow[c];
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    inv = chain_row_inv(lrow, dim, lane, eps);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      int c4 = lane + 64 * i;
+      if (c4 < n4) *reinterpret_cast<v4f*>(lrow + 4 * c4) = v[i];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    // Reference-order sum of squares on lanes 0..7.
+    float sum = 0.0f;
+    const int head = dim & ~7;
+    if (lane < 8) {
+      float acc = 0.0f;
+#pragma unroll 16
+      for (int c = lane; c < head; c += 8) {
+        float e = lrow[c];
+        acc = fmaf(e, e, acc);
+      }
+      float s = acc + __shfl_down(acc, 4, 8);
+      float t = s + __shfl_down(s, 2, 8);
+      sum = t + __shfl_down(t, 1, 8);
+      for (int c = head; c < dim; c++) sum += lrow[c] * lrow[c];
+    }
+    sum = __shfl(sum, 0);
+    inv = 1.0f / sqrtf(sum / (float)dim + eps);
   }
-  sum = __shfl(sum, 0);
-  const float inv = 1.0f / sqrtf(sum / (float)dim + eps);
 
 #pragma unroll
   for (int i = 0; i < NV; i++) {
@@ -150,28 +196,29 @@ static hipError_t launch_norm(const float* x, const float* w, float eps, int64_t
                               float* y, int8_t* xq, float* dx, uint16_t* xb, hipStream_t s) {
   if (rows == 0) return hipSuccess;
   const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
-  const size_t lds = (size_t)NORM_WAVES * dim * sizeof(float);
+  const size_t lds = (size_t)NORM_WAVES * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
+  const bool chain = dim % 32 == 0;
   switch (nv) {
-#define NORM_CASE(N)                                                                        \
-  case N:                                                                                   \
-    rmsnorm_row_kernel<N, MODE><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w, eps, rows, (int)dim, \
-                                                                   y, xq, dx, xb);          \
+#define NORM_CASE(N, NK)                                                                      \
+  case N:                                                                                     \
+    if (chain)                                                                                \
+      rmsnorm_row_kernel<NK, MODE, true><<<grid, 64 * NORM_WAVES, lds, s>>>(                  \
+          x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
+    else                                                                                      \
+      rmsnorm_row_kernel<NK, MODE, false><<<grid, 64 * NORM_WAVES, lds, s>>>(                 \
+          x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
     break;
-    NORM_CASE(1)
-    NORM_CASE(2)
-    NORM_CASE(3)
-    NORM_CASE(4)
-    NORM_CASE(5)
-    NORM_CASE(6)
-    NORM_CASE(8)
+    NORM_CASE(1, 1)
+    NORM_CASE(2, 2)
+    NORM_CASE(3, 3)
+    NORM_CASE(4, 4)
+    NORM_CASE(5, 5)
+    NORM_CASE(6, 6)
+    NORM_CASE(7, 8)
+    NORM_CASE(8, 8)
 #undef NORM_CASE
     default:
-      if (nv == 7) {
-        rmsnorm_row_kernel<8, MODE><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w, eps, rows, (int)dim,
-                                                                       y, xq, dx, xb);
-        break;
-      }
       return hipErrorInvalidValue;  // dim > 2048: callers validate this
   }
   return hipGetLastError();
@@ -201,25 +248,6 @@ hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_
 // reference reduction order, so h and the quantized activations are
 // bit-identical to the CPU path.  One row per wave.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_row_inv(const float* lrow, int dim, int lane, float eps) {
-  float sum = 0.0f;
-  const int head = dim & ~7;
-  if (lane < 8) {
-    float acc = 0.0f;
-#pragma unroll 16
-    for (int c = lane; c < head; c += 8) {
-      float e = lrow[c];
-      acc = fmaf(e, e, acc);
-    }
-    float s = acc + __shfl_down(acc, 4, 8);
-    float t = s + __shfl_down(s, 2, 8);
-    sum = t + __shfl_down(t, 1, 8);
-    for (int c = head; c < dim; c++) sum += lrow[c] * lrow[c];
-  }
-  sum = __shfl(sum, 0);
-  return 1.0f / sqrtf(sum / (float)dim + eps);
-}
-
 template <int NV, bool QNEXT>
 __global__ void __launch_bounds__(64 * NORM_WAVES)
 residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_post,
@@ -230,18 +258,19 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   const int wave = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * NORM_WAVES + wave;
   if (row >= rows) return;
-  float* lrow = lds_rows + wave * dim;
+  float* lrow = lds_rows + wave * (dim + 32);
   const int n4 = dim >> 2;
+  const int S = chain_stride(dim);
   v4f v[NV];
 #pragma unroll
   for (int i = 0; i < NV; i++) {
     int c4 = lane + 64 * i;
     v[i] = c4 < n4 ? *reinterpret_cast<const v4f*>(x + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
-    if (c4 < n4) *reinterpret_cast<v4f*>(lrow + 4 * c4) = v[i];
+    if (c4 < n4) stage_chains(lrow, S, c4, v[i]);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  const float inv = wave_row_inv(lrow, dim, lane, eps);
+  const float inv = chain_row_inv(lrow, dim, lane, eps);
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int i = 0; i < NV; i++) {
@@ -252,13 +281,13 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
 #pragma unroll
       for (int e = 0; e < 4; e++) v[i][e] = hv[e] + (v[i][e] * inv) * wv[e];
       *reinterpret_cast<v4f*>(h + row * dim + 4 * c4) = v[i];
-      if (QNEXT) *reinterpret_cast<v4f*>(lrow + 4 * c4) = v[i];
+      if (QNEXT) stage_chains(lrow, S, c4, v[i]);
     }
   }
   if constexpr (QNEXT) {
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
-    const float inv2 = wave_row_inv(lrow, dim, lane, eps);
+    const float inv2 = chain_row_inv(lrow, dim, lane, eps);
 #pragma unroll
     for (int i = 0; i < NV; i++) {
       const int c4 = lane + 64 * i;
@@ -293,7 +322,7 @@ hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, c
   if (rows == 0) return hipSuccess;
   if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
   const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
-  const size_t lds = (size_t)NORM_WAVES * dim * sizeof(float);
+  const size_t lds = (size_t)NORM_WAVES * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
   const bool q = xq != nullptr;
 #define RES_CASE(N)                                                                              \
