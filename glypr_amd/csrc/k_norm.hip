@@ -110,11 +110,13 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
   const float* xr = x + row * dim;
   const int n4 = dim >> 2;
 
-  v4f v[NV];
+  // row and weights are loaded together: one memory latency, not two
+  v4f v[NV], wv[NV];
 #pragma unroll
   for (int i = 0; i < NV; i++) {
     int c4 = lane + 64 * i;
     v[i] = c4 < n4 ? *reinterpret_cast<const v4f*>(xr + 4 * c4) : v4f{0, 0, 0, 0};
+    wv[i] = (w && c4 < n4) ? *reinterpret_cast<const v4f*>(w + 4 * c4) : v4f{1, 1, 1, 1};
   }
   float inv;
   if constexpr (CHAIN) {
@@ -158,10 +160,9 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
   for (int i = 0; i < NV; i++) {
     const int c4 = lane + 64 * i;
     const bool ok = c4 < n4;
-    v4f wv = (w && ok) ? *reinterpret_cast<const v4f*>(w + 4 * c4) : v4f{1, 1, 1, 1};
     v4f yv;
 #pragma unroll
-    for (int e = 0; e < 4; e++) yv[e] = w ? (v[i][e] * inv) * wv[e] : v[i][e] * inv;
+    for (int e = 0; e < 4; e++) yv[e] = w ? (v[i][e] * inv) * wv[i][e] : v[i][e] * inv;
     if constexpr (MODE == OUT_F32) {
       if (ok) *reinterpret_cast<v4f*>(y + row * dim + 4 * c4) = yv;
     } else if constexpr (MODE == OUT_BF16) {
@@ -261,11 +262,21 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   float* lrow = lds_rows + wave * (dim + 32);
   const int n4 = dim >> 2;
   const int S = chain_stride(dim);
-  v4f v[NV];
+  // every input is loaded up front: one memory latency for the row
+  v4f v[NV], hv[NV], wp[NV], wn[NV];
 #pragma unroll
   for (int i = 0; i < NV; i++) {
-    int c4 = lane + 64 * i;
-    v[i] = c4 < n4 ? *reinterpret_cast<const v4f*>(x + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
+    const int c4 = lane + 64 * i;
+    const bool ok = c4 < n4;
+    v[i] = ok ? *reinterpret_cast<const v4f*>(x + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
+    hv[i] = ok ? *reinterpret_cast<const v4f*>(h + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
+    wp[i] = ok ? *reinterpret_cast<const v4f*>(w_post + 4 * c4) : v4f{0, 0, 0, 0};
+    wn[i] = (QNEXT && w_next && ok) ? *reinterpret_cast<const v4f*>(w_next + 4 * c4)
+                                    : v4f{1, 1, 1, 1};
+  }
+#pragma unroll
+  for (int i = 0; i < NV; i++) {
+    const int c4 = lane + 64 * i;
     if (c4 < n4) stage_chains(lrow, S, c4, v[i]);
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -276,10 +287,8 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   for (int i = 0; i < NV; i++) {
     int c4 = lane + 64 * i;
     if (c4 < n4) {
-      v4f wv = *reinterpret_cast<const v4f*>(w_post + 4 * c4);
-      v4f hv = *reinterpret_cast<const v4f*>(h + row * dim + 4 * c4);
 #pragma unroll
-      for (int e = 0; e < 4; e++) v[i][e] = hv[e] + (v[i][e] * inv) * wv[e];
+      for (int e = 0; e < 4; e++) v[i][e] = hv[i][e] + (v[i][e] * inv) * wp[i][e];
       *reinterpret_cast<v4f*>(h + row * dim + 4 * c4) = v[i];
       if (QNEXT) stage_chains(lrow, S, c4, v[i]);
     }
@@ -292,12 +301,11 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
     for (int i = 0; i < NV; i++) {
       const int c4 = lane + 64 * i;
       const bool ok = c4 < n4;
-      v4f wv = (w_next && ok) ? *reinterpret_cast<const v4f*>(w_next + 4 * c4) : v4f{1, 1, 1, 1};
       v4f yv;
       float a = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        yv[e] = w_next ? (v[i][e] * inv2) * wv[e] : v[i][e] * inv2;
+        yv[e] = w_next ? (v[i][e] * inv2) * wn[i][e] : v[i][e] * inv2;
         a = fmaxf(a, fabsf(yv[e]));
       }
       a = fmaxf(a, __shfl_xor(a, 1, 8));
