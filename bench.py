@@ -373,6 +373,8 @@ def main():
     ap.add_argument("--variant", choices=["int8", "bf16"], default="int8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
+    ap.add_argument("--extras", default="c1,c3,c4,c5",
+                    help="comma list of the extra workloads to run (c1, c3, c4, c5)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain device copy of MIB MiB (calibrates rocprof "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -407,7 +409,8 @@ def main():
                                 "launches_per_step": v["launches"] // args.steps}
                             for k, v in kern.items()},
              "pct_mfma_peak_c2": round(100 * tops / peak, 3)}
-    if not args.no_extra:
+    todo = set() if args.no_extra else {e.strip() for e in args.extras.split(",") if e.strip()}
+    if "c3" in todo:
         for vname, v in (("int8", INT8_EXACT), ("bf16", BF16_DEQUANT)):
             Lx, msx, kx = run_workload(ctx, 16384, v, max(10, args.steps // 10), 3)
             t = Lx.ops_per_step() / (msx / 1e3) / 1e12
@@ -417,13 +420,18 @@ def main():
                 "pct_mfma_peak": round(100 * t / pk, 2),
                 "kernels_us": {k: round(vv["us_per_launch"], 2) for k, vv in kx.items()}}
             del Lx
+    if "c1" in todo:
         extra["c1_int8"] = c1_linear(ctx, args.steps)
+    if "c4" in todo or "c5" in todo:
         rng = np.random.default_rng(7)
         tensors = model_tensors(rng, 24, 262144)
-        extra["c4"] = run_backbone(ctx, tensors, 24, 262144, 512, max(10, args.steps // 10), 3)
-        extra["c5"] = run_backbone(ctx, tensors, 24, 262144, 8192, 3, 1)
-        if not args.no_cpu:
-            extra["c4"]["cpu_baseline"] = cpu_backbone_baseline(tensors, 24, 262144, 512)
+        if "c4" in todo:
+            extra["c4"] = run_backbone(ctx, tensors, 24, 262144, 512,
+                                       max(10, args.steps // 10), 3)
+            if not args.no_cpu:
+                extra["c4"]["cpu_baseline"] = cpu_backbone_baseline(tensors, 24, 262144, 512)
+        if "c5" in todo:
+            extra["c5"] = run_backbone(ctx, tensors, 24, 262144, 8192, 3, 1)
         del tensors
 
     line = {

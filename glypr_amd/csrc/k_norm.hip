@@ -379,8 +379,8 @@ hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, h
 // (latency-bound: milliseconds at t = 8192), so the sum here is chunked:
 // pool_partial sums POOL_CHUNK-token chunks per column (sequentially inside a
 // chunk), pool_finalize adds the chunk sums in chunk order, divides, and runs
-// the norms.  Deterministic (fixed order) and within a few f32 ulps of the
-// sequential sum; tested against a float64 mean.
+// the norms with block-wide tree reductions.  Deterministic (fixed order) and
+// within a few f32 ulps of the sequential sums; tested against float64.
 // ---------------------------------------------------------------------------
 constexpr int POOL_CHUNK = 64;
 
@@ -403,54 +403,61 @@ __global__ void __launch_bounds__(256) pool_partial_kernel(const float* __restri
   partial[chunk * d + col] = s;
 }
 
+// Sum of v over the 1024 threads of the block (fixed tree: wave shuffles,
+// then the 16 wave sums in order).  Every thread gets the total.
+__device__ __forceinline__ float block_sum_1024(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) t += red[i];
+  return t;
+}
+
 __global__ void __launch_bounds__(1024) pool_finalize_kernel(const float* __restrict__ partial,
                                                              const uint8_t* __restrict__ mask,
                                                              int64_t t, int64_t d, int64_t trunc,
                                                              float* __restrict__ out,
                                                              float* __restrict__ pooled) {
-  __shared__ float s_norm;
-  __shared__ float s_cnt;
+  __shared__ float red[16];
   const int64_t nchunk = (t + POOL_CHUNK - 1) / POOL_CHUNK;
-  if (threadIdx.x == 0) {
-    float cnt = 0.0f;
-    if (mask) {
-      for (int64_t j = 0; j < t; j++) cnt += mask[j] ? 1.0f : 0.0f;
-      if (cnt < 1e-9f) cnt = 1e-9f;
-    }
-    s_cnt = cnt;
+  float cnt = 0.0f;
+  if (mask) {
+    float c = 0.0f;
+    for (int64_t j = threadIdx.x; j < t; j += blockDim.x) c += mask[j] ? 1.0f : 0.0f;
+    cnt = block_sum_1024(c, red);
+    if (cnt < 1e-9f) cnt = 1e-9f;
   }
-  __syncthreads();
   const float inv_t = (float)(1.0 / (double)t);
+  float ss = 0.0f;
   for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
     float s = 0.0f;
     for (int64_t c = 0; c < nchunk; c++) s += partial[c * d + i];
-    pooled[i] = mask ? s / s_cnt : s * inv_t + 0.0f;
+    const float v = mask ? s / cnt : s * inv_t + 0.0f;
+    pooled[i] = v;
+    ss += v * v;
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float ss = 0.0f;
-    for (int64_t i = 0; i < d; i++) ss += pooled[i] * pooled[i];
-    float n = sqrtf(ss);
-    s_norm = n < 1e-12f ? 1e-12f : n;
-  }
-  __syncthreads();
+  const float n1 = sqrtf(block_sum_1024(ss, red));
+  const float nrm = n1 < 1e-12f ? 1e-12f : n1;
   const int64_t td = (trunc > 0 && trunc < d) ? trunc : d;
-  float nrm = s_norm;
   if (td == d) {
     for (int64_t i = threadIdx.x; i < d; i += blockDim.x) out[i] = pooled[i] / nrm;
     return;
   }
-  for (int64_t i = threadIdx.x; i < d; i += blockDim.x) pooled[i] = pooled[i] / nrm;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float ss = 0.0f;
-    for (int64_t i = 0; i < td; i++) ss += pooled[i] * pooled[i];
-    float n = sqrtf(ss);
-    s_norm = n < 1e-12f ? 1e-12f : n;
+  // MRL: keep the first td of the normalised vector and normalise again
+  float ss2 = 0.0f;
+  for (int64_t i = threadIdx.x; i < td; i += blockDim.x) {
+    const float v = pooled[i] / nrm;
+    pooled[i] = v;
+    ss2 += v * v;
   }
-  __syncthreads();
-  nrm = s_norm;
-  for (int64_t i = threadIdx.x; i < td; i += blockDim.x) out[i] = pooled[i] / nrm;
+  const float n2 = sqrtf(block_sum_1024(ss2, red));
+  const float nrm2 = n2 < 1e-12f ? 1e-12f : n2;
+  for (int64_t i = threadIdx.x; i < td; i += blockDim.x) out[i] = pooled[i] / nrm2;
 }
 
 size_t pool_scratch_floats(int64_t t, int64_t d) {
