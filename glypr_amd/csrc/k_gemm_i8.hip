@@ -226,30 +226,59 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
         }
       }
   } else {
+    // h = geglu(gate, up); a row's 32-wide Q8_0 block of h is one 32-lane
+    // half-wave.  The 32 lanes reduce the block amax together, then one lane
+    // per row derives the scale (through a per-wave LDS table in the
+    // now-free A tile) instead of all 32 repeating the two divisions.
     const int nbh = F / QK;
+    float* t_amax = reinterpret_cast<float*>(&As[0][0]) + wave * (3 * WTM);
+    float* t_id = t_amax + WTM;
+    float* t_dq = t_amax + 2 * WTM;
 #pragma unroll
     for (int p = 0; p < TN / 2; p++) {
       const int hc = (n0 >> 1) + ((wn * WTN) >> 6) * 32 + p * 32 + lrow;
+      float h[TM][16];
 #pragma unroll
       for (int tm = 0; tm < TM; tm++) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int gm = m0 + wm * WTM + tm * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-          float h = geglu_scalar(acc[tm][2 * p][r], acc[tm][2 * p + 1][r]);
-          float a = fmaxf(0.0f, fabsf(h));
+          h[tm][r] = geglu_scalar(acc[tm][2 * p][r], acc[tm][2 * p + 1][r]);
+          float a = fmaxf(0.0f, fabsf(h[tm][r]));
           a = fmaxf(a, __shfl_xor(a, 1));
           a = fmaxf(a, __shfl_xor(a, 2));
           a = fmaxf(a, __shfl_xor(a, 4));
           a = fmaxf(a, __shfl_xor(a, 8));
           a = fmaxf(a, __shfl_xor(a, 16));
-          QScale sc = q8_scale(a);
-          int q = quant_round(h * sc.id);
+          if (lrow == 0) t_amax[tm * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3)] = a;
+        }
+      }
+      // LDS serves a wave's accesses in order; the fences keep the compiler
+      // from moving the table reads above the writes.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (int row = lane; row < WTM; row += 64) {
+        const QScale q = q8_scale(t_amax[row]);
+        t_id[row] = q.id;
+        t_dq[row] = q.dq;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int lr = tm * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+          const int gm = m0 + wm * WTM + lr;
+          const int q = quant_round(h[tm][r] * t_id[lr]);
           if (gm < M && hc < F) {
             Hq[(int64_t)gm * F + hc] = (int8_t)q;
-            if (lrow == 0) dH[(int64_t)gm * nbh + (hc >> 5)] = sc.dq;
+            if (lrow == 0) dH[(int64_t)gm * nbh + (hc >> 5)] = t_dq[lr];
           }
         }
       }
+      __builtin_amdgcn_wave_barrier();   // the table is reused by the next pair
     }
   }
 }
