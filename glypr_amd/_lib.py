@@ -20,6 +20,7 @@ GLYPR_ERR_HIP = 5
 GLYPR_ERR_OOM = 6
 GLYPR_ERR_RANGE = 7
 GLYPR_ERR_UNSUPPORTED = 8
+GLYPR_ERR_NOT_FOUND = 9
 
 INT8_EXACT = 0
 BF16_DEQUANT = 1
@@ -59,6 +60,24 @@ SIGNATURES = {
     "glypr_hip_model_finalize": (_int, [_vp]),
     "glypr_hip_model_embed": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "glypr_hip_model_destroy": (_int, [_vp]),
+    "glypr_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "glypr_gguf_close": (_int, [_vp]),
+    "glypr_gguf_version": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32),
+                                  ctypes.POINTER(ctypes.c_uint32)]),
+    "glypr_gguf_tensor_count": (_int, [_vp, ctypes.POINTER(_i64)]),
+    "glypr_gguf_tensor_info": (_int, [_vp, _i64, ctypes.POINTER(ctypes.c_char_p),
+                                      ctypes.POINTER(_int), ctypes.POINTER(_int),
+                                      ctypes.POINTER(_i64), ctypes.POINTER(_vp),
+                                      ctypes.POINTER(_i64)]),
+    "glypr_gguf_find_tensor": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_i64)]),
+    "glypr_gguf_get_u64": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "glypr_gguf_get_f64": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "glypr_gguf_get_str": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]),
+    "glypr_gguf_get_array": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_int),
+                                    ctypes.POINTER(_i64)]),
+    "glypr_gguf_get_array_u64": (_int, [_vp, ctypes.c_char_p, _i64,
+                                        ctypes.POINTER(ctypes.c_uint64)]),
+    "glypr_hip_model_load_gguf": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "glypr_hip_profile_enable": (_int, [_vp, _int]),
     "glypr_hip_profile_read": (_int, [_vp, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(_i64)]),

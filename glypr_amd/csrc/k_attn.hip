@@ -166,7 +166,8 @@ __device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
 // V^T rows are 64 B (4 chunks); the O^T tiles read rows 16 t + l16.
 __device__ __forceinline__ int vswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-// 16 bytes per lane, global (uniform base + lane byte offset) -> LDS (lane i -> lds_base + 16 i).
+// 16 bytes per lane, global (uniform base + lane byte offset) -> LDS (lane i ->
+// lds_base + 16 i).  Sets m0 itself; the attention kernel has no other m0 user.
 __device__ __forceinline__ void attn_dma16(const void* base, int voff, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");

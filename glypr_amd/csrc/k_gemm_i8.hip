@@ -307,6 +307,9 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 // ---------------------------------------------------------------------------
 typedef long v1l;
 
+// LDS DMA helpers.  They set m0 themselves; the compiler keeps m0 reserved
+// and the kernels that use them contain no other m0 user (no LDS-DMA
+// builtins, GWS or indexed register moves), which the build's assembly shows.
 // 16 bytes per lane, global -> LDS (lane i -> lds_base + 16 i); the address
 // is the uniform base plus the lane's 32-bit offset.
 __device__ __forceinline__ void dma16(const int8_t* base, int voff, uint32_t lds_base) {

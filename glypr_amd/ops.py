@@ -7,12 +7,13 @@ on the context's device.
 from __future__ import annotations
 
 import ctypes
+import os
 from typing import Optional, Sequence
 
 import numpy as np
 import torch
 
-from ._lib import BF16_DEQUANT, INT8_EXACT, check, lib
+from ._lib import BF16_DEQUANT, GLYPR_ERR_UNSUPPORTED, INT8_EXACT, GlyprError, check, lib
 
 __all__ = ["Context", "Q8Weight", "INT8_EXACT", "BF16_DEQUANT", "q8_0_matmul",
            "rmsnorm_q8_0_matmul", "rmsnorm", "geglu", "mlp", "rmsnorm_mlp", "dequantize",
@@ -250,8 +251,104 @@ class ModelConfig(ctypes.Structure):
                 ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double)]
 
 
+class Gguf:
+    """A memory-mapped, parsed GGUF v2/v3 file (glypr_gguf_*); host only."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(lib().glypr_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h
+
+    def version(self):
+        v, a = ctypes.c_uint32(), ctypes.c_uint32()
+        check(lib().glypr_gguf_version(self.handle, ctypes.byref(v), ctypes.byref(a)))
+        return v.value, a.value
+
+    def tensors(self):
+        """[{name, type, dims (ne order), nbytes, data (address or None)}]"""
+        n = ctypes.c_int64()
+        check(lib().glypr_gguf_tensor_count(self.handle, ctypes.byref(n)))
+        out = []
+        for i in range(n.value):
+            name, typ, nd = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_int()
+            ne = (ctypes.c_int64 * 4)()
+            data, nb = ctypes.c_void_p(), ctypes.c_int64()
+            check(lib().glypr_gguf_tensor_info(self.handle, i, ctypes.byref(name),
+                                               ctypes.byref(typ), ctypes.byref(nd), ne,
+                                               ctypes.byref(data), ctypes.byref(nb)))
+            out.append({"name": name.value.decode(), "type": typ.value,
+                        "dims": tuple(ne[:nd.value]), "nbytes": nb.value, "data": data.value})
+        return out
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        """A copy of the tensor's bytes as stored in the file."""
+        idx = ctypes.c_int64()
+        check(lib().glypr_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(idx)))
+        t = self.tensors()[idx.value]
+        if t["data"] is None:
+            raise GlyprError(GLYPR_ERR_UNSUPPORTED, f"tensor {name!r} has an unsized ggml type")
+        return np.ctypeslib.as_array((ctypes.c_uint8 * t["nbytes"]).from_address(t["data"])).copy()
+
+    def u64(self, key: str) -> int:
+        v = ctypes.c_uint64()
+        check(lib().glypr_gguf_get_u64(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def f64(self, key: str) -> float:
+        v = ctypes.c_double()
+        check(lib().glypr_gguf_get_f64(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def str(self, key: str) -> str:
+        v = ctypes.c_char_p()
+        check(lib().glypr_gguf_get_str(self.handle, key.encode(), ctypes.byref(v)))
+        return v.value.decode()
+
+    def array_u64(self, key: str):
+        et, n = ctypes.c_int(), ctypes.c_int64()
+        check(lib().glypr_gguf_get_array(self.handle, key.encode(), ctypes.byref(et),
+                                         ctypes.byref(n)))
+        out = []
+        for i in range(n.value):
+            v = ctypes.c_uint64()
+            check(lib().glypr_gguf_get_array_u64(self.handle, key.encode(), i, ctypes.byref(v)))
+            out.append(v.value)
+        return out
+
+    def close(self):
+        if self.handle:
+            lib().glypr_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Model:
     """The text backbone (glypr_hip_model_*): tensors by their GGUF names."""
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, path: str) -> "Model":
+        """glypr_hip_model_load_gguf: config and tensors from a GGUF file."""
+        with Gguf(path) as g:
+            hidden = g.u64("gemma-embedding2.embedding_length")
+        m = cls.__new__(cls)
+        m.ctx = ctx
+        m.cfg = {"hidden": hidden}
+        h = ctypes.c_void_p()
+        m.handle = None
+        check(lib().glypr_hip_model_load_gguf(ctx.handle, os.fsencode(path), ctypes.byref(h)))
+        m.handle = h
+        return m
 
     def __init__(self, ctx: Context, **cfg):
         defaults = dict(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256, n_layers=24,

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define GLYPR_HIP_ABI_VERSION 1
+#define GLYPR_HIP_ABI_VERSION 2
 
 typedef enum glypr_status {
   GLYPR_OK = 0,
@@ -41,7 +41,8 @@ typedef enum glypr_status {
   GLYPR_ERR_HIP = 5,         /* HIP runtime error (message has the HIP error) */
   GLYPR_ERR_OOM = 6,         /* device allocation failed */
   GLYPR_ERR_RANGE = 7,       /* token id >= vocab */
-  GLYPR_ERR_UNSUPPORTED = 8  /* unknown variant or flag */
+  GLYPR_ERR_UNSUPPORTED = 8, /* unknown variant or flag, unsupported file layout */
+  GLYPR_ERR_NOT_FOUND = 9    /* GGUF metadata key or tensor absent */
 } glypr_status;
 
 /* Numerics of the Q8_0 GEMM.
@@ -235,6 +236,42 @@ int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, in
                           float* out, float* hidden, glypr_stream stream);
 
 int glypr_hip_model_destroy(glypr_model* model);
+
+/* ---- GGUF v3 files ------------------------------------------------------ */
+
+/* gguf_file::Content::read as glypr calls it (lib.rs:180-186, model.rs:235):
+ * memory-map and parse a GGUF (v2/v3) file.  Header, metadata and tensor table
+ * are validated with bounds checks (GLYPR_ERR_SHAPE on a truncated or corrupt
+ * file, GLYPR_ERR_UNSUPPORTED on another version).  Host only: no device is
+ * touched. */
+typedef struct glypr_gguf glypr_gguf;
+int glypr_gguf_open(const char* path, glypr_gguf** out);
+int glypr_gguf_close(glypr_gguf* g);
+int glypr_gguf_version(const glypr_gguf* g, uint32_t* version, uint32_t* alignment);
+/* Content::tensor_infos: name, ggml type (0 = F32, 8 = Q8_0, ...), dims ne[0..3]
+ * (ne[0] innermost; unused dims are 1), the mapped bytes and their size
+ * (nbytes = -1, data = NULL for a ggml type this reader does not size). */
+int glypr_gguf_tensor_count(const glypr_gguf* g, int64_t* n);
+int glypr_gguf_tensor_info(const glypr_gguf* g, int64_t i, const char** name, int* type,
+                           int* n_dims, int64_t* ne, const void** data, int64_t* nbytes);
+int glypr_gguf_find_tensor(const glypr_gguf* g, const char* name, int64_t* index);
+/* Content::metadata lookups (the get_u32 / get_f64 helpers of config.rs:9-40):
+ * integer and bool values as u64, numbers as f64; GLYPR_ERR_NOT_FOUND if the
+ * key is absent, GLYPR_ERR_UNSUPPORTED if it has another type. */
+int glypr_gguf_get_u64(const glypr_gguf* g, const char* key, uint64_t* out);
+int glypr_gguf_get_f64(const glypr_gguf* g, const char* key, double* out);
+int glypr_gguf_get_str(const glypr_gguf* g, const char* key, const char** out);
+int glypr_gguf_get_array(const glypr_gguf* g, const char* key, int* elem_type, int64_t* len);
+int glypr_gguf_get_array_u64(const glypr_gguf* g, const char* key, int64_t i, uint64_t* out);
+
+/* GlyprEmbedder::load_gguf_q8 -> EmbeddingGemma2Model::from_gguf_content
+ * (lib.rs:180-186; model.rs:244-488) with TextConfig::from_gguf_metadata
+ * (config.rs:79-189): the config from the gemma-embedding2.* keys, then every
+ * tensor glypr_hip_model_set_tensor names, then finalize.  Per-Layer
+ * Embedding tensors are ignored (the backbone omits that block).  Layouts the
+ * backend does not run (a layer pattern other than 5 sliding + 1 full,
+ * per-layer kv heads or head dims) give GLYPR_ERR_UNSUPPORTED. */
+int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model** out);
 
 /* ---- per-kernel timing --------------------------------------------------- */
 

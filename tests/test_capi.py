@@ -17,7 +17,7 @@ HEADER = os.path.join(ROOT, "include", "glypr_hip.h")
 def declared_symbols():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(glypr_hip_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(glypr_(?:hip|gguf)_\w+)\s*\(", text)))
 
 
 def test_header_declares_the_bound_symbols():
@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_symbols():
         assert hasattr(L, name), name
-    assert L.glypr_hip_abi_version() == 1
+    assert L.glypr_hip_abi_version() == 2
 
 
 def _has_gpu():

@@ -184,3 +184,31 @@ def test_model_forward_vs_oracle(ctx, oracle, n_layers, t, vocab):
     again = host(m.embed(ids, trunc=256))
     assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
     m.close()
+
+
+def test_model_from_gguf_matches_set_tensor(ctx, oracle, tmp_path):
+    """glypr_hip_model_load_gguf (config from gemma-embedding2.* metadata, tensors
+    by name) builds the same model as set_tensor: bit-identical embeddings."""
+    import gguf_util as gu
+    say("model from a GGUF file vs the same tensors through set_tensor")
+    n_layers, vocab, t = 6, 2000, 300
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=11)
+    path = tmp_path / "tiny.gguf"
+    gu.model_gguf(path, {k: (np.asarray(v[0], np.float32) if not v[3] else v[0], v[1], v[2], v[3])
+                         for k, v in tensors.items()},
+                  n_layers, 768, 1152, 3, 1, 256)
+    g = Model.from_gguf(ctx, str(path))
+    ids = oracle.uniform_ids(t, seed=5, vocab=vocab)
+    a = host(m.embed(ids, trunc=256))
+    b = host(g.embed(ids, trunc=256))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    g.close()
+    m.close()
+    # a layer layout the backend does not run is refused, not mis-run
+    bad = tmp_path / "bad.gguf"
+    gu.model_gguf(bad, {k: (np.asarray(v[0], np.float32) if not v[3] else v[0], v[1], v[2], v[3])
+                        for k, v in tensors.items()}, n_layers, 768, 1152, 3, 1, 256,
+                  extra_meta=[("gemma-embedding2.attention.key_length", gu.U32, 512)])
+    from glypr_amd._lib import GlyprError
+    with pytest.raises(GlyprError):
+        Model.from_gguf(ctx, str(bad))
