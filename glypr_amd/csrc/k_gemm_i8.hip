@@ -351,7 +351,7 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   constexpr int SA = NB * BM, SB = NB * BN;
   static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 1152");
   static_assert((UA + UB) % NW == 0, "stage units must split evenly over the waves");
-  static_assert(RING >= 3, "ring needs >= 3 slots");
+  static_assert(RING >= 2, "ring needs >= 2 slots");
   static_assert(!GEGLU || (TNW == 2 && WN == 2), "GeGLU tile: 2 waves x (gate, up)");
   constexpr int SLOT = (BM + BN) * BK;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
@@ -588,7 +588,7 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
                           hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
   if (small_ok(M, K))
-    return run_small<2, 2, 1, false, 4>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+    return run_small<1, 2, 1, false, 3>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
   int64_t big_tiles = ((M + 127) / 128) * ((N + 127) / 128);
   if (big_tiles >= 512)
     return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
