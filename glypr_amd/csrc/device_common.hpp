@@ -28,6 +28,35 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
 
+// ---------------------------------------------------------------------------
+// Cross-lane max through DPP (a VALU operand modifier: no LDS round trip, as
+// __shfl_xor's ds_bpermute would be).  Max is order-free, so these give the
+// same bits as any other reduction order.  DPP controls: quad_perm 0x00-0xFF,
+// row_mirror 0x140, row_half_mirror 0x141, row_bcast:15 0x142 (a row is 16
+// lanes).
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_mov(float old, float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
+                                                    ROW_MASK, 0xF, false));
+}
+// max over each aligned group of 8 lanes; every lane of the group gets it
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v, v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_mov<0x4E>(v, v));    // quad_perm [2,3,0,1]
+  return fmaxf(v, dpp_mov<0x141>(v, v));  // row_half_mirror: quad 0 <-> quad 1
+}
+// max over each row of 16 lanes; every lane of the row gets it
+__device__ __forceinline__ float max16(float v) {
+  v = max8(v);
+  return fmaxf(v, dpp_mov<0x140>(v, v));  // row_mirror: 8-lane halves swap
+}
+// max over lanes 0-31 and over lanes 32-63; valid in lanes 16-31 and 48-63
+__device__ __forceinline__ float max32_hi(float v) {
+  v = max16(v);
+  return fmaxf(v, dpp_mov<0x142, 0xA>(v, v));  // rows 1, 3 take lane 15 of rows 0, 2
+}
+
 // Rust `f32::round(v) as i8`: half away from zero, saturating, NaN -> 0.
 __device__ __forceinline__ int quant_round(float v) {
   float r = roundf(v);

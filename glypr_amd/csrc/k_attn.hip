@@ -416,9 +416,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
     float a = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(y[e]));
-    a = fmaxf(a, __shfl_xor(a, 1, 8));
-    a = fmaxf(a, __shfl_xor(a, 2, 8));
-    a = fmaxf(a, __shfl_xor(a, 4, 8));
+    a = max8(a);
     QScale sc = q8_scale(a);
     uint32_t packed = 0;
 #pragma unroll

@@ -129,9 +129,7 @@ __global__ void __launch_bounds__(256) quantize_planar_kernel(const float* __res
   float a = 0.0f;
 #pragma unroll
   for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(v[e]));
-  a = fmaxf(a, __shfl_xor(a, 1, 8));
-  a = fmaxf(a, __shfl_xor(a, 2, 8));
-  a = fmaxf(a, __shfl_xor(a, 4, 8));
+  a = max8(a);
   QScale sc = q8_scale(a);
   uint32_t packed = 0;
 #pragma unroll
@@ -164,9 +162,7 @@ __global__ void __launch_bounds__(256) quantize_gguf_kernel(const float* __restr
   float a = 0.0f;
 #pragma unroll
   for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(v[e]));
-  a = fmaxf(a, __shfl_xor(a, 1, 8));
-  a = fmaxf(a, __shfl_xor(a, 2, 8));
-  a = fmaxf(a, __shfl_xor(a, 4, 8));
+  a = max8(a);
   QScale sc = q8_scale(a);
   uint32_t q0 = (uint32_t)(quant_round(v[0] * sc.id) & 0xFF);
   uint32_t q1 = (uint32_t)(quant_round(v[1] * sc.id) & 0xFF);

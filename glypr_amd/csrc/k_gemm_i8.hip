@@ -243,13 +243,8 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           h[tm][r] = geglu_scalar(acc[tm][2 * p][r], acc[tm][2 * p + 1][r]);
-          float a = fmaxf(0.0f, fabsf(h[tm][r]));
-          a = fmaxf(a, __shfl_xor(a, 1));
-          a = fmaxf(a, __shfl_xor(a, 2));
-          a = fmaxf(a, __shfl_xor(a, 4));
-          a = fmaxf(a, __shfl_xor(a, 8));
-          a = fmaxf(a, __shfl_xor(a, 16));
-          if (lrow == 0) t_amax[tm * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3)] = a;
+          const float a = max32_hi(fmaxf(0.0f, fabsf(h[tm][r])));
+          if (lrow == 31) t_amax[tm * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3)] = a;
         }
       }
       // LDS serves a wave's accesses in order; the fences keep the compiler
@@ -501,11 +496,7 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       h[r] = geglu_scalar(acc[0][r], acc[1][r]);
-      float v = fmaxf(0.0f, fabsf(h[r]));
-      v = fmaxf(v, __shfl_xor(v, 1));
-      v = fmaxf(v, __shfl_xor(v, 2));
-      v = fmaxf(v, __shfl_xor(v, 4));
-      v = fmaxf(v, __shfl_xor(v, 8));
+      const float v = max16(fmaxf(0.0f, fabsf(h[r])));
       if (l16 == 0) amax_x[wn * BM + wm * 16 + 4 * lq + r] = v;
     }
     __syncthreads();
@@ -571,8 +562,251 @@ inline bool small_ok(int64_t M, int64_t K) {
   return M <= SMALL_M_MAX && K <= SMALL_K_MAX && K % BK == 0;
 }
 
+// ---------------------------------------------------------------------------
+// Large-M variant (M > 2048: batched sequences, long contexts).  The exact
+// epilogue (3 VALU ops per output and block) binds.  On gfx950 the MFMA pipe
+// and the VALU do not overlap for this MFMA -> dependent-epilogue pattern, so
+// the cost per output and block is (VALU ops + MFMA cycles): the kernel uses
+// the full-rate v_mfma_i32_32x32x32_i8 (2 cycles per output and block, half
+// of the 16x16x32 form).  Structure:
+//  - 4 waves stacked along M; wave w owns rows 32w..32w+31 of a 128 x 128
+//    tile and all 128 columns (4 MFMA tiles of 32 x 32, 64 accumulators);
+//  - every stage (128 bytes of K = 4 blocks) arrives by LDS DMA into a
+//    two-slot ring: A tile [128][128 B] and B tile [128][128 B] (16-byte
+//    chunk c of row r at c ^ ((r >> 1) & 7): conflict-free ds_read_b128),
+//    then the A and B scales of the stage as [block][row] f32 (dword DMA), so
+//    the 16 row scales of a lane's 32 x 32 outputs are 4 ds_read_b128;
+//    48 units, 12 per wave: "stage s has landed" is vmcnt(0) + barrier and
+//    the next stage streams in under the current stage's compute;
+//  - 2 workgroups per CU (72 KB LDS, <= 256 VGPRs each);
+//  - the tile order is XCD-aware: the 8 XCDs get contiguous ranges of the
+//    row-major tile list, so the tiles sharing an A row block share an L2.
+// Rows past M/N are clamped to a valid row (their outputs are never stored).
+//
+// GEGLU: B rows of a tile are [gate c..c+31, up c..c+31, gate c+32..c+63,
+// up c+32..c+63], so a Q8_0 block of h is one MFMA tile pair: the block amax
+// is a 32-lane reduction, and each wave derives its 64 (row, block) scales one
+// per lane through a per-wave LDS table instead of repeating the divisions.
+// ---------------------------------------------------------------------------
+constexpr int BIG_BM = 128, BIG_BN = 128;
+
+__device__ __forceinline__ void dma4(const int8_t* base, int voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ int big_swz(int row) { return (row >> 1) & 7; }
+
+template <bool GEGLU>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_i8_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
+                   const int8_t* __restrict__ B, const float* __restrict__ dB,
+                   float* __restrict__ C, int8_t* __restrict__ Hq, float* __restrict__ dH,
+                   int M, int N, int K, int ldc, int F, int tiles_n) {
+  constexpr int NW = 4, TN = 4;
+  constexpr int UA = BIG_BM / 8, UB = BIG_BN / 8;        // 1 KB operand units
+  constexpr int USA = KB * BIG_BM / 64, USB = KB * BIG_BN / 64;   // 256 B scale units
+  constexpr int NU = UA + UB + USA + USB;
+  constexpr int UPW = NU / NW;
+  constexpr int OFF_SA = (UA + UB) * 1024, OFF_SB = OFF_SA + KB * BIG_BM * 4;
+  constexpr int SLOT = OFF_SB + KB * BIG_BN * 4;
+  static_assert(NU % NW == 0 && (UA + UB) % NW == 0 && USA % NW == 0,
+                "every unit index j must be of one kind across the waves");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * SLOT];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-aware tile id: workgroup i runs on XCD i % 8.
+  const int nblk = gridDim.x, id = blockIdx.x;
+  const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
+  const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
+  const int tmi = W / tiles_n;
+  const int m0 = tmi * BIG_BM, n0 = (W - tmi * tiles_n) * BIG_BN;
+  const int hc0 = n0 >> 1;
+  const int nb = K / QK, nst = K / BK;
+
+  auto b_row = [&](int nl) -> int {
+    if (!GEGLU) return n0 + nl < N ? n0 + nl : N - 1;
+    const int t = nl >> 5;
+    int c = hc0 + (t >> 1) * 32 + (nl & 31);
+    if (c >= F) c = F - 1;
+    return (t & 1) ? F + c : c;
+  };
+  auto a_row = [&](int ml) -> int { return m0 + ml < M ? m0 + ml : M - 1; };
+
+  // this wave's DMA units: uniform base + per-lane offset.  Unit u = 4 j + wave:
+  // [0, UA) A rows, [UA, UA+UB) B rows (8 rows x 128 B, +128 B per stage),
+  // then A scales and B scales (64 rows of one block, +16 B per stage).
+  const int rsub = lane >> 3, pch = lane & 7;
+  const int8_t* ubase[UPW];
+  int uvoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; j++) {
+    const int u = j * NW + wave;
+    if (u < UA) {
+      const int row = u * 8 + rsub;
+      ubase[j] = A;
+      uvoff[j] = a_row(row) * K + ((pch ^ big_swz(row)) << 4);
+    } else if (u < UA + UB) {
+      const int row = (u - UA) * 8 + rsub;
+      ubase[j] = B;
+      uvoff[j] = b_row(row) * K + ((pch ^ big_swz(row)) << 4);
+    } else if (u < UA + UB + USA) {
+      const int v = u - UA - UB, kb = v / (BIG_BM / 64);
+      ubase[j] = reinterpret_cast<const int8_t*>(dA);
+      uvoff[j] = (a_row((v % (BIG_BM / 64)) * 64 + lane) * nb + kb) * 4;
+    } else {
+      const int v = u - UA - UB - USA, kb = v / (BIG_BN / 64);
+      ubase[j] = reinterpret_cast<const int8_t*>(dB);
+      uvoff[j] = (b_row((v % (BIG_BN / 64)) * 64 + lane) * nb + kb) * 4;
+    }
+  }
+  auto lds_unit = [&](int slot, int u) -> uint32_t {
+    int off;
+    if (u < UA + UB) off = u * 1024;
+    else off = OFF_SA + (u - UA - UB) * 256;   // A then B scales, [block][row]
+    return lds_u32(ring + slot * SLOT + off);
+  };
+  auto issue = [&](int st, int slot) {
+#pragma unroll
+    for (int j = 0; j < UPW; j++) {
+      const int u = j * NW + wave;
+      if (j * NW < UA + UB) dma16(ubase[j] + st * BK, uvoff[j], lds_unit(slot, u));
+      else dma4(ubase[j] + st * KB * 4, uvoff[j], lds_unit(slot, u));
+    }
+  };
+  issue(0, 0);
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int arow = wave * 32 + lrow;
+  // operand chunk of block kb: bytes 32 kb + 16 lhalf of the row
+  int offA[KB], offB[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    const int ch = 2 * kb + lhalf;
+    offA[kb] = arow * BK + ((ch ^ big_swz(arow)) << 4);
+    offB[kb] = (BIG_BM + lrow) * BK + ((ch ^ big_swz(lrow)) << 4);   // tile tn: + 32 tn rows
+  }
+  // A scales of rows 32 w + 8 g + 4 lhalf + (0..3): b128 g at + 32 g
+  const int offX = OFF_SA + (wave * 32 + 4 * lhalf) * 4;
+  const int offW = OFF_SB + lrow * 4;   // B scale of tile tn, block kb: + (kb * 128 + 32 tn) * 4
+  v16i magic;
+#pragma unroll
+  for (int i = 0; i < 16; i++) magic[i] = MAGIC;
+  float acc[TN][16];
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[tn][r] = 0.0f;
+
+  auto stage = [&](const uint8_t* slot) {
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+      const v4i af = *reinterpret_cast<const v4i*>(slot + offA[kb]);
+      v4f xv[4];
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        xv[g] = *reinterpret_cast<const v4f*>(slot + offX + kb * BIG_BM * 4 + 32 * g);
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const v4i bf = *reinterpret_cast<const v4i*>(slot + offB[kb] + 32 * BK * tn);
+        const float wd = *reinterpret_cast<const float*>(slot + offW + (kb * BIG_BN + 32 * tn) * 4);
+        const float wc = wd * NEG_MAGIC;
+        const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, magic, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float t = fmaf(__int_as_float(d[r]), wd, wc);   // round(S * d_w)
+          float u = t * xv[r >> 2][r & 3];                 // round(. * d_x)
+          acc[tn][r] = acc[tn][r] + u;                     // round(acc + .)
+        }
+      }
+    }
+  };
+
+#pragma unroll 1
+  for (int st = 0; st < nst; st++) {
+    const int r = st & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (st + 1 < nst) issue(st + 1, r ^ 1);
+    stage(ring + r * SLOT);
+  }
+
+  // output rows of register r: 32 w + 8 (r >> 2) + 4 lhalf + (r & 3)
+  const int row0 = m0 + wave * 32 + 4 * lhalf;
+  if constexpr (!GEGLU) {
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      const int gn = n0 + 32 * tn + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int gm = row0 + 8 * (r >> 2) + (r & 3);
+        if (gm < M && gn < N) C[(int64_t)gm * ldc + gn] = acc[tn][r];
+      }
+    }
+  } else {
+    // h block p (columns c + 32 p .. +31) of row (r, lhalf) is lane lrow's
+    // value of geglu(acc[2p][r], acc[2p+1][r]).  Scale table per wave in the
+    // ring slot of stage nst - 2, which every wave finished before the last
+    // barrier: amax[lhalf][p][r], then (id, dq) per entry.
+    const int nbh = F / QK;
+    float* tab = reinterpret_cast<float*>(ring + (((nst - 1) & 1) ^ 1) * SLOT) + wave * 192;
+    float h[2][16];
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        h[p][r] = geglu_scalar(acc[2 * p][r], acc[2 * p + 1][r]);
+        const float v = max32_hi(fmaxf(0.0f, fabsf(h[p][r])));
+        if (lrow == 31) tab[lhalf * 32 + p * 16 + r] = v;
+      }
+    // LDS serves a wave's accesses in order; the fences keep the compiler
+    // from moving the table accesses across each other.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    {
+      const QScale q = q8_scale(tab[lane]);
+      tab[64 + lane] = q.id;
+      tab[128 + lane] = q.dq;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int c = hc0;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      const int hb = c + 32 * p;   // first column of the h block
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int gm = row0 + 8 * (r >> 2) + (r & 3);
+        const int e = lhalf * 32 + p * 16 + r;
+        if (gm < M && hb < F) {
+          Hq[(int64_t)gm * F + hb + lrow] = (int8_t)quant_round(h[p][r] * tab[64 + e]);
+          if (lrow == 0) dH[(int64_t)gm * nbh + (hb >> 5)] = tab[128 + e];
+        }
+      }
+    }
+  }
+}
+
+template <bool GEGLU>
+hipError_t run_big(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                   float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K,
+                   int64_t ldc, int64_t F, hipStream_t s) {
+  const int64_t tiles_n = (Nrows + BIG_BN - 1) / BIG_BN;
+  const int64_t tiles = ((M + BIG_BM - 1) / BIG_BM) * tiles_n;
+  gemm_i8_big_kernel<GEGLU><<<dim3((unsigned)tiles), 256, 0, s>>>(
+      xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
+  return hipGetLastError();
+}
+
+// The large-M kernel addresses operands with 32-bit offsets.
+inline bool big_ok(int64_t M, int64_t Nrows, int64_t K) {
+  return K % BK == 0 && M * K < (int64_t(1) << 31) && Nrows * K < (int64_t(1) << 31);
+}
+
 template <int BM, int BN, int WM, int WN, bool GEGLU>
-hipError_t run(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw, float* y,
+hipError_t run(const int8_t* xq,const float* dx, const int8_t* wq, const float* dw, float* y,
                int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K, int64_t ldc,
                int64_t F, hipStream_t s) {
   dim3 grid((unsigned)((Nrows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
@@ -589,6 +823,8 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
   if (M == 0 || N == 0) return hipSuccess;
   if (small_ok(M, K))
     return run_small<1, 2, 1, false, 3>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+  if (big_ok(M, N, K))
+    return run_big<false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
   int64_t big_tiles = ((M + 127) / 128) * ((N + 127) / 128);
   if (big_tiles >= 512)
     return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
@@ -601,6 +837,8 @@ hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t*
   if (M == 0 || F == 0) return hipSuccess;
   if (small_ok(M, K))
     return run_small<2, 2, 2, true, 3>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+  if (big_ok(M, 2 * F, K))
+    return run_big<true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
   int64_t big_tiles = ((M + 127) / 128) * ((2 * F + 127) / 128);
   if (big_tiles >= 512)
     return run<128, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);

@@ -112,6 +112,35 @@ def test_matmul_int8_large_tile_path(ctx, oracle):
     assert_bits_equal(y, oracle.matmul(x, wb, n), "large-tile matmul")
 
 
+@pytest.mark.parametrize("m,k,n", [(2100, 128, 70), (2177, 256, 300), (3000, 1152, 129),
+                                   (2049, 96, 200)])
+def test_matmul_int8_large_m_ragged(ctx, oracle, m, k, n):
+    """Large-M kernels with partial row/column tiles, one K stage, and K that is not a
+    multiple of 128 (the register-staged fallback)."""
+    say(f"matmul INT8_EXACT large-M ragged m={m} k={k} n={n}")
+    x = oracle.normal(m * k, seed=300 + m).reshape(m, k)
+    wb = oracle.q8_0_weight(n, k, seed=400 + n)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    y = host(ops.q8_0_matmul(ctx, w, dev(x), INT8_EXACT))
+    assert_bits_equal(y, oracle.matmul(x, wb, n), f"matmul {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,H,F", [(2200, 256, 96), (2500, 128, 160)])
+def test_mlp_large_m_ragged(ctx, oracle, m, H, F):
+    """GeGLU epilogue of the large-M kernel when the last tile holds a partial h block
+    pair (F not a multiple of 64) and M is not a multiple of 128."""
+    say(f"mlp large-M ragged m={m} H={H} F={F}")
+    x = oracle.normal(m * H, seed=m + 6).reshape(m, H)
+    gb, ub, db = (oracle.q8_0_weight(F, H, seed=21), oracle.q8_0_weight(F, H, seed=22),
+                  oracle.q8_0_weight(H, F, seed=23))
+    g = Q8Weight.from_gguf(ctx, gb, F, H)
+    u = Q8Weight.from_gguf(ctx, ub, F, H)
+    d = Q8Weight.from_gguf(ctx, db, H, F)
+    gu, views = Q8Weight.concat(ctx, [g, u])
+    y = host(ops.mlp(ctx, gu, d, dev(x), INT8_EXACT))
+    assert_bits_equal(y, _mlp_ref(oracle, x, gb, ub, db, H, F), "mlp")
+
+
 def test_matmul_deterministic_and_c3_rows(ctx, oracle):
     """C3 size (M = 16384): two runs are bit-identical (no LDS race) and 64 random
     rows match the oracle bit for bit."""
