@@ -53,6 +53,12 @@ SIGNATURES = {
     "glypr_hip_rmsnorm_mlp": (_int, [_vp, _vp, _vp, _vp, _vp, _f32, _vp, _i64, _int, _vp]),
     "glypr_hip_q8_0_embed_gather": (_int, [_vp, _vp, _vp, _i64, _f32, _vp, _vp]),
     "glypr_hip_pool_normalize": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp]),
+    "glypr_hip_quantize_binary": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "glypr_hip_quantize_int8": (_int, [_vp, _vp, _i64, _vp, _vp]),
+    "glypr_hip_hamming": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp]),
+    "glypr_hip_binary_cosine": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp]),
+    "glypr_hip_int8_dot": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp]),
+    "glypr_hip_int8_cosine": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp]),
     "glypr_hip_attention": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _vp, _i64, _i64, _i64, _i64,
                                    _i64, _vp, _vp]),
     "glypr_hip_model_create": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
@@ -84,7 +90,7 @@ SIGNATURES = {
     "glypr_hip_kernel_name": (ctypes.c_char_p, [_int]),
 }
 
-KERNEL_COUNT = 16
+KERNEL_COUNT = 18
 
 
 class GlyprError(RuntimeError):

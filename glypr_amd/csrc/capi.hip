@@ -6,11 +6,13 @@
 // launched or allocated before all three pass, so every error path can be
 // exercised on a machine without a GPU.
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
 
 #include <new>
+#include <vector>
 
 #include "host_common.hpp"
 #include "internal.hpp"
@@ -165,6 +167,7 @@ int glypr_hip_ctx_destroy(glypr_hip_ctx* ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ids) (void)hipFree(ctx->ids);
     if (ctx->mask) (void)hipFree(ctx->mask);
+    if (ctx->bcos) (void)hipFree(ctx->bcos);
     for (auto& r : ctx->prof) {
       (void)hipEventDestroy(r.start);
       (void)hipEventDestroy(r.stop);
@@ -500,10 +503,132 @@ int glypr_hip_pool_normalize(glypr_hip_ctx* ctx, const float* tokens, const uint
   return GLYPR_OK;
 }
 
+// ---- output-vector codecs (util.rs:52-197) -------------------------------
+
+int glypr_hip_quantize_binary(glypr_hip_ctx* ctx, const float* x, int64_t n, int64_t dim,
+                              uint64_t* out, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(n >= 0 && dim > 0, GLYPR_ERR_SHAPE, "shape (n=%lld, dim=%lld)", (long long)n,
+              (long long)dim);
+  GLYPR_CHECK(dim % 64 == 0, GLYPR_ERR_SHAPE,
+              "binary quantization requires dim to be a multiple of 64, got %lld",
+              (long long)dim);
+  GLYPR_CHECK(x != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "x or out is NULL");
+  GLYPR_CHECK(aligned16(x) && aligned16(out), GLYPR_ERR_ALIGNMENT,
+              "x and out must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  LAUNCH(GLYPR_K_VEC_ENCODE, (hipStream_t)stream,
+         launch_quantize_binary(x, n, dim, out, (hipStream_t)stream), "quantize_binary launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_quantize_int8(glypr_hip_ctx* ctx, const float* x, int64_t count, int8_t* out,
+                            glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(count >= 0, GLYPR_ERR_SHAPE, "count %lld", (long long)count);
+  GLYPR_CHECK(x != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "x or out is NULL");
+  GLYPR_CHECK(aligned16(x) && aligned16(out), GLYPR_ERR_ALIGNMENT,
+              "x and out must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  LAUNCH(GLYPR_K_VEC_ENCODE, (hipStream_t)stream,
+         launch_quantize_int8(x, count, out, (hipStream_t)stream), "quantize_int8 launch");
+  return GLYPR_OK;
+}
+
+static int check_pairs(int64_t na, int64_t nb, int64_t len, const void* a, const void* b,
+                       const void* out) {
+  GLYPR_CHECK(na >= 0 && nb >= 0 && len >= 0, GLYPR_ERR_SHAPE, "shape (na=%lld, nb=%lld, %lld)",
+              (long long)na, (long long)nb, (long long)len);
+  GLYPR_CHECK(a != nullptr && b != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG,
+              "a, b or out is NULL");
+  GLYPR_CHECK(aligned16(a) && aligned16(b) && aligned16(out), GLYPR_ERR_ALIGNMENT,
+              "a, b and out must be 16-byte aligned");
+  return GLYPR_OK;
+}
+
+int glypr_hip_hamming(glypr_hip_ctx* ctx, const uint64_t* a, int64_t na, const uint64_t* b,
+                      int64_t nb, int64_t words, uint32_t* out, glypr_stream stream) {
+  clear_error();
+  RET_IF(check_pairs(na, nb, words, a, b, out));
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  LAUNCH(GLYPR_K_VEC_SEARCH, (hipStream_t)stream,
+         launch_hamming(a, na, b, nb, words, out, (hipStream_t)stream), "hamming launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_binary_cosine(glypr_hip_ctx* ctx, const uint64_t* a, int64_t na,
+                            const uint64_t* b, int64_t nb, int64_t words, float* out,
+                            glypr_stream stream) {
+  clear_error();
+  RET_IF(check_pairs(na, nb, words, a, b, out));
+  GLYPR_CHECK(words <= (int64_t(1) << 20), GLYPR_ERR_SHAPE, "words %lld > 2^20",
+              (long long)words);
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const int64_t dim = words * 64;
+  if (ctx->bcos_dim != dim) {
+    // binary_cosine_similarity evaluates (PI * (h as f32 / dim as f32)).cos() in
+    // f32 with the platform libm; h is an integer in [0, dim], so the table is
+    // that exact expression per h.  dim 0 -> 1.0 (the reference's early return).
+    std::vector<float> host((size_t)dim + 1);
+    const float pi = 3.14159265358979323846f;
+    for (int64_t h = 0; h <= dim; h++)
+      host[(size_t)h] = dim == 0 ? 1.0f : cosf(pi * ((float)h / (float)dim));
+    RET_IF(ensure_staging(ctx->bcos, ctx->bcos_cap, host.size()));
+    GLYPR_TRY_HIP(hipMemcpy(ctx->bcos, host.data(), host.size() * sizeof(float),
+                            hipMemcpyHostToDevice),
+                  "binary cosine table upload");
+    ctx->bcos_dim = dim;
+  }
+  LAUNCH(GLYPR_K_VEC_SEARCH, (hipStream_t)stream,
+         launch_binary_cosine(a, na, b, nb, words, ctx->bcos, out, (hipStream_t)stream),
+         "binary_cosine launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_int8_dot(glypr_hip_ctx* ctx, const int8_t* a, int64_t na, const int8_t* b,
+                       int64_t nb, int64_t dim, int32_t* out, glypr_stream stream) {
+  clear_error();
+  RET_IF(check_pairs(na, nb, dim, a, b, out));
+  GLYPR_CHECK(dim <= 65536, GLYPR_ERR_SHAPE, "dim %lld > 65536 (i32 sums must not wrap)",
+              (long long)dim);
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  LAUNCH(GLYPR_K_VEC_SEARCH, (hipStream_t)stream,
+         launch_int8_dot(a, na, b, nb, dim, out, (hipStream_t)stream), "int8_dot launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_int8_cosine(glypr_hip_ctx* ctx, const int8_t* a, int64_t na, const int8_t* b,
+                          int64_t nb, int64_t dim, float* out, glypr_stream stream) {
+  clear_error();
+  RET_IF(check_pairs(na, nb, dim, a, b, out));
+  GLYPR_CHECK(dim <= 65536, GLYPR_ERR_SHAPE, "dim %lld > 65536 (i32 sums must not wrap)",
+              (long long)dim);
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  RET_IF(ensure_ws(ctx, (size_t)(na + nb) * sizeof(int32_t)));
+  LAUNCH(GLYPR_K_VEC_SEARCH, (hipStream_t)stream,
+         launch_int8_cosine(a, na, b, nb, dim, (int32_t*)ctx->ws, out, (hipStream_t)stream),
+         "int8_cosine launch");
+  return GLYPR_OK;
+}
+
 static const char* const kKernelNames[GLYPR_K_COUNT] = {
     "quantize",   "rmsnorm_quant",  "gemm_i8", "gemm_i8_geglu", "to_bf16", "rmsnorm_bf16",
     "gemm_bf16",  "gemm_bf16_geglu", "rmsnorm", "geglu",         "gather",  "dequant",
-    "pool",       "qkv_post",       "attention", "residual_norm"};
+    "pool",       "qkv_post",       "attention", "residual_norm", "vec_encode", "vec_search"};
 
 const char* glypr_hip_kernel_name(int id) {
   return (id >= 0 && id < GLYPR_K_COUNT) ? kKernelNames[id] : "";

@@ -49,6 +49,9 @@ struct glypr_hip_ctx {
   size_t ids_cap = 0;
   uint8_t* mask = nullptr;  // pooling-mask staging
   size_t mask_cap = 0;
+  float* bcos = nullptr;    // binary-cosine table cos(pi * h / dim), h = 0 .. dim
+  size_t bcos_cap = 0;
+  int64_t bcos_dim = -1;    // dim the table holds (-1: none)
 };
 
 namespace glypr {
@@ -114,6 +117,21 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
 hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t* wq,
                                 const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
                                 int64_t K, hipStream_t s);
+
+// ---- k_vec.hip ----
+hipError_t launch_quantize_binary(const float* x, int64_t n, int64_t dim, uint64_t* out,
+                                  hipStream_t s);
+hipError_t launch_quantize_int8(const float* x, int64_t count, int8_t* out, hipStream_t s);
+hipError_t launch_hamming(const uint64_t* a, int64_t na, const uint64_t* b, int64_t nb,
+                          int64_t words, uint32_t* out, hipStream_t s);
+// table: cos(pi * h / (64 words)) for h = 0 .. 64 words (f32, device)
+hipError_t launch_binary_cosine(const uint64_t* a, int64_t na, const uint64_t* b, int64_t nb,
+                                int64_t words, const float* table, float* out, hipStream_t s);
+hipError_t launch_int8_dot(const int8_t* a, int64_t na, const int8_t* b, int64_t nb, int64_t dim,
+                           int32_t* out, hipStream_t s);
+// norms: scratch of na + nb int32
+hipError_t launch_int8_cosine(const int8_t* a, int64_t na, const int8_t* b, int64_t nb,
+                              int64_t dim, int32_t* norms, float* out, hipStream_t s);
 
 // ---- k_gemm_bf16.hip ----
 hipError_t launch_gemm_bf16(const uint16_t* xb, const int8_t* wq, const float* dw, float* y,

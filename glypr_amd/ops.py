@@ -228,6 +228,75 @@ def pool_normalize(ctx: Context, tokens: torch.Tensor, mask=None, trunc: int = 0
     return out
 
 
+# ---- output-vector codecs (glypr-core util.rs:52-197) ----------------------
+# Binary codes are u64 words carried in int64 tensors (same bits); hamming
+# distances come back as int32 (they never exceed 2^31).
+
+def quantize_binary(ctx: Context, x: torch.Tensor, out: Optional[torch.Tensor] = None
+                    ) -> torch.Tensor:
+    """quantize_binary (util.rs:52-71) per row: f32 [n, dim] -> words [n, dim/64]."""
+    ctx._check_tensor(x, "x")
+    n, dim = x.shape
+    if out is None:
+        out = torch.empty((n, dim // 64), dtype=torch.int64, device=x.device)
+    check(lib().glypr_hip_quantize_binary(ctx.handle, _ptr(x), n, dim, _ptr(out), ctx.stream))
+    return out
+
+
+def quantize_int8(ctx: Context, x: torch.Tensor, out: Optional[torch.Tensor] = None
+                  ) -> torch.Tensor:
+    """quantize_int8 (util.rs:128-133), elementwise."""
+    ctx._check_tensor(x, "x")
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    check(lib().glypr_hip_quantize_int8(ctx.handle, _ptr(x), x.numel(), _ptr(out), ctx.stream))
+    return out
+
+
+def _pairs(ctx: Context, a: torch.Tensor, b: torch.Tensor, dtype, name: str):
+    ctx._check_tensor(a, "a", dtype)
+    ctx._check_tensor(b, "b", dtype)
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1]:
+        raise ValueError(f"{name}: a [na, d] and b [nb, d] must share d")
+    return a.shape[0], b.shape[0], a.shape[1]
+
+
+def hamming(ctx: Context, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """hamming_distance (util.rs:75-109) for all pairs -> int32 [na, nb]."""
+    na, nb, w = _pairs(ctx, a, b, torch.int64, "hamming")
+    out = torch.empty((na, nb), dtype=torch.int32, device=a.device)
+    check(lib().glypr_hip_hamming(ctx.handle, _ptr(a), na, _ptr(b), nb, w, _ptr(out),
+                                  ctx.stream))
+    return out
+
+
+def binary_cosine(ctx: Context, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """binary_cosine_similarity (util.rs:112-119) for all pairs -> f32 [na, nb]."""
+    na, nb, w = _pairs(ctx, a, b, torch.int64, "binary_cosine")
+    out = torch.empty((na, nb), dtype=torch.float32, device=a.device)
+    check(lib().glypr_hip_binary_cosine(ctx.handle, _ptr(a), na, _ptr(b), nb, w, _ptr(out),
+                                        ctx.stream))
+    return out
+
+
+def int8_dot(ctx: Context, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """int8_dot_product (util.rs:137-176) for all pairs -> int32 [na, nb]."""
+    na, nb, d = _pairs(ctx, a, b, torch.int8, "int8_dot")
+    out = torch.empty((na, nb), dtype=torch.int32, device=a.device)
+    check(lib().glypr_hip_int8_dot(ctx.handle, _ptr(a), na, _ptr(b), nb, d, _ptr(out),
+                                   ctx.stream))
+    return out
+
+
+def int8_cosine(ctx: Context, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """int8_cosine_similarity (util.rs:181-197) for all pairs -> f32 [na, nb]."""
+    na, nb, d = _pairs(ctx, a, b, torch.int8, "int8_cosine")
+    out = torch.empty((na, nb), dtype=torch.float32, device=a.device)
+    check(lib().glypr_hip_int8_cosine(ctx.handle, _ptr(a), na, _ptr(b), nb, d, _ptr(out),
+                                      ctx.stream))
+    return out
+
+
 def attention(ctx: Context, qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor,
               eps: float, cos_t: torch.Tensor, sin_t: torch.Tensor, n_heads: int, n_kv_heads: int,
               head_dim: int = 256, window: int = 0,

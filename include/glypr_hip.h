@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define GLYPR_HIP_ABI_VERSION 2
+#define GLYPR_HIP_ABI_VERSION 3
 
 typedef enum glypr_status {
   GLYPR_OK = 0,
@@ -172,6 +172,39 @@ int glypr_hip_pool_normalize(glypr_hip_ctx* ctx, const float* tokens, const uint
                              int64_t t, int64_t d, int64_t trunc, float* out,
                              glypr_stream stream);
 
+/* ---- output-vector codecs (serving) --------------------------------------- */
+
+/* quantize_binary (util.rs:52-71): bit i of word i/64 is x[i] > 0 (NaN -> 0).
+ * x [n][dim] f32 -> out [n][dim/64] u64.  dim % 64 != 0 -> GLYPR_ERR_SHAPE
+ * (the reference's bail). */
+int glypr_hip_quantize_binary(glypr_hip_ctx* ctx, const float* x, int64_t n, int64_t dim,
+                              uint64_t* out, glypr_stream stream);
+/* quantize_int8 (util.rs:128-133): (x * 127).round().clamp(-127, 127) as i8,
+ * round half away from zero, NaN -> 0.  x [count] -> out [count]. */
+int glypr_hip_quantize_int8(glypr_hip_ctx* ctx, const float* x, int64_t count, int8_t* out,
+                            glypr_stream stream);
+/* hamming_distance (util.rs:75-109) between every pair: out[i][j] =
+ * popcount(a_i XOR b_j) over `words` u64 words.  a [na][words],
+ * b [nb][words] -> out [na][nb] u32. */
+int glypr_hip_hamming(glypr_hip_ctx* ctx, const uint64_t* a, int64_t na, const uint64_t* b,
+                      int64_t nb, int64_t words, uint32_t* out, glypr_stream stream);
+/* binary_cosine_similarity (util.rs:112-119) between every pair:
+ * cos(PI * (h as f32 / dim as f32)) in f32 with dim = 64 words, evaluated by
+ * the host libm's cosf once per h (a table per dim); words 0 -> 1.0.
+ * -> out [na][nb] f32. */
+int glypr_hip_binary_cosine(glypr_hip_ctx* ctx, const uint64_t* a, int64_t na,
+                            const uint64_t* b, int64_t nb, int64_t words, float* out,
+                            glypr_stream stream);
+/* int8_dot_product (util.rs:137-176) between every pair, exact i32 on int8
+ * MFMA.  a [na][dim], b [nb][dim] -> out [na][nb].  dim <= 65536. */
+int glypr_hip_int8_dot(glypr_hip_ctx* ctx, const int8_t* a, int64_t na, const int8_t* b,
+                       int64_t nb, int64_t dim, int32_t* out, glypr_stream stream);
+/* int8_cosine_similarity (util.rs:181-197) between every pair:
+ * dot / (sqrt(|a|^2) * sqrt(|b|^2)) in f32, clamped to [-1, 1]; 0 when either
+ * squared norm is 0.  -> out [na][nb] f32.  dim <= 65536. */
+int glypr_hip_int8_cosine(glypr_hip_ctx* ctx, const int8_t* a, int64_t na, const int8_t* b,
+                          int64_t nb, int64_t dim, float* out, glypr_stream stream);
+
 /* ---- attention core ------------------------------------------------------ */
 
 /* SelfAttention::forward between the projections and o_proj
@@ -293,7 +326,9 @@ typedef enum glypr_kernel_id {
   GLYPR_K_QKV_POST = 13,      /* q/k/v norms + RoPE + f16 split */
   GLYPR_K_ATTENTION = 14,     /* flash attention */
   GLYPR_K_RESIDUAL_NORM = 15, /* residual + RMSNorm (+ next prologue) */
-  GLYPR_K_COUNT = 16
+  GLYPR_K_VEC_ENCODE = 16,    /* binary / int8 output-vector quantization */
+  GLYPR_K_VEC_SEARCH = 17,    /* all-pairs hamming / cosine over encoded vectors */
+  GLYPR_K_COUNT = 18
 } glypr_kernel_id;
 
 /* The per-op device timing of forward_profiled (profile.rs:53-56, 63-429),

@@ -421,6 +421,75 @@ float orc_cosine(const float* a, const float* b, int64_t n) {
 }
 
 /* ======================================================================== */
+/* Output-vector codecs (glypr-core util.rs:52-197).                         */
+/* ======================================================================== */
+
+/* quantize_binary (util.rs:52-71): dim % 64 != 0 is an error (-1); bit i of
+ * word i / 64 is set when x[i] > 0.0 (false for NaN and -0.0). */
+int orc_quantize_binary(const float* x, int64_t dim, uint64_t* words) {
+  if (dim % 64 != 0) return -1;
+  for (int64_t w = 0; w < dim / 64; w++) words[w] = 0;
+  for (int64_t i = 0; i < dim; i++)
+    if (x[i] > 0.0f) words[i / 64] |= (uint64_t)1 << (i % 64);
+  return 0;
+}
+
+/* hamming_distance (util.rs:75-109): total popcount of a XOR b.  The
+ * reference's four-lane partial sums are integers, so the order is free. */
+uint32_t orc_hamming(const uint64_t* a, const uint64_t* b, int64_t words) {
+  uint32_t s = 0;
+  for (int64_t w = 0; w < words; w++) s += (uint32_t)__builtin_popcountll(a[w] ^ b[w]);
+  return s;
+}
+
+/* binary_cosine_similarity (util.rs:112-119): dim = 64 words; dim 0 -> 1.0;
+ * (PI * (h as f32 / dim as f32)).cos() in f32 with the platform cosf, as
+ * Rust's f32::cos calls it. */
+float orc_binary_cosine(const uint64_t* a, const uint64_t* b, int64_t words) {
+  const int64_t dim = words * 64;
+  if (dim == 0) return 1.0f;
+  const float h = (float)orc_hamming(a, b, words);
+  return cosf(3.14159265358979323846f * (h / (float)dim));
+}
+
+/* quantize_int8 (util.rs:128-133): (v * 127.0).round().clamp(-127.0, 127.0)
+ * as i8.  f32 round is half away from zero (roundf); the saturating `as i8`
+ * cast maps NaN to 0. */
+void orc_quantize_int8(const float* x, int64_t n, int8_t* q) {
+  for (int64_t i = 0; i < n; i++) {
+    float r = roundf(x[i] * 127.0f);
+    if (r != r) {
+      q[i] = 0;
+      continue;
+    }
+    if (r < -127.0f) r = -127.0f;
+    if (r > 127.0f) r = 127.0f;
+    q[i] = (int8_t)r;
+  }
+}
+
+/* int8_dot_product (util.rs:137-176): i32 sum of products.  Rust release
+ * arithmetic wraps, so the sum is taken mod 2^32 (order-free). */
+int32_t orc_int8_dot(const int8_t* a, const int8_t* b, int64_t n) {
+  uint32_t s = 0;
+  for (int64_t i = 0; i < n; i++) s += (uint32_t)((int32_t)a[i] * (int32_t)b[i]);
+  return (int32_t)s;
+}
+
+/* int8_cosine_similarity (util.rs:181-197): 0 when either squared norm is 0,
+ * else (dot as f32 / (sqrt(na as f32) * sqrt(nb as f32))).clamp(-1, 1). */
+float orc_int8_cosine(const int8_t* a, const int8_t* b, int64_t n) {
+  const int32_t na = orc_int8_dot(a, a, n), nb = orc_int8_dot(b, b, n);
+  if (na == 0 || nb == 0) return 0.0f;
+  const int32_t dot = orc_int8_dot(a, b, n);
+  const float denom = sqrtf((float)na) * sqrtf((float)nb);
+  float c = (float)dot / denom;
+  if (c < -1.0f) c = -1.0f;
+  if (c > 1.0f) c = 1.0f;
+  return c;
+}
+
+/* ======================================================================== */
 /* Seeded synthetic inputs: SplitMix64, Box-Muller in double.                */
 /* ======================================================================== */
 

@@ -31,6 +31,10 @@
  *  - rope_tables: closed form (f32 product, float64 cos/sin).
  *  - encoder_layer / model_forward: an independent float64 statement of the
  *    whole forward at small dimensions, both layer types.
+ *  - vector codecs (binary / int8 quantize, hamming, int8 dot, both cosines):
+ *    the reference's own known answers (tests/quantization.rs:10-31,
+ *    util.rs:273-306), brute-force bit/integer sums, complement and symmetry
+ *    invariants, and the float64 cosine within f32 rounding.
  * Parity unpinned (no runnable reference vector exists offline): the exact f32
  * bit pattern of candle's vec_dot accumulation (scalar vec_dot_unopt order is
  * restated; AVX/NEON builds differ in the last bits), pulp's RMSNorm lane order
@@ -110,6 +114,14 @@ void orc_l2_normalize(const float* x, int64_t n, float* y);
 float orc_cosine(const float* a, const float* b, int64_t n);
 
 /* ---- Synthetic inputs (seeded, shared by tests, bench and the CPU baseline) ---- */
+/* Output-vector codecs (glypr-core util.rs:52-197). */
+int orc_quantize_binary(const float* x, int64_t dim, uint64_t* words);
+uint32_t orc_hamming(const uint64_t* a, const uint64_t* b, int64_t words);
+float orc_binary_cosine(const uint64_t* a, const uint64_t* b, int64_t words);
+void orc_quantize_int8(const float* x, int64_t n, int8_t* q);
+int32_t orc_int8_dot(const int8_t* a, const int8_t* b, int64_t n);
+float orc_int8_cosine(const int8_t* a, const int8_t* b, int64_t n);
+
 uint64_t orc_splitmix64(uint64_t* state);
 void orc_fill_normal(float* out, int64_t n, uint64_t seed, float mean, float stddev);
 void orc_fill_uniform_ids(uint32_t* ids, int64_t n, uint64_t seed, uint32_t vocab);

@@ -28,6 +28,8 @@ _f64p = ctypes.POINTER(ctypes.c_double)
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_i8p = ctypes.POINTER(ctypes.c_int8)
 _i64 = ctypes.c_int64
 
 
@@ -82,6 +84,12 @@ def lib():
             "orc_pool_normalize": (None, [_f32p, _u8p, _i64, _i64, _i64, _f32p]),
             "orc_l2_normalize": (None, [_f32p, _i64, _f32p]),
             "orc_cosine": (ctypes.c_float, [_f32p, _f32p, _i64]),
+            "orc_quantize_binary": (ctypes.c_int, [_f32p, _i64, _u64p]),
+            "orc_hamming": (ctypes.c_uint32, [_u64p, _u64p, _i64]),
+            "orc_binary_cosine": (ctypes.c_float, [_u64p, _u64p, _i64]),
+            "orc_quantize_int8": (None, [_f32p, _i64, _i8p]),
+            "orc_int8_dot": (ctypes.c_int32, [_i8p, _i8p, _i64]),
+            "orc_int8_cosine": (ctypes.c_float, [_i8p, _i8p, _i64]),
             "orc_fill_normal": (None, [_f32p, _i64, ctypes.c_uint64, ctypes.c_float,
                                        ctypes.c_float]),
             "orc_fill_uniform_ids": (None, [_u32p, _i64, ctypes.c_uint64, ctypes.c_uint32]),
@@ -248,6 +256,71 @@ def pool_normalize(tokens: np.ndarray, mask: Optional[np.ndarray] = None,
     out = np.empty(td, np.float32)
     mk = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
     lib().orc_pool_normalize(_p(tok, _f32p), _p(mk, _u8p), t, d, trunc, _p(out, _f32p))
+    return out
+
+
+# --------------------------------------------------------- vector codecs ----
+# glypr-core util.rs:52-197; the C restatement holds the citations.
+
+def quantize_binary(x: np.ndarray) -> np.ndarray:
+    """f32 [n, dim] -> u64 [n, dim/64]; ValueError when dim % 64 != 0."""
+    x = np.ascontiguousarray(np.atleast_2d(x), dtype=np.float32)
+    n, dim = x.shape
+    out = np.zeros((n, max(dim // 64, 0)), np.uint64)
+    for r in range(n):
+        row = np.ascontiguousarray(x[r])
+        dst = out[r] if dim >= 64 else np.zeros(1, np.uint64)
+        if lib().orc_quantize_binary(_p(row, _f32p), dim, _p(dst, _u64p)) != 0:
+            raise ValueError(f"binary quantization requires a multiple of 64, got {dim}")
+    return out
+
+
+def hamming(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """All pairs: u64 [na, w], [nb, w] -> u32 [na, nb]."""
+    a = np.ascontiguousarray(np.atleast_2d(a), dtype=np.uint64)
+    b = np.ascontiguousarray(np.atleast_2d(b), dtype=np.uint64)
+    out = np.empty((a.shape[0], b.shape[0]), np.uint32)
+    for i in range(a.shape[0]):
+        for j in range(b.shape[0]):
+            out[i, j] = lib().orc_hamming(_p(a[i], _u64p), _p(b[j], _u64p), a.shape[1])
+    return out
+
+
+def binary_cosine(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(np.atleast_2d(a), dtype=np.uint64)
+    b = np.ascontiguousarray(np.atleast_2d(b), dtype=np.uint64)
+    out = np.empty((a.shape[0], b.shape[0]), np.float32)
+    for i in range(a.shape[0]):
+        for j in range(b.shape[0]):
+            out[i, j] = lib().orc_binary_cosine(_p(a[i], _u64p), _p(b[j], _u64p), a.shape[1])
+    return out
+
+
+def quantize_int8(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.int8)
+    lib().orc_quantize_int8(_p(x, _f32p), x.size, _p(out, _i8p))
+    return out
+
+
+def int8_dot(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """All pairs: i8 [na, d], [nb, d] -> i32 [na, nb]."""
+    a = np.ascontiguousarray(np.atleast_2d(a), dtype=np.int8)
+    b = np.ascontiguousarray(np.atleast_2d(b), dtype=np.int8)
+    out = np.empty((a.shape[0], b.shape[0]), np.int32)
+    for i in range(a.shape[0]):
+        for j in range(b.shape[0]):
+            out[i, j] = lib().orc_int8_dot(_p(a[i], _i8p), _p(b[j], _i8p), a.shape[1])
+    return out
+
+
+def int8_cosine(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(np.atleast_2d(a), dtype=np.int8)
+    b = np.ascontiguousarray(np.atleast_2d(b), dtype=np.int8)
+    out = np.empty((a.shape[0], b.shape[0]), np.float32)
+    for i in range(a.shape[0]):
+        for j in range(b.shape[0]):
+            out[i, j] = lib().orc_int8_cosine(_p(a[i], _i8p), _p(b[j], _i8p), a.shape[1])
     return out
 
 

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_symbols():
         assert hasattr(L, name), name
-    assert L.glypr_hip_abi_version() == 2
+    assert L.glypr_hip_abi_version() == 3
 
 
 def _has_gpu():
@@ -106,6 +106,34 @@ def test_elementwise_validation():
     assert L.glypr_hip_q8_0_embed_gather(NULL, NULL, FAKE, 4, 1.0, FAKE, NULL) == \
         _lib.GLYPR_ERR_INVALID_ARG
     assert L.glypr_hip_q8_0_embed_gather(NULL, FAKE, FAKE, -1, 1.0, FAKE, NULL) == \
+        _lib.GLYPR_ERR_SHAPE
+
+
+def test_vector_codec_validation():
+    """quantize_binary bails on dims that are not a multiple of 64
+    (util.rs:53-59, tests/quantization.rs:12-14); the all-pairs searches reject
+    negative sizes, NULL and misaligned buffers, and int8 dims whose i32 sums
+    could wrap, all before touching a device."""
+    L = _lib.lib()
+    for dim in (63, 65):
+        assert L.glypr_hip_quantize_binary(NULL, FAKE, 1, dim, FAKE, NULL) == \
+            _lib.GLYPR_ERR_SHAPE
+        assert "multiple of 64" in _lib.last_error()
+    assert L.glypr_hip_quantize_binary(NULL, FAKE, 1, 128, FAKE, NULL) == \
+        _lib.GLYPR_ERR_INVALID_ARG   # shape accepted; ctx NULL
+    assert L.glypr_hip_quantize_binary(NULL, MISALIGNED, 1, 128, FAKE, NULL) == \
+        _lib.GLYPR_ERR_ALIGNMENT
+    assert L.glypr_hip_quantize_int8(NULL, FAKE, -1, FAKE, NULL) == _lib.GLYPR_ERR_SHAPE
+    assert L.glypr_hip_quantize_int8(NULL, NULL, 4, FAKE, NULL) == _lib.GLYPR_ERR_INVALID_ARG
+    for fn in (L.glypr_hip_hamming, L.glypr_hip_binary_cosine, L.glypr_hip_int8_dot,
+               L.glypr_hip_int8_cosine):
+        assert fn(NULL, FAKE, -1, FAKE, 1, 4, FAKE, NULL) == _lib.GLYPR_ERR_SHAPE
+        assert fn(NULL, FAKE, 1, NULL, 1, 4, FAKE, NULL) == _lib.GLYPR_ERR_INVALID_ARG
+        assert fn(NULL, FAKE, 1, FAKE, 1, 4, MISALIGNED, NULL) == _lib.GLYPR_ERR_ALIGNMENT
+        assert fn(NULL, FAKE, 1, FAKE, 1, 4, FAKE, NULL) == _lib.GLYPR_ERR_INVALID_ARG
+    assert L.glypr_hip_int8_dot(NULL, FAKE, 1, FAKE, 1, 65537, FAKE, NULL) == \
+        _lib.GLYPR_ERR_SHAPE
+    assert L.glypr_hip_int8_cosine(NULL, FAKE, 1, FAKE, 1, 65537, FAKE, NULL) == \
         _lib.GLYPR_ERR_SHAPE
 
 
