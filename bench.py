@@ -183,6 +183,50 @@ def c1_linear(ctx, steps):
             "note": "quantize + GEMM, two kernels"}
 
 
+def vec_search(ctx, steps):
+    """Output-vector codecs (util.rs:52-197) on the serving path: encode a
+    1M x 256 f32 embedding database (MRL-256) to int8 and binary codes, then
+    score 32 queries against it (all pairs).  Each kernel is HBM-bound; the
+    algorithmic bytes are its reads plus its writes."""
+    import torch
+    from glypr_amd import ops
+    nb, na, dim = 1 << 20, 32, 256
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    emb = torch.randn((nb, dim), device="cuda", generator=g)
+    emb = emb / emb.norm(dim=1, keepdim=True)
+    q8 = ops.quantize_int8(ctx, emb)
+    qb = ops.quantize_binary(ctx, emb)
+    cases = {
+        "quantize_int8": (lambda: ops.quantize_int8(ctx, emb, out=q8), nb * dim * 5),
+        "quantize_binary": (lambda: ops.quantize_binary(ctx, emb, out=qb),
+                            nb * dim * 4 + nb * dim // 8),
+        "int8_cosine": (lambda: ops.int8_cosine(ctx, q8[:na].contiguous(), q8),
+                        2 * nb * dim + na * nb * 4),
+        "hamming": (lambda: ops.hamming(ctx, qb[:na].contiguous(), qb),
+                    nb * dim // 8 + na * nb * 4),
+        "binary_cosine": (lambda: ops.binary_cosine(ctx, qb[:na].contiguous(), qb),
+                          nb * dim // 8 + na * nb * 4),
+    }
+    out = {"database": f"{nb} x {dim} (MRL-256), {na} queries, all pairs"}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / steps * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "algorithmic_bytes": nbytes,
+                     "gb_per_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del emb, q8, qb
+    return out
+
+
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "traffic.json")
 
@@ -373,8 +417,8 @@ def main():
     ap.add_argument("--variant", choices=["int8", "bf16"], default="int8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
-    ap.add_argument("--extras", default="c1,c3,c4,c5",
-                    help="comma list of the extra workloads to run (c1, c3, c4, c5)")
+    ap.add_argument("--extras", default="c1,c3,c4,c5,vec",
+                    help="comma list of the extra workloads to run (c1, c3, c4, c5, vec)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain device copy of MIB MiB (calibrates rocprof "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -422,6 +466,8 @@ def main():
             del Lx
     if "c1" in todo:
         extra["c1_int8"] = c1_linear(ctx, args.steps)
+    if "vec" in todo:
+        extra["vec_codecs"] = vec_search(ctx, 20)
     if "c4" in todo or "c5" in todo:
         rng = np.random.default_rng(7)
         tensors = model_tensors(rng, 24, 262144)

@@ -618,7 +618,7 @@ int glypr_hip_int8_cosine(glypr_hip_ctx* ctx, const int8_t* a, int64_t na, const
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  RET_IF(ensure_ws(ctx, (size_t)(na + nb) * sizeof(int32_t)));
+  RET_IF(ensure_ws(ctx, (size_t)na * sizeof(int32_t)));
   LAUNCH(GLYPR_K_VEC_SEARCH, (hipStream_t)stream,
          launch_int8_cosine(a, na, b, nb, dim, (int32_t*)ctx->ws, out, (hipStream_t)stream),
          "int8_cosine launch");

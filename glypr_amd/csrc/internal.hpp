@@ -129,7 +129,7 @@ hipError_t launch_binary_cosine(const uint64_t* a, int64_t na, const uint64_t* b
                                 int64_t words, const float* table, float* out, hipStream_t s);
 hipError_t launch_int8_dot(const int8_t* a, int64_t na, const int8_t* b, int64_t nb, int64_t dim,
                            int32_t* out, hipStream_t s);
-// norms: scratch of na + nb int32
+// norms: scratch of na int32 (the queries' squared norms)
 hipError_t launch_int8_cosine(const int8_t* a, int64_t na, const int8_t* b, int64_t nb,
                               int64_t dim, int32_t* norms, float* out, hipStream_t s);
 

@@ -2,18 +2,20 @@
 // 52-197): 1-bit and symmetric int8 quantization of embeddings, and all-pairs
 // similarity between a query set and a database of encoded vectors.
 //
-//  - quantize_binary: bit i of word i/64 is (x[i] > 0).  One wave per word:
-//    lane i holds element 64 w + i and the wave's ballot IS the word.
+//  - quantize_binary: bit i of word i/64 is (x[i] > 0).  Lane i holds element
+//    64 w + i, so the wave's ballot IS word w; a wave handles 8 words per
+//    iteration (8 loads in flight) in a grid-stride loop.
 //  - quantize_int8: (x * 127).round().clamp(-127, 127) as i8, NaN -> 0.
 //  - hamming / binary cosine: one thread per database row, the row's words in
 //    registers, the query words read wave-uniformly (scalar loads); every
 //    database byte is read once from HBM.  The binary cosine looks up
 //    cos(pi * h / dim) in a host-built table (h takes only dim + 1 values).
 //  - int8 dot / int8 cosine: the all-pairs product is an int8 GEMM with exact
-//    i32 sums, so it runs on v_mfma_i32_16x16x32_i8: a wave holds 16 database
-//    rows against up to 64 queries, streaming K in 32-byte steps; the database
-//    is read once per 64-query group.  Integer sums are order-free, so the
-//    result equals the reference's 4-lane sum bit for bit.
+//    i32 sums, so it runs on v_mfma_i32_16x16x64_i8: a wave holds 16 database
+//    rows against up to 64 queries, streaming K in 64-byte steps (16 bytes per
+//    lane); the database is read once per 64-query group, and for the cosine
+//    its row norms are summed from the same fragments.  Integer sums are
+//    order-free, so the result equals the reference's 4-lane sum bit for bit.
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -23,15 +25,27 @@ namespace {
 
 typedef long v1l;
 
+constexpr int BIN_WPW = 8;   // words per wave per iteration
+
 __global__ void __launch_bounds__(256) quantize_binary_kernel(const float* __restrict__ x,
                                                               int64_t words,
                                                               unsigned long long* __restrict__ out) {
-  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (w >= words) return;   // whole wave exits together
   const int lane = threadIdx.x & 63;
-  const float v = x[w * 64 + lane];
-  const unsigned long long bits = __ballot(v > 0.0f);
-  if (lane == 0) out[w] = bits;
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t w0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * BIN_WPW; w0 < words;
+       w0 += nwaves * BIN_WPW) {
+    float v[BIN_WPW];
+#pragma unroll
+    for (int t = 0; t < BIN_WPW; t++)
+      v[t] = w0 + t < words ? x[(w0 + t) * 64 + lane] : 0.0f;
+    unsigned long long mine = 0;
+#pragma unroll
+    for (int t = 0; t < BIN_WPW; t++) {
+      const unsigned long long bits = __ballot(v[t] > 0.0f);
+      if (lane == t) mine = bits;
+    }
+    if (lane < BIN_WPW && w0 + lane < words) out[w0 + lane] = mine;
+  }
 }
 
 __global__ void __launch_bounds__(256) quantize_int8_kernel(const float* __restrict__ x,
@@ -107,28 +121,40 @@ __global__ void __launch_bounds__(256) int8_row_norms_kernel(const int8_t* __res
   if (lane == 0) out[r] = s;
 }
 
-// 8 bytes of row `row` at byte k (zero past dim).  FAST: dim % 8 == 0 and
-// 8-byte aligned rows, so a k < dim chunk is whole.
+// 16 bytes of row `row` at byte k (zero past dim).  FAST: dim % 16 == 0 and
+// 16-byte aligned rows, so a k < dim chunk is whole.
 template <bool FAST>
-__device__ __forceinline__ v1l load8(const int8_t* base, int64_t row, int64_t dim, int64_t k) {
+__device__ __forceinline__ v4i load16(const int8_t* base, int64_t row, int64_t dim, int64_t k) {
   const int8_t* p = base + row * dim + k;
-  if (FAST) return k < dim ? *reinterpret_cast<const v1l*>(p) : (v1l)0;
-  uint64_t v = 0;
+  if (FAST) return k < dim ? *reinterpret_cast<const v4i*>(p) : v4i{0, 0, 0, 0};
+  v4i v = {0, 0, 0, 0};
 #pragma unroll
-  for (int e = 0; e < 8; e++)
-    if (k + e < dim) v |= (uint64_t)(uint8_t)p[e] << (8 * e);
-  return (v1l)v;
+  for (int e = 0; e < 16; e++)
+    if (k + e < dim) v[e >> 2] |= (int)(uint8_t)p[e] << (8 * (e & 3));
+  return v;
+}
+
+__device__ __forceinline__ int32_t sq_sum16(v4i v) {
+  int32_t s = 0;
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    const int32_t b = (int8_t)(v[e >> 2] >> (8 * (e & 3)));
+    s += b * b;
+  }
+  return s;
 }
 
 // All-pairs int8 dot on MFMA.  A wave: database rows j0 .. j0+15 (output
 // column = lane & 15) against MT tiles of 16 queries (output rows
-// 16 t + 4 (lane >> 4) + r).  COS: the epilogue applies int8_cosine_similarity
-// with the precomputed row norms.
+// 16 t + 4 (lane >> 4) + r).  Lane (l16, lq) feeds bytes k0 + 16 lq .. +15 of
+// its rows to both operands.  COS: the epilogue applies
+// int8_cosine_similarity with the queries' norms and the database rows' norms
+// summed here from the same fragments.
 template <int MT, bool FAST, bool COS>
 __global__ void __launch_bounds__(256) int8_pairs_kernel(
     const int8_t* __restrict__ a, int64_t na, const int8_t* __restrict__ b, int64_t nb,
     int64_t dim, int32_t* __restrict__ out_d, const int32_t* __restrict__ norm_a,
-    const int32_t* __restrict__ norm_b, float* __restrict__ out_c) {
+    float* __restrict__ out_c) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, lq = lane >> 4;
   const int64_t j0 = ((int64_t)blockIdx.x * 4 + wave) * 16;
@@ -141,18 +167,24 @@ __global__ void __launch_bounds__(256) int8_pairs_kernel(
   v4i acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; t++) acc[t] = v4i{0, 0, 0, 0};
-  for (int64_t k0 = 0; k0 < dim; k0 += 32) {
-    const int64_t k = k0 + 8 * lq;
-    const v1l bf = load8<FAST>(b, jr, dim, k);
+  int32_t nsq = 0;
+#pragma unroll 2
+  for (int64_t k0 = 0; k0 < dim; k0 += 64) {
+    const int64_t k = k0 + 16 * lq;
+    const v4i bf = load16<FAST>(b, jr, dim, k);
+    if (COS) nsq += sq_sum16(bf);
 #pragma unroll
     for (int t = 0; t < MT; t++) {
-      const v1l af = load8<FAST>(a, ir[t], dim, k);
-      acc[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, acc[t], 0, 0, 0);
+      const v4i af = load16<FAST>(a, ir[t], dim, k);
+      acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af, bf, acc[t], 0, 0, 0);
     }
+  }
+  if (COS) {   // row l16's norm: its four 16-byte slices sit in lanes l16 + 16 lq
+    nsq += __shfl_xor(nsq, 16);
+    nsq += __shfl_xor(nsq, 32);
   }
   const int64_t j = j0 + l16;
   if (j >= nb) return;
-  const int32_t nbj = COS ? norm_b[j] : 0;
 #pragma unroll
   for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -164,8 +196,8 @@ __global__ void __launch_bounds__(256) int8_pairs_kernel(
       } else {
         const int32_t nai = norm_a[i];
         float c = 0.0f;
-        if (nai != 0 && nbj != 0) {
-          const float denom = sqrtf((float)nai) * sqrtf((float)nbj);
+        if (nai != 0 && nsq != 0) {
+          const float denom = sqrtf((float)nai) * sqrtf((float)nsq);
           c = fminf(fmaxf((float)acc[t][r] / denom, -1.0f), 1.0f);
         }
         out_c[i * nb + j] = c;
@@ -196,19 +228,27 @@ hipError_t run_hamming(const unsigned long long* a, int64_t na, const unsigned l
 #undef GLYPR_HAMMING_W
 }
 
-template <bool COS>
-hipError_t run_int8_pairs(const int8_t* a, int64_t na, const int8_t* b, int64_t nb, int64_t dim,
-                          int32_t* out_d, const int32_t* norm_a, const int32_t* norm_b,
-                          float* out_c, hipStream_t s) {
-  constexpr int MT = 4;
+template <int MT, bool COS>
+hipError_t run_int8_pairs_mt(const int8_t* a, int64_t na, const int8_t* b, int64_t nb,
+                             int64_t dim, int32_t* out_d, const int32_t* norm_a, float* out_c,
+                             hipStream_t s) {
   const dim3 grid((unsigned)((nb + 63) / 64), (unsigned)((na + 16 * MT - 1) / (16 * MT)));
-  if (dim % 8 == 0)
+  if (dim % 16 == 0)
     int8_pairs_kernel<MT, true, COS><<<grid, 256, 0, s>>>(a, na, b, nb, dim, out_d, norm_a,
-                                                          norm_b, out_c);
+                                                          out_c);
   else
     int8_pairs_kernel<MT, false, COS><<<grid, 256, 0, s>>>(a, na, b, nb, dim, out_d, norm_a,
-                                                           norm_b, out_c);
+                                                           out_c);
   return hipGetLastError();
+}
+
+// Query tiles per wave: just enough 16-row tiles for na (at most 4 per pass).
+template <bool COS>
+hipError_t run_int8_pairs(const int8_t* a, int64_t na, const int8_t* b, int64_t nb, int64_t dim,
+                          int32_t* out_d, const int32_t* norm_a, float* out_c, hipStream_t s) {
+  if (na <= 16) return run_int8_pairs_mt<1, COS>(a, na, b, nb, dim, out_d, norm_a, out_c, s);
+  if (na <= 32) return run_int8_pairs_mt<2, COS>(a, na, b, nb, dim, out_d, norm_a, out_c, s);
+  return run_int8_pairs_mt<4, COS>(a, na, b, nb, dim, out_d, norm_a, out_c, s);
 }
 
 }  // namespace
@@ -217,7 +257,8 @@ hipError_t launch_quantize_binary(const float* x, int64_t n, int64_t dim, uint64
                                   hipStream_t s) {
   const int64_t words = n * (dim / 64);
   if (words == 0) return hipSuccess;
-  quantize_binary_kernel<<<(unsigned)((words + 3) / 4), 256, 0, s>>>(
+  const int64_t blocks = (words + 4 * BIN_WPW - 1) / (4 * BIN_WPW);
+  quantize_binary_kernel<<<(unsigned)(blocks < 16384 ? blocks : 16384), 256, 0, s>>>(
       x, words, reinterpret_cast<unsigned long long*>(out));
   return hipGetLastError();
 }
@@ -247,19 +288,16 @@ hipError_t launch_binary_cosine(const uint64_t* a, int64_t na, const uint64_t* b
 hipError_t launch_int8_dot(const int8_t* a, int64_t na, const int8_t* b, int64_t nb, int64_t dim,
                            int32_t* out, hipStream_t s) {
   if (na == 0 || nb == 0) return hipSuccess;
-  return run_int8_pairs<false>(a, na, b, nb, dim, out, nullptr, nullptr, nullptr, s);
+  return run_int8_pairs<false>(a, na, b, nb, dim, out, nullptr, nullptr, s);
 }
 
 hipError_t launch_int8_cosine(const int8_t* a, int64_t na, const int8_t* b, int64_t nb,
                               int64_t dim, int32_t* norms, float* out, hipStream_t s) {
   if (na == 0 || nb == 0) return hipSuccess;
   int8_row_norms_kernel<<<(unsigned)((na + 3) / 4), 256, 0, s>>>(a, na, dim, norms);
-  hipError_t e = hipGetLastError();
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  int8_row_norms_kernel<<<(unsigned)((nb + 3) / 4), 256, 0, s>>>(b, nb, dim, norms + na);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return run_int8_pairs<true>(a, na, b, nb, dim, nullptr, norms, norms + na, out, s);
+  return run_int8_pairs<true>(a, na, b, nb, dim, nullptr, norms, out, s);
 }
 
 }  // namespace glypr
