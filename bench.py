@@ -363,7 +363,8 @@ def cpu_backbone_baseline(tensors, n_layers, vocab, t, seconds=10.0):
     n = 0
     while n == 0 or time.perf_counter() - t0 < seconds:
         rc = po.lib().orc_model_forward(ctypes.byref(cfg), u8("token_embd.weight"), layers,
-                                        f32("output_norm.weight"), ids.ctypes.data_as(po._u32p),
+                                        f32("output_norm.weight"), None, None, None,
+                                        ids.ctypes.data_as(po._u32p),
                                         t, 256, out.ctypes.data_as(po._f32p), None, cores)
         assert rc == 0
         n += 1

@@ -492,6 +492,19 @@ int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model*
   cfg.rope_theta_sliding = opt_f("rope.freq_base_swa", 10000.0);
   cfg.rope_theta_full = opt_f("rope.freq_base", 1000000.0);
   clear_error();
+  // TextPLE (model.rs:257-275) and the embedding projection (model.rs:472-473)
+  // when the file has them
+  int64_t pi = -1, oi = -1;
+  const bool has_ple = glypr_gguf_find_tensor(g, "per_layer_model_proj.weight", &pi) == GLYPR_OK;
+  const bool has_out = glypr_gguf_find_tensor(g, "output.weight", &oi) == GLYPR_OK;
+  clear_error();
+  cfg.ple_dim = 0;
+  if (has_ple) {
+    uint64_t pd = 0;
+    RET_IF(req_u("embedding_length_per_layer_input", &pd));
+    cfg.ple_dim = (int64_t)pd;
+  }
+  cfg.out_dim = has_out ? g->tensors[(size_t)oi].ne[1] : 0;
 
   glypr_model* m = nullptr;
   RET_IF(glypr_hip_model_create(ctx, &cfg, &m));
@@ -512,11 +525,20 @@ int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model*
   static const char* kLayer[] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate",
                                  "ffn_up", "ffn_down", "attn_norm", "post_attention_norm",
                                  "ffn_norm", "post_ffw_norm", "attn_q_norm", "attn_k_norm"};
-  for (uint64_t i = 0; rc == GLYPR_OK && i < layers; i++)
+  static const char* kPle[] = {"inp_gate", "proj", "post_norm", "layer_output_scale"};
+  for (uint64_t i = 0; rc == GLYPR_OK && i < layers; i++) {
     for (const char* nm : kLayer) {
       rc = load("blk." + std::to_string(i) + "." + nm + ".weight");
       if (rc != GLYPR_OK) break;
     }
+    for (const char* nm : kPle) {
+      if (rc != GLYPR_OK || !has_ple) break;
+      rc = load("blk." + std::to_string(i) + "." + nm + ".weight");
+    }
+  }
+  if (rc == GLYPR_OK && has_ple) rc = load("per_layer_model_proj.weight");
+  if (rc == GLYPR_OK && has_ple) rc = load("per_layer_proj_norm.weight");
+  if (rc == GLYPR_OK && has_out) rc = load("output.weight");
   if (rc == GLYPR_OK) rc = glypr_hip_model_finalize(m);
   if (rc != GLYPR_OK) {
     std::string msg = glypr_hip_last_error();

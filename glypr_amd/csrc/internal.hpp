@@ -87,9 +87,17 @@ hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t
                        float* out, float* scratch, hipStream_t s);
 
 // h = h + rmsnorm(x; w_post); if xq: (xq, dx) = Q8_0(rmsnorm(h; w_next)).  dim % 32 == 0.
+// scalar (device, nullable): h = (h + RMSNorm(x)) * scalar.  plain_q: xq/dx
+// receive Q8_0 of h itself instead of Q8_0 of RMSNorm(h; w_next).
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
-                                hipStream_t s);
+                                hipStream_t s, const float* scalar = nullptr,
+                                bool plain_q = false);
+// x = x * mul + 0 (f32), in place
+hipError_t launch_affine(float* x, int64_t n, float mul, hipStream_t s);
+// Q8_0 of geglu(g, u): g [rows][dim], u row r at u + r * u_stride
+hipError_t launch_geglu_quant(const float* g, const float* u, int64_t u_stride, int64_t rows,
+                              int64_t dim, int8_t* hq, float* dh, hipStream_t s);
 
 // ---- k_attn.hip ----
 // Attention operands are padded to Tp = attn_padded_len(T) tokens.

@@ -249,11 +249,16 @@ hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_
 // reference reduction order, so h and the quantized activations are
 // bit-identical to the CPU path.  One row per wave.
 // ---------------------------------------------------------------------------
-template <int NV, bool QNEXT>
+// NEXT: 0 = only h; 1 = also Q8_0 of RMSNorm(h; w_next); 2 = also Q8_0 of h
+// itself (the input of a projection that has no norm in front).  scalar
+// (device, nullable): forward_residual_add's layer_scalar, h = (h + n) * s.
+template <int NV, int NEXT>
 __global__ void __launch_bounds__(64 * NORM_WAVES)
 residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_post,
-                     float* __restrict__ h, const float* __restrict__ w_next, float eps,
-                     int64_t rows, int dim, int8_t* __restrict__ xq, float* __restrict__ dx) {
+                     float* __restrict__ h, const float* __restrict__ w_next,
+                     const float* __restrict__ scalar, float eps, int64_t rows, int dim,
+                     int8_t* __restrict__ xq, float* __restrict__ dx) {
+  constexpr bool QNEXT = NEXT != 0;
   extern __shared__ float lds_rows[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -283,20 +288,27 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   __builtin_amdgcn_wave_barrier();
   const float inv = chain_row_inv(lrow, dim, lane, eps);
   __builtin_amdgcn_wave_barrier();
+  const float sv = scalar ? *scalar : 1.0f;
 #pragma unroll
   for (int i = 0; i < NV; i++) {
     int c4 = lane + 64 * i;
     if (c4 < n4) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) v[i][e] = hv[i][e] + (v[i][e] * inv) * wp[i][e];
+      for (int e = 0; e < 4; e++) {
+        const float sum = hv[i][e] + (v[i][e] * inv) * wp[i][e];
+        v[i][e] = scalar ? sum * sv : sum;
+      }
       *reinterpret_cast<v4f*>(h + row * dim + 4 * c4) = v[i];
-      if (QNEXT) stage_chains(lrow, S, c4, v[i]);
+      if (NEXT == 1) stage_chains(lrow, S, c4, v[i]);
     }
   }
   if constexpr (QNEXT) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    const float inv2 = chain_row_inv(lrow, dim, lane, eps);
+    float inv2 = 1.0f;
+    if constexpr (NEXT == 1) {
+      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_wave_barrier();
+      inv2 = chain_row_inv(lrow, dim, lane, eps);
+    }
 #pragma unroll
     for (int i = 0; i < NV; i++) {
       const int c4 = lane + 64 * i;
@@ -305,12 +317,11 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
       float a = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        yv[e] = w_next ? (v[i][e] * inv2) * wn[i][e] : v[i][e] * inv2;
+        if (NEXT == 2) yv[e] = v[i][e];
+        else yv[e] = w_next ? (v[i][e] * inv2) * wn[i][e] : v[i][e] * inv2;
         a = fmaxf(a, fabsf(yv[e]));
       }
-      a = fmaxf(a, __shfl_xor(a, 1, 8));
-      a = fmaxf(a, __shfl_xor(a, 2, 8));
-      a = fmaxf(a, __shfl_xor(a, 4, 8));
+      a = max8(a);
       QScale sc = q8_scale(a);
       uint32_t packed = 0;
 #pragma unroll
@@ -326,21 +337,22 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
 
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
-                                hipStream_t s) {
+                                hipStream_t s, const float* scalar, bool plain_q) {
   if (rows == 0) return hipSuccess;
   if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
   const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
   const size_t lds = (size_t)NORM_WAVES * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
-  const bool q = xq != nullptr;
-#define RES_CASE(N)                                                                              \
-  case N:                                                                                        \
-    if (q)                                                                                       \
-      residual_norm_kernel<N, true><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w_post, h, w_next, eps,  \
-                                                                       rows, (int)dim, xq, dx);  \
-    else                                                                                         \
-      residual_norm_kernel<N, false><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w_post, h, w_next, eps, \
-                                                                        rows, (int)dim, xq, dx); \
+  const int mode = xq == nullptr ? 0 : (plain_q ? 2 : 1);
+#define RES_LAUNCH(N, MODE)                                                                    \
+  residual_norm_kernel<N, MODE><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w_post, h, w_next,       \
+                                                                   scalar, eps, rows,          \
+                                                                   (int)dim, xq, dx)
+#define RES_CASE(N)                                                                            \
+  case N:                                                                                      \
+    if (mode == 0) RES_LAUNCH(N, 0);                                                           \
+    else if (mode == 1) RES_LAUNCH(N, 1);                                                      \
+    else RES_LAUNCH(N, 2);                                                                     \
     break;
   switch (nv) {
     RES_CASE(1)
@@ -351,6 +363,7 @@ hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, c
       return hipErrorInvalidValue;
   }
 #undef RES_CASE
+#undef RES_LAUNCH
   return hipGetLastError();
 }
 
@@ -369,6 +382,73 @@ hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, h
   int64_t grid = (n + 255) / 256;
   if (grid > 65536) grid = 65536;
   geglu_kernel<<<(unsigned)grid, 256, 0, s>>>(g, u, out, n);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// candle's Tensor * f64 on f32 (affine(mul, 0)): y = v * f32(mul) + 0.0f, two
+// roundings (the + 0 turns a -0 product into +0).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) affine_kernel(float* x, int64_t n, float mul) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    x[i] = x[i] * mul + 0.0f;
+}
+
+hipError_t launch_affine(float* x, int64_t n, float mul, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  int64_t grid = (n + 255) / 256;
+  if (grid > 65536) grid = 65536;
+  affine_kernel<<<(unsigned)grid, 256, 0, s>>>(x, n, mul);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// TextPLEBlock's cpu_geglu(gate, per_layer_input) (ple.rs:136-138) followed by
+// BlockQ8_0::from_float of each 32-block: the proj GEMM's int8 operand.  gate
+// [rows][dim] contiguous; row r of the per-layer input at u + r * u_stride.
+// Eight lanes per 32-block, four elements each (the quantizer's layout).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) geglu_quant_kernel(const float* __restrict__ g,
+                                                          const float* __restrict__ u,
+                                                          int64_t u_stride, int64_t rows, int dim,
+                                                          int8_t* __restrict__ hq,
+                                                          float* __restrict__ dh) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int nbr = dim / QK;
+  const int64_t b = gid >> 3;
+  const int j = threadIdx.x & 7;
+  const bool ok = b < rows * nbr;
+  const int64_t r = ok ? b / nbr : 0;
+  const int col = ok ? (int)(b - r * nbr) * QK + 4 * j : 0;
+  v4f hv = {0, 0, 0, 0};
+  if (ok) {
+    const v4f gv = *reinterpret_cast<const v4f*>(g + r * dim + col);
+    const v4f uv = *reinterpret_cast<const v4f*>(u + r * u_stride + col);
+#pragma unroll
+    for (int e = 0; e < 4; e++) hv[e] = geglu_scalar(gv[e], uv[e]);
+  }
+  float a = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(hv[e]));
+  a = max8(a);
+  const QScale sc = q8_scale(a);
+  uint32_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++) packed |= ((uint32_t)(quant_round(hv[e] * sc.id) & 0xFF)) << (8 * e);
+  if (ok) {
+    *reinterpret_cast<uint32_t*>(hq + r * dim + col) = packed;
+    if (j == 0) dh[r * nbr + col / QK] = sc.dq;
+  }
+}
+
+hipError_t launch_geglu_quant(const float* g, const float* u, int64_t u_stride, int64_t rows,
+                              int64_t dim, int8_t* hq, float* dh, hipStream_t s) {
+  if (rows == 0) return hipSuccess;
+  if (dim % QK != 0 || u_stride % 4 != 0) return hipErrorInvalidValue;
+  const int64_t threads = rows * (dim / QK) * 8;
+  geglu_quant_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(g, u, u_stride, rows,
+                                                                       (int)dim, hq, dh);
   return hipGetLastError();
 }
 

@@ -5,15 +5,20 @@
 //   RMSNorm             norm.rs:4-95           (device f32 weight + eps)
 //   SelfAttention       attention/mod.rs:33-277
 //   MLP                 mlp.rs:6-70
-//   EncoderLayer        layer.rs:8-50          (PLE block and layer scalar omitted)
-//   EmbeddingGemma2Model model.rs:244-705      (gather, layers, final norm, pooling)
+//   EncoderLayer        layer.rs:8-50          (PLE block + layer scalar when ple_dim > 0)
+//   TextPLE/TextPLEBlock ple.rs:20-145
+//   EmbeddingGemma2Model model.rs:244-705      (gather, PLE inputs, layers, final norm,
+//                                               embedding projection, pooling)
 // The forward pass runs every projection as an INT8_EXACT Q8_0 GEMM and fuses
 // what the reference computes in separate ops:
 //   - each RMSNorm that feeds a projection is the GEMM's quantizing prologue;
 //   - forward_residual_add of one sublayer and the next sublayer's input
 //     RMSNorm are one kernel (residual_norm);
 //   - q/k/v and gate/up are single fused GEMMs (try_concat, linear.rs:82-148);
-//   - GeGLU is the gate/up GEMM's epilogue.
+//   - GeGLU is the gate/up GEMM's epilogue;
+//   - the PLE block's geglu(gate, per-layer input) is fused with the Q8_0
+//     quantization of the proj GEMM's operand, and its forward_residual_add
+//     with the layer scalar feeds the next layer's input norm.
 // The GEMMs, norms, GeGLU and residual adds are bit-exact with the CPU path;
 // attention (f16 MFMA with split operands, see k_attn.hip) and the chunked
 // pooling sum differ from it at f32-rounding level.
@@ -77,11 +82,20 @@ struct MLP {
   LinearOp fused_gate_up;  // try_concat([gate, up])
 };
 
+// TextPLEBlock (ple.rs:96-145) + the layer scalar (layer.rs:16, 45-49).
+struct PLEBlock {
+  LinearOp gate;        // inp_gate [ple_dim][hidden]
+  LinearOp projection;  // proj [hidden][ple_dim]
+  RMSNorm norm;         // post_norm [hidden]
+  float* layer_scalar = nullptr;  // device, 1 value
+};
+
 struct EncoderLayer {
   SelfAttention self_attn;
   MLP mlp;
   RMSNorm input_layernorm, post_attention_layernorm, pre_feedforward_layernorm,
       post_feedforward_layernorm;
+  PLEBlock ple_block;
   bool full_attention = false;
 };
 
@@ -96,13 +110,17 @@ struct glypr_model {
   LinearOp token_embd;
   std::vector<EncoderLayer> layers;
   RMSNorm norm;  // output_norm
+  // TextPLE (ple.rs:20-85): per_layer_model_proj + per_layer_proj_norm
+  LinearOp ple_projection;
+  RMSNorm ple_norm;
+  LinearOp embedding_projection;  // output.weight
   bool finalized = false;
   // RoPE tables [rope_cap][head_dim] for the sliding and full layer types.
   DevBuf cos_s, sin_s, cos_f, sin_f;
   int64_t rope_cap = 0;
   // activations
   DevBuf h, xq, dx, qkv, attn_q, attn_k, attn_vt, attn_scratch, cq, dc, proj, hq,
-      dh, normed, pooled, ids;
+      dh, normed, pooled, ids, ple, ple_gate, tokens;
   int64_t cap_t = 0;
 };
 
@@ -175,10 +193,17 @@ int ensure_activations(glypr_model* m, int64_t t) {
   RET_IF(m->cq.ensure((size_t)(t * qd)));
   RET_IF(m->dc.ensure((size_t)(t * (qd / 32)) * 4));
   RET_IF(m->proj.ensure((size_t)(t * c.hidden) * 4));
-  RET_IF(m->hq.ensure((size_t)(t * c.ffn)));
-  RET_IF(m->dh.ensure((size_t)(t * (c.ffn / 32)) * 4));
+  const int64_t hw = c.ffn > c.ple_dim ? c.ffn : c.ple_dim;   // GeGLU outputs (Q8_0)
+  RET_IF(m->hq.ensure((size_t)(t * hw)));
+  RET_IF(m->dh.ensure((size_t)(t * (hw / 32)) * 4));
   RET_IF(m->normed.ensure((size_t)(t * c.hidden) * 4));
-  RET_IF(m->pooled.ensure(pool_scratch_floats(t, c.hidden) * 4));
+  const int64_t width = c.out_dim > 0 ? c.out_dim : c.hidden;
+  RET_IF(m->pooled.ensure(pool_scratch_floats(t, width) * 4));
+  if (c.ple_dim > 0) {
+    RET_IF(m->ple.ensure((size_t)(t * c.n_layers * c.ple_dim) * 4));
+    RET_IF(m->ple_gate.ensure((size_t)(t * c.ple_dim) * 4));
+  }
+  if (c.out_dim > 0) RET_IF(m->tokens.ensure((size_t)(t * c.out_dim) * 4));
   RET_IF(m->ids.ensure((size_t)t * 4));
   m->cap_t = t;
   return GLYPR_OK;
@@ -195,6 +220,9 @@ void free_model(glypr_model* m) {
   };
   drop(m->token_embd);
   dropn(m->norm);
+  drop(m->ple_projection);
+  dropn(m->ple_norm);
+  drop(m->embedding_projection);
   for (auto& L : m->layers) {
     drop(L.self_attn.q);
     drop(L.self_attn.k);
@@ -211,10 +239,16 @@ void free_model(glypr_model* m) {
     dropn(L.post_attention_layernorm);
     dropn(L.pre_feedforward_layernorm);
     dropn(L.post_feedforward_layernorm);
+    drop(L.ple_block.gate);
+    drop(L.ple_block.projection);
+    dropn(L.ple_block.norm);
+    if (L.ple_block.layer_scalar) (void)hipFree(L.ple_block.layer_scalar);
+    L.ple_block.layer_scalar = nullptr;
   }
   for (DevBuf* b : {&m->cos_s, &m->sin_s, &m->cos_f, &m->sin_f, &m->h, &m->xq, &m->dx, &m->qkv,
                     &m->attn_q, &m->attn_k, &m->attn_vt, &m->attn_scratch,
-                    &m->cq, &m->dc, &m->proj, &m->hq, &m->dh, &m->normed, &m->pooled, &m->ids})
+                    &m->cq, &m->dc, &m->proj, &m->hq, &m->dh, &m->normed, &m->pooled, &m->ids,
+                    &m->ple, &m->ple_gate, &m->tokens})
     b->release();
 }
 
@@ -290,6 +324,9 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
               (long long)cfg->head_dim);
   GLYPR_CHECK(cfg->n_heads > 0 && cfg->n_kv_heads > 0 && cfg->n_heads % cfg->n_kv_heads == 0,
               GLYPR_ERR_SHAPE, "n_heads must be a positive multiple of n_kv_heads");
+  GLYPR_CHECK(cfg->ple_dim >= 0 && cfg->ple_dim % 32 == 0 && cfg->out_dim >= 0, GLYPR_ERR_SHAPE,
+              "ple_dim (%lld) must be a non-negative multiple of 32, out_dim (%lld) >= 0",
+              (long long)cfg->ple_dim, (long long)cfg->out_dim);
   RET_IF(check_ctx(ctx));
   glypr_model* m = new (std::nothrow) glypr_model();
   GLYPR_CHECK(m != nullptr, GLYPR_ERR_OOM, "host allocation failed");
@@ -325,17 +362,23 @@ int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* dat
     op.w = nullptr;
     return glypr_hip_q8_0_weight_create(m->ctx, (const uint8_t*)data, rows, cols, &op.w);
   };
-  auto set_norm = [&](RMSNorm& nm, int64_t len) -> int {
+  auto set_norm_raw = [&](float*& dst, int64_t len) -> int {
     GLYPR_CHECK(dtype == 0, GLYPR_ERR_UNSUPPORTED, "%s must be f32", name);
     GLYPR_CHECK(rows * cols == len, GLYPR_ERR_SHAPE, "%s has %lld values, expected %lld", name,
                 (long long)(rows * cols), (long long)len);
-    if (nm.weight) (void)hipFree(nm.weight);
-    nm.weight = nullptr;
-    return upload_f32((const float*)data, len, &nm.weight);
+    if (dst) (void)hipFree(dst);
+    dst = nullptr;
+    return upload_f32((const float*)data, len, &dst);
   };
+  auto set_norm = [&](RMSNorm& nm, int64_t len) -> int { return set_norm_raw(nm.weight, len); };
 
   if (n == "token_embd.weight") return set_q8(m->token_embd, c.vocab, c.hidden);
   if (n == "output_norm.weight") return set_norm(m->norm, c.hidden);
+  if (c.ple_dim > 0 && n == "per_layer_model_proj.weight")
+    return set_q8(m->ple_projection, c.n_layers * c.ple_dim, c.hidden);
+  if (c.ple_dim > 0 && n == "per_layer_proj_norm.weight") return set_norm(m->ple_norm, c.ple_dim);
+  if (c.out_dim > 0 && n == "output.weight")
+    return set_q8(m->embedding_projection, c.out_dim, c.hidden);
   int layer = -1, consumed = 0;
   char field[64] = {0};
   if (sscanf(name, "blk.%d.%63[^.].weight%n", &layer, field, &consumed) == 2 &&
@@ -355,6 +398,12 @@ int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* dat
     if (f == "ffn_gate") return set_q8(L.mlp.gate, c.ffn, c.hidden);
     if (f == "ffn_up") return set_q8(L.mlp.up, c.ffn, c.hidden);
     if (f == "ffn_down") return set_q8(L.mlp.down, c.hidden, c.ffn);
+    if (c.ple_dim > 0) {
+      if (f == "inp_gate") return set_q8(L.ple_block.gate, c.ple_dim, c.hidden);
+      if (f == "proj") return set_q8(L.ple_block.projection, c.hidden, c.ple_dim);
+      if (f == "post_norm") return set_norm(L.ple_block.norm, c.hidden);
+      if (f == "layer_output_scale") return set_norm_raw(L.ple_block.layer_scalar, 1);
+    }
   }
   return set_error(GLYPR_ERR_INVALID_ARG, "unknown tensor name '%s'", name);
 }
@@ -365,6 +414,10 @@ int glypr_hip_model_finalize(glypr_model* m) {
   if (m->finalized) return GLYPR_OK;
   GLYPR_CHECK(m->token_embd.w && m->norm.weight, GLYPR_ERR_INVALID_ARG,
               "token_embd.weight or output_norm.weight missing");
+  GLYPR_CHECK(m->cfg.ple_dim == 0 || (m->ple_projection.w && m->ple_norm.weight),
+              GLYPR_ERR_INVALID_ARG, "per_layer_model_proj / per_layer_proj_norm missing");
+  GLYPR_CHECK(m->cfg.out_dim == 0 || m->embedding_projection.w, GLYPR_ERR_INVALID_ARG,
+              "output.weight missing");
   for (size_t i = 0; i < m->layers.size(); i++) {
     EncoderLayer& L = m->layers[i];
     GLYPR_CHECK(L.self_attn.q.w && L.self_attn.k.w && L.self_attn.v.w && L.self_attn.o.w &&
@@ -373,6 +426,10 @@ int glypr_hip_model_finalize(glypr_model* m) {
                     L.post_attention_layernorm.weight && L.pre_feedforward_layernorm.weight &&
                     L.post_feedforward_layernorm.weight,
                 GLYPR_ERR_INVALID_ARG, "layer %zu is missing tensors", i);
+    GLYPR_CHECK(m->cfg.ple_dim == 0 ||
+                    (L.ple_block.gate.w && L.ple_block.projection.w && L.ple_block.norm.weight &&
+                     L.ple_block.layer_scalar),
+                GLYPR_ERR_INVALID_ARG, "layer %zu is missing its Per-Layer-Embedding tensors", i);
     const glypr_q8w* qkv[3] = {L.self_attn.q.w, L.self_attn.k.w, L.self_attn.v.w};
     RET_IF(glypr_hip_q8_0_weight_concat(m->ctx, qkv, 3, &L.self_attn.fused_qkv.w, nullptr));
     const glypr_q8w* gu[2] = {L.mlp.gate.w, L.mlp.up.w};
@@ -418,6 +475,22 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
          launch_gather(m->token_embd.w->qs(), m->token_embd.w->dw(), H, m->ids.as<uint32_t>(), t,
                        embed_scale, h, s),
          "gather launch");
+  // TextPLE::project_and_norm_per_layer (ple.rs:48-85): per_layer_model_proj of
+  // the scaled embeddings, * hidden^-0.5 (f64 powf, applied as candle's f32
+  // affine), RMSNorm over ple_dim.  Layer l's input is row t*NL + l of [t*NL][P].
+  const int64_t P = c.ple_dim, NL = c.n_layers;
+  float* ple = dev_f32(m->ple);
+  if (P > 0) {
+    LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(h, t, H, xq, dx, s), "quantize launch");
+    const glypr_q8w* wpl = m->ple_projection.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, wpl->qs(), wpl->dw(), ple, t, NL * P, H, NL * P, s),
+           "per-layer projection launch");
+    LAUNCH(GLYPR_K_RMSNORM, s, launch_affine(ple, t * NL * P, (float)pow((double)H, -0.5), s),
+           "per-layer scale launch");
+    LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(ple, m->ple_norm.weight, c.eps, ple, t * NL, P, s),
+           "per-layer norm launch");
+  }
   // layer 0 input_layernorm as the qkv GEMM's prologue
   LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
          launch_rmsnorm_quant(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xq, dx, s),
@@ -461,18 +534,62 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
            launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wd->qs(), wd->dw(),
                           dev_f32(m->proj), t, H, F, H, s),
            "down gemm launch");
-    // post_feedforward_layernorm.forward_residual_add + next layer's input norm
     const float* w_next = last ? nullptr : m->layers[li + 1].input_layernorm.weight;
+    if (P == 0) {
+      // post_feedforward_layernorm.forward_residual_add + next layer's input norm
+      LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+             launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h,
+                                  w_next, c.eps, t, H, last ? nullptr : xq, last ? nullptr : dx,
+                                  s),
+             "residual_norm launch");
+      continue;
+    }
+    // post_feedforward_layernorm.forward_residual_add, then Q8_0 of h itself
+    // for the PLE block's inp_gate (no norm in front of it)
     LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
-           launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h, w_next,
-                                c.eps, t, H, last ? nullptr : xq, last ? nullptr : dx, s),
+           launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h, nullptr,
+                                c.eps, t, H, xq, dx, s, nullptr, true),
+           "residual_norm launch");
+    // ---- TextPLEBlock::forward_with_scalar (ple.rs:118-145)
+    const glypr_q8w* wg = L.ple_block.gate.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, wg->qs(), wg->dw(), dev_f32(m->ple_gate), t, P, H, P, s),
+           "per-layer gate launch");
+    LAUNCH(GLYPR_K_GEGLU, s,
+           launch_geglu_quant(dev_f32(m->ple_gate), ple + (int64_t)li * P, NL * P, t, P,
+                              m->hq.as<int8_t>(), dev_f32(m->dh), s),
+           "per-layer geglu launch");
+    const glypr_q8w* wpj = L.ple_block.projection.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wpj->qs(), wpj->dw(),
+                          dev_f32(m->proj), t, H, P, H, s),
+           "per-layer proj launch");
+    // post_norm.forward_residual_add(.., layer_scalar) + next layer's input norm
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.ple_block.norm.weight, h, w_next, c.eps, t, H,
+                                last ? nullptr : xq, last ? nullptr : dx, s,
+                                L.ple_block.layer_scalar, false),
            "residual_norm launch");
   }
-  // model.rs:576: final norm (the embedding projection is not part of this backbone)
-  float* normed = hidden ? hidden : dev_f32(m->normed);
-  LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, normed, t, H, s),
-         "final rmsnorm launch");
-  LAUNCH(GLYPR_K_POOL, s, launch_pool(normed, nullptr, t, H, trunc, out, dev_f32(m->pooled), s),
+  // model.rs:576-577: final norm, then the embedding projection when present
+  const int64_t width = c.out_dim > 0 ? c.out_dim : H;
+  float* tokens = hidden;
+  if (c.out_dim > 0) {
+    if (!tokens) tokens = dev_f32(m->tokens);
+    LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
+           launch_rmsnorm_quant(h, m->norm.weight, c.eps, t, H, xq, dx, s),
+           "rmsnorm_quant launch");
+    const glypr_q8w* we = m->embedding_projection.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, we->qs(), we->dw(), tokens, t, c.out_dim, H, c.out_dim, s),
+           "embedding projection launch");
+  } else {
+    if (!tokens) tokens = dev_f32(m->normed);
+    LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, tokens, t, H, s),
+           "final rmsnorm launch");
+  }
+  LAUNCH(GLYPR_K_POOL, s,
+         launch_pool(tokens, nullptr, t, width, trunc, out, dev_f32(m->pooled), s),
          "pool launch");
   return GLYPR_OK;
 }

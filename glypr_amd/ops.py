@@ -317,7 +317,8 @@ class ModelConfig(ctypes.Structure):
                 ("n_kv_heads", ctypes.c_int64), ("head_dim", ctypes.c_int64),
                 ("n_layers", ctypes.c_int64), ("vocab", ctypes.c_int64),
                 ("sliding_window", ctypes.c_int64), ("eps", ctypes.c_float),
-                ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double)]
+                ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double),
+                ("ple_dim", ctypes.c_int64), ("out_dim", ctypes.c_int64)]
 
 
 class Gguf:
@@ -410,9 +411,11 @@ class Model:
         """glypr_hip_model_load_gguf: config and tensors from a GGUF file."""
         with Gguf(path) as g:
             hidden = g.u64("gemma-embedding2.embedding_length")
+            dims = {t["name"]: t["dims"] for t in g.tensors()}
         m = cls.__new__(cls)
         m.ctx = ctx
-        m.cfg = {"hidden": hidden}
+        out = dims.get("output.weight")
+        m.cfg = {"hidden": hidden, "out_dim": out[1] if out else 0}
         h = ctypes.c_void_p()
         m.handle = None
         check(lib().glypr_hip_model_load_gguf(ctx.handle, os.fsencode(path), ctypes.byref(h)))
@@ -422,7 +425,7 @@ class Model:
     def __init__(self, ctx: Context, **cfg):
         defaults = dict(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256, n_layers=24,
                         vocab=262144, sliding_window=512, eps=1e-6, rope_theta_sliding=10000.0,
-                        rope_theta_full=1e6)
+                        rope_theta_full=1e6, ple_dim=0, out_dim=0)
         defaults.update(cfg)
         self.cfg = defaults
         self.ctx = ctx
@@ -443,7 +446,7 @@ class Model:
     def embed(self, ids, trunc: int = 0, hidden: Optional[torch.Tensor] = None,
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
-        H = self.cfg["hidden"]
+        H = self.cfg.get("out_dim") or self.cfg["hidden"]   # embedding width
         td = trunc if 0 < trunc < H else H
         if out is None:
             out = torch.empty(td, dtype=torch.float32, device=f"cuda:{self.ctx.device}")

@@ -237,14 +237,20 @@ typedef struct glypr_model_config {
   float eps;                   /* rms_norm_eps, 1e-6 */
   double rope_theta_sliding;   /* 10000 (config.rs:171-172) */
   double rope_theta_full;      /* 1e6 (config.rs:173-174) */
+  int64_t ple_dim;             /* hidden_size_per_layer_input (config.rs:100-101);
+                                * 0 = no Per-Layer-Embedding block (configs 4-5) */
+  int64_t out_dim;             /* rows of output.weight, the embedding projection
+                                * (model.rs:472-473, 577); 0 = none */
 } glypr_model_config;
 
 typedef struct glypr_model glypr_model;
 
-/* EmbeddingGemma2Model::from_gguf_content (model.rs:244-488), minus the
- * Per-Layer-Embedding block: an empty model whose tensors arrive through
- * glypr_hip_model_set_tensor.  Layer i is full attention iff (i+1) % 6 == 0
- * (config.rs:131-140), sliding otherwise. */
+/* EmbeddingGemma2Model::from_gguf_content (model.rs:244-488): an empty model
+ * whose tensors arrive through glypr_hip_model_set_tensor.  Layer i is full
+ * attention iff (i+1) % 6 == 0 (config.rs:131-140), sliding otherwise.  With
+ * ple_dim > 0 (a multiple of 32) every layer ends with the TextPLEBlock and its
+ * layer scalar (layer.rs:45-49); with out_dim > 0 the final norm feeds the
+ * embedding projection. */
 int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
                            glypr_model** out);
 
@@ -252,8 +258,13 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
  * "output_norm.weight", "blk.{i}.{attn_norm, post_attention_norm, ffn_norm,
  * post_ffw_norm, attn_q_norm, attn_k_norm}.weight" (f32, dtype 0) and
  * "blk.{i}.{attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up,
- * ffn_down}.weight" (Q8_0 GGUF blocks, dtype 1).  Host memory; rows x cols
- * is the GGUF (out_dim, in_dim). */
+ * ffn_down}.weight" (Q8_0 GGUF blocks, dtype 1).  With ple_dim > 0 also
+ * "per_layer_model_proj.weight" (Q8_0, n_layers*ple_dim x hidden),
+ * "per_layer_proj_norm.weight" (f32 [ple_dim]) and per layer "inp_gate"
+ * (Q8_0, ple_dim x hidden), "proj" (Q8_0, hidden x ple_dim), "post_norm"
+ * (f32 [hidden]) and "layer_output_scale" (f32 [1]); with out_dim > 0
+ * "output.weight" (Q8_0, out_dim x hidden).  Host memory; rows x cols is the
+ * GGUF (out_dim, in_dim). */
 int glypr_hip_model_set_tensor(glypr_model* model, const char* name, const void* data,
                                int64_t rows, int64_t cols, int dtype);
 
@@ -262,9 +273,11 @@ int glypr_hip_model_set_tensor(glypr_model* model, const char* name, const void*
 int glypr_hip_model_finalize(glypr_model* model);
 
 /* forward (model.rs:498-578) + pool_and_normalize (model.rs:654-705) for one
- * sequence: ids (host, tokenizer output) -> out [trunc] on the device.
- * hidden (nullable, device [t][hidden]) receives the final-normed token
- * states.  Only GLYPR_Q8_INT8_EXACT is supported here. */
+ * sequence: ids (host, tokenizer output) -> out [trunc, or the embedding
+ * width when trunc is 0 or wider] on the device.  hidden (nullable, device
+ * [t][width]) receives the unpooled token embeddings: the projection's output,
+ * or the final-normed states without one.  The embedding width is out_dim
+ * when set, else hidden.  Every projection runs as INT8_EXACT. */
 int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, int64_t trunc,
                           float* out, float* hidden, glypr_stream stream);
 
@@ -300,10 +313,12 @@ int glypr_gguf_get_array_u64(const glypr_gguf* g, const char* key, int64_t i, ui
 /* GlyprEmbedder::load_gguf_q8 -> EmbeddingGemma2Model::from_gguf_content
  * (lib.rs:180-186; model.rs:244-488) with TextConfig::from_gguf_metadata
  * (config.rs:79-189): the config from the gemma-embedding2.* keys, then every
- * tensor glypr_hip_model_set_tensor names, then finalize.  Per-Layer
- * Embedding tensors are ignored (the backbone omits that block).  Layouts the
- * backend does not run (a layer pattern other than 5 sliding + 1 full,
- * per-layer kv heads or head dims) give GLYPR_ERR_UNSUPPORTED. */
+ * tensor glypr_hip_model_set_tensor names, then finalize.  A file with
+ * "per_layer_model_proj.weight" runs the Per-Layer-Embedding path (ple_dim from
+ * gemma-embedding2.embedding_length_per_layer_input), one with
+ * "output.weight" the embedding projection.  Layouts the backend does not run
+ * (a layer pattern other than 5 sliding + 1 full, per-layer kv heads or head
+ * dims, tensors in other ggml types) give GLYPR_ERR_UNSUPPORTED. */
 int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model** out);
 
 /* ---- per-kernel timing --------------------------------------------------- */

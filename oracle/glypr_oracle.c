@@ -629,7 +629,7 @@ static void orc_linear(const uint8_t* w, int64_t n, int64_t k, const float* x, i
 }
 
 void orc_encoder_layer(const orc_model_config* cfg, const orc_layer_weights* w, int64_t layer_idx,
-                       float* hidden, int64_t t, int threads) {
+                       float* hidden, const float* per_layer_input, int64_t t, int threads) {
   int64_t H = cfg->hidden, F = cfg->ffn, nh = cfg->n_heads, nkv = cfg->n_kv_heads,
           hd = cfg->head_dim;
   int full = orc_layer_is_full(layer_idx);
@@ -682,28 +682,79 @@ void orc_encoder_layer(const orc_model_config* cfg, const orc_layer_weights* w, 
   orc_rmsnorm(attn, w->post_ffn_norm, cfg->eps, normed, t, H, threads);
   for (int64_t i = 0; i < t * H; i++) hidden[i] = hidden[i] + normed[i];
 
+  /* 3. TextPLEBlock::forward_with_scalar (ple.rs:118-145): gate = inp_gate(h),
+   * cpu_geglu(gate, per_layer_input), proj, then post_norm.forward_residual_add
+   * with the layer scalar (norm.rs:65-95): (h + RMSNorm(p)) * scalar. */
+  if (cfg->ple_dim > 0) {
+    const int64_t P = cfg->ple_dim;
+    float* pg = (float*)malloc((size_t)(t * P) * sizeof(float));
+    orc_linear(w->ple_gate, P, H, hidden, t, pg, threads);
+    orc_geglu(pg, per_layer_input, pg, t * P, threads);
+    orc_linear(w->ple_proj, H, P, pg, t, attn, threads);
+    orc_rmsnorm(attn, w->ple_post_norm, cfg->eps, normed, t, H, threads);
+    const float sc = w->layer_scalar ? w->layer_scalar[0] : 1.0f;
+    for (int64_t i = 0; i < t * H; i++) {
+      const float sum = hidden[i] + normed[i];
+      hidden[i] = w->layer_scalar ? sum * sc : sum;
+    }
+    free(pg);
+  }
+
   free(normed); free(qb); free(kb); free(vb); free(qh); free(kh); free(vh);
   free(ctxb); free(attn); free(gate); free(up); free(cos_t); free(sin_t);
 }
 
 int orc_model_forward(const orc_model_config* cfg, const uint8_t* embed_table,
                       const orc_layer_weights* layers, const float* final_norm,
-                      const uint32_t* ids, int64_t t, int64_t trunc, float* out,
-                      float* hidden_out, int threads) {
-  int64_t H = cfg->hidden;
+                      const uint8_t* ple_model_proj, const float* ple_proj_norm,
+                      const uint8_t* out_proj, const uint32_t* ids, int64_t t, int64_t trunc,
+                      float* out, float* hidden_out, int threads) {
+  int64_t H = cfg->hidden, L = cfg->n_layers, P = cfg->ple_dim;
   float* hidden = (float*)malloc((size_t)(t * H) * sizeof(float));
   float scale = (float)sqrt((double)H);   /* embed_scale f64 -> affine mul as f32 */
   if (orc_embed_gather(embed_table, cfg->vocab, H, ids, t, scale, hidden) != 0) {
     free(hidden);
     return -1;
   }
-  for (int64_t l = 0; l < cfg->n_layers; l++)
-    orc_encoder_layer(cfg, &layers[l], l, hidden, t, threads);
+  /* TextPLE::project_and_norm_per_layer (ple.rs:48-85): projection of the
+   * scaled embeddings, * hidden^-0.5 (f64 powf, applied as an f32 affine mul),
+   * RMSNorm over ple_dim, then each layer's [t][ple_dim] slice. */
+  float* ple = NULL;
+  float* slice = NULL;
+  if (P > 0) {
+    float* raw = (float*)malloc((size_t)(t * L * P) * sizeof(float));
+    ple = (float*)malloc((size_t)(t * L * P) * sizeof(float));
+    slice = (float*)malloc((size_t)(t * P) * sizeof(float));
+    orc_linear(ple_model_proj, L * P, H, hidden, t, raw, threads);
+    const float ps = (float)pow((double)H, -0.5);
+    for (int64_t i = 0; i < t * L * P; i++) raw[i] = raw[i] * ps + 0.0f;
+    orc_rmsnorm(raw, ple_proj_norm, cfg->eps, ple, t * L, P, threads);
+    free(raw);
+  }
+  for (int64_t l = 0; l < L; l++) {
+    if (P > 0)
+      for (int64_t i = 0; i < t; i++)
+        memcpy(slice + i * P, ple + (i * L + l) * P, (size_t)P * sizeof(float));
+    orc_encoder_layer(cfg, &layers[l], l, hidden, P > 0 ? slice : NULL, t, threads);
+  }
   float* normed = (float*)malloc((size_t)(t * H) * sizeof(float));
   orc_rmsnorm(hidden, final_norm, cfg->eps, normed, t, H, threads);  /* model.rs:576 */
-  if (hidden_out) memcpy(hidden_out, normed, (size_t)(t * H) * sizeof(float));
-  orc_pool_normalize(normed, NULL, t, H, trunc, out);
+  /* embedding_projection.forward (model.rs:577) */
+  int64_t D = H;
+  float* tokens = normed;
+  float* projected = NULL;
+  if (cfg->out_dim > 0) {
+    D = cfg->out_dim;
+    projected = (float*)malloc((size_t)(t * D) * sizeof(float));
+    orc_linear(out_proj, D, H, normed, t, projected, threads);
+    tokens = projected;
+  }
+  if (hidden_out) memcpy(hidden_out, tokens, (size_t)(t * D) * sizeof(float));
+  orc_pool_normalize(tokens, NULL, t, D, trunc, out);
   free(hidden);
   free(normed);
+  free(projected);
+  free(ple);
+  free(slice);
   return 0;
 }

@@ -128,7 +128,7 @@ void orc_fill_uniform_ids(uint32_t* ids, int64_t n, uint64_t seed, uint32_t voca
 /* GGUF Q8_0 weight [n][k/32]: qs uniform in [-127,127], d = f16(|N(0,sigma)|/127). */
 void orc_make_q8_0_weight(uint8_t* blocks, int64_t n, int64_t k, uint64_t seed, float sigma);
 
-/* ---- Backbone (configs 4-5; layer.rs:20-50 minus PLE) ---- */
+/* ---- Backbone (configs 4-5 run without PLE; layer.rs:20-50, ple.rs) ---- */
 typedef struct {
   int64_t hidden;       /* 768 */
   int64_t ffn;          /* 1152 */
@@ -141,6 +141,8 @@ typedef struct {
   float eps;            /* 1e-6 */
   double rope_theta_sliding; /* 10000 */
   double rope_theta_full;    /* 1e6 */
+  int64_t ple_dim;      /* hidden_size_per_layer_input; 0 = no PLE (configs 4-5) */
+  int64_t out_dim;      /* rows of output.weight; 0 = no embedding projection */
 } orc_model_config;
 
 /* Per-layer weights, host memory.  Q8_0 tensors are GGUF blocks. */
@@ -158,21 +160,32 @@ typedef struct {
   const float* post_ffn_norm;  /* [hidden] */
   const float* q_norm;         /* [head_dim] */
   const float* k_norm;         /* [head_dim] */
+  /* TextPLEBlock (ple.rs:96-145) and the layer scalar; unused when ple_dim 0 */
+  const uint8_t* ple_gate;     /* inp_gate [ple_dim][hidden] */
+  const uint8_t* ple_proj;     /* proj [hidden][ple_dim] */
+  const float* ple_post_norm;  /* post_norm [hidden] */
+  const float* layer_scalar;   /* layer_output_scale [1] */
 } orc_layer_weights;
 
 /* layer_types: 0 = sliding, 1 = full (config.rs:131-140). */
 int orc_layer_is_full(int64_t layer_idx);
 /* RoPE tables (rope.rs:14-87): cos/sin f32 [t][head_dim]. */
 void orc_rope_tables(int64_t head_dim, double theta, int64_t t, float* cos_t, float* sin_t);
-/* One encoder layer in place on hidden [t][hidden]. */
+/* One encoder layer in place on hidden [t][hidden].  per_layer_input
+ * [t][ple_dim] (this layer's PLE slice) when cfg->ple_dim > 0, else NULL. */
 void orc_encoder_layer(const orc_model_config* cfg, const orc_layer_weights* w, int64_t layer_idx,
-                       float* hidden, int64_t t, int threads);
-/* Full forward: gather*sqrt(hidden) -> layers -> final norm -> pool/L2/MRL.
- * final_norm [hidden]; out [trunc]. */
+                       float* hidden, const float* per_layer_input, int64_t t, int threads);
+/* Full forward: gather*sqrt(hidden) -> [PLE inputs] -> layers -> final norm
+ * -> [embedding projection] -> pool/L2/MRL.  final_norm [hidden];
+ * ple_model_proj [n_layers*ple_dim][hidden] and ple_proj_norm [ple_dim] when
+ * ple_dim > 0; out_proj [out_dim][hidden] when out_dim > 0 (else NULL).
+ * out [trunc or out dim]; hidden_out [t][out dim] (the unpooled token
+ * embeddings), out dim = out_dim or hidden. */
 int orc_model_forward(const orc_model_config* cfg, const uint8_t* embed_table,
                       const orc_layer_weights* layers, const float* final_norm,
-                      const uint32_t* ids, int64_t t, int64_t trunc, float* out,
-                      float* hidden_out /* nullable [t][hidden] */, int threads);
+                      const uint8_t* ple_model_proj, const float* ple_proj_norm,
+                      const uint8_t* out_proj, const uint32_t* ids, int64_t t, int64_t trunc,
+                      float* out, float* hidden_out /* nullable */, int threads);
 /* Attention core for one sequence (attention/standard.rs, chunked.rs):
  * q [n_heads][t][hd], k,v [n_kv][t][hd] -> ctx [t][n_heads*hd]; window 0 = full. */
 void orc_attention(const float* q, const float* k, const float* v, int64_t n_heads,

@@ -45,13 +45,16 @@ class ModelConfig(ctypes.Structure):
     _fields_ = [("hidden", _i64), ("ffn", _i64), ("n_heads", _i64), ("n_kv_heads", _i64),
                 ("head_dim", _i64), ("n_layers", _i64), ("vocab", _i64),
                 ("sliding_window", _i64), ("eps", ctypes.c_float),
-                ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double)]
+                ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double),
+                ("ple_dim", _i64), ("out_dim", _i64)]
 
 
 class LayerWeights(ctypes.Structure):
     _fields_ = [(n, _u8p) for n in ("q", "k", "v", "o", "gate", "up", "down")] + \
                [(n, _f32p) for n in ("input_norm", "post_attn_norm", "pre_ffn_norm",
-                                     "post_ffn_norm", "q_norm", "k_norm")]
+                                     "post_ffn_norm", "q_norm", "k_norm")] + \
+               [("ple_gate", _u8p), ("ple_proj", _u8p), ("ple_post_norm", _f32p),
+                ("layer_scalar", _f32p)]
 
 
 def lib():
@@ -99,10 +102,11 @@ def lib():
             "orc_attention": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64, _i64, _f32p,
                                      ctypes.c_int]),
             "orc_encoder_layer": (None, [ctypes.POINTER(ModelConfig),
-                                         ctypes.POINTER(LayerWeights), _i64, _f32p, _i64,
+                                         ctypes.POINTER(LayerWeights), _i64, _f32p, _f32p, _i64,
                                          ctypes.c_int]),
             "orc_model_forward": (ctypes.c_int, [ctypes.POINTER(ModelConfig),
-                                                 _u8p, ctypes.POINTER(LayerWeights), _f32p, _u32p,
+                                                 _u8p, ctypes.POINTER(LayerWeights), _f32p,
+                                                 _u8p, _f32p, _u8p, _u32p,
                                                  _i64, _i64, _f32p, _f32p, ctypes.c_int]),
         }
         for name, (res, args) in sig.items():
@@ -370,15 +374,23 @@ def model_forward(tensors: dict, ids: np.ndarray, trunc: int, *, hidden: int, ff
                   sliding_window: int = 512, eps: float = 1e-6, theta_sliding: float = 1e4,
                   theta_full: float = 1e6, threads: int = 0):
     """orc_model_forward over GGUF-named tensors {name: array} (Q8_0 tensors as
-    block bytes, norms as f32).  Returns (pooled [trunc or hidden], final-normed
-    token states [t, hidden])."""
+    block bytes, norms as f32).  The PLE block runs when
+    `per_layer_model_proj.weight` is present (ple_dim = its rows / n_layers),
+    the embedding projection when `output.weight` is.  Returns (pooled
+    [trunc or out dim], unpooled token embeddings [t, out dim])."""
+    ple_dim = 0
+    if "per_layer_model_proj.weight" in tensors:
+        ple_dim = tensors["per_layer_model_proj.weight"].shape[0] // n_layers
+    out_dim = tensors["output.weight"].shape[0] if "output.weight" in tensors else 0
     cfg = ModelConfig(hidden=hidden, ffn=ffn, n_heads=n_heads, n_kv_heads=n_kv_heads,
                       head_dim=head_dim, n_layers=n_layers, vocab=vocab,
                       sliding_window=sliding_window, eps=eps, rope_theta_sliding=theta_sliding,
-                      rope_theta_full=theta_full)
+                      rope_theta_full=theta_full, ple_dim=ple_dim, out_dim=out_dim)
     keep = []
 
     def arr(name, dt, ptype):
+        if name not in tensors:
+            return ctypes.cast(None, ptype)
         a = np.ascontiguousarray(tensors[name], dtype=dt)
         keep.append(a)
         return _p(a, ptype)
@@ -391,13 +403,20 @@ def model_forward(tensors: dict, ids: np.ndarray, trunc: int, *, hidden: int, ff
               ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")],
             *[arr(p + n + ".weight", np.float32, _f32p) for n in
               ("attn_norm", "post_attention_norm", "ffn_norm", "post_ffw_norm", "attn_q_norm",
-               "attn_k_norm")])
+               "attn_k_norm")],
+            arr(p + "inp_gate.weight", np.uint8, _u8p), arr(p + "proj.weight", np.uint8, _u8p),
+            arr(p + "post_norm.weight", np.float32, _f32p),
+            arr(p + "layer_output_scale.weight", np.float32, _f32p))
     ids = np.ascontiguousarray(ids, np.uint32)
     t = ids.size
-    out = np.empty(trunc if 0 < trunc < hidden else hidden, np.float32)
-    states = np.empty((t, hidden), np.float32)
+    d = out_dim or hidden
+    out = np.empty(trunc if 0 < trunc < d else d, np.float32)
+    states = np.empty((t, d), np.float32)
     rc = lib().orc_model_forward(ctypes.byref(cfg), arr("token_embd.weight", np.uint8, _u8p),
                                  layers, arr("output_norm.weight", np.float32, _f32p),
+                                 arr("per_layer_model_proj.weight", np.uint8, _u8p),
+                                 arr("per_layer_proj_norm.weight", np.float32, _f32p),
+                                 arr("output.weight", np.uint8, _u8p),
                                  _p(ids, _u32p), t, trunc, _p(out, _f32p), _p(states, _f32p),
                                  threads)
     if rc != 0:

@@ -92,7 +92,9 @@ def test_attention_core_vs_oracle(ctx, oracle, t, window, qk_scale):
 QK_NORM_SCALE = np.float32(0.25)
 
 
-def make_model(ctx, oracle, n_layers, vocab, seed=0):
+def make_model(ctx, oracle, n_layers, vocab, seed=0, ple_dim=0, out_dim=0):
+    """The BASELINE backbone; ple_dim / out_dim > 0 add the real model's
+    Per-Layer-Embedding path (ple.rs) and embedding projection (output.weight)."""
     H, F, nq, nkv, hd = 768, 1152, 3, 1, 256
     rng_seed = seed * 1000
     tensors = {}
@@ -112,7 +114,25 @@ def make_model(ctx, oracle, n_layers, vocab, seed=0):
             if name in ("attn_q_norm", "attn_k_norm"):
                 w = w * QK_NORM_SCALE
             tensors[f"blk.{i}.{name}.weight"] = (w, 1, n, False)
-    m = Model(ctx, n_layers=n_layers, vocab=vocab)
+        if ple_dim:
+            tensors[f"blk.{i}.inp_gate.weight"] = (
+                oracle.q8_0_weight(ple_dim, H, seed=b + 70, sigma=0.05), ple_dim, H, True)
+            tensors[f"blk.{i}.proj.weight"] = (
+                oracle.q8_0_weight(H, ple_dim, seed=b + 71, sigma=0.05), H, ple_dim, True)
+            tensors[f"blk.{i}.post_norm.weight"] = \
+                (1 + 0.1 * oracle.normal(H, seed=b + 72), 1, H, False)
+            tensors[f"blk.{i}.layer_output_scale.weight"] = \
+                (np.array([0.6 + 0.05 * i], np.float32), 1, 1, False)
+    if ple_dim:
+        tensors["per_layer_model_proj.weight"] = (
+            oracle.q8_0_weight(n_layers * ple_dim, H, seed=rng_seed + 3, sigma=0.05),
+            n_layers * ple_dim, H, True)
+        tensors["per_layer_proj_norm.weight"] = \
+            (1 + 0.1 * oracle.normal(ple_dim, seed=rng_seed + 4), 1, ple_dim, False)
+    if out_dim:
+        tensors["output.weight"] = (oracle.q8_0_weight(out_dim, H, seed=rng_seed + 5, sigma=0.05),
+                                    out_dim, H, True)
+    m = Model(ctx, n_layers=n_layers, vocab=vocab, ple_dim=ple_dim, out_dim=out_dim)
     for name, (data, r, c, q8) in tensors.items():
         m.set_tensor(name, data, r, c, q8)
     m.finalize()
@@ -150,7 +170,7 @@ def oracle_forward(oracle, tensors, n_layers, vocab, ids, trunc):
     out = np.empty(trunc if 0 < trunc < 768 else 768, np.float32)
     hidden = np.empty((t, 768), np.float32)
     rc = oracle.lib().orc_model_forward(ctypes_byref(oracle, cfg), u8("token_embd.weight"), layers,
-                                        f32("output_norm.weight"),
+                                        f32("output_norm.weight"), None, None, None,
                                         ids.ctypes.data_as(oracle._u32p), t, trunc,
                                         out.ctypes.data_as(oracle._f32p),
                                         hidden.ctypes.data_as(oracle._f32p), 0)
@@ -186,6 +206,35 @@ def test_model_forward_vs_oracle(ctx, oracle, n_layers, t, vocab):
     m.close()
 
 
+def test_model_with_ple_and_projection_vs_oracle(ctx, oracle):
+    """The real EmbeddingGemma-2 layer: TextPLE inputs, every layer's
+    TextPLEBlock with its layer scalar (layer.rs:45-49, ple.rs), and the
+    output.weight embedding projection (model.rs:577), against the oracle."""
+    n_layers, vocab, t, P, D = 6, 2000, 300, 256, 512
+    say(f"backbone + PLE (ple_dim={P}) + projection (out_dim={D}) layers={n_layers} t={t}")
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=21, ple_dim=P, out_dim=D)
+    ids = oracle.uniform_ids(t, seed=9, vocab=vocab)
+    tokens = torch.empty((t, D), dtype=torch.float32, device="cuda")
+    got = host(m.embed(ids, trunc=256, hidden=tokens))
+    flat = {k: (v[0] if v[3] else np.asarray(v[0], np.float32).reshape(-1)) for k, v in tensors.items()}
+    ref, ref_tokens = oracle.model_forward(flat, ids, 256, hidden=768, ffn=1152, n_heads=3,
+                                           n_kv_heads=1, head_dim=256, n_layers=n_layers,
+                                           vocab=vocab)
+    assert ref_tokens.shape == (t, D)
+    cos = float(got @ ref / np.linalg.norm(got) / np.linalg.norm(ref))
+    gt = host(tokens)
+    row_cos = (gt * ref_tokens).sum(1) / np.linalg.norm(gt, axis=1) / \
+        np.linalg.norm(ref_tokens, axis=1)
+    say(f"  final embedding cosine {cos:.8f}, token cosine min {row_cos.min():.8f}")
+    assert cos >= 0.9999 and row_cos.min() >= 0.999
+    # the PLE path is live: the same backbone without it embeds differently
+    m2, _ = make_model(ctx, oracle, n_layers, vocab, seed=21, out_dim=D)
+    other = host(m2.embed(ids, trunc=256))
+    assert float(other @ got / np.linalg.norm(other) / np.linalg.norm(got)) < 0.999
+    m2.close()
+    m.close()
+
+
 def test_model_from_gguf_matches_set_tensor(ctx, oracle, tmp_path):
     """glypr_hip_model_load_gguf (config from gemma-embedding2.* metadata, tensors
     by name) builds the same model as set_tensor: bit-identical embeddings."""
@@ -212,3 +261,18 @@ def test_model_from_gguf_matches_set_tensor(ctx, oracle, tmp_path):
     from glypr_amd._lib import GlyprError
     with pytest.raises(GlyprError):
         Model.from_gguf(ctx, str(bad))
+    # a file with the Per-Layer-Embedding tensors and output.weight loads the
+    # full layer (ple_dim from embedding_length_per_layer_input)
+    P, D = 128, 256
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=12, ple_dim=P, out_dim=D)
+    path = tmp_path / "ple.gguf"
+    gu.model_gguf(path, {k: (np.asarray(v[0], np.float32) if not v[3] else v[0], v[1], v[2], v[3])
+                         for k, v in tensors.items()},
+                  n_layers, 768, 1152, 3, 1, 256,
+                  extra_meta=[("gemma-embedding2.embedding_length_per_layer_input", gu.U32, P)])
+    g = Model.from_gguf(ctx, str(path))
+    a = host(m.embed(ids, trunc=200))
+    b = host(g.embed(ids, trunc=200))
+    assert a.shape == (200,) and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    g.close()
+    m.close()

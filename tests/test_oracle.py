@@ -342,8 +342,11 @@ def test_rope_tables_closed_form(oracle, hd, theta):
 
 def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, window, eps=1e-6):
     """Independent float64 statement of forward_embeds (model.rs:498-578) over the
-    layer order of layer.rs:20-50 (no PLE): the same Q8_0 quantization of every
-    GEMM input (oracle quantizer, pinned above), everything else in float64."""
+    layer order of layer.rs:20-50: the same Q8_0 quantization of every GEMM input
+    (oracle quantizer, pinned above), everything else in float64.  With
+    `per_layer_model_proj.weight` present it adds TextPLE (ple.rs:48-85) and each
+    layer's TextPLEBlock with the layer scalar (ple.rs:118-145, norm.rs:65-95);
+    with `output.weight` the embedding projection (model.rs:577)."""
     def deq(name, n, k):
         return oracle.dequantize_rows(tensors[name], k).reshape(n, k).astype(np.float64)
 
@@ -363,9 +366,17 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
         rot = np.concatenate([-x[:, hd // 2:], x[:, :hd // 2]], 1)
         return x * np.cos(e) + rot * np.sin(e)
 
+    def gelu_tanh(x):
+        return 0.5 * x * (1 + np.tanh(np.sqrt(2 / np.pi) * (x + 0.044715 * x ** 3)))
+
     t = ids.size
     table = oracle.dequantize_rows(tensors["token_embd.weight"], H).reshape(-1, H)
     h = (table[ids] * np.float32(np.sqrt(H))).astype(np.float64)
+    ple = None
+    if "per_layer_model_proj.weight" in tensors:
+        P = tensors["per_layer_model_proj.weight"].shape[0] // n_layers
+        raw = lin(h, "per_layer_model_proj.weight", n_layers * P, H) * float(H) ** -0.5
+        ple = rms(raw.reshape(t, n_layers, P), tensors["per_layer_proj_norm.weight"])
     idx = np.arange(t)
     for l in range(n_layers):
         p = f"blk.{l}."
@@ -391,13 +402,87 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
         x = rms(h, tensors[p + "ffn_norm.weight"])
         gt = lin(x, p + "ffn_gate.weight", F, H)
         up = lin(x, p + "ffn_up.weight", F, H)
-        act = 0.5 * gt * (1 + np.tanh(np.sqrt(2 / np.pi) * (gt + 0.044715 * gt ** 3))) * up
+        act = gelu_tanh(gt) * up
         h = h + rms(lin(act, p + "ffn_down.weight", H, F), tensors[p + "post_ffw_norm.weight"])
+        if ple is not None:
+            P = ple.shape[2]
+            a = gelu_tanh(lin(h, p + "inp_gate.weight", P, H)) * ple[:, l, :]
+            h = (h + rms(lin(a, p + "proj.weight", H, P), tensors[p + "post_norm.weight"])) * \
+                float(tensors[p + "layer_output_scale.weight"][0])
     states = rms(h, tensors["output_norm.weight"])
+    if "output.weight" in tensors:
+        states = lin(states, "output.weight", tensors["output.weight"].shape[0], H)
     pooled = states.mean(0)
     pooled /= max(np.linalg.norm(pooled), 1e-12)
     m = pooled[:trunc]
     return m / max(np.linalg.norm(m), 1e-12), states
+
+
+def _small_model(oracle, H, F, nh, nkv, hd, L, vocab, rng, ple_dim=0, out_dim=0):
+    tensors = {"token_embd.weight": oracle.q8_0_weight(vocab, H, 100, 0.02),
+               "output_norm.weight": (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)}
+    seed = 200
+    for l in range(L):
+        for name, n, k in [("attn_q", nh * hd, H), ("attn_k", nkv * hd, H),
+                           ("attn_v", nkv * hd, H), ("attn_output", H, nh * hd),
+                           ("ffn_gate", F, H), ("ffn_up", F, H), ("ffn_down", H, F)]:
+            tensors[f"blk.{l}.{name}.weight"] = oracle.q8_0_weight(n, k, seed, 0.02)
+            seed += 1
+        for name, n in [("attn_norm", H), ("post_attention_norm", H), ("ffn_norm", H),
+                        ("post_ffw_norm", H), ("attn_q_norm", hd), ("attn_k_norm", hd)]:
+            w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+            if name in ("attn_q_norm", "attn_k_norm"):
+                w = (w * 0.25).astype(np.float32)
+            tensors[f"blk.{l}.{name}.weight"] = w
+        if ple_dim:
+            tensors[f"blk.{l}.inp_gate.weight"] = oracle.q8_0_weight(ple_dim, H, seed, 0.05)
+            tensors[f"blk.{l}.proj.weight"] = oracle.q8_0_weight(H, ple_dim, seed + 1, 0.05)
+            seed += 2
+            tensors[f"blk.{l}.post_norm.weight"] = \
+                (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+            tensors[f"blk.{l}.layer_output_scale.weight"] = \
+                np.array([0.5 + 0.5 * rng.random()], np.float32)
+    if ple_dim:
+        tensors["per_layer_model_proj.weight"] = oracle.q8_0_weight(L * ple_dim, H, 900, 0.05)
+        tensors["per_layer_proj_norm.weight"] = \
+            (1 + 0.1 * rng.standard_normal(ple_dim)).astype(np.float32)
+    if out_dim:
+        tensors["output.weight"] = oracle.q8_0_weight(out_dim, H, 901, 0.05)
+    return tensors
+
+
+def test_model_forward_with_ple_vs_float64_statement(oracle):
+    """TextPLE + TextPLEBlock + layer scalar + embedding projection: the oracle
+    against the float64 statement; each added part changes the output, so a
+    dropped term fails."""
+    H, F, nh, nkv, hd, L, vocab, t, W, P, D = 128, 192, 2, 1, 64, 6, 1000, 40, 8, 64, 96
+    rng = np.random.default_rng(12)
+    tensors = _small_model(oracle, H, F, nh, nkv, hd, L, vocab, rng, ple_dim=P, out_dim=D)
+    ids = rng.integers(0, vocab, t).astype(np.uint32)
+    kw = dict(hidden=H, ffn=F, n_heads=nh, n_kv_heads=nkv, head_dim=hd, n_layers=L, vocab=vocab,
+              sliding_window=W)
+    out, states = oracle.model_forward(tensors, ids, 32, **kw)
+    assert states.shape == (t, D) and out.shape == (32,)
+    ref_out, ref_states = _forward_f64(oracle, tensors, ids, 32, H, F, nh, nkv, hd, L, W)
+    row_cos = (states * ref_states).sum(1) / np.linalg.norm(states, axis=1) / \
+        np.linalg.norm(ref_states, axis=1)
+    # Each Q8_0 quantization point (PLE adds two GEMM inputs per layer and the
+    # projection one) rounds the f32 oracle value and the float64-derived one
+    # separately, so isolated int8 flips cost ~3e-5 of row cosine each; a
+    # dropped term costs orders of magnitude more (no layer scalar: 0.64).
+    assert row_cos.min() > 0.9995 and row_cos.mean() > 0.9999, (row_cos.min(), row_cos.mean())
+    assert float(out @ ref_out) > 0.99999
+    # every part is live: dropping the scalars, the PLE block or the projection shows
+    no_scalar = {k: (np.ones(1, np.float32) if k.endswith("layer_output_scale.weight") else v)
+                 for k, v in tensors.items()}
+    o2, _ = oracle.model_forward(no_scalar, ids, 32, **kw)
+    no_ple = {k: v for k, v in tensors.items()
+              if not any(s in k for s in ("per_layer", "inp_gate", ".proj.", "post_norm",
+                                          "layer_output_scale"))}
+    o3, _ = oracle.model_forward(no_ple, ids, 32, **kw)
+    no_out = {k: v for k, v in tensors.items() if k != "output.weight"}
+    _, s4 = oracle.model_forward(no_out, ids, 32, **kw)
+    assert float(o2 @ out) < 0.9999 and float(o3 @ out) < 0.9999 and s4.shape == (t, H)
 
 
 def test_model_forward_vs_float64_statement(oracle):
