@@ -89,13 +89,33 @@ class Layer:
         return 2 * self.m * LAYER_NK
 
 
+PRO_QUANT_M, PRO_NORM_M = 1024, 256   # the library routes to its prologue-fused GEMM up to these M
+
+
+def int8_routes(m: int):
+    """Kernel that runs each C2/C3 projection at M = m in the INT8_EXACT variant
+    (the C ABI's routing): (name, n, k, activation input)."""
+    return [("gemm_i8_pro" if m <= PRO_NORM_M else "gemm_i8", NQ + 2 * NKV, H, "norm"),
+            ("gemm_i8_pro" if m <= PRO_QUANT_M else "gemm_i8", H, NQ, "quant"),
+            ("gemm_i8_geglu", 2 * F, H, "norm"),
+            ("gemm_i8", H, F, "int8")]
+
+
 def kernel_bytes(kernel: str, m: int, variant: int):
     """Algorithmic HBM bytes of every launch of `kernel` in one C2/C3 step:
     each operand read once and each result written once."""
     nb = lambda k: k // 32
-    if kernel == "gemm_i8":     # qkv, o, down on int8 activations, f32 out
-        return sum(m * k + 4 * m * nb(k) + n * k + 4 * n * nb(k) + 4 * m * n
-                   for (n, k) in [(NQ + 2 * NKV, H), (H, NQ), (H, F)])
+    if kernel in ("gemm_i8", "gemm_i8_pro"):
+        tot = 0
+        for name, n, k, act in int8_routes(m):
+            if name != kernel:
+                continue
+            w = n * k + 4 * n * nb(k)
+            if kernel == "gemm_i8_pro":      # f32 activations in (+ the norm weight)
+                tot += 4 * m * k + (4 * k if act == "norm" else 0) + w + 4 * m * n
+            else:                            # Q8_0 activations in
+                tot += m * k + 4 * m * nb(k) + w + 4 * m * n
+        return tot
     if kernel == "gemm_i8_geglu":
         return m * H + 4 * m * nb(H) + 2 * F * H + 4 * 2 * F * nb(H) + m * F + 4 * m * nb(F)
     if kernel == "gemm_bf16":
@@ -103,10 +123,12 @@ def kernel_bytes(kernel: str, m: int, variant: int):
                    for (n, k) in [(NQ + 2 * NKV, H), (H, NQ), (H, F)])
     if kernel == "gemm_bf16_geglu":
         return 2 * m * H + 2 * F * H + 4 * 2 * F * nb(H) + 2 * m * F
-    if kernel == "rmsnorm_quant":   # two launches (qkv, mlp)
-        return 2 * (4 * m * H + 4 * H + m * H + 4 * m * nb(H))
+    if kernel == "rmsnorm_quant":   # the RMSNorm prologues not fused into a GEMM
+        launches = sum(1 for name, _, _, act in int8_routes(m)
+                       if act == "norm" and name != "gemm_i8_pro")
+        return launches * (4 * m * H + 4 * H + m * H + 4 * m * nb(H))
     if kernel == "quantize":
-        return 4 * m * NQ + m * NQ + 4 * m * nb(NQ)
+        return 0 if m <= PRO_QUANT_M else 4 * m * NQ + m * NQ + 4 * m * nb(NQ)
     if kernel in ("rmsnorm_bf16",):
         return 2 * (4 * m * H + 4 * H + 2 * m * H)
     if kernel == "to_bf16":
@@ -115,7 +137,9 @@ def kernel_bytes(kernel: str, m: int, variant: int):
 
 
 def kernel_ops(kernel: str, m: int):
-    if kernel in ("gemm_i8", "gemm_bf16"):
+    if kernel in ("gemm_i8", "gemm_i8_pro"):
+        return sum(2 * m * n * k for name, n, k, _ in int8_routes(m) if name == kernel)
+    if kernel == "gemm_bf16":
         return 2 * m * ((NQ + 2 * NKV) * H + H * NQ + H * F)
     if kernel in ("gemm_i8_geglu", "gemm_bf16_geglu"):
         return 2 * m * 2 * F * H
@@ -180,7 +204,7 @@ def c1_linear(ctx, steps):
     w.close()
     return {"us_per_call": round(ms * 1e3, 3), "tops": round(ops_ / (ms / 1e3) / 1e12, 2),
             "hbm_frac_algorithmic": round(nbytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-            "note": "quantize + GEMM, two kernels"}
+            "note": "one launch: the activation quantization runs as the GEMM prologue"}
 
 
 def vec_search(ctx, steps):

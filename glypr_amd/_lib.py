@@ -90,7 +90,7 @@ SIGNATURES = {
     "glypr_hip_kernel_name": (ctypes.c_char_p, [_int]),
 }
 
-KERNEL_COUNT = 18
+KERNEL_COUNT = 19
 
 
 class GlyprError(RuntimeError):

@@ -44,6 +44,12 @@ int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const fl
                 float eps, bool norm, float* y, int64_t m, int variant, hipStream_t s) {
   const int64_t n = w->n, k = w->k;
   if (variant == GLYPR_Q8_INT8_EXACT) {
+    if (gemm_i8_pro_ok(m, k, norm)) {
+      LAUNCH(GLYPR_K_GEMM_I8_PRO, s,
+             launch_gemm_i8_pro(x, norm_w, eps, norm, w->qs(), w->dw(), y, m, n, k, n, s),
+             "gemm_i8_pro launch");
+      return GLYPR_OK;
+    }
     RET_IF(ensure_ws(ctx, q8_act_bytes(m, k)));
     Carve c(ctx->ws);
     int8_t* xq = c.take<int8_t>((size_t)(m * k));
@@ -628,7 +634,8 @@ int glypr_hip_int8_cosine(glypr_hip_ctx* ctx, const int8_t* a, int64_t na, const
 static const char* const kKernelNames[GLYPR_K_COUNT] = {
     "quantize",   "rmsnorm_quant",  "gemm_i8", "gemm_i8_geglu", "to_bf16", "rmsnorm_bf16",
     "gemm_bf16",  "gemm_bf16_geglu", "rmsnorm", "geglu",         "gather",  "dequant",
-    "pool",       "qkv_post",       "attention", "residual_norm", "vec_encode", "vec_search"};
+    "pool",       "qkv_post",       "attention", "residual_norm", "vec_encode", "vec_search",
+    "gemm_i8_pro"};
 
 const char* glypr_hip_kernel_name(int id) {
   return (id >= 0 && id < GLYPR_K_COUNT) ? kKernelNames[id] : "";

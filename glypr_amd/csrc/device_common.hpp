@@ -46,6 +46,35 @@ __device__ __forceinline__ float max8(float v) {
   v = fmaxf(v, dpp_mov<0x4E>(v, v));    // quad_perm [2,3,0,1]
   return fmaxf(v, dpp_mov<0x141>(v, v));  // row_half_mirror: quad 0 <-> quad 1
 }
+// max8 for values that are >= +0 and never NaN (block amax of |x|, which
+// starts from 0 and ignores NaN like Rust's f32::max): their bit patterns
+// order like the floats, so the reduction is an integer max.
+__device__ __forceinline__ float max8_nonneg(float v) {
+  uint32_t u = __float_as_uint(v);
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0xB1, 0xF, 0xF, false));
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x4E, 0xF, 0xF, false));
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x141, 0xF, 0xF, false));
+  return __uint_as_float(u);
+}
+// v of lane I of each aligned group of 8 lanes, to every lane of the group
+// (ds_swizzle bit mode: lane' = (lane & 0x18) | I within each 32 lanes).
+template <int I>
+__device__ __forceinline__ float bcast8(float v) {
+  static_assert(I >= 0 && I < 8, "lane index");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (I << 5)));
+}
+__device__ __forceinline__ float bcast8(float v, int i) {
+  switch (i) {
+    case 0: return bcast8<0>(v);
+    case 1: return bcast8<1>(v);
+    case 2: return bcast8<2>(v);
+    case 3: return bcast8<3>(v);
+    case 4: return bcast8<4>(v);
+    case 5: return bcast8<5>(v);
+    case 6: return bcast8<6>(v);
+    default: return bcast8<7>(v);
+  }
+}
 // max over each row of 16 lanes; every lane of the row gets it
 __device__ __forceinline__ float max16(float v) {
   v = max8(v);
@@ -58,10 +87,17 @@ __device__ __forceinline__ float max32_hi(float v) {
 }
 
 // Rust `f32::round(v) as i8`: half away from zero, saturating, NaN -> 0.
+// s = RN(v + copysign(pred(0.5), v)) truncates to round-half-away(v) for every
+// finite v (pred(0.5) = 0.5 - 2^-25 keeps v = pred(0.5) from reaching 1, and
+// exact ties still round up because the sum's rounding goes to the even
+// neighbour, the integer); v_cvt_i32_f32 truncates, saturates out-of-range
+// values and maps NaN to 0; med3 clamps to [-128, 127].  Identical to
+// clamp(roundf(v)) with NaN -> 0 for all 2^32 inputs (tests/test_round.py).
 __device__ __forceinline__ int quant_round(float v) {
-  float r = roundf(v);
-  r = fminf(fmaxf(r, -128.0f), 127.0f);
-  return (v != v) ? 0 : (int)r;
+  const float s = v + __builtin_copysignf(0.49999997f, v);
+  int i;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(i) : "v"(s));
+  return min(max(i, -128), 127);
 }
 
 // BlockQ8_0::from_float scale: d = amax / 127; id = d != 0 ? 1/d : 0.

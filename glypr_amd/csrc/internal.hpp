@@ -126,6 +126,16 @@ hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t*
                                 const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
                                 int64_t K, hipStream_t s);
 
+// The int8 GEMM with the activation prologue fused: x is f32 [M][K],
+// quantized to Q8_0 inside the GEMM (norm: of RMSNorm(x; nw, eps), nw
+// nullable), bit-identical to launch_quantize_planar / launch_rmsnorm_quant
+// followed by launch_gemm_i8.  gemm_i8_pro_ok says where it is the faster
+// route (small M).
+bool gemm_i8_pro_ok(int64_t M, int64_t K, bool norm);
+hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
+                              const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
+                              int64_t K, int64_t ldc, hipStream_t s);
+
 // ---- k_vec.hip ----
 hipError_t launch_quantize_binary(const float* x, int64_t n, int64_t dim, uint64_t* out,
                                   hipStream_t s);

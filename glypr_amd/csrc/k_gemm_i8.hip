@@ -320,6 +320,20 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
 
+// s_waitcnt vmcnt(min(later, L) * U): wait until at most `later` stages of U
+// DMA units each are still in flight (`later` is wave-uniform; the immediate
+// must be <= 63).
+template <int U, int L>
+__device__ __forceinline__ void vm_wait_units(int later) {
+  static_assert(L * U <= 63, "vmcnt immediate out of range");
+  if constexpr (L <= 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    if (later >= L) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(L * U) : "memory");
+    else vm_wait_units<U, L - 1>(later);
+  }
+}
+
 constexpr int SMALL_NB_MAX = 36;   // K <= 1152
 
 // WM x WN waves; wave (wm, wn) owns rows 16 wm.. and TNW 16-row B tiles.
@@ -399,15 +413,15 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     ubase[j] = u < UA ? A : B;
     uvoff[j] = grow * K + ((pch ^ (row & 7)) << 4);
   }
-  // stage st (clamped to the last one) into ring slot `slot`
+  // stage st into ring slot `slot`
   auto issue = [&](int st, int slot) {
-    const int sc8 = (st < NST ? st : NST - 1) * BK;
 #pragma unroll
     for (int j = 0; j < UPW; j++)
-      dma16(ubase[j] + sc8, uvoff[j], lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
+      dma16(ubase[j] + st * BK, uvoff[j], lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
   };
 #pragma unroll
-  for (int st = 0; st < RING - 1; st++) issue(st, st);
+  for (int st = 0; st < RING - 1; st++)
+    if (st < NST) issue(st, st);
 
   const int l16 = lane & 15, lq = lane >> 4;   // lq: 8-byte K slice (operands) / row quad (out)
   const int arow = wm * 16 + l16;
@@ -431,15 +445,19 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
     for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
 
+  // Every wait counts exactly the DMA units issued after stage st (a uniform
+  // branch picks the immediate in the last RING - 2 stages): no stage is
+  // fetched twice.
 #pragma unroll 1
   for (int g = 0; g < NST; g += RING) {
 #pragma unroll
     for (int r = 0; r < RING; r++) {
       const int st = g + r;
       if (st < NST) {
-        asm volatile("s_waitcnt vmcnt(%0)" :: "n"((RING - 2) * UPW) : "memory");
+        const int later = (st + RING - 2 < NST - 1 ? st + RING - 2 : NST - 1) - st;
+        vm_wait_units<UPW, RING - 2>(later);
         __syncthreads();
-        issue(st + RING - 1, (r + RING - 1) % RING);
+        if (st + RING - 1 < NST) issue(st + RING - 1, (r + RING - 1) % RING);
         const uint8_t* slot = ring + r * SLOT;
         v4i d[KB][TNW];
 #pragma unroll
@@ -560,6 +578,265 @@ constexpr int64_t SMALL_M_MAX = 2048;
 constexpr int64_t SMALL_K_MAX = 32 * SMALL_NB_MAX;
 inline bool small_ok(int64_t M, int64_t K) {
   return M <= SMALL_M_MAX && K <= SMALL_K_MAX && K % BK == 0;
+}
+
+// ---------------------------------------------------------------------------
+// Small-M GEMM with the activation prologue fused (one launch per op): the
+// workgroup reads its 16 rows of f32 x and builds their Q8_0 operand in LDS
+// itself, while the weight stages stream in by LDS DMA.
+//   PRO_QUANT: BlockQ8_0::from_float of x (QMatMul::forward's quantization);
+//   PRO_NORM:  the same of RMSNorm(x; w) (RmsNorm::forward, then QMatMul).
+// The prologue's arithmetic is the standalone kernels' (rmsnorm_row_kernel,
+// quantize_planar_kernel) op for op, so the int8 operand and its scales are
+// bit-identical to the two-launch path:
+//  - chain lanes: lane j of a row runs the reference's FMA chain j over
+//    x[8c + j] (c in order) straight from global memory, then the AVX2
+//    horizontal sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) and
+//    inv = 1/sqrt(sum/K + eps);
+//  - quantization: eight lanes per 32-block, four values each.
+// Every workgroup along N repeats its rows' prologue, so the tile is wide
+// (BN = 128 B rows on 4 waves) to keep that repetition at N/128.
+// The int8 tile stays resident for the whole K range in the ring-slot layout
+// (stage-major [stage][16 rows][128 B], XOR-swizzled chunks), so the MFMA
+// operand reads are those of gemm_i8_small_kernel.
+// ---------------------------------------------------------------------------
+enum { PRO_QUANT = 1, PRO_NORM = 2 };
+
+template <int PRO, int WN, int TNW, int RING, int NB>
+__global__ void __launch_bounds__(WN * 64)
+gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, float eps,
+                   const int8_t* __restrict__ B, const float* __restrict__ dB,
+                   float* __restrict__ C, int M, int N, int ldc) {
+  constexpr int K = NB * QK, NST = NB / KB;
+  constexpr int NW = WN, BM = 16;
+  constexpr int BN = WN * 16 * TNW;
+  constexpr int UB = BN / 8;               // 1 KB DMA units per stage
+  constexpr int UPW = UB / NW;
+  constexpr int SA = NB * BM, SB = NB * BN;
+  constexpr int SLOT = BN * BK;
+  constexpr int LPR = NW * 64 / BM;        // lanes per row in the prologue
+  constexpr int PARTS = LPR / 8;           // 8-lane groups per row
+  constexpr int BPP = NB / PARTS;          // blocks per group
+  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 1152");
+  static_assert(UB % NW == 0 && RING >= 2, "stage units must split evenly over the waves");
+  static_assert(LPR >= 8 && LPR <= 64 && NB % PARTS == 0, "prologue lane layout");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
+  __shared__ __attribute__((aligned(16))) uint8_t ares[BM * K];
+  __shared__ __attribute__((aligned(16))) float sc[SA + SB + 256];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  // B row of tile-local row nl (rows past N repeat the last one; never stored)
+  auto b_row = [&](int nl) -> int { return n0 + nl < N ? n0 + nl : N - 1; };
+
+  // ---- B scales [BN][NB] by DMA, 16 B (four blocks) per lane
+  constexpr int NQ = NB / 4;
+  constexpr int SCB = SB / 4;
+  for (int c0 = wave * 64; c0 < SCB; c0 += NW * 64) {
+    const int c = c0 + lane < SCB ? c0 + lane : SCB - 1;
+    const int r = c / NQ, q = c - r * NQ;
+    dma16_flat(dB + (int64_t)b_row(r) * NB + 4 * q, lds_u32(sc + SA + 4 * c0));
+  }
+  // ---- B stages: this wave's DMA units (8 rows x 128 B each)
+  const int rsub = lane >> 3, pch = lane & 7;
+  int uvoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; j++) {
+    const int row = (j * NW + wave) * 8 + rsub;
+    uvoff[j] = b_row(row) * K + ((pch ^ (row & 7)) << 4);
+  }
+  auto issue = [&](int st, int slot) {
+#pragma unroll
+    for (int j = 0; j < UPW; j++)
+      dma16(B + st * BK, uvoff[j], lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
+  };
+#pragma unroll
+  for (int st = 0; st < RING - 1; st++)
+    if (st < NST) issue(st, st);
+
+  // ---- prologue: row pr of the tile on lanes [pr * LPR, pr * LPR + LPR);
+  // 8-lane group `part` quantizes blocks [part * BPP, part * BPP + BPP).
+  {
+    const int pr = tid / LPR, pl = tid % LPR;
+    const int pj = pl & 7, part = pl >> 3;
+    const int gm = m0 + pr < M ? m0 + pr : M - 1;
+    const float* xr = X + (int64_t)gm * K;
+    // every operand of the lane is loaded before any is used: one memory
+    // latency, not one per block (ones for a missing norm weight: x * 1 is x)
+    constexpr bool NORM = PRO == PRO_NORM;
+    v4f xv[BPP], wv[NORM ? BPP : 1];
+#pragma unroll
+    for (int i = 0; i < BPP; i++) {
+      const int col = QK * (part * BPP + i) + 4 * pj;
+      xv[i] = *reinterpret_cast<const v4f*>(xr + col);
+      if constexpr (NORM)
+        wv[i] = nw ? *reinterpret_cast<const v4f*>(nw + col) : v4f{1.0f, 1.0f, 1.0f, 1.0f};
+    }
+    float inv = 1.0f;
+    if constexpr (NORM) {
+      float acc = 0.0f;
+      if (part == 0) {
+#pragma unroll
+        for (int c = 0; c < K / 8; c++) {
+          const float e = xr[8 * c + pj];
+          acc = fmaf(e, e, acc);
+        }
+      }
+      const float s = acc + __shfl_down(acc, 4, 8);
+      const float t = s + __shfl_down(s, 2, 8);
+      const float sum = __shfl(t + __shfl_down(t, 1, 8), lane - pl);
+      inv = 1.0f / sqrtf(sum / (float)K + eps);
+    }
+    // Blocks go in groups of up to 8.  The 8 lanes of a block hold the same
+    // amax, so lane j derives the scale of block g0 + j once (two IEEE
+    // divisions) and the group broadcasts the inverses, instead of every lane
+    // dividing for every block.
+#pragma unroll
+    for (int g0 = 0; g0 < BPP; g0 += 8) {
+      const int G = BPP - g0 < 8 ? BPP - g0 : 8;
+      v4f yv[8];
+      float am[8];
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        yv[i] = xv[g0 + i];
+        if constexpr (NORM) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) yv[i][e] = (xv[g0 + i][e] * inv) * wv[g0 + i][e];
+        }
+        float a = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(yv[i][e]));
+        am[i] = max8_nonneg(a);
+      }
+      float asel = am[0];
+#pragma unroll
+      for (int i = 1; i < G; i++) asel = pj == i ? am[i] : asel;
+      const QScale q = q8_scale(asel);
+      if (pj < G) sc[pr * NB + part * BPP + g0 + pj] = q.dq;
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        const float id = bcast8(q.id, i);
+        uint32_t packed = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          packed |= ((uint32_t)(quant_round(yv[i][e] * id) & 0xFF)) << (8 * e);
+        const int col = QK * (part * BPP + g0 + i) + 4 * pj;
+        const int st = col >> 7, qb = col & (BK - 1);
+        *reinterpret_cast<uint32_t*>(ares + st * (BM * BK) + pr * BK +
+                                     (((qb >> 4) ^ (pr & 7)) << 4) + (qb & 15)) = packed;
+      }
+    }
+  }
+
+  const int l16 = lane & 15, lq = lane >> 4;
+  int offA[KB], offB[TNW][KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    const int ch = 2 * kb + (lq >> 1);
+    offA[kb] = l16 * BK + ((ch ^ (l16 & 7)) << 4) + ((lq & 1) << 3);
+#pragma unroll
+    for (int t = 0; t < TNW; t++) {
+      const int brow = wn * 16 * TNW + t * 16 + l16;
+      offB[t][kb] = brow * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+    }
+  }
+  const float* xrow = sc + (4 * lq) * NB;                    // row 4 lq + r at xrow + r NB
+  const float* wrow = sc + SA + (wn * 16 * TNW + l16) * NB;  // tile t at wrow + 16 t NB
+  const v4i magic = {MAGIC, MAGIC, MAGIC, MAGIC};
+  float acc[TNW][4];
+#pragma unroll
+  for (int t = 0; t < TNW; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
+
+  // The prologue's own loads have all been consumed, so the DMA waits below
+  // count only ring units.  The first barrier also publishes the prologue's
+  // LDS writes.
+#pragma unroll 1
+  for (int g = 0; g < NST; g += RING) {
+#pragma unroll
+    for (int r = 0; r < RING; r++) {
+      const int st = g + r;
+      if (st < NST) {
+        const int later = (st + RING - 2 < NST - 1 ? st + RING - 2 : NST - 1) - st;
+        vm_wait_units<UPW, RING - 2>(later);
+        __syncthreads();
+        if (st + RING - 1 < NST) issue(st + RING - 1, (r + RING - 1) % RING);
+        const uint8_t* slot = ring + r * SLOT;
+        const uint8_t* aslot = ares + st * (BM * BK);
+        v4i d[KB][TNW];
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+          const v1l af = *reinterpret_cast<const v1l*>(aslot + offA[kb]);
+#pragma unroll
+          for (int t = 0; t < TNW; t++) {
+            const v1l bf = *reinterpret_cast<const v1l*>(slot + offB[t][kb]);
+            d[kb][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, magic, 0, 0, 0);
+          }
+        }
+        v4f xq[4], wq[TNW];
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++)
+          xq[rr] = *reinterpret_cast<const v4f*>(xrow + rr * NB + st * KB);
+#pragma unroll
+        for (int t = 0; t < TNW; t++)
+          wq[t] = *reinterpret_cast<const v4f*>(wrow + t * 16 * NB + st * KB);
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+          for (int t = 0; t < TNW; t++) {
+            const float wd = wq[t][kb];
+            const float wc = wd * NEG_MAGIC;
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+              float tt = fmaf(__int_as_float(d[kb][t][rr]), wd, wc);  // round(S * d_w)
+              float u = tt * xq[rr][kb];                              // round(. * d_x)
+              acc[t][rr] = acc[t][rr] + u;                            // round(acc + .)
+            }
+          }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const int grow0 = m0 + 4 * lq;
+#pragma unroll
+  for (int t = 0; t < TNW; t++) {
+    const int gn = n0 + wn * 16 * TNW + t * 16 + l16;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      if (grow0 + r < M && gn < N) C[(int64_t)(grow0 + r) * ldc + gn] = acc[t][r];
+  }
+}
+
+template <int PRO, int WN, int TNW, int RING>
+hipError_t run_pro(const float* x, const float* nw, float eps, const int8_t* wq, const float* dw,
+                   float* y, int64_t M, int64_t N, int64_t K, int64_t ldc, hipStream_t s) {
+  constexpr int BN = WN * 16 * TNW;
+  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + 15) / 16));
+#define GLYPR_PRO_NB(nb)                                                                  \
+  case nb:                                                                                \
+    gemm_i8_pro_kernel<PRO, WN, TNW, RING, nb><<<grid, WN * 64, 0, s>>>(                  \
+        x, nw, eps, wq, dw, y, (int)M, (int)N, (int)ldc);                                 \
+    break;
+  switch (K / QK) {
+    GLYPR_PRO_NB(4)
+    GLYPR_PRO_NB(8)
+    GLYPR_PRO_NB(12)
+    GLYPR_PRO_NB(16)
+    GLYPR_PRO_NB(20)
+    GLYPR_PRO_NB(24)
+    GLYPR_PRO_NB(28)
+    GLYPR_PRO_NB(32)
+    GLYPR_PRO_NB(36)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef GLYPR_PRO_NB
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -829,6 +1106,22 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
   if (big_tiles >= 512)
     return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
   return run<64, 64, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+}
+
+// The prologue is repeated by every workgroup along N, so fusing pays only
+// while the saved launch outweighs that repetition (measured on MI355X at
+// EmbeddingGemma widths: quantize up to M = 1024, RMSNorm up to M = 256).
+bool gemm_i8_pro_ok(int64_t M, int64_t K, bool norm) {
+  return small_ok(M, K) && M <= (norm ? 256 : 1024);
+}
+
+hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
+                              const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
+                              int64_t K, int64_t ldc, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  if (!small_ok(M, K)) return hipErrorInvalidValue;
+  if (norm) return run_pro<PRO_NORM, 4, 2, 3>(x, nw, eps, wq, dw, y, M, N, K, ldc, s);
+  return run_pro<PRO_QUANT, 4, 2, 3>(x, nullptr, 0.0f, wq, dw, y, M, N, K, ldc, s);
 }
 
 hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t* wq,

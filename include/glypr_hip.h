@@ -343,7 +343,8 @@ typedef enum glypr_kernel_id {
   GLYPR_K_RESIDUAL_NORM = 15, /* residual + RMSNorm (+ next prologue) */
   GLYPR_K_VEC_ENCODE = 16,    /* binary / int8 output-vector quantization */
   GLYPR_K_VEC_SEARCH = 17,    /* all-pairs hamming / cosine over encoded vectors */
-  GLYPR_K_COUNT = 18
+  GLYPR_K_GEMM_I8_PRO = 18,   /* INT8_EXACT GEMM with the quantize / RMSNorm prologue fused */
+  GLYPR_K_COUNT = 19
 } glypr_kernel_id;
 
 /* The per-op device timing of forward_profiled (profile.rs:53-56, 63-429),

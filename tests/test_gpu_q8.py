@@ -191,6 +191,65 @@ def test_rmsnorm_matmul_bit_exact(ctx, oracle, m):
     assert_bits_equal(y, ref, "rmsnorm+matmul")
 
 
+def _prologue_rows(oracle, m, k, seed):
+    """Activations that stress the quantize prologue: random rows plus, where m
+    allows, an all-zero row (amax 0: scale 0, inverse 0), a row of huge values,
+    a row of denormal-sized values and a row with one outlier per block."""
+    x = oracle.normal(m * k, seed=seed).reshape(m, k) * np.float32(3.0)
+    if m >= 5:
+        x[1] = 0.0
+        x[2] *= np.float32(1e5)
+        x[3] *= np.float32(1e-38)
+        x[4, ::32] = np.float32(-5e4)
+    return x
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 128, 1), (17, 256, 70), (33, 384, 129), (16, 1152, 300),
+                                   (200, 640, 128), (256, 768, 1280), (257, 768, 1280),
+                                   (600, 512, 200), (1024, 768, 768), (1025, 768, 768),
+                                   (2048, 896, 257)])
+def test_fused_prologue_matmul_bit_exact(ctx, oracle, m, k, n):
+    """Small-M matmuls with the quantize / RMSNorm prologue inside the GEMM
+    (quantize up to M = 1024, RMSNorm up to M = 256) and the two-launch route
+    just past those bounds: ragged M and N tiles, every K stage count from 1
+    to 7, special rows, and RMSNorm with and without a weight."""
+    say(f"fused-prologue matmul m={m} k={k} n={n}")
+    x = _prologue_rows(oracle, m, k, seed=500 + m)
+    wb = oracle.q8_0_weight(n, k, seed=600 + n)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    xd = dev(x)
+    y = host(ops.q8_0_matmul(ctx, w, xd, INT8_EXACT))
+    assert_bits_equal(y, oracle.matmul(x, wb, n), "quantize prologue")
+    nw = 1 + 0.1 * oracle.normal(k, seed=k)
+    y = host(ops.rmsnorm_q8_0_matmul(ctx, w, xd, dev(nw), 1e-6, INT8_EXACT))
+    assert_bits_equal(y, oracle.matmul(oracle.rmsnorm(x, nw, 1e-6), wb, n), "rmsnorm prologue")
+    y = host(ops.rmsnorm_q8_0_matmul(ctx, w, xd, None, 1e-5, INT8_EXACT))
+    assert_bits_equal(y, oracle.matmul(oracle.rmsnorm(x, None, 1e-5), wb, n),
+                      "rmsnorm prologue, no weight")
+
+
+@pytest.mark.parametrize("m,H,F", [(1, 128, 32), (19, 256, 96), (64, 1152, 160),
+                                   (300, 512, 64), (2048, 768, 1152)])
+def test_mlp_ragged_small_m_bit_exact(ctx, oracle, m, H, F):
+    """Small-M gate/up GEMM with the GeGLU epilogue: h widths that end inside a
+    GeGLU tile, partial M tiles and the special activation rows."""
+    say(f"mlp ragged m={m} H={H} F={F}")
+    x = _prologue_rows(oracle, m, H, seed=700 + m)
+    gb, ub, db = (oracle.q8_0_weight(F, H, seed=21), oracle.q8_0_weight(F, H, seed=22),
+                  oracle.q8_0_weight(H, F, seed=23))
+    g = Q8Weight.from_gguf(ctx, gb, F, H)
+    u = Q8Weight.from_gguf(ctx, ub, F, H)
+    d = Q8Weight.from_gguf(ctx, db, H, F)
+    gu, _ = Q8Weight.concat(ctx, [g, u])
+    xd = dev(x)
+    y = host(ops.mlp(ctx, gu, d, xd, INT8_EXACT))
+    assert_bits_equal(y, _mlp_ref(oracle, x, gb, ub, db, H, F), "mlp")
+    nw = 1 + 0.1 * oracle.normal(H, seed=H + 1)
+    y = host(ops.rmsnorm_mlp(ctx, gu, d, xd, dev(nw), 1e-6, INT8_EXACT))
+    assert_bits_equal(y, _mlp_ref(oracle, oracle.rmsnorm(x, nw, 1e-6), gb, ub, db, H, F),
+                      "rmsnorm+mlp")
+
+
 def test_geglu_bit_exact(ctx, oracle):
     say("geglu elementwise [512 x 1152] + KAT points")
     g = oracle.normal(512 * 1152, seed=61, std=3.0)
