@@ -75,6 +75,18 @@ __device__ __forceinline__ float bcast8(float v, int i) {
     default: return bcast8<7>(v);
   }
 }
+// max16 for values that are >= +0 and never NaN (see max8_nonneg)
+__device__ __forceinline__ float max16_nonneg(float v) {
+  uint32_t u = __float_as_uint(max8_nonneg(v));
+  u = max(u, (uint32_t)__builtin_amdgcn_update_dpp((int)u, (int)u, 0x140, 0xF, 0xF, false));
+  return __uint_as_float(u);
+}
+// v of lane I of each aligned group of 16 lanes, to every lane of the group
+template <int I>
+__device__ __forceinline__ float bcast16(float v) {
+  static_assert(I >= 0 && I < 16, "lane index");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x10 | (I << 5)));
+}
 // max over each row of 16 lanes; every lane of the row gets it
 __device__ __forceinline__ float max16(float v) {
   v = max8(v);
@@ -115,6 +127,48 @@ __device__ __forceinline__ QScale q8_scale(float amax) {
   s.dbits = f32_to_f16_bits(s.d);
   s.dq = f16_bits_to_f32(s.dbits);
   return s;
+}
+
+// ---------------------------------------------------------------------------
+// LDS DMA (global_load_lds): global memory straight into LDS, no register
+// round trip.  The helpers set m0 themselves; the compiler keeps m0 reserved
+// and the kernels that use them contain no other m0 user (no LDS-DMA
+// builtins, GWS or indexed register moves), which the build's assembly shows.
+// ---------------------------------------------------------------------------
+typedef long v1l;
+
+// 16 bytes per lane, global -> LDS (lane i -> lds_base + 16 i); the address
+// is the uniform base plus the lane's 32-bit offset.
+__device__ __forceinline__ void dma16(const int8_t* base, int voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
+}
+// 16 bytes per lane from a per-lane 64-bit address (lane i -> lds_base + 16 i).
+__device__ __forceinline__ void dma16_flat(const void* g, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(g), "s"(lds_base) : "memory", "m0");
+}
+// 4 bytes per lane (lane i -> lds_base + 4 i).
+__device__ __forceinline__ void dma4(const int8_t* base, int voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+
+// s_waitcnt vmcnt(min(later, L) * U): wait until at most `later` stages of U
+// DMA units each are still in flight (`later` is wave-uniform; the immediate
+// must be <= 63).
+template <int U, int L>
+__device__ __forceinline__ void vm_wait_units(int later) {
+  static_assert(L * U <= 63, "vmcnt immediate out of range");
+  if constexpr (L <= 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    if (later >= L) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(L * U) : "memory");
+    else vm_wait_units<U, L - 1>(later);
+  }
 }
 
 // ---------------------------------------------------------------------------

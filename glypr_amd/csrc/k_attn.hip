@@ -166,13 +166,6 @@ __device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
 // V^T rows are 64 B (4 chunks); the O^T tiles read rows 16 t + l16.
 __device__ __forceinline__ int vswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-// 16 bytes per lane, global (uniform base + lane byte offset) -> LDS (lane i ->
-// lds_base + 16 i).  Sets m0 itself; the attention kernel has no other m0 user.
-__device__ __forceinline__ void attn_dma16(const void* base, int voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
-}
-
 template <int G, int AQS>
 __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     const f16* __restrict__ q16, const f16* __restrict__ kk, const f16* __restrict__ vt,
@@ -248,8 +241,8 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
       const int u = w + NWV * j;
       if (u < 32) {
         const f16* dst = u < 16 ? &Ks[sl][u * 512] : &Vs[sl][(u - 16) * 512];
-        attn_dma16(u < 16 ? kb_base : vb_base, uoff[j],
-                   __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)dst));
+        dma16(reinterpret_cast<const int8_t*>(u < 16 ? kb_base : vb_base), uoff[j],
+              lds_u32(dst));
       }
     }
   };

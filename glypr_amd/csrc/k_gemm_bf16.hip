@@ -28,6 +28,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// GeGLU of the BF16_DEQUANT path, whose h is rounded to bf16 (relative
+// error up to 2^-9): tanh(z) = 1 - 2 / (exp2(2 z log2 e) + 1) on the
+// hardware exp2 and reciprocal (~1e-6 relative), the same tanh-GELU
+// constants and the +-10 clamp of geglu_scalar_f32 (cpu_simd/geglu.rs:6-18).
+__device__ __forceinline__ float geglu_bf16(float g, float u) {
+  if (g <= -10.0f) return 0.0f;
+  if (g >= 10.0f) return g * u;
+  const float inner = 0.7978846f * (g + 0.044715f * (g * g * g));
+  const float e = __builtin_amdgcn_exp2f(2.0f * 1.44269504f * inner);
+  const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+  return 0.5f * g * (1.0f + th) * u;
+}
+
 // 16 int8 -> 16 bf16 (32 bytes) scaled by d.
 __device__ __forceinline__ void dequant16(v4i q, float d, v4i& lo, v4i& hi) {
   const float c = -128.0f * d;
@@ -189,7 +202,7 @@ gemm_bf16_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ B,
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int gm = m0 + wm * WTM + tm * 32 + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-          float h = geglu_scalar(acc[tm][2 * p][r], acc[tm][2 * p + 1][r]);
+          float h = geglu_bf16(acc[tm][2 * p][r], acc[tm][2 * p + 1][r]);
           if (gm < M && hc < F) Hb[(int64_t)gm * F + hc] = __builtin_bit_cast(uint16_t, (__bf16)h);
         }
     }
@@ -205,11 +218,210 @@ hipError_t run(const uint16_t* xb, const int8_t* wq, const float* dw, float* y, 
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Large-M variant (M > 2048, K % 64 == 0).  128 x 256 tiles on 4 waves side
+// by side along N, 128 x 64 outputs each (4 x 2 v_mfma_f32_32x32x16_bf16
+// tiles), so every B column is dequantized by exactly one wave; every
+// 64-K stage arrives by LDS DMA into a two-slot ring:
+//   A  [128 rows][128 B] bf16, 16-byte chunk c of row r at c ^ ((r >> 1) & 7);
+//   B  [256 rows][64 B]  int8, chunk c of row r at c ^ ((r >> 2) & 3);
+//   dB [2 blocks][256 rows] f32.
+// Per 32-K block a lane reads 16 consecutive K of its A row (two b128) and
+// of its B column (one b128 of int8), dequantizes the latter in registers
+// (dequant16: the exact q*d, then bf16 round-to-nearest-even, as the staged
+// path) and runs two MFMA k-steps on K {0..7, 16..23} and {8..15, 24..31} of
+// the block; A and B use the same order, so every product is formed once.
+// XCD-aware tile order as in the int8 large-M kernel; 68 KB of LDS, so two
+// workgroups share a CU.
+// ---------------------------------------------------------------------------
+constexpr int BFB_BM = 128, BFB_BN = 256, BFB_BK = 64;
+
+template <bool GEGLU>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ B,
+                     const float* __restrict__ dB, float* __restrict__ C,
+                     uint16_t* __restrict__ Hb, int M, int N, int K, int ldc, int F,
+                     int tiles_n) {
+  constexpr int NW = 4, TM = 4, TN = 2;
+  constexpr int UA = BFB_BM / 8;         // 1 KB units: 8 A rows of 128 B
+  constexpr int UB = BFB_BN / 16;        // 1 KB units: 16 B rows of 64 B
+  constexpr int USB = 2 * BFB_BN / 64;   // 256 B units: 64 scales of one block
+  constexpr int NU = UA + UB + USB, UPW = NU / NW;
+  constexpr int OFF_B = UA * 1024, OFF_SB = OFF_B + UB * 1024;
+  constexpr int SLOT = OFF_SB + 2 * BFB_BN * 4;
+  static_assert(UA % NW == 0 && UB % NW == 0 && USB % NW == 0,
+                "every unit index j must be of one kind across the waves");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * SLOT];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave;
+  // XCD-aware tile id: workgroup i runs on XCD i % 8.
+  const int nblk = gridDim.x, id = blockIdx.x;
+  const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
+  const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
+  const int tmi = W / tiles_n;
+  const int m0 = tmi * BFB_BM, n0 = (W - tmi * tiles_n) * BFB_BN;
+  const int hc0 = n0 >> 1;
+  const int nb = K / QK, nst = K / BFB_BK;
+
+  // GEGLU: 32-row tiles alternate gate and up of the same 32 h columns.
+  auto b_row = [&](int nl) -> int {
+    if (!GEGLU) return n0 + nl < N ? n0 + nl : N - 1;
+    const int t = nl >> 5;
+    int c = hc0 + (t >> 1) * 32 + (nl & 31);
+    if (c >= F) c = F - 1;
+    return (t & 1) ? F + c : c;
+  };
+  auto a_row = [&](int ml) -> int { return m0 + ml < M ? m0 + ml : M - 1; };
+
+  // this wave's DMA units, unit u = 4 j + wave: [0, UA) A, [UA, UA + UB) B,
+  // then the B scales of block u / 4 of the stage, 64 rows each.
+  const int8_t* ubase[UPW];
+  int uvoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; j++) {
+    const int u = j * NW + wave;
+    if (j * NW < UA) {
+      const int row = u * 8 + (lane >> 3), c = lane & 7;
+      ubase[j] = reinterpret_cast<const int8_t*>(A);
+      uvoff[j] = a_row(row) * (2 * K) + ((c ^ ((row >> 1) & 7)) << 4);
+    } else if (j * NW < UA + UB) {
+      const int row = (u - UA) * 16 + (lane >> 2), c = lane & 3;
+      ubase[j] = B;
+      uvoff[j] = b_row(row) * K + ((c ^ ((row >> 2) & 3)) << 4);
+    } else {
+      const int v = u - UA - UB, kb = v / (BFB_BN / 64);
+      ubase[j] = reinterpret_cast<const int8_t*>(dB);
+      uvoff[j] = (b_row((v % (BFB_BN / 64)) * 64 + lane) * nb + kb) * 4;
+    }
+  }
+  auto issue = [&](int st, int slot) {
+    uint8_t* base = ring + slot * SLOT;
+#pragma unroll
+    for (int j = 0; j < UPW; j++) {
+      const int u = j * NW + wave;
+      if (j * NW < UA)
+        dma16(ubase[j] + st * (2 * BFB_BK), uvoff[j], lds_u32(base + u * 1024));
+      else if (j * NW < UA + UB)
+        dma16(ubase[j] + st * BFB_BK, uvoff[j], lds_u32(base + OFF_B + (u - UA) * 1024));
+      else
+        dma4(ubase[j] + st * 8, uvoff[j], lds_u32(base + OFF_SB + (u - UA - UB) * 256));
+    }
+  };
+  issue(0, 0);
+
+  // fragment offsets; the swizzles depend on lrow only (tile rows are
+  // multiples of 32)
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  int offA[TM][2][2], offB[TN][2], offS[TN][2];
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int row = 32 * tm + lrow, q = 4 * p + 2 * lhalf + h;
+        offA[tm][p][h] = row * 128 + ((q ^ ((row >> 1) & 7)) << 4);
+      }
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      const int row = 64 * wn + 32 * tn + lrow, c = 2 * p + lhalf;
+      offB[tn][p] = OFF_B + row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
+      offS[tn][p] = OFF_SB + (p * BFB_BN + row) * 4;
+    }
+  }
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
+
+#pragma unroll 1
+  for (int st = 0; st < nst; st++) {
+    const int r = st & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (st + 1 < nst) issue(st + 1, r ^ 1);
+    const uint8_t* slot = ring + r * SLOT;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      v8bf a[TM][2];
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+          a[tm][h] = *reinterpret_cast<const v8bf*>(slot + offA[tm][p][h]);
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const v4i q = *reinterpret_cast<const v4i*>(slot + offB[tn][p]);
+        const float d = *reinterpret_cast<const float*>(slot + offS[tn][p]);
+        v4i lo, hi;
+        dequant16(q, d, lo, hi);
+        const v8bf b0 = __builtin_bit_cast(v8bf, lo), b1 = __builtin_bit_cast(v8bf, hi);
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++) {
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][0], b0, acc[tm][tn], 0, 0, 0);
+          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][1], b1, acc[tm][tn], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // output rows of register r: 8 (r >> 2) + 4 lhalf + (r & 3) of the 32-row tile
+  if constexpr (!GEGLU) {
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const int gn = n0 + 64 * wn + 32 * tn + lrow;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int gm = m0 + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+          if (gm < M && gn < N) C[(int64_t)gm * ldc + gn] = acc[tm][tn][r];
+        }
+      }
+  } else {
+    // tiles 0 and 1 of the wave are gate and up of h columns hc0 + 32 wn ..
+    const int hc = hc0 + 32 * wn + lrow;
+#pragma unroll
+    for (int qp = 0; qp < TN / 2; qp++) {
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int gm = m0 + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+          const float h = geglu_bf16(acc[tm][2 * qp][r], acc[tm][2 * qp + 1][r]);
+          if (gm < M && hc < F) Hb[(int64_t)gm * F + hc] = __builtin_bit_cast(uint16_t, (__bf16)h);
+        }
+    }
+  }
+}
+
+template <bool GEGLU>
+hipError_t run_big(const uint16_t* xb, const int8_t* wq, const float* dw, float* y, uint16_t* hb,
+                   int64_t M, int64_t Nrows, int64_t K, int64_t ldc, int64_t F, hipStream_t s) {
+  const int64_t tiles_n = (Nrows + BFB_BN - 1) / BFB_BN;
+  const int64_t tiles = ((M + BFB_BM - 1) / BFB_BM) * tiles_n;
+  gemm_bf16_big_kernel<GEGLU><<<dim3((unsigned)tiles), 256, 0, s>>>(
+      xb, wq, dw, y, hb, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
+  return hipGetLastError();
+}
+
+// The large-M kernel addresses operands with 32-bit offsets.
+inline bool big_ok(int64_t M, int64_t Nrows, int64_t K) {
+  return M > 2048 && K % BFB_BK == 0 && 2 * M * K < (int64_t(1) << 31) &&
+         Nrows * K < (int64_t(1) << 31);
+}
+
 }  // namespace
 
 hipError_t launch_gemm_bf16(const uint16_t* xb, const int8_t* wq, const float* dw, float* y,
                             int64_t M, int64_t N, int64_t K, int64_t ldc, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
+  if (big_ok(M, N, K)) return run_big<false>(xb, wq, dw, y, nullptr, M, N, K, ldc, 0, s);
   int64_t big_tiles = ((M + 255) / 256) * ((N + 127) / 128);
   if (big_tiles >= 256)
     return run<256, 128, 4, 2, false>(xb, wq, dw, y, nullptr, M, N, K, ldc, 0, s);
@@ -219,6 +431,7 @@ hipError_t launch_gemm_bf16(const uint16_t* xb, const int8_t* wq, const float* d
 hipError_t launch_gemm_bf16_geglu(const uint16_t* xb, const int8_t* wq, const float* dw,
                                   uint16_t* hb, int64_t M, int64_t F, int64_t K, hipStream_t s) {
   if (M == 0 || F == 0) return hipSuccess;
+  if (big_ok(M, 2 * F, K)) return run_big<true>(xb, wq, dw, nullptr, hb, M, 2 * F, K, 0, F, s);
   int64_t big_tiles = ((M + 255) / 256) * ((2 * F + 127) / 128);
   if (big_tiles >= 256)
     return run<256, 128, 4, 2, true>(xb, wq, dw, nullptr, hb, M, 2 * F, K, 0, F, s);

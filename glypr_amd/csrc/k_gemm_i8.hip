@@ -300,40 +300,6 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 // chunk (i%8) ^ (row & 7).  Rows past M/N are clamped to a valid row (their
 // outputs are never stored).
 // ---------------------------------------------------------------------------
-typedef long v1l;
-
-// LDS DMA helpers.  They set m0 themselves; the compiler keeps m0 reserved
-// and the kernels that use them contain no other m0 user (no LDS-DMA
-// builtins, GWS or indexed register moves), which the build's assembly shows.
-// 16 bytes per lane, global -> LDS (lane i -> lds_base + 16 i); the address
-// is the uniform base plus the lane's 32-bit offset.
-__device__ __forceinline__ void dma16(const int8_t* base, int voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
-}
-// 16 bytes per lane from a per-lane 64-bit address (lane i -> lds_base + 16 i).
-__device__ __forceinline__ void dma16_flat(const void* g, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(g), "s"(lds_base) : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_u32(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
-}
-
-// s_waitcnt vmcnt(min(later, L) * U): wait until at most `later` stages of U
-// DMA units each are still in flight (`later` is wave-uniform; the immediate
-// must be <= 63).
-template <int U, int L>
-__device__ __forceinline__ void vm_wait_units(int later) {
-  static_assert(L * U <= 63, "vmcnt immediate out of range");
-  if constexpr (L <= 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  } else {
-    if (later >= L) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(L * U) : "memory");
-    else vm_wait_units<U, L - 1>(later);
-  }
-}
-
 constexpr int SMALL_NB_MAX = 36;   // K <= 1152
 
 // WM x WN waves; wave (wm, wn) owns rows 16 wm.. and TNW 16-row B tiles.
@@ -506,32 +472,29 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     }
   } else {
     // h = geglu(gate, up); a row's 32-wide block spans waves wn = 0, 1: each
-    // wave reduces its 16 columns, then one lane per row derives the scale.
-    __shared__ float s_id[BM], s_dq[BM];
+    // wave reduces its 16 columns and publishes the row maxima; after the one
+    // barrier, lane l16 = r of each 16-lane group derives the scale of row
+    // 4 lq + r and the group broadcasts it.
     const int nbh = F / QK;
     const int hc = hc0 + wn * 16 + l16;
     float h[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       h[r] = geglu_scalar(acc[0][r], acc[1][r]);
-      const float v = max16(fmaxf(0.0f, fabsf(h[r])));
+      const float v = max16_nonneg(fmaxf(0.0f, fabsf(h[r])));
       if (l16 == 0) amax_x[wn * BM + wm * 16 + 4 * lq + r] = v;
     }
     __syncthreads();
-    if (tid < BM) {
-      const QScale q = q8_scale(fmaxf(amax_x[tid], amax_x[BM + tid]));
-      s_id[tid] = q.id;
-      s_dq[tid] = q.dq;
-    }
-    __syncthreads();
+    const int lrs = wm * 16 + 4 * lq + (l16 & 3);
+    const QScale q = q8_scale(fmaxf(amax_x[lrs], amax_x[BM + lrs]));
+    const float ids[4] = {bcast16<0>(q.id), bcast16<1>(q.id), bcast16<2>(q.id),
+                          bcast16<3>(q.id)};
+    if (hc < F) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int lr = wm * 16 + 4 * lq + r;
-      const int gm = grow0 + r;
-      if (gm < M && hc < F) {
-        Hq[(int64_t)gm * F + hc] = (int8_t)quant_round(h[r] * s_id[lr]);
-        if (wn == 0 && l16 == 0) dH[(int64_t)gm * nbh + (hc >> 5)] = s_dq[lr];
-      }
+      for (int r = 0; r < 4; r++)
+        if (grow0 + r < M) Hq[(int64_t)(grow0 + r) * F + hc] = (int8_t)quant_round(h[r] * ids[r]);
+      if (wn == 0 && l16 < 4 && grow0 + l16 < M)
+        dH[(int64_t)(grow0 + l16) * nbh + (hc >> 5)] = q.dq;
     }
   }
 }
@@ -867,10 +830,6 @@ hipError_t run_pro(const float* x, const float* nw, float eps, const int8_t* wq,
 // ---------------------------------------------------------------------------
 constexpr int BIG_BM = 128, BIG_BN = 128;
 
-__device__ __forceinline__ void dma4(const int8_t* base, int voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
-               :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
-}
 __device__ __forceinline__ int big_swz(int row) { return (row >> 1) & 7; }
 
 template <bool GEGLU>

@@ -23,7 +23,6 @@ namespace glypr {
 
 namespace {
 
-typedef long v1l;
 
 constexpr int BIN_WPW = 8;   // words per wave per iteration
 

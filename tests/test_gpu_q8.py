@@ -364,7 +364,8 @@ def test_pool_vs_f64_and_oracle(ctx, oracle):
 # ------------------------------------------------------------ bf16 variant -
 
 @pytest.mark.parametrize("m,k,n", [(19, 256, 128), (512, 768, 1152), (4096, 768, 1152),
-                                   (300, 1152, 768)])
+                                   (300, 1152, 768), (2049, 64, 300), (3000, 1152, 70),
+                                   (4100, 768, 1280), (2500, 96, 257)])
 def test_matmul_bf16_dequant_within_bf16_bound(ctx, oracle, m, k, n):
     """BF16_DEQUANT vs the float64 dequant oracle: both operands rounded to bf16
     (relative error <= 2^-8 each), f32 accumulation:
@@ -382,9 +383,11 @@ def test_matmul_bf16_dequant_within_bf16_bound(ctx, oracle, m, k, n):
     assert cos.min() > 0.9999
 
 
-def test_mlp_bf16_dequant(ctx, oracle):
-    m, H, F = 512, 768, 1152
-    say("mlp BF16_DEQUANT m=512")
+@pytest.mark.parametrize("m,H,F", [(512, 768, 1152), (2200, 256, 96), (3000, 768, 1152)])
+def test_mlp_bf16_dequant(ctx, oracle, m, H, F):
+    """BF16_DEQUANT gate/up + GeGLU + down vs the float64 dequant oracle; the
+    large-M shapes run the 128 x 256 tile kernel (partial h tiles for F = 96)."""
+    say(f"mlp BF16_DEQUANT m={m} H={H} F={F}")
     x = oracle.normal(m * H, seed=400).reshape(m, H)
     gb, ub, db = (oracle.q8_0_weight(F, H, seed=41), oracle.q8_0_weight(F, H, seed=42),
                   oracle.q8_0_weight(H, F, seed=43))
