@@ -234,15 +234,16 @@ hipError_t run(const uint16_t* xb, const int8_t* wq, const float* dw, float* y, 
 // XCD-aware tile order as in the int8 large-M kernel; 68 KB of LDS, so two
 // workgroups share a CU.
 // ---------------------------------------------------------------------------
-constexpr int BFB_BM = 128, BFB_BN = 256, BFB_BK = 64;
+constexpr int BFB_BN = 256, BFB_BK = 64;
 
-template <bool GEGLU>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+// TM 32-row MFMA tiles per wave (BM = 32 TM rows per workgroup).
+template <bool GEGLU, int TM>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TM == 2 ? 3 : 2)))
 gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ B,
                      const float* __restrict__ dB, float* __restrict__ C,
                      uint16_t* __restrict__ Hb, int M, int N, int K, int ldc, int F,
                      int tiles_n) {
-  constexpr int NW = 4, TM = 4, TN = 2;
+  constexpr int NW = 4, TN = 2, BFB_BM = 32 * TM;
   constexpr int UA = BFB_BM / 8;         // 1 KB units: 8 A rows of 128 B
   constexpr int UB = BFB_BN / 16;        // 1 KB units: 16 B rows of 64 B
   constexpr int USB = 2 * BFB_BN / 64;   // 256 B units: 64 scales of one block
@@ -400,12 +401,13 @@ gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ 
   }
 }
 
-template <bool GEGLU>
+template <bool GEGLU, int TM>
 hipError_t run_big(const uint16_t* xb, const int8_t* wq, const float* dw, float* y, uint16_t* hb,
                    int64_t M, int64_t Nrows, int64_t K, int64_t ldc, int64_t F, hipStream_t s) {
+  constexpr int BM = 32 * TM;
   const int64_t tiles_n = (Nrows + BFB_BN - 1) / BFB_BN;
-  const int64_t tiles = ((M + BFB_BM - 1) / BFB_BM) * tiles_n;
-  gemm_bf16_big_kernel<GEGLU><<<dim3((unsigned)tiles), 256, 0, s>>>(
+  const int64_t tiles = ((M + BM - 1) / BM) * tiles_n;
+  gemm_bf16_big_kernel<GEGLU, TM><<<dim3((unsigned)tiles), 256, 0, s>>>(
       xb, wq, dw, y, hb, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
   return hipGetLastError();
 }
@@ -421,7 +423,7 @@ inline bool big_ok(int64_t M, int64_t Nrows, int64_t K) {
 hipError_t launch_gemm_bf16(const uint16_t* xb, const int8_t* wq, const float* dw, float* y,
                             int64_t M, int64_t N, int64_t K, int64_t ldc, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (big_ok(M, N, K)) return run_big<false>(xb, wq, dw, y, nullptr, M, N, K, ldc, 0, s);
+  if (big_ok(M, N, K)) return run_big<false, 4>(xb, wq, dw, y, nullptr, M, N, K, ldc, 0, s);
   int64_t big_tiles = ((M + 255) / 256) * ((N + 127) / 128);
   if (big_tiles >= 256)
     return run<256, 128, 4, 2, false>(xb, wq, dw, y, nullptr, M, N, K, ldc, 0, s);
@@ -431,7 +433,7 @@ hipError_t launch_gemm_bf16(const uint16_t* xb, const int8_t* wq, const float* d
 hipError_t launch_gemm_bf16_geglu(const uint16_t* xb, const int8_t* wq, const float* dw,
                                   uint16_t* hb, int64_t M, int64_t F, int64_t K, hipStream_t s) {
   if (M == 0 || F == 0) return hipSuccess;
-  if (big_ok(M, 2 * F, K)) return run_big<true>(xb, wq, dw, nullptr, hb, M, 2 * F, K, 0, F, s);
+  if (big_ok(M, 2 * F, K)) return run_big<true, 4>(xb, wq, dw, nullptr, hb, M, 2 * F, K, 0, F, s);
   int64_t big_tiles = ((M + 255) / 256) * ((2 * F + 127) / 128);
   if (big_tiles >= 256)
     return run<256, 128, 4, 2, true>(xb, wq, dw, nullptr, hb, M, 2 * F, K, 0, F, s);
