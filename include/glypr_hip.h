@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define GLYPR_HIP_ABI_VERSION 3
+#define GLYPR_HIP_ABI_VERSION 4
 
 typedef enum glypr_status {
   GLYPR_OK = 0,
