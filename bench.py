@@ -289,9 +289,12 @@ def roofline_for(kern, m, variant, steps, workload="C2"):
 QK_NORM_SCALE = 0.25
 
 
-def model_tensors(rng, n_layers, vocab, hidden=H, ffn=F, nq=3, nkv=1, hd=256):
+def model_tensors(rng, n_layers, vocab, hidden=H, ffn=F, nq=3, nkv=1, hd=256, dense=False):
     """Synthetic EmbeddingGemma backbone tensors by GGUF name: Q8_0 projections with
-    BASELINE's distribution, norm weights 1 + 0.1 N(0,1) (q/k norms x 0.25)."""
+    BASELINE's distribution, norm weights 1 + 0.1 N(0,1) (q/k norms x 0.25).
+    dense: the projections are bf16 weights of the same shapes, N(0, 0.02) rounded
+    to bf16 (config 5's bf16-weight variant); the token table stays Q8_0."""
+    from glypr_amd.ops import f32_to_bf16_bits
     t = {"token_embd.weight": (q8_0_weight(rng, vocab, hidden), vocab, hidden, True),
          "output_norm.weight": ((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32), 1,
                                 hidden, False)}
@@ -300,7 +303,11 @@ def model_tensors(rng, n_layers, vocab, hidden=H, ffn=F, nq=3, nkv=1, hd=256):
                            ("attn_v", nkv * hd, hidden), ("attn_output", hidden, nq * hd),
                            ("ffn_gate", ffn, hidden), ("ffn_up", ffn, hidden),
                            ("ffn_down", hidden, ffn)]:
-            t[f"blk.{i}.{name}.weight"] = (q8_0_weight(rng, n, k), n, k, True)
+            if dense:
+                w = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+                t[f"blk.{i}.{name}.weight"] = (f32_to_bf16_bits(w), n, k, False)
+            else:
+                t[f"blk.{i}.{name}.weight"] = (q8_0_weight(rng, n, k), n, k, True)
         for name, n in [("attn_norm", hidden), ("post_attention_norm", hidden),
                         ("ffn_norm", hidden), ("post_ffw_norm", hidden), ("attn_q_norm", hd),
                         ("attn_k_norm", hd)]:
@@ -350,7 +357,7 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1):
     return {"ms_per_embedding": round(ms, 4), "embeddings_per_s": round(1000.0 / ms, 2),
             "tokens_per_s": round(t * 1000.0 / ms, 1),
             "gemm_ops_per_embedding": 2 * t * n_layers * LAYER_NK,
-            "q8_gemm_tops": round(2 * t * n_layers * LAYER_NK / (ms / 1e3) / 1e12, 2),
+            "gemm_tops": round(2 * t * n_layers * LAYER_NK / (ms / 1e3) / 1e12, 2),
             "split_ms_profiled": split, "gemm_ms": round(gemm, 4), "attention_ms": round(att, 4)}
 
 
@@ -504,6 +511,11 @@ def main():
         if "c5" in todo:
             extra["c5"] = run_backbone(ctx, tensors, 24, 262144, 8192, 3, 1)
         del tensors
+        if "c5" in todo:
+            dense = model_tensors(np.random.default_rng(8), 24, 262144, dense=True)
+            extra["c5_bf16w"] = run_backbone(ctx, dense, 24, 262144, 8192, 3, 1)
+            extra["c5_bf16w"]["weights"] = "dense bf16 projections (8,454,144 B per layer)"
+            del dense
 
     line = {
         "metric": "Q8_0 matmul TOPS (% MFMA peak); 512-tok embeddings/sec on 1 MI355X",

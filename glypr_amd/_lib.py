@@ -46,6 +46,9 @@ SIGNATURES = {
     "glypr_hip_q8_0_dequantize": (_int, [_vp, _vp, _vp, _vp]),
     "glypr_hip_q8_0_quantize": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "glypr_hip_q8_0_matmul": (_int, [_vp, _vp, _vp, _vp, _i64, _int, _vp]),
+    "glypr_hip_bf16_weight_create": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "glypr_hip_bf16_weight_destroy": (_int, [_vp]),
+    "glypr_hip_bf16_matmul": (_int, [_vp, _vp, _vp, _vp, _i64, _vp]),
     "glypr_hip_rmsnorm": (_int, [_vp, _vp, _vp, _f32, _vp, _i64, _i64, _vp]),
     "glypr_hip_rmsnorm_q8_0_matmul": (_int, [_vp, _vp, _vp, _vp, _f32, _vp, _i64, _int, _vp]),
     "glypr_hip_geglu": (_int, [_vp, _vp, _vp, _vp, _i64, _vp]),
@@ -90,7 +93,7 @@ SIGNATURES = {
     "glypr_hip_kernel_name": (ctypes.c_char_p, [_int]),
 }
 
-KERNEL_COUNT = 19
+KERNEL_COUNT = 20
 
 
 class GlyprError(RuntimeError):

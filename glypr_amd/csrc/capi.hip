@@ -339,6 +339,73 @@ int glypr_hip_q8_0_dequantize(glypr_hip_ctx* ctx, const glypr_q8w* w, float* out
   return GLYPR_OK;
 }
 
+int glypr_hip_bf16_weight_create(glypr_hip_ctx* ctx, const uint16_t* bf16_rows, int64_t n,
+                                 int64_t k, glypr_bf16w** out) {
+  clear_error();
+  GLYPR_CHECK(out != nullptr && bf16_rows != nullptr, GLYPR_ERR_INVALID_ARG,
+              "bf16_rows or out is NULL");
+  *out = nullptr;
+  GLYPR_CHECK(n > 0 && k > 0, GLYPR_ERR_SHAPE, "weight shape (%lld, %lld) must be positive",
+              (long long)n, (long long)k);
+  GLYPR_CHECK(k % 64 == 0, GLYPR_ERR_UNSUPPORTED,
+              "in_dim %lld: dense bf16 weights need a multiple of 64", (long long)k);
+  GLYPR_CHECK(2 * n * k < (int64_t(1) << 31), GLYPR_ERR_SHAPE, "weight of %lld x %lld too large",
+              (long long)n, (long long)k);
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  glypr_bf16w* w = new (std::nothrow) glypr_bf16w();
+  GLYPR_CHECK(w != nullptr, GLYPR_ERR_OOM, "host allocation failed");
+  w->n = n;
+  w->k = k;
+  w->device = ctx->device;
+  hipError_t e = hipMalloc((void**)&w->p, (size_t)(n * k) * 2);
+  if (e == hipSuccess) e = hipMemcpy(w->p, bf16_rows, (size_t)(n * k) * 2, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    if (w->p) (void)hipFree(w->p);
+    delete w;
+    return hip_error(e, "bf16 weight upload");
+  }
+  *out = w;
+  return GLYPR_OK;
+}
+
+int glypr_hip_bf16_weight_destroy(glypr_bf16w* w) {
+  clear_error();
+  if (!w) return GLYPR_OK;
+  {
+    DeviceScope ds(w->device);
+    if (w->p) (void)hipFree(w->p);
+  }
+  delete w;
+  return GLYPR_OK;
+}
+
+int glypr_hip_bf16_matmul(glypr_hip_ctx* ctx, const glypr_bf16w* w, const float* x, float* y,
+                          int64_t m, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
+  GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
+  GLYPR_CHECK(m == 0 || (x != nullptr && y != nullptr), GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(aligned16(x) && aligned16(y), GLYPR_ERR_ALIGNMENT, "x and y must be 16-byte aligned");
+  GLYPR_CHECK(2 * m * w->k < (int64_t(1) << 31), GLYPR_ERR_SHAPE, "m = %lld too large",
+              (long long)m);
+  RET_IF(check_ctx(ctx));
+  GLYPR_CHECK(w->device == ctx->device, GLYPR_ERR_DEVICE,
+              "w lives on device %d, context is device %d", w->device, ctx->device);
+  if (m == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  hipStream_t s = (hipStream_t)stream;
+  RET_IF(ensure_ws(ctx, align_up((size_t)(m * w->k) * 2, 256)));
+  uint16_t* xb = reinterpret_cast<uint16_t*>(ctx->ws);
+  LAUNCH(GLYPR_K_TO_BF16, s, launch_to_bf16(x, m * w->k, xb, s), "to_bf16 launch");
+  LAUNCH(GLYPR_K_GEMM_BF16W, s, launch_gemm_bf16w(xb, w->p, y, m, w->n, w->k, w->n, s),
+         "gemm_bf16w launch");
+  return GLYPR_OK;
+}
+
 int glypr_hip_q8_0_quantize(glypr_hip_ctx* ctx, const float* x, int64_t m, int64_t k,
                             uint8_t* out_blocks, glypr_stream stream) {
   clear_error();
@@ -635,7 +702,7 @@ static const char* const kKernelNames[GLYPR_K_COUNT] = {
     "quantize",   "rmsnorm_quant",  "gemm_i8", "gemm_i8_geglu", "to_bf16", "rmsnorm_bf16",
     "gemm_bf16",  "gemm_bf16_geglu", "rmsnorm", "geglu",         "gather",  "dequant",
     "pool",       "qkv_post",       "attention", "residual_norm", "vec_encode", "vec_search",
-    "gemm_i8_pro"};
+    "gemm_i8_pro", "gemm_bf16w"};
 
 const char* glypr_hip_kernel_name(int id) {
   return (id >= 0 && id < GLYPR_K_COUNT) ? kKernelNames[id] : "";

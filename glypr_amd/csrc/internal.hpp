@@ -29,6 +29,12 @@ struct glypr_q8w {
   const float* dw() const { return buf->dw + row0 * (k / 32); }
 };
 
+struct glypr_bf16w {
+  uint16_t* p = nullptr;  // [n][k] bf16
+  int64_t n = 0, k = 0;
+  int device = 0;
+};
+
 struct ProfRec {
   int kernel;
   hipEvent_t start, stop;
@@ -89,10 +95,12 @@ hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t
 // h = h + rmsnorm(x; w_post); if xq: (xq, dx) = Q8_0(rmsnorm(h; w_next)).  dim % 32 == 0.
 // scalar (device, nullable): h = (h + RMSNorm(x)) * scalar.  plain_q: xq/dx
 // receive Q8_0 of h itself instead of Q8_0 of RMSNorm(h; w_next).
+// xb (nullable, instead of xq): bf16 of RMSNorm(h; w_next), the next dense-bf16
+// GEMM's operand.
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
                                 hipStream_t s, const float* scalar = nullptr,
-                                bool plain_q = false);
+                                bool plain_q = false, uint16_t* xb = nullptr);
 // x = x * mul + 0 (f32), in place
 hipError_t launch_affine(float* x, int64_t n, float mul, hipStream_t s);
 // Q8_0 of geglu(g, u): g [rows][dim], u row r at u + r * u_stride
@@ -109,11 +117,12 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
                            const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
                            uint16_t* vt16, hipStream_t s);
 size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t window);
-// ctx (f32 [T][nq*hd]) and/or (cq, dc) (Q8_0 planar) may be null.
+// ctx (f32 [T][nq*hd]), (cq, dc) (Q8_0 planar) and cb (bf16 [T][nq*hd]) may
+// each be null.
 hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
                             float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
                             int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
-                            hipStream_t s);
+                            hipStream_t s, uint16_t* cb = nullptr);
 
 // ---- k_gemm_i8.hip ----
 // y[m,n] = sum_b ((float)S_b * dw[n,b]) * dx[m,b], sequential over b (exact).
@@ -135,6 +144,15 @@ bool gemm_i8_pro_ok(int64_t M, int64_t K, bool norm);
 hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
                               const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
                               int64_t K, int64_t ldc, hipStream_t s);
+
+// ---- k_gemm_bf16.hip, dense bf16 weights ----
+// y = xb . wb^T (xb bf16 [M][K], wb bf16 [N][K]), f32 out; the GeGLU form takes
+// wb = [gate; up] (2F rows) and writes h bf16 [M][F].  K % 64 == 0.
+bool gemm_bf16w_ok(int64_t M, int64_t Nrows, int64_t K);
+hipError_t launch_gemm_bf16w(const uint16_t* xb, const uint16_t* wb, float* y, int64_t M,
+                             int64_t N, int64_t K, int64_t ldc, hipStream_t s);
+hipError_t launch_gemm_bf16w_geglu(const uint16_t* xb, const uint16_t* wb, uint16_t* hb,
+                                   int64_t M, int64_t F, int64_t K, hipStream_t s);
 
 // ---- k_vec.hip ----
 hipError_t launch_quantize_binary(const float* x, int64_t n, int64_t dim, uint64_t* out,

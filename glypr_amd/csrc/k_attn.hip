@@ -372,7 +372,8 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
 // holds partition p's (m, l); readlane broadcasts them.
 __global__ void __launch_bounds__(256) attn_combine_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml, int T, int Tp, int nq,
-    int kparts, float* __restrict__ ctx, int8_t* __restrict__ cq, float* __restrict__ dc) {
+    int kparts, float* __restrict__ ctx, int8_t* __restrict__ cq, float* __restrict__ dc,
+    uint16_t* __restrict__ cb) {
   const int lane = threadIdx.x & 63;
   const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (task >= (int64_t)T * nq) return;
@@ -405,6 +406,14 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
   for (int e = 0; e < 4; e++) y[e] = acc[e] * inv;
   const int64_t col = (int64_t)h * QKV_HD + 4 * lane;
   if (ctx) *reinterpret_cast<v4f*>(ctx + q * width + col) = y;
+  if (cb) {
+    // bf16, round to nearest even (the dense-bf16 o projection's operand)
+    uint32_t* dst = reinterpret_cast<uint32_t*>(cb + q * width + col);
+    dst[0] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[0]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[1]) << 16);
+    dst[1] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[2]) |
+             ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[3]) << 16);
+  }
   if (cq) {
     float a = 0.0f;
 #pragma unroll
@@ -451,7 +460,7 @@ size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t wind
 hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
                             float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
                             int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
-                            hipStream_t s) {
+                            hipStream_t s, uint16_t* cb) {
   if (hd != QKV_HD || Tp % ATTN_TP_ALIGN != 0 || Tp < T || nq % nkv != 0)
     return hipErrorInvalidValue;
   const int64_t G = nq / nkv;
@@ -480,7 +489,7 @@ hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   attn_combine_kernel<<<(unsigned)((T * nq + 3) / 4), 256, 0, s>>>(
-      part_o, part_ml, (int)T, (int)Tp, (int)nq, kparts, ctx, cq, dc);
+      part_o, part_ml, (int)T, (int)Tp, (int)nq, kparts, ctx, cq, dc, cb);
   return hipGetLastError();
 }
 

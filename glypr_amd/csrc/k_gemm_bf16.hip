@@ -418,6 +418,162 @@ inline bool big_ok(int64_t M, int64_t Nrows, int64_t K) {
          Nrows * K < (int64_t(1) << 31);
 }
 
+// ---------------------------------------------------------------------------
+// Dense bf16 weights (LinearOp over an F16/BF16 GGUF tensor, linear.rs:48-54,
+// at bf16): C = A . B^T with A bf16 [M][K] and B bf16 [N][K], f32 accumulate.
+// 128 x 128 tiles on a 2 x 2 grid of waves (64 x 64 outputs each, 2 x 2
+// v_mfma_f32_32x32x16_bf16 tiles); each 64-K stage of A and B arrives by LDS
+// DMA into a two-slot ring, both [128 rows][128 B] with chunk c of row r at
+// c ^ ((r >> 1) & 7); 64 KB of LDS, two workgroups per CU.  Per 32-K block a
+// lane takes 16 consecutive K of its A row and B column (two b128 each) as two
+// MFMA k-steps, the same order on both sides.  GEGLU: 32-row tiles alternate
+// gate and up of the same 32 h columns; h = geglu(gate, up) leaves as bf16.
+// ---------------------------------------------------------------------------
+constexpr int BFW_BM = 128, BFW_BN = 128, BFW_BK = 64;
+
+template <bool GEGLU>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+gemm_bf16w_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                  float* __restrict__ C, uint16_t* __restrict__ Hb, int M, int N, int K,
+                  int ldc, int F, int tiles_n) {
+  constexpr int NW = 4, TM = 2, TN = 2;
+  constexpr int UA = BFW_BM / 8, UB = BFW_BN / 8;   // 1 KB units: 8 rows of 128 B
+  constexpr int UPW = (UA + UB) / NW;
+  constexpr int SLOT = (UA + UB) * 1024;
+  static_assert(UA % NW == 0 && UB % NW == 0, "every unit index j must be of one kind");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * SLOT];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nblk = gridDim.x, id = blockIdx.x;
+  const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
+  const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
+  const int tmi = W / tiles_n;
+  const int m0 = tmi * BFW_BM, n0 = (W - tmi * tiles_n) * BFW_BN;
+  const int hc0 = n0 >> 1;
+  const int nst = K / BFW_BK;
+
+  auto b_row = [&](int nl) -> int {
+    if (!GEGLU) return n0 + nl < N ? n0 + nl : N - 1;
+    const int t = nl >> 5;
+    int c = hc0 + (t >> 1) * 32 + (nl & 31);
+    if (c >= F) c = F - 1;
+    return (t & 1) ? F + c : c;
+  };
+  auto a_row = [&](int ml) -> int { return m0 + ml < M ? m0 + ml : M - 1; };
+
+  const int8_t* ubase[UPW];
+  int uvoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; j++) {
+    const int u = j * NW + wave;
+    const int row = (u < UA ? u : u - UA) * 8 + (lane >> 3), c = lane & 7;
+    const int grow = u < UA ? a_row(row) : b_row(row);
+    ubase[j] = reinterpret_cast<const int8_t*>(u < UA ? A : B);
+    uvoff[j] = grow * (2 * K) + ((c ^ ((row >> 1) & 7)) << 4);
+  }
+  auto issue = [&](int st, int slot) {
+#pragma unroll
+    for (int j = 0; j < UPW; j++)
+      dma16(ubase[j] + st * (2 * BFW_BK), uvoff[j],
+            lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
+  };
+  issue(0, 0);
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  int offA[TM][2][2], offB[TN][2][2];
+#pragma unroll
+  for (int p = 0; p < 2; p++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 4 * p + 2 * lhalf + h;
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++) {
+        const int row = 64 * wm + 32 * tm + lrow;
+        offA[tm][p][h] = row * 128 + ((q ^ ((row >> 1) & 7)) << 4);
+      }
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const int row = 64 * wn + 32 * tn + lrow;
+        offB[tn][p][h] = UA * 1024 + row * 128 + ((q ^ ((row >> 1) & 7)) << 4);
+      }
+    }
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
+
+#pragma unroll 1
+  for (int st = 0; st < nst; st++) {
+    const int r = st & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (st + 1 < nst) issue(st + 1, r ^ 1);
+    const uint8_t* slot = ring + r * SLOT;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      v8bf a[TM][2], b[TN][2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+          a[tm][h] = *reinterpret_cast<const v8bf*>(slot + offA[tm][p][h]);
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++)
+          b[tn][h] = *reinterpret_cast<const v8bf*>(slot + offB[tn][p][h]);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+          for (int tn = 0; tn < TN; tn++)
+            acc[tm][tn] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][h], b[tn][h], acc[tm][tn], 0, 0, 0);
+    }
+  }
+
+  // output rows of register r: 8 (r >> 2) + 4 lhalf + (r & 3) of the 32-row tile
+  if constexpr (!GEGLU) {
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const int gn = n0 + 64 * wn + 32 * tn + lrow;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int gm = m0 + 64 * wm + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+          if (gm < M && gn < N) C[(int64_t)gm * ldc + gn] = acc[tm][tn][r];
+        }
+      }
+  } else {
+    // tiles 0 and 1 of the wave are gate and up of h columns hc0 + 32 wn ..
+    const int hc = hc0 + 32 * wn + lrow;
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int gm = m0 + 64 * wm + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+        const float h = geglu_bf16(acc[tm][0][r], acc[tm][1][r]);
+        if (gm < M && hc < F) Hb[(int64_t)gm * F + hc] = __builtin_bit_cast(uint16_t, (__bf16)h);
+      }
+  }
+}
+
+template <bool GEGLU>
+hipError_t run_dense(const uint16_t* xb, const uint16_t* wb, float* y, uint16_t* hb, int64_t M,
+                     int64_t Nrows, int64_t K, int64_t ldc, int64_t F, hipStream_t s) {
+  const int64_t tiles_n = (Nrows + BFW_BN - 1) / BFW_BN;
+  const int64_t tiles = ((M + BFW_BM - 1) / BFW_BM) * tiles_n;
+  gemm_bf16w_kernel<GEGLU><<<dim3((unsigned)tiles), 256, 0, s>>>(
+      xb, wb, y, hb, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_gemm_bf16(const uint16_t* xb, const int8_t* wq, const float* dw, float* y,
@@ -438,6 +594,28 @@ hipError_t launch_gemm_bf16_geglu(const uint16_t* xb, const int8_t* wq, const fl
   if (big_tiles >= 256)
     return run<256, 128, 4, 2, true>(xb, wq, dw, nullptr, hb, M, 2 * F, K, 0, F, s);
   return run<64, 128, 2, 2, true>(xb, wq, dw, nullptr, hb, M, 2 * F, K, 0, F, s);
+}
+
+}  // namespace glypr
+
+namespace glypr {
+
+bool gemm_bf16w_ok(int64_t M, int64_t Nrows, int64_t K) {
+  return K % BFW_BK == 0 && 2 * M * K < (int64_t(1) << 31) && 2 * Nrows * K < (int64_t(1) << 31);
+}
+
+hipError_t launch_gemm_bf16w(const uint16_t* xb, const uint16_t* wb, float* y, int64_t M,
+                             int64_t N, int64_t K, int64_t ldc, hipStream_t s) {
+  if (M == 0 || N == 0) return hipSuccess;
+  if (!gemm_bf16w_ok(M, N, K)) return hipErrorInvalidValue;
+  return run_dense<false>(xb, wb, y, nullptr, M, N, K, ldc, 0, s);
+}
+
+hipError_t launch_gemm_bf16w_geglu(const uint16_t* xb, const uint16_t* wb, uint16_t* hb,
+                                   int64_t M, int64_t F, int64_t K, hipStream_t s) {
+  if (M == 0 || F == 0) return hipSuccess;
+  if (!gemm_bf16w_ok(M, 2 * F, K) || F % 32 != 0) return hipErrorInvalidValue;
+  return run_dense<true>(xb, wb, nullptr, hb, M, 2 * F, K, 0, F, s);
 }
 
 }  // namespace glypr

@@ -250,15 +250,17 @@ hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_
 // bit-identical to the CPU path.  One row per wave.
 // ---------------------------------------------------------------------------
 // NEXT: 0 = only h; 1 = also Q8_0 of RMSNorm(h; w_next); 2 = also Q8_0 of h
-// itself (the input of a projection that has no norm in front).  scalar
-// (device, nullable): forward_residual_add's layer_scalar, h = (h + n) * s.
+// itself (the input of a projection that has no norm in front); 3 = bf16 of
+// RMSNorm(h; w_next) (dense-bf16 weights).  scalar (device, nullable):
+// forward_residual_add's layer_scalar, h = (h + n) * s.
 template <int NV, int NEXT>
 __global__ void __launch_bounds__(64 * NORM_WAVES)
 residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_post,
                      float* __restrict__ h, const float* __restrict__ w_next,
                      const float* __restrict__ scalar, float eps, int64_t rows, int dim,
-                     int8_t* __restrict__ xq, float* __restrict__ dx) {
+                     int8_t* __restrict__ xq, float* __restrict__ dx, uint16_t* __restrict__ xb) {
   constexpr bool QNEXT = NEXT != 0;
+  constexpr bool CHAIN2 = NEXT == 1 || NEXT == 3;
   extern __shared__ float lds_rows[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -299,12 +301,12 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
         v[i][e] = scalar ? sum * sv : sum;
       }
       *reinterpret_cast<v4f*>(h + row * dim + 4 * c4) = v[i];
-      if (NEXT == 1) stage_chains(lrow, S, c4, v[i]);
+      if (CHAIN2) stage_chains(lrow, S, c4, v[i]);
     }
   }
   if constexpr (QNEXT) {
     float inv2 = 1.0f;
-    if constexpr (NEXT == 1) {
+    if constexpr (CHAIN2) {
       __builtin_amdgcn_s_waitcnt(0);
       __builtin_amdgcn_wave_barrier();
       inv2 = chain_row_inv(lrow, dim, lane, eps);
@@ -320,6 +322,14 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
         if (NEXT == 2) yv[e] = v[i][e];
         else yv[e] = w_next ? (v[i][e] * inv2) * wn[i][e] : v[i][e] * inv2;
         a = fmaxf(a, fabsf(yv[e]));
+      }
+      if constexpr (NEXT == 3) {
+        if (ok) {
+          uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
+          dst[0] = bf16_rne(yv[0]) | (bf16_rne(yv[1]) << 16);
+          dst[1] = bf16_rne(yv[2]) | (bf16_rne(yv[3]) << 16);
+        }
+        continue;
       }
       a = max8(a);
       QScale sc = q8_scale(a);
@@ -337,22 +347,23 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
 
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
-                                hipStream_t s, const float* scalar, bool plain_q) {
+                                hipStream_t s, const float* scalar, bool plain_q, uint16_t* xb) {
   if (rows == 0) return hipSuccess;
   if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
   const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
   const size_t lds = (size_t)NORM_WAVES * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
-  const int mode = xq == nullptr ? 0 : (plain_q ? 2 : 1);
+  const int mode = xb != nullptr ? 3 : xq == nullptr ? 0 : (plain_q ? 2 : 1);
 #define RES_LAUNCH(N, MODE)                                                                    \
   residual_norm_kernel<N, MODE><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w_post, h, w_next,       \
                                                                    scalar, eps, rows,          \
-                                                                   (int)dim, xq, dx)
+                                                                   (int)dim, xq, dx, xb)
 #define RES_CASE(N)                                                                            \
   case N:                                                                                      \
     if (mode == 0) RES_LAUNCH(N, 0);                                                           \
     else if (mode == 1) RES_LAUNCH(N, 1);                                                      \
-    else RES_LAUNCH(N, 2);                                                                     \
+    else if (mode == 2) RES_LAUNCH(N, 2);                                                      \
+    else RES_LAUNCH(N, 3);                                                                     \
     break;
   switch (nv) {
     RES_CASE(1)

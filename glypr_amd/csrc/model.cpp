@@ -64,7 +64,8 @@ struct DevBuf {
 };
 
 struct LinearOp {
-  glypr_q8w* w = nullptr;
+  glypr_q8w* w = nullptr;     // Q8_0 weight
+  glypr_bf16w* wb = nullptr;  // or a dense bf16 weight (F16/BF16 GGUF tensors)
 };
 
 struct RMSNorm {
@@ -115,12 +116,13 @@ struct glypr_model {
   RMSNorm ple_norm;
   LinearOp embedding_projection;  // output.weight
   bool finalized = false;
+  bool dense = false;  // projections are dense bf16 weights (activations run in bf16)
   // RoPE tables [rope_cap][head_dim] for the sliding and full layer types.
   DevBuf cos_s, sin_s, cos_f, sin_f;
   int64_t rope_cap = 0;
   // activations
   DevBuf h, xq, dx, qkv, attn_q, attn_k, attn_vt, attn_scratch, cq, dc, proj, hq,
-      dh, normed, pooled, ids, ple, ple_gate, tokens;
+      dh, normed, pooled, ids, ple, ple_gate, tokens, xb, hb;
   int64_t cap_t = 0;
 };
 
@@ -204,6 +206,10 @@ int ensure_activations(glypr_model* m, int64_t t) {
     RET_IF(m->ple_gate.ensure((size_t)(t * c.ple_dim) * 4));
   }
   if (c.out_dim > 0) RET_IF(m->tokens.ensure((size_t)(t * c.out_dim) * 4));
+  if (m->dense) {
+    RET_IF(m->xb.ensure((size_t)(t * wide) * 2));
+    RET_IF(m->hb.ensure((size_t)(t * c.ffn) * 2));
+  }
   RET_IF(m->ids.ensure((size_t)t * 4));
   m->cap_t = t;
   return GLYPR_OK;
@@ -212,7 +218,9 @@ int ensure_activations(glypr_model* m, int64_t t) {
 void free_model(glypr_model* m) {
   auto drop = [](LinearOp& l) {
     if (l.w) glypr_hip_q8_0_weight_destroy(l.w);
+    if (l.wb) glypr_hip_bf16_weight_destroy(l.wb);
     l.w = nullptr;
+    l.wb = nullptr;
   };
   auto dropn = [](RMSNorm& n) {
     if (n.weight) (void)hipFree(n.weight);
@@ -248,8 +256,39 @@ void free_model(glypr_model* m) {
   for (DevBuf* b : {&m->cos_s, &m->sin_s, &m->cos_f, &m->sin_f, &m->h, &m->xq, &m->dx, &m->qkv,
                     &m->attn_q, &m->attn_k, &m->attn_vt, &m->attn_scratch,
                     &m->cq, &m->dc, &m->proj, &m->hq, &m->dh, &m->normed, &m->pooled, &m->ids,
-                    &m->ple, &m->ple_gate, &m->tokens})
+                    &m->ple, &m->ple_gate, &m->tokens, &m->xb, &m->hb})
     b->release();
+}
+
+// LinearOp::try_concat (linear.rs:82-148) for dense bf16 weights: one
+// [sum of rows][k] buffer.
+int concat_bf16(glypr_hip_ctx* ctx, const glypr_bf16w* const* parts, int count,
+                glypr_bf16w** out) {
+  int64_t n = 0;
+  const int64_t k = parts[0]->k;
+  for (int i = 0; i < count; i++) {
+    GLYPR_CHECK(parts[i]->k == k, GLYPR_ERR_SHAPE, "concat of differing in_dim");
+    n += parts[i]->n;
+  }
+  glypr_bf16w* w = new (std::nothrow) glypr_bf16w();
+  GLYPR_CHECK(w != nullptr, GLYPR_ERR_OOM, "host allocation failed");
+  w->n = n;
+  w->k = k;
+  w->device = ctx->device;
+  hipError_t e = hipMalloc((void**)&w->p, (size_t)(n * k) * 2);
+  int64_t off = 0;
+  for (int i = 0; i < count && e == hipSuccess; i++) {
+    e = hipMemcpy(w->p + off * k, parts[i]->p, (size_t)(parts[i]->n * k) * 2,
+                  hipMemcpyDeviceToDevice);
+    off += parts[i]->n;
+  }
+  if (e != hipSuccess) {
+    if (w->p) (void)hipFree(w->p);
+    delete w;
+    return hip_error(e, "bf16 weight concat");
+  }
+  *out = w;
+  return GLYPR_OK;
 }
 
 // The attention core shared by glypr_hip_attention and the model forward:
@@ -259,14 +298,72 @@ int attention_core(glypr_hip_ctx* ctx, const float* qkv, const float* qnw, const
                    float eps, const float* cos_t, const float* sin_t, int64_t t, int64_t nq,
                    int64_t nkv, int64_t hd, int64_t window, uint16_t* q16, uint16_t* k16,
                    uint16_t* vt16, float* scratch, float* out, int8_t* cq, float* dc,
-                   hipStream_t s) {
+                   hipStream_t s, uint16_t* cb = nullptr) {
   const int64_t tp = attn_padded_len(t);
   LAUNCH(GLYPR_K_QKV_POST, s,
          launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q16, k16, vt16, s),
          "qkv_post launch");
   LAUNCH(GLYPR_K_ATTENTION, s,
-         launch_attention(q16, k16, vt16, scratch, out, cq, dc, t, tp, nq, nkv, hd, window, s),
+         launch_attention(q16, k16, vt16, scratch, out, cq, dc, t, tp, nq, nkv, hd, window, s, cb),
          "attention launch");
+  return GLYPR_OK;
+}
+
+// The layers, final norm and pooling with dense bf16 projections (the
+// bf16-weight variant of configs 4-5): each GEMM takes bf16 activations
+// (nearest even) from the norm kernels and the attention combine, the
+// residual stream h stays f32, GeGLU leaves the gate/up GEMM as bf16.
+int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, int64_t t, int64_t trunc, float* out,
+                  float* hidden, hipStream_t s) {
+  const glypr_model_config& c = m->cfg;
+  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
+  const int64_t qd = nq * hd;
+  float* h = dev_f32(m->h);
+  uint16_t* xb = m->xb.as<uint16_t>();
+  uint16_t* hb = m->hb.as<uint16_t>();
+  LAUNCH(GLYPR_K_RMSNORM_BF16, s,
+         launch_rmsnorm_bf16(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xb, s),
+         "rmsnorm_bf16 launch");
+  for (size_t li = 0; li < m->layers.size(); li++) {
+    EncoderLayer& L = m->layers[li];
+    const bool last = li + 1 == m->layers.size();
+    const glypr_bf16w* wqkv = L.self_attn.fused_qkv.wb;
+    LAUNCH(GLYPR_K_GEMM_BF16W, s,
+           launch_gemm_bf16w(xb, wqkv->p, dev_f32(m->qkv), t, wqkv->n, H, wqkv->n, s),
+           "qkv gemm launch");
+    const float* cos_t = dev_f32(L.full_attention ? m->cos_f : m->cos_s);
+    const float* sin_t = dev_f32(L.full_attention ? m->sin_f : m->sin_s);
+    RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
+                          L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
+                          L.full_attention ? 0 : c.sliding_window, m->attn_q.as<uint16_t>(),
+                          m->attn_k.as<uint16_t>(), m->attn_vt.as<uint16_t>(),
+                          dev_f32(m->attn_scratch), nullptr, nullptr, nullptr, s, xb));
+    const glypr_bf16w* wo = L.self_attn.o.wb;
+    LAUNCH(GLYPR_K_GEMM_BF16W, s,
+           launch_gemm_bf16w(xb, wo->p, dev_f32(m->proj), t, H, qd, H, s), "o gemm launch");
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.post_attention_layernorm.weight, h,
+                                L.pre_feedforward_layernorm.weight, c.eps, t, H, nullptr,
+                                nullptr, s, nullptr, false, xb),
+           "residual_norm launch");
+    const glypr_bf16w* wgu = L.mlp.fused_gate_up.wb;
+    LAUNCH(GLYPR_K_GEMM_BF16W, s, launch_gemm_bf16w_geglu(xb, wgu->p, hb, t, F, H, s),
+           "gate/up GeGLU launch");
+    const glypr_bf16w* wd = L.mlp.down.wb;
+    LAUNCH(GLYPR_K_GEMM_BF16W, s,
+           launch_gemm_bf16w(hb, wd->p, dev_f32(m->proj), t, H, F, H, s), "down gemm launch");
+    const float* w_next = last ? nullptr : m->layers[li + 1].input_layernorm.weight;
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h, w_next,
+                                c.eps, t, H, nullptr, nullptr, s, nullptr, false,
+                                last ? nullptr : xb),
+           "residual_norm launch");
+  }
+  float* tokens = hidden ? hidden : dev_f32(m->normed);
+  LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, tokens, t, H, s),
+         "final rmsnorm launch");
+  LAUNCH(GLYPR_K_POOL, s, launch_pool(tokens, nullptr, t, H, trunc, out, dev_f32(m->pooled), s),
+         "pool launch");
   return GLYPR_OK;
 }
 
@@ -344,8 +441,8 @@ int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* dat
   clear_error();
   GLYPR_CHECK(m != nullptr && name != nullptr && data != nullptr, GLYPR_ERR_INVALID_ARG,
               "model, name or data is NULL");
-  GLYPR_CHECK(dtype == 0 || dtype == 1, GLYPR_ERR_UNSUPPORTED, "dtype %d (0 = f32, 1 = Q8_0)",
-              dtype);
+  GLYPR_CHECK(dtype >= 0 && dtype <= 2, GLYPR_ERR_UNSUPPORTED,
+              "dtype %d (0 = f32, 1 = Q8_0, 2 = bf16)", dtype);
   GLYPR_CHECK(!m->finalized, GLYPR_ERR_INVALID_ARG, "model already finalized");
   const glypr_model_config& c = m->cfg;
   DeviceScope ds(m->ctx->device);
@@ -361,6 +458,18 @@ int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* dat
     if (op.w) glypr_hip_q8_0_weight_destroy(op.w);
     op.w = nullptr;
     return glypr_hip_q8_0_weight_create(m->ctx, (const uint8_t*)data, rows, cols, &op.w);
+  };
+  // a layer projection: Q8_0 blocks (dtype 1) or dense bf16 rows (dtype 2)
+  auto set_lin = [&](LinearOp& op, int64_t er, int64_t ec) -> int {
+    if (dtype != 2) return set_q8(op, er, ec);
+    GLYPR_CHECK(rows == er && cols == ec, GLYPR_ERR_SHAPE,
+                "%s has shape (%lld, %lld), expected (%lld, %lld)", name, (long long)rows,
+                (long long)cols, (long long)er, (long long)ec);
+    if (op.w) glypr_hip_q8_0_weight_destroy(op.w);
+    if (op.wb) glypr_hip_bf16_weight_destroy(op.wb);
+    op.w = nullptr;
+    op.wb = nullptr;
+    return glypr_hip_bf16_weight_create(m->ctx, (const uint16_t*)data, rows, cols, &op.wb);
   };
   auto set_norm_raw = [&](float*& dst, int64_t len) -> int {
     GLYPR_CHECK(dtype == 0, GLYPR_ERR_UNSUPPORTED, "%s must be f32", name);
@@ -391,13 +500,13 @@ int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* dat
     if (f == "post_ffw_norm") return set_norm(L.post_feedforward_layernorm, c.hidden);
     if (f == "attn_q_norm") return set_norm(L.self_attn.q_norm, c.head_dim);
     if (f == "attn_k_norm") return set_norm(L.self_attn.k_norm, c.head_dim);
-    if (f == "attn_q") return set_q8(L.self_attn.q, qd, c.hidden);
-    if (f == "attn_k") return set_q8(L.self_attn.k, kvd, c.hidden);
-    if (f == "attn_v") return set_q8(L.self_attn.v, kvd, c.hidden);
-    if (f == "attn_output") return set_q8(L.self_attn.o, c.hidden, qd);
-    if (f == "ffn_gate") return set_q8(L.mlp.gate, c.ffn, c.hidden);
-    if (f == "ffn_up") return set_q8(L.mlp.up, c.ffn, c.hidden);
-    if (f == "ffn_down") return set_q8(L.mlp.down, c.hidden, c.ffn);
+    if (f == "attn_q") return set_lin(L.self_attn.q, qd, c.hidden);
+    if (f == "attn_k") return set_lin(L.self_attn.k, kvd, c.hidden);
+    if (f == "attn_v") return set_lin(L.self_attn.v, kvd, c.hidden);
+    if (f == "attn_output") return set_lin(L.self_attn.o, c.hidden, qd);
+    if (f == "ffn_gate") return set_lin(L.mlp.gate, c.ffn, c.hidden);
+    if (f == "ffn_up") return set_lin(L.mlp.up, c.ffn, c.hidden);
+    if (f == "ffn_down") return set_lin(L.mlp.down, c.hidden, c.ffn);
     if (c.ple_dim > 0) {
       if (f == "inp_gate") return set_q8(L.ple_block.gate, c.ple_dim, c.hidden);
       if (f == "proj") return set_q8(L.ple_block.projection, c.hidden, c.ple_dim);
@@ -418,18 +527,46 @@ int glypr_hip_model_finalize(glypr_model* m) {
               GLYPR_ERR_INVALID_ARG, "per_layer_model_proj / per_layer_proj_norm missing");
   GLYPR_CHECK(m->cfg.out_dim == 0 || m->embedding_projection.w, GLYPR_ERR_INVALID_ARG,
               "output.weight missing");
+  DeviceScope ds(m->ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  // every layer projection is Q8_0, or every one is dense bf16
+  int n_q8 = 0, n_bf = 0;
+  for (auto& L : m->layers)
+    for (const LinearOp* op : {&L.self_attn.q, &L.self_attn.k, &L.self_attn.v, &L.self_attn.o,
+                               &L.mlp.gate, &L.mlp.up, &L.mlp.down}) {
+      n_q8 += op->w != nullptr;
+      n_bf += op->wb != nullptr;
+    }
+  GLYPR_CHECK(n_q8 == 0 || n_bf == 0, GLYPR_ERR_UNSUPPORTED,
+              "layer projections mix Q8_0 and bf16 weights");
+  m->dense = n_bf > 0;
+  if (m->dense) {
+    GLYPR_CHECK(m->cfg.ple_dim == 0 && m->cfg.out_dim == 0, GLYPR_ERR_UNSUPPORTED,
+                "dense bf16 projections are supported without the Per-Layer-Embedding block "
+                "and the embedding projection");
+    GLYPR_CHECK(m->cfg.hidden % 64 == 0 && m->cfg.ffn % 64 == 0, GLYPR_ERR_UNSUPPORTED,
+                "dense bf16 projections need hidden and ffn multiples of 64");
+  }
+  auto has = [](const LinearOp& op) { return op.w != nullptr || op.wb != nullptr; };
   for (size_t i = 0; i < m->layers.size(); i++) {
     EncoderLayer& L = m->layers[i];
-    GLYPR_CHECK(L.self_attn.q.w && L.self_attn.k.w && L.self_attn.v.w && L.self_attn.o.w &&
-                    L.mlp.gate.w && L.mlp.up.w && L.mlp.down.w && L.self_attn.q_norm.weight &&
-                    L.self_attn.k_norm.weight && L.input_layernorm.weight &&
-                    L.post_attention_layernorm.weight && L.pre_feedforward_layernorm.weight &&
-                    L.post_feedforward_layernorm.weight,
+    GLYPR_CHECK(has(L.self_attn.q) && has(L.self_attn.k) && has(L.self_attn.v) &&
+                    has(L.self_attn.o) && has(L.mlp.gate) && has(L.mlp.up) && has(L.mlp.down) &&
+                    L.self_attn.q_norm.weight && L.self_attn.k_norm.weight &&
+                    L.input_layernorm.weight && L.post_attention_layernorm.weight &&
+                    L.pre_feedforward_layernorm.weight && L.post_feedforward_layernorm.weight,
                 GLYPR_ERR_INVALID_ARG, "layer %zu is missing tensors", i);
     GLYPR_CHECK(m->cfg.ple_dim == 0 ||
                     (L.ple_block.gate.w && L.ple_block.projection.w && L.ple_block.norm.weight &&
                      L.ple_block.layer_scalar),
                 GLYPR_ERR_INVALID_ARG, "layer %zu is missing its Per-Layer-Embedding tensors", i);
+    if (m->dense) {
+      const glypr_bf16w* qkv[3] = {L.self_attn.q.wb, L.self_attn.k.wb, L.self_attn.v.wb};
+      RET_IF(concat_bf16(m->ctx, qkv, 3, &L.self_attn.fused_qkv.wb));
+      const glypr_bf16w* gu[2] = {L.mlp.gate.wb, L.mlp.up.wb};
+      RET_IF(concat_bf16(m->ctx, gu, 2, &L.mlp.fused_gate_up.wb));
+      continue;
+    }
     const glypr_q8w* qkv[3] = {L.self_attn.q.w, L.self_attn.k.w, L.self_attn.v.w};
     RET_IF(glypr_hip_q8_0_weight_concat(m->ctx, qkv, 3, &L.self_attn.fused_qkv.w, nullptr));
     const glypr_q8w* gu[2] = {L.mlp.gate.w, L.mlp.up.w};
@@ -491,6 +628,7 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
     LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(ple, m->ple_norm.weight, c.eps, ple, t * NL, P, s),
            "per-layer norm launch");
   }
+  if (m->dense) return forward_dense(m, ctx, t, trunc, out, hidden, s);
   // layer 0 input_layernorm as the qkv GEMM's prologue
   LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
          launch_rmsnorm_quant(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xq, dx, s),

@@ -15,7 +15,8 @@ import torch
 
 from ._lib import BF16_DEQUANT, GLYPR_ERR_UNSUPPORTED, INT8_EXACT, GlyprError, check, lib
 
-__all__ = ["Context", "Q8Weight", "INT8_EXACT", "BF16_DEQUANT", "q8_0_matmul",
+__all__ = ["Context", "Q8Weight", "BF16Weight", "INT8_EXACT", "BF16_DEQUANT", "q8_0_matmul",
+           "bf16_matmul", "f32_to_bf16_bits",
            "rmsnorm_q8_0_matmul", "rmsnorm", "geglu", "mlp", "rmsnorm_mlp", "dequantize",
            "quantize", "embed_gather", "pool_normalize"]
 
@@ -112,6 +113,54 @@ class Q8Weight:
             self.close()
         except Exception:
             pass
+
+
+class BF16Weight:
+    """Opaque dense bf16 weight handle (LinearOp over an F16/BF16 tensor)."""
+
+    def __init__(self, handle, n: int, k: int):
+        self.handle = handle
+        self.n = n
+        self.k = k
+
+    @classmethod
+    def from_bf16(cls, ctx: Context, rows: np.ndarray) -> "BF16Weight":
+        """rows: uint16 [n, k] holding bf16 bit patterns."""
+        b = np.ascontiguousarray(rows, dtype=np.uint16)
+        if b.ndim != 2:
+            raise ValueError("rows must be [n, k]")
+        h = ctypes.c_void_p()
+        check(lib().glypr_hip_bf16_weight_create(ctx.handle, b.ctypes.data_as(ctypes.c_void_p),
+                                                 b.shape[0], b.shape[1], ctypes.byref(h)))
+        return cls(h, b.shape[0], b.shape[1])
+
+    def close(self):
+        if self.handle:
+            lib().glypr_hip_bf16_weight_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round f32 to bf16 (nearest even) and return the uint16 bit patterns."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def bf16_matmul(ctx: Context, w: BF16Weight, x: torch.Tensor,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    ctx._check_tensor(x, "x")
+    m = x.numel() // w.k
+    y = _out(x, (*x.shape[:-1], w.n), out)
+    check(lib().glypr_hip_bf16_matmul(ctx.handle, w.handle, _ptr(x), _ptr(y), m, ctx.stream))
+    return y
 
 
 def _out(x: torch.Tensor, shape, out: Optional[torch.Tensor]):
@@ -435,10 +484,15 @@ class Model:
         self.handle = h
 
     def set_tensor(self, name: str, data: np.ndarray, rows: int, cols: int, q8_0: bool):
+        """q8_0: data holds GGUF Q8_0 blocks; otherwise f32 values, or, for a
+        layer projection given as a uint16 array, dense bf16 bit patterns."""
         a = np.ascontiguousarray(data)
+        dtype = 1 if q8_0 else (2 if a.dtype == np.uint16 else 0)
+        if dtype == 0:
+            a = np.ascontiguousarray(a, dtype=np.float32)
         check(lib().glypr_hip_model_set_tensor(self.handle, name.encode(),
                                                a.ctypes.data_as(ctypes.c_void_p), rows, cols,
-                                               1 if q8_0 else 0))
+                                               dtype))
 
     def finalize(self):
         check(lib().glypr_hip_model_finalize(self.handle))

@@ -60,6 +60,7 @@ typedef enum glypr_q8_variant {
 
 typedef struct glypr_hip_ctx glypr_hip_ctx; /* per-device context + workspace */
 typedef struct glypr_q8w glypr_q8w;         /* Q8_0 weight on one device */
+typedef struct glypr_bf16w glypr_bf16w;     /* dense bf16 weight on one device */
 typedef void* glypr_stream;                 /* hipStream_t */
 
 /* ---- library / context ------------------------------------------------- */
@@ -109,6 +110,22 @@ int glypr_hip_q8_0_weight_shape(const glypr_q8w* w, int64_t* n, int64_t* k);
  * out[r][j] = f32(d) * q, bit-exact. */
 int glypr_hip_q8_0_dequantize(glypr_hip_ctx* ctx, const glypr_q8w* w, float* out,
                               glypr_stream stream);
+
+/* ---- dense bf16 weights (LinearOp over an F16/BF16 tensor) ------------ */
+
+/* LinearOp::from_gguf_tensor, dense arm (linear.rs:48-54: F32/F16/BF16
+ * tensors become a plain Linear; on Metal the model dtype is BF16,
+ * lib.rs:222-229).  `bf16_rows` is host memory, n rows of k bf16 values (the
+ * GGUF (out_dim, in_dim) layout).  k % 64 != 0 -> GLYPR_ERR_UNSUPPORTED. */
+int glypr_hip_bf16_weight_create(glypr_hip_ctx* ctx, const uint16_t* bf16_rows, int64_t n,
+                                 int64_t k, glypr_bf16w** out);
+int glypr_hip_bf16_weight_destroy(glypr_bf16w* w);
+
+/* LinearOp::forward (linear.rs:150-172) for a dense bf16 weight: x f32 [m,k]
+ * rounded to bf16 (nearest even), y f32 [m,n] = x . w^T on bf16 MFMA with f32
+ * accumulation. */
+int glypr_hip_bf16_matmul(glypr_hip_ctx* ctx, const glypr_bf16w* w, const float* x, float* y,
+                          int64_t m, glypr_stream stream);
 
 /* ---- Q8_0 activations --------------------------------------------------- */
 
@@ -258,7 +275,10 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
  * "output_norm.weight", "blk.{i}.{attn_norm, post_attention_norm, ffn_norm,
  * post_ffw_norm, attn_q_norm, attn_k_norm}.weight" (f32, dtype 0) and
  * "blk.{i}.{attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up,
- * ffn_down}.weight" (Q8_0 GGUF blocks, dtype 1).  With ple_dim > 0 also
+ * ffn_down}.weight" (Q8_0 GGUF blocks, dtype 1, or dense bf16 rows, dtype 2 (the
+ * F16/BF16 arm of linear.rs:48-54); all seven projections of every layer share
+ * one kind, and dense ones need hidden, ffn % 64 == 0, ple_dim == 0 and
+ * out_dim == 0).  With ple_dim > 0 also
  * "per_layer_model_proj.weight" (Q8_0, n_layers*ple_dim x hidden),
  * "per_layer_proj_norm.weight" (f32 [ple_dim]) and per layer "inp_gate"
  * (Q8_0, ple_dim x hidden), "proj" (Q8_0, hidden x ple_dim), "post_norm"
@@ -277,7 +297,8 @@ int glypr_hip_model_finalize(glypr_model* model);
  * width when trunc is 0 or wider] on the device.  hidden (nullable, device
  * [t][width]) receives the unpooled token embeddings: the projection's output,
  * or the final-normed states without one.  The embedding width is out_dim
- * when set, else hidden.  Every projection runs as INT8_EXACT. */
+ * when set, else hidden.  Q8_0 projections run as INT8_EXACT; dense bf16 ones
+ * take bf16 activations (nearest even) with f32 accumulation. */
 int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, int64_t trunc,
                           float* out, float* hidden, glypr_stream stream);
 
@@ -344,7 +365,8 @@ typedef enum glypr_kernel_id {
   GLYPR_K_VEC_ENCODE = 16,    /* binary / int8 output-vector quantization */
   GLYPR_K_VEC_SEARCH = 17,    /* all-pairs hamming / cosine over encoded vectors */
   GLYPR_K_GEMM_I8_PRO = 18,   /* INT8_EXACT GEMM with the quantize / RMSNorm prologue fused */
-  GLYPR_K_COUNT = 19
+  GLYPR_K_GEMM_BF16W = 19,    /* GEMM on dense bf16 weights (+ GeGLU epilogue) */
+  GLYPR_K_COUNT = 20
 } glypr_kernel_id;
 
 /* The per-op device timing of forward_profiled (profile.rs:53-56, 63-429),

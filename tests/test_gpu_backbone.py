@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from glypr_amd import ops
+from glypr_amd import _lib, ops
 from glypr_amd.ops import Model
 
 pytestmark = pytest.mark.gpu
@@ -92,9 +92,11 @@ def test_attention_core_vs_oracle(ctx, oracle, t, window, qk_scale):
 QK_NORM_SCALE = np.float32(0.25)
 
 
-def make_model(ctx, oracle, n_layers, vocab, seed=0, ple_dim=0, out_dim=0):
+def make_model(ctx, oracle, n_layers, vocab, seed=0, ple_dim=0, out_dim=0, dense=False):
     """The BASELINE backbone; ple_dim / out_dim > 0 add the real model's
-    Per-Layer-Embedding path (ple.rs) and embedding projection (output.weight)."""
+    Per-Layer-Embedding path (ple.rs) and embedding projection (output.weight).
+    dense: the layer projections are dense bf16 weights, the Q8_0 values rounded
+    to bf16 (the bf16-weight variant of configs 4-5)."""
     H, F, nq, nkv, hd = 768, 1152, 3, 1, 256
     rng_seed = seed * 1000
     tensors = {}
@@ -106,7 +108,12 @@ def make_model(ctx, oracle, n_layers, vocab, seed=0, ple_dim=0, out_dim=0):
                                           ("attn_v", nkv * hd, H), ("attn_output", H, nq * hd),
                                           ("ffn_gate", F, H), ("ffn_up", F, H),
                                           ("ffn_down", H, F)]):
-            tensors[f"blk.{i}.{name}.weight"] = (oracle.q8_0_weight(n, k, seed=b + j), n, k, True)
+            wq = oracle.q8_0_weight(n, k, seed=b + j)
+            if dense:
+                wd = oracle.dequantize_rows(wq, k).reshape(n, k)
+                tensors[f"blk.{i}.{name}.weight"] = (ops.f32_to_bf16_bits(wd), n, k, False)
+            else:
+                tensors[f"blk.{i}.{name}.weight"] = (wq, n, k, True)
         for j, (name, n) in enumerate([("attn_norm", H), ("post_attention_norm", H),
                                        ("ffn_norm", H), ("post_ffw_norm", H),
                                        ("attn_q_norm", hd), ("attn_k_norm", hd)]):
@@ -204,6 +211,48 @@ def test_model_forward_vs_oracle(ctx, oracle, n_layers, t, vocab):
     again = host(m.embed(ids, trunc=256))
     assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
     m.close()
+
+
+@pytest.mark.parametrize("n_layers,t,vocab", [(2, 64, 2000), (6, 600, 2000)])
+def test_dense_bf16_model_vs_float64(ctx, oracle, n_layers, t, vocab):
+    """The bf16-weight backbone (dense bf16 projections, bf16 activations into
+    every GEMM, f32 accumulation) against the float64 statement of the same
+    forward on the same bf16 weights.  Bound: bf16 activation rounding (2^-9
+    relative per GEMM input) and the f16 attention operands."""
+    from test_oracle import _forward_f64
+    say(f"dense bf16 backbone layers={n_layers} t={t}")
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=n_layers + 40, dense=True)
+    ids = oracle.uniform_ids(t, seed=t + 1, vocab=vocab)
+    hidden = torch.empty((t, 768), dtype=torch.float32, device="cuda")
+    got = host(m.embed(ids, trunc=256, hidden=hidden))
+    ref, ref_states = _forward_f64(oracle, {k: v[0] for k, v in tensors.items()}, ids, 256, 768,
+                                   1152, 3, 1, 256, n_layers, 512)
+    cos = float(got @ ref / np.linalg.norm(got) / np.linalg.norm(ref))
+    gh = host(hidden).astype(np.float64)
+    row_cos = (gh * ref_states).sum(1) / np.linalg.norm(gh, axis=1) / \
+        np.linalg.norm(ref_states, axis=1)
+    say(f"  embedding cosine {cos:.8f}, token-state cosine min {row_cos.min():.6f}")
+    assert cos >= 0.9995
+    assert row_cos.min() >= 0.995
+    again = host(m.embed(ids, trunc=256))
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+    m.close()
+
+
+def test_dense_bf16_model_rejects_mixed_and_ple(ctx, oracle):
+    """All seven projections of every layer share one weight kind; dense
+    projections run without the Per-Layer-Embedding block."""
+    m, tensors = make_model(ctx, oracle, 1, 500, seed=3, dense=True)
+    m.close()
+    bad = Model(ctx, n_layers=1, vocab=500)
+    for name, (data, r, c, q8) in tensors.items():
+        if name == "blk.0.ffn_down.weight":
+            data, q8 = oracle.q8_0_weight(r, c, seed=9), True
+        bad.set_tensor(name, data, r, c, q8)
+    with pytest.raises(_lib.GlyprError) as e:
+        bad.finalize()
+    assert e.value.code == _lib.GLYPR_ERR_UNSUPPORTED
+    bad.close()
 
 
 def test_model_with_ple_and_projection_vs_oracle(ctx, oracle):

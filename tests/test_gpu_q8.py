@@ -383,6 +383,32 @@ def test_matmul_bf16_dequant_within_bf16_bound(ctx, oracle, m, k, n):
     assert cos.min() > 0.9999
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 64, 1), (100, 768, 1152), (600, 1152, 257),
+                                   (4100, 768, 1280)])
+def test_dense_bf16_weight_matmul_within_bound(ctx, oracle, m, k, n):
+    """LinearOp::forward over a dense bf16 weight: x rounded to bf16 (relative
+    error <= 2^-9), exact bf16 weights, f32 accumulation:
+    |y - y64| <= 2^-8 * (|x| @ |w|^T) + 1e-6 against float64 x @ w^T."""
+    say(f"dense bf16 matmul m={m} k={k} n={n}")
+    x = oracle.normal(m * k, seed=900 + m).reshape(m, k)
+    wf = 0.02 * oracle.normal(n * k, seed=901 + n).reshape(n, k)
+    bits = ops.f32_to_bf16_bits(wf)
+    w64 = (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    w = ops.BF16Weight.from_bf16(ctx, bits)
+    y = host(ops.bf16_matmul(ctx, w, dev(x)))
+    y64 = x.astype(np.float64) @ w64.T
+    bound = 2.0 ** -8 * (np.abs(x).astype(np.float64) @ np.abs(w64).T) + 1e-6
+    assert np.all(np.abs(y - y64) <= bound)
+    w.close()
+
+
+def test_dense_bf16_weight_shape_errors(ctx, oracle):
+    bits = ops.f32_to_bf16_bits(np.ones((4, 96), np.float32))
+    with pytest.raises(_lib.GlyprError) as e:
+        ops.BF16Weight.from_bf16(ctx, bits)
+    assert e.value.code == _lib.GLYPR_ERR_UNSUPPORTED
+
+
 @pytest.mark.parametrize("m,H,F", [(512, 768, 1152), (2200, 256, 96), (3000, 768, 1152)])
 def test_mlp_bf16_dequant(ctx, oracle, m, H, F):
     """BF16_DEQUANT gate/up + GeGLU + down vs the float64 dequant oracle; the

@@ -346,11 +346,18 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
     (oracle quantizer, pinned above), everything else in float64.  With
     `per_layer_model_proj.weight` present it adds TextPLE (ple.rs:48-85) and each
     layer's TextPLEBlock with the layer scalar (ple.rs:118-145, norm.rs:65-95);
-    with `output.weight` the embedding projection (model.rs:577)."""
+    with `output.weight` the embedding projection (model.rs:577).  A projection
+    given as a uint16 [n, k] array is a dense bf16 weight (linear.rs:48-54): its
+    exact values, and no quantization of its input."""
     def deq(name, n, k):
-        return oracle.dequantize_rows(tensors[name], k).reshape(n, k).astype(np.float64)
+        w = tensors[name]
+        if w.dtype == np.uint16:
+            return (w.astype(np.uint32) << 16).view(np.float32).reshape(n, k).astype(np.float64)
+        return oracle.dequantize_rows(w, k).reshape(n, k).astype(np.float64)
 
     def lin(x, name, n, k):
+        if tensors[name].dtype == np.uint16:
+            return x.astype(np.float64) @ deq(name, n, k).T
         xq = oracle.dequantize_rows(oracle.quantize_rows(x.astype(np.float32)), k)
         return xq.reshape(x.shape[0], k).astype(np.float64) @ deq(name, n, k).T
 
