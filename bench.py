@@ -180,6 +180,29 @@ def run_workload(ctx, m, variant, steps, warmup, seed=0):
     return L, ms, kern
 
 
+def c2_cold(ctx, variant, rounds=5, copies=24):
+    """C2 with every step on its own layer instance (weights, activations and
+    outputs, ~13 MB each): 24 copies exceed the 256 MB Infinity Cache, so each
+    step streams its operands from HBM instead of the MALL-resident warm loop."""
+    import torch
+    layers = [Layer(ctx, 512, seed=100 + i) for i in range(copies)]
+    for L in layers:
+        L.step(ctx, variant)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(rounds):
+        for L in layers:
+            L.step(ctx, variant)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (rounds * copies)
+    ops_ = layers[0].ops_per_step()
+    del layers
+    return {"tops": round(ops_ / (ms / 1e3) / 1e12, 3), "ms_per_step": round(ms, 5),
+            "copies": copies, "note": f"{copies} layer instances rotated, ~{copies * 13} MB"}
+
+
 def c1_linear(ctx, steps):
     """one Q8_0 linear, X f32 [512, 768] -> Y f32 [512, 1152]."""
     import torch
@@ -428,17 +451,50 @@ def cpu_baseline(seconds=10.0):
         u = po.matmul(xn, b["up"], F, threads=cores)
         po.matmul(po.geglu(g, u, threads=cores), b["down"], H, threads=cores)
 
-    step()
-    t0 = time.perf_counter()
-    n = 0
-    while time.perf_counter() - t0 < seconds:
-        step()
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    return {"value": round(2 * m * LAYER_NK / dt / 1e12, 5), "unit": "TOPS", "cores": cores,
-            "kind": "port", "ms_per_step": round(dt * 1e3, 3),
-            "sample": f"C2 layer at T=512, {n} steps over {seconds:.0f}s, candle-default-x86 "
-                      "scalar vec_dot semantics (oracle/glypr_oracle.c, gcc -O3 x86-64-v3)"}
+    def sample(threads, budget):
+        nonlocal cores
+        saved, cores = cores, threads
+        step()                      # warm-up
+        times = []
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget or len(times) < 3:
+            t1 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t1)
+        cores = saved
+        return np.array(times)
+
+    multi = sample(cores, seconds)
+    single = sample(1, seconds / 2)
+    med = float(np.median(multi))
+    return {"value": round(2 * m * LAYER_NK / med / 1e12, 5), "unit": "TOPS", "cores": cores,
+            "kind": "port", "ms_per_step": round(med * 1e3, 3),
+            "ms_per_step_p95": round(float(np.percentile(multi, 95)) * 1e3, 3),
+            "ms_per_step_min": round(float(multi.min()) * 1e3, 3),
+            "one_thread": {"value": round(2 * m * LAYER_NK / float(np.median(single)) / 1e12, 5),
+                           "ms_per_step": round(float(np.median(single)) * 1e3, 3)},
+            "host": host_cpu(),
+            "sample": f"C2 layer at T=512, {len(multi)} steps over {seconds:.0f}s on {cores} "
+                      f"threads and {len(single)} on 1 (median; p95 and min beside it), "
+                      "candle-default-x86 scalar vec_dot semantics (oracle/glypr_oracle.c, "
+                      "gcc -O3 x86-64-v3)"}
+
+
+def host_cpu():
+    """nproc, model name and the SIMD flags of this host (/proc/cpuinfo)."""
+    model, flags = "", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and not model:
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    simd = [x for x in ("avx2", "fma", "avx512f", "avx512_vnni", "avx512_bf16", "amx_int8")
+            if x in flags]
+    return {"nproc": os.cpu_count(), "model": model, "simd": simd}
 
 
 def main():
@@ -449,8 +505,8 @@ def main():
     ap.add_argument("--variant", choices=["int8", "bf16"], default="int8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
-    ap.add_argument("--extras", default="c1,c3,c4,c5,vec",
-                    help="comma list of the extra workloads to run (c1, c3, c4, c5, vec)")
+    ap.add_argument("--extras", default="c1,cold,c3,c4,c5,vec",
+                    help="comma list of the extra workloads to run (c1, cold, c3, c4, c5, vec)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain device copy of MIB MiB (calibrates rocprof "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -494,10 +550,15 @@ def main():
             extra[f"c3_{vname}"] = {
                 "tops": round(t, 2), "ms_per_step": round(msx, 4),
                 "pct_mfma_peak": round(100 * t / pk, 2),
+                "hbm_frac_algorithmic": round(
+                    sum(kernel_bytes(k, 16384, v) for k in kx) / (msx / 1e3) / 1e9
+                    / HBM_PEAK_GBS, 4),
                 "kernels_us": {k: round(vv["us_per_launch"], 2) for k, vv in kx.items()}}
             del Lx
     if "c1" in todo:
         extra["c1_int8"] = c1_linear(ctx, args.steps)
+    if "cold" in todo:
+        extra["c2_cold"] = c2_cold(ctx, variant)
     if "vec" in todo:
         extra["vec_codecs"] = vec_search(ctx, 20)
     if "c4" in todo or "c5" in todo:
