@@ -87,6 +87,27 @@ __device__ __forceinline__ float bcast16(float v) {
   static_assert(I >= 0 && I < 16, "lane index");
   return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x10 | (I << 5)));
 }
+// 4 x 4 transpose inside each quad of lanes: lane 4k + i holds v[j] =
+// M[i][j] on entry and M[j][i] on exit (two butterfly stages over lane bits
+// 0 and 1; each moves the off-diagonal pairs with one quad_perm DPP).  Used to
+// turn an MFMA tile's column-per-lane layout into row-contiguous vectors.
+__device__ __forceinline__ void quad_transpose4(float (&v)[4]) {
+  const int i = __lane_id();
+  // stage over lane bit 0: pairs (0,1) and (2,3)
+  const bool h1 = (i & 1) != 0;
+  const float s0 = h1 ? v[0] : v[1], s2 = h1 ? v[2] : v[3];
+  const float r0 = dpp_mov<0xB1>(s0, s0), r2 = dpp_mov<0xB1>(s2, s2);  // quad_perm [1,0,3,2]
+  const float a0 = h1 ? r0 : v[0], a1 = h1 ? v[1] : r0;
+  const float a2 = h1 ? r2 : v[2], a3 = h1 ? v[3] : r2;
+  // stage over lane bit 1: pairs (0,2) and (1,3)
+  const bool h2 = (i & 2) != 0;
+  const float t0 = h2 ? a0 : a2, t1 = h2 ? a1 : a3;
+  const float q0 = dpp_mov<0x4E>(t0, t0), q1 = dpp_mov<0x4E>(t1, t1);  // quad_perm [2,3,0,1]
+  v[0] = h2 ? q0 : a0;
+  v[1] = h2 ? q1 : a1;
+  v[2] = h2 ? a2 : q0;
+  v[3] = h2 ? a3 : q1;
+}
 // max over each row of 16 lanes; every lane of the row gets it
 __device__ __forceinline__ float max16(float v) {
   v = max8(v);

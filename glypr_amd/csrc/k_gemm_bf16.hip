@@ -422,26 +422,36 @@ inline bool big_ok(int64_t M, int64_t Nrows, int64_t K) {
 // Dense bf16 weights (LinearOp over an F16/BF16 GGUF tensor, linear.rs:48-54,
 // at bf16): C = A . B^T with A bf16 [M][K] and B bf16 [N][K], f32 accumulate.
 // 128 x 128 tiles on a 2 x 2 grid of waves (64 x 64 outputs each, 2 x 2
-// v_mfma_f32_32x32x16_bf16 tiles); each 64-K stage of A and B arrives by LDS
-// DMA into a two-slot ring, both [128 rows][128 B] with chunk c of row r at
-// c ^ ((r >> 1) & 7); 64 KB of LDS, two workgroups per CU.  Per 32-K block a
-// lane takes 16 consecutive K of its A row and B column (two b128 each) as two
-// MFMA k-steps, the same order on both sides.  GEGLU: 32-row tiles alternate
-// gate and up of the same 32 h columns; h = geglu(gate, up) leaves as bf16.
+// v_mfma_f32_32x32x16_bf16 tiles).  K streams through an LDS ring of RING
+// slots, BKE K per stage (one or two 32-K blocks), A and B each [128 rows]
+// [2 BKE bytes] by LDS DMA, 16-byte chunk c of row r at c ^ swz(r); the waits
+// count exactly the units issued after each stage, so RING - 1 stages are in
+// flight.  Per 32-K block a lane takes 16 consecutive K of its A row and B
+// column (two b128 each) as two MFMA k-steps, the same order on both sides.
+// GEGLU: 32-row tiles alternate gate and up of the same 32 h columns; h =
+// geglu(gate, up) leaves as bf16.
 // ---------------------------------------------------------------------------
-constexpr int BFW_BM = 128, BFW_BN = 128, BFW_BK = 64;
+constexpr int BFW_BM = 128, BFW_BN = 128;
 
-template <bool GEGLU>
+template <bool GEGLU, int BKE, int RING, bool VEC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_bf16w_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
                   float* __restrict__ C, uint16_t* __restrict__ Hb, int M, int N, int K,
                   int ldc, int F, int tiles_n) {
   constexpr int NW = 4, TM = 2, TN = 2;
-  constexpr int UA = BFW_BM / 8, UB = BFW_BN / 8;   // 1 KB units: 8 rows of 128 B
+  constexpr int ROWB = 2 * BKE;                 // bytes per LDS row per stage
+  constexpr int CPR = ROWB / 16;                // 16-byte chunks per row (4 or 8)
+  constexpr int RPU = 1024 / ROWB;              // rows per 1 KB DMA unit
+  constexpr int UA = BFW_BM / RPU, UB = BFW_BN / RPU;
   constexpr int UPW = (UA + UB) / NW;
   constexpr int SLOT = (UA + UB) * 1024;
-  static_assert(UA % NW == 0 && UB % NW == 0, "every unit index j must be of one kind");
-  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * SLOT];
+  constexpr int NBLK = BKE / 32;                // 32-K blocks per stage
+  static_assert(BKE == 32 || BKE == 64, "stage of one or two 32-K blocks");
+  static_assert(UA % NW == 0 && UB % NW == 0 && RING >= 2, "unit kinds per j; ring");
+  // 8 chunks per row: swizzle by (r >> 1) & 7; 4 chunks: by (r >> 2) & 3.
+  // Either keeps any 16 consecutive rows' b128 reads on distinct banks.
+  auto swz = [](int r) -> int { return CPR == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -452,7 +462,7 @@ gemm_bf16w_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
   const int tmi = W / tiles_n;
   const int m0 = tmi * BFW_BM, n0 = (W - tmi * tiles_n) * BFW_BN;
   const int hc0 = n0 >> 1;
-  const int nst = K / BFW_BK;
+  const int nst = K / BKE;
 
   auto b_row = [&](int nl) -> int {
     if (!GEGLU) return n0 + nl < N ? n0 + nl : N - 1;
@@ -468,35 +478,36 @@ gemm_bf16w_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
 #pragma unroll
   for (int j = 0; j < UPW; j++) {
     const int u = j * NW + wave;
-    const int row = (u < UA ? u : u - UA) * 8 + (lane >> 3), c = lane & 7;
+    const int row = (u < UA ? u : u - UA) * RPU + lane / CPR, c = lane % CPR;
     const int grow = u < UA ? a_row(row) : b_row(row);
     ubase[j] = reinterpret_cast<const int8_t*>(u < UA ? A : B);
-    uvoff[j] = grow * (2 * K) + ((c ^ ((row >> 1) & 7)) << 4);
+    uvoff[j] = grow * (2 * K) + ((c ^ swz(row)) << 4);
   }
   auto issue = [&](int st, int slot) {
 #pragma unroll
     for (int j = 0; j < UPW; j++)
-      dma16(ubase[j] + st * (2 * BFW_BK), uvoff[j],
-            lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
+      dma16(ubase[j] + st * ROWB, uvoff[j], lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
   };
-  issue(0, 0);
+#pragma unroll
+  for (int st = 0; st < RING - 1; st++)
+    if (st < nst) issue(st, st);
 
   const int lrow = lane & 31, lhalf = lane >> 5;
-  int offA[TM][2][2], offB[TN][2][2];
+  int offA[TM][NBLK][2], offB[TN][NBLK][2];
 #pragma unroll
-  for (int p = 0; p < 2; p++)
+  for (int p = 0; p < NBLK; p++)
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const int q = 4 * p + 2 * lhalf + h;
 #pragma unroll
       for (int tm = 0; tm < TM; tm++) {
         const int row = 64 * wm + 32 * tm + lrow;
-        offA[tm][p][h] = row * 128 + ((q ^ ((row >> 1) & 7)) << 4);
+        offA[tm][p][h] = row * ROWB + ((q ^ swz(row)) << 4);
       }
 #pragma unroll
       for (int tn = 0; tn < TN; tn++) {
         const int row = 64 * wn + 32 * tn + lrow;
-        offB[tn][p][h] = UA * 1024 + row * 128 + ((q ^ ((row >> 1) & 7)) << 4);
+        offB[tn][p][h] = UA * 1024 + row * ROWB + ((q ^ swz(row)) << 4);
       }
     }
   v16f acc[TM][TN];
@@ -508,58 +519,96 @@ gemm_bf16w_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
       for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
 
 #pragma unroll 1
-  for (int st = 0; st < nst; st++) {
-    const int r = st & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (st + 1 < nst) issue(st + 1, r ^ 1);
-    const uint8_t* slot = ring + r * SLOT;
+  for (int g = 0; g < nst; g += RING) {
 #pragma unroll
-    for (int p = 0; p < 2; p++) {
-      v8bf a[TM][2], b[TN][2];
+    for (int r = 0; r < RING; r++) {
+      const int st = g + r;
+      if (st < nst) {
+        const int later = (st + RING - 2 < nst - 1 ? st + RING - 2 : nst - 1) - st;
+        vm_wait_units<UPW, RING - 2>(later);
+        __syncthreads();
+        if (st + RING - 1 < nst) issue(st + RING - 1, (r + RING - 1) % RING);
+        const uint8_t* slot = ring + r * SLOT;
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
+        for (int p = 0; p < NBLK; p++) {
+          v8bf a[TM][2], b[TN][2];
 #pragma unroll
-        for (int tm = 0; tm < TM; tm++)
-          a[tm][h] = *reinterpret_cast<const v8bf*>(slot + offA[tm][p][h]);
+          for (int h = 0; h < 2; h++) {
 #pragma unroll
-        for (int tn = 0; tn < TN; tn++)
-          b[tn][h] = *reinterpret_cast<const v8bf*>(slot + offB[tn][p][h]);
+            for (int tm = 0; tm < TM; tm++)
+              a[tm][h] = *reinterpret_cast<const v8bf*>(slot + offA[tm][p][h]);
+#pragma unroll
+            for (int tn = 0; tn < TN; tn++)
+              b[tn][h] = *reinterpret_cast<const v8bf*>(slot + offB[tn][p][h]);
+          }
+#pragma unroll
+          for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+              for (int tn = 0; tn < TN; tn++)
+                acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][h], b[tn][h],
+                                                                      acc[tm][tn], 0, 0, 0);
+        }
       }
-#pragma unroll
-      for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-          for (int tn = 0; tn < TN; tn++)
-            acc[tm][tn] =
-                __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][h], b[tn][h], acc[tm][tn], 0, 0, 0);
     }
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // output rows of register r: 8 (r >> 2) + 4 lhalf + (r & 3) of the 32-row tile
+  // Output rows of register r: 8 (r >> 2) + 4 lhalf + (r & 3) of the 32-row
+  // tile, column lrow.  VEC (the host checked that N, ldc or F are multiples
+  // of 4 and the output 16- or 8-byte aligned): a quad transpose of registers
+  // 4g .. 4g + 3 gives lane 4k + i row 8g + 4 lhalf + i, columns 4k .. 4k + 3,
+  // one 16-byte (8-byte for bf16 h) store instead of four scalar ones.
+  const int qi = lane & 3, qc = lrow & ~3;
   if constexpr (!GEGLU) {
 #pragma unroll
     for (int tm = 0; tm < TM; tm++)
 #pragma unroll
       for (int tn = 0; tn < TN; tn++) {
-        const int gn = n0 + 64 * wn + 32 * tn + lrow;
+        const int gn = n0 + 64 * wn + 32 * tn + (VEC ? qc : lrow);
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int gm = m0 + 64 * wm + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-          if (gm < M && gn < N) C[(int64_t)gm * ldc + gn] = acc[tm][tn][r];
+        for (int g = 0; g < 4; g++) {
+          float v[4] = {acc[tm][tn][4 * g], acc[tm][tn][4 * g + 1], acc[tm][tn][4 * g + 2],
+                        acc[tm][tn][4 * g + 3]};
+          const int gr = m0 + 64 * wm + 32 * tm + 8 * g + 4 * lhalf;
+          if constexpr (VEC) {
+            quad_transpose4(v);
+            if (gr + qi < M && gn < N)
+              *reinterpret_cast<float4*>(C + (int64_t)(gr + qi) * ldc + gn) =
+                  make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+              if (gr + j < M && gn < N) C[(int64_t)(gr + j) * ldc + gn] = v[j];
+          }
         }
       }
   } else {
     // tiles 0 and 1 of the wave are gate and up of h columns hc0 + 32 wn ..
-    const int hc = hc0 + 32 * wn + lrow;
+    const int hc = hc0 + 32 * wn + (VEC ? qc : lrow);
 #pragma unroll
     for (int tm = 0; tm < TM; tm++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int gm = m0 + 64 * wm + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-        const float h = geglu_bf16(acc[tm][0][r], acc[tm][1][r]);
-        if (gm < M && hc < F) Hb[(int64_t)gm * F + hc] = __builtin_bit_cast(uint16_t, (__bf16)h);
+      for (int g = 0; g < 4; g++) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = geglu_bf16(acc[tm][0][4 * g + j], acc[tm][1][4 * g + j]);
+        const int gr = m0 + 64 * wm + 32 * tm + 8 * g + 4 * lhalf;
+        if constexpr (VEC) {
+          quad_transpose4(v);
+          const uint32_t lo = __builtin_bit_cast(uint16_t, (__bf16)v[0]) |
+                              (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[1]) << 16;
+          const uint32_t hi = __builtin_bit_cast(uint16_t, (__bf16)v[2]) |
+                              (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[3]) << 16;
+          if (gr + qi < M && hc < F)
+            *reinterpret_cast<uint2*>(Hb + (int64_t)(gr + qi) * F + hc) = make_uint2(lo, hi);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            if (gr + j < M && hc < F)
+              Hb[(int64_t)(gr + j) * F + hc] = __builtin_bit_cast(uint16_t, (__bf16)v[j]);
+        }
       }
   }
 }
@@ -569,8 +618,15 @@ hipError_t run_dense(const uint16_t* xb, const uint16_t* wb, float* y, uint16_t*
                      int64_t Nrows, int64_t K, int64_t ldc, int64_t F, hipStream_t s) {
   const int64_t tiles_n = (Nrows + BFW_BN - 1) / BFW_BN;
   const int64_t tiles = ((M + BFW_BM - 1) / BFW_BM) * tiles_n;
-  gemm_bf16w_kernel<GEGLU><<<dim3((unsigned)tiles), 256, 0, s>>>(
-      xb, wb, y, hb, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
+  const bool vec = GEGLU ? F % 4 == 0 && (reinterpret_cast<uintptr_t>(hb) & 7) == 0
+                         : Nrows % 4 == 0 && ldc % 4 == 0 &&
+                               (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  if (vec)
+    gemm_bf16w_kernel<GEGLU, 64, 2, true><<<dim3((unsigned)tiles), 256, 0, s>>>(
+        xb, wb, y, hb, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
+  else
+    gemm_bf16w_kernel<GEGLU, 64, 2, false><<<dim3((unsigned)tiles), 256, 0, s>>>(
+        xb, wb, y, hb, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
   return hipGetLastError();
 }
 
@@ -601,7 +657,7 @@ hipError_t launch_gemm_bf16_geglu(const uint16_t* xb, const int8_t* wq, const fl
 namespace glypr {
 
 bool gemm_bf16w_ok(int64_t M, int64_t Nrows, int64_t K) {
-  return K % BFW_BK == 0 && 2 * M * K < (int64_t(1) << 31) && 2 * Nrows * K < (int64_t(1) << 31);
+  return K % 64 == 0 && 2 * M * K < (int64_t(1) << 31) && 2 * Nrows * K < (int64_t(1) << 31);
 }
 
 hipError_t launch_gemm_bf16w(const uint16_t* xb, const uint16_t* wb, float* y, int64_t M,
