@@ -250,6 +250,35 @@ def test_mlp_ragged_small_m_bit_exact(ctx, oracle, m, H, F):
                       "rmsnorm+mlp")
 
 
+def test_rmsnorm_calls_repeat_and_interleave(ctx, oracle):
+    """RMSNorm-prologue matmul and MLP calls at H = 768, F = 1152 repeated and
+    interleaved on one context (one shared activation workspace), across the
+    fused-prologue and two-launch routes: ragged M and N and the special rows
+    stay bit-exact on every call."""
+    H, F = 768, 1152
+    gb, ub, db = (oracle.q8_0_weight(F, H, seed=31), oracle.q8_0_weight(F, H, seed=32),
+                  oracle.q8_0_weight(H, F, seed=33))
+    g = Q8Weight.from_gguf(ctx, gb, F, H)
+    u = Q8Weight.from_gguf(ctx, ub, F, H)
+    d = Q8Weight.from_gguf(ctx, db, H, F)
+    gu, _ = Q8Weight.concat(ctx, [g, u])
+    nw = 1 + 0.1 * oracle.normal(H, seed=34)
+    nwd = dev(nw)
+    plain = {n: (oracle.q8_0_weight(n, H, seed=40 + n), None) for n in (70, 1280)}
+    plain = {n: (wb, Q8Weight.from_gguf(ctx, wb, n, H)) for n, (wb, _) in plain.items()}
+    cases = [(3, 70), (512, 1280), (37, 1280), (2047, 70), (512, 1280), (1, 1280), (130, 70)]
+    for rep, (m, n) in enumerate(cases):
+        say(f"rmsnorm call {rep}: m={m} n={n}")
+        x = _prologue_rows(oracle, m, H, seed=900 + rep)
+        xd = dev(x)
+        xn = oracle.rmsnorm(x, nw, 1e-6)
+        wb, w = plain[n]
+        y = host(ops.rmsnorm_q8_0_matmul(ctx, w, xd, nwd, 1e-6, INT8_EXACT))
+        assert_bits_equal(y, oracle.matmul(xn, wb, n), f"rmsnorm+matmul call {rep}")
+        y = host(ops.rmsnorm_mlp(ctx, gu, d, xd, nwd, 1e-6, INT8_EXACT))
+        assert_bits_equal(y, _mlp_ref(oracle, xn, gb, ub, db, H, F), f"rmsnorm+mlp call {rep}")
+
+
 def test_geglu_bit_exact(ctx, oracle):
     say("geglu elementwise [512 x 1152] + KAT points")
     g = oracle.normal(512 * 1152, seed=61, std=3.0)
