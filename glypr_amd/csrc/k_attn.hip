@@ -27,9 +27,12 @@ typedef _Float16 f16;
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// qkv_post.  One wave per (token, head slot); slots 0..nq-1 are q heads,
-// nq..nq+nkv-1 k heads, then nkv v heads.  hd == 256: lane l holds dims
-// 4l..4l+3.  RMSNorm follows simd_rmsnorm_row_f32's order (eight FMA chains,
+// qkv_post.  q and k: one wave per (token, head slot); slots 0..nq-1 are q
+// heads, nq..nq+nkv-1 k heads.  hd == 256: lane l holds dims 4l..4l+3 and
+// writes them as one 8-byte store.  v (the blocks after the q/k blocks): one
+// wave per 4 consecutive tokens of a head, so each lane writes its 4 dims of
+// the transposed vt as four 8-byte runs of 4 tokens; the same eight chains and
+// horizontal sum per token, run by lanes 8 i + j (token i, chain j).  RMSNorm follows simd_rmsnorm_row_f32's order (eight FMA chains,
 // lane j = dims j, j+8, ...; see k_norm.hip) so it is bit-exact with the CPU
 // path; RoPE is x*cos + rot*sin with both products rounded (no FMA), rot =
 // -x[i+128] for i < 128 and x[i-128] otherwise: lane l's partner is l ^ 32.
@@ -38,25 +41,83 @@ typedef _Float16 f16;
 // ---------------------------------------------------------------------------
 constexpr int QKV_HD = 256;
 
+constexpr int QKV_V_TOK = 4;   // tokens per v wave (8 lanes each)
+constexpr int QKV_V_LDS = QKV_V_TOK * 8 * (QKV_HD / 8 + 4);   // floats per v wave
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
 __global__ void __launch_bounds__(256) qkv_post_kernel(
     const float* __restrict__ qkv, int T, int Tp, int nq, int nkv, const float* __restrict__ qnw,
     const float* __restrict__ knw, float eps, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, f16* __restrict__ q16,
-    f16* __restrict__ k16, f16* __restrict__ vt16) {
-  __shared__ float lrows[4][QKV_HD];
+    f16* __restrict__ k16, f16* __restrict__ vt16, int qk_blocks) {
+  // per wave: a q/k row (QKV_HD floats) or the chain-major v rows (QKV_V_LDS)
+  static_assert(QKV_V_LDS >= QKV_HD, "shared staging sized by the v rows");
+  __shared__ __attribute__((aligned(16))) float lds_rows[4][QKV_V_LDS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slots = nq + 2 * nkv;
+  if ((int)blockIdx.x >= qk_blocks) {
+    // v: wave = QKV_V_TOK consecutive tokens of one head; lane 8 i + j runs
+    // chain j of token i from the chain-major LDS copy, then lane l stores dims
+    // 4l .. 4l+3 of the tokens as four runs of vt rows.
+    const int64_t vtask = (int64_t)((int)blockIdx.x - qk_blocks) * 4 + wave;
+    const int per_head = Tp / QKV_V_TOK;
+    if (vtask >= (int64_t)nkv * per_head) return;
+    const int head = (int)(vtask / per_head), t0 = (int)(vtask % per_head) * QKV_V_TOK;
+    constexpr int S = QKV_HD / 8 + 4;   // chain stride, as chain_stride() in k_norm.hip
+    float* lv = lds_rows[wave];
+    v4f x[QKV_V_TOK];
+#pragma unroll
+    for (int i = 0; i < QKV_V_TOK; i++) {
+      const int t = t0 + i;
+      x[i] = t < T ? *reinterpret_cast<const v4f*>(qkv + (int64_t)t * slots * QKV_HD +
+                                                   (int64_t)(nq + nkv + head) * QKV_HD + 4 * lane)
+                   : v4f{0, 0, 0, 0};
+      const int j0 = 4 * (lane & 1), idx = lane >> 1;
+#pragma unroll
+      for (int k = 0; k < 4; k++) lv[i * 8 * S + (j0 + k) * S + idx] = x[i][k];
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    // lanes past 8 QKV_V_TOK repeat a staged token (their sums are unused)
+    const int ti = (lane >> 3) % QKV_V_TOK;
+    const v4f* src = reinterpret_cast<const v4f*>(lv + ti * 8 * S + (lane & 7) * S);
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < QKV_HD / 32; c++) {
+      const v4f e = src[c];
+      acc = fmaf(e[0], e[0], acc);
+      acc = fmaf(e[1], e[1], acc);
+      acc = fmaf(e[2], e[2], acc);
+      acc = fmaf(e[3], e[3], acc);
+    }
+    const float s4 = acc + __shfl_down(acc, 4, 8);
+    const float s2 = s4 + __shfl_down(s4, 2, 8);
+    const float sum = s2 + __shfl_down(s2, 1, 8);
+    const float inv = 1.0f / sqrtf(sum / (float)QKV_HD + eps);   // valid on lanes 8 i
+    v4h yh[4];
+#pragma unroll
+    for (int i = 0; i < QKV_V_TOK; i++) {
+      const float inv_i = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), 8 * i));
+#pragma unroll
+      for (int e = 0; e < 4; e++) yh[e][i] = (f16)(x[i][e] * inv_i);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      *reinterpret_cast<v4h*>(vt16 + ((int64_t)head * QKV_HD + 4 * lane + e) * Tp + t0) = yh[e];
+    return;
+  }
+  const int qk_slots = nq + nkv;
   const int64_t task = (int64_t)blockIdx.x * 4 + wave;
-  if (task >= (int64_t)Tp * slots) return;
-  const int t = (int)(task / slots), slot = (int)(task % slots);
-  const int kind = slot < nq ? 0 : (slot < nq + nkv ? 1 : 2);
-  const int head = kind == 0 ? slot : (kind == 1 ? slot - nq : slot - nq - nkv);
+  if (task >= (int64_t)Tp * qk_slots) return;
+  const int t = (int)(task / qk_slots), slot = (int)(task % qk_slots);
+  const int kind = slot < nq ? 0 : 1;
+  const int head = kind == 0 ? slot : slot - nq;
 
   v4f y = {0, 0, 0, 0};
   if (t < T) {
     const float* src = qkv + (int64_t)t * (nq + 2 * nkv) * QKV_HD + (int64_t)slot * QKV_HD;
     v4f x = *reinterpret_cast<const v4f*>(src + 4 * lane);
-    float* lrow = lrows[wave];
+    float* lrow = lds_rows[wave];
     *reinterpret_cast<v4f*>(lrow + 4 * lane) = x;
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
@@ -74,18 +135,21 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     }
     sum = __shfl(sum, 0);
     const float inv = 1.0f / sqrtf(sum / (float)QKV_HD + eps);
-    const float* w = kind == 0 ? qnw : (kind == 1 ? knw : nullptr);
+    const float* w = kind == 0 ? qnw : knw;
     v4f wv = w ? *reinterpret_cast<const v4f*>(w + 4 * lane) : v4f{1, 1, 1, 1};
 #pragma unroll
     for (int e = 0; e < 4; e++) y[e] = w ? (x[e] * inv) * wv[e] : x[e] * inv;
-    if (kind < 2) {
+    {
       v4f c = *reinterpret_cast<const v4f*>(cos_t + (int64_t)t * QKV_HD + 4 * lane);
       v4f s = *reinterpret_cast<const v4f*>(sin_t + (int64_t)t * QKV_HD + 4 * lane);
       v4f r;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        float partner = __shfl_xor(y[e], 32);
-        r[e] = lane < 32 ? -partner : partner;
+        // v_permlane32_swap of y with itself: lanes < 32 get (own, lane + 32),
+        // lanes >= 32 get (lane - 32, own)
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[e]),
+                                                        __float_as_uint(y[e]), false, false);
+        r[e] = lane < 32 ? -__uint_as_float(p[1]) : __uint_as_float(p[0]);
       }
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -95,18 +159,9 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
       }
     }
   }
-  if (kind == 0) {
-    const int64_t off = ((int64_t)head * Tp + t) * QKV_HD + 4 * lane;
-#pragma unroll
-    for (int e = 0; e < 4; e++) q16[off + e] = (f16)y[e];
-  } else if (kind == 1) {
-    const int64_t off = ((int64_t)head * Tp + t) * QKV_HD + 4 * lane;
-#pragma unroll
-    for (int e = 0; e < 4; e++) k16[off + e] = (f16)y[e];
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; e++) vt16[((int64_t)head * QKV_HD + 4 * lane + e) * Tp + t] = (f16)y[e];
-  }
+  const v4h yh = {(f16)y[0], (f16)y[1], (f16)y[2], (f16)y[3]};
+  f16* out = kind == 0 ? q16 : k16;
+  *reinterpret_cast<v4h*>(out + ((int64_t)head * Tp + t) * QKV_HD + 4 * lane) = yh;
 }
 
 hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
@@ -114,11 +169,13 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
                            const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
                            uint16_t* vt16, hipStream_t s) {
   if (hd != QKV_HD) return hipErrorInvalidValue;
-  const int64_t tasks = Tp * (nq + 2 * nkv);
-  qkv_post_kernel<<<(unsigned)((tasks + 3) / 4), 256, 0, s>>>(
+  if (Tp % 64 != 0) return hipErrorInvalidValue;
+  const int64_t qk_blocks = (Tp * (nq + nkv) + 3) / 4;
+  const int64_t v_blocks = (nkv * (Tp / QKV_V_TOK) + 3) / 4;
+  qkv_post_kernel<<<(unsigned)(qk_blocks + v_blocks), 256, 0, s>>>(
       qkv, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
       reinterpret_cast<f16*>(q16), reinterpret_cast<f16*>(k16),
-      reinterpret_cast<f16*>(vt16));
+      reinterpret_cast<f16*>(vt16), (int)qk_blocks);
   return hipGetLastError();
 }
 
@@ -150,6 +207,7 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 // B (32 x 16): column l%16, same k; D (16 x 16): column l%16, rows 4(l/16)+r.
 // ---------------------------------------------------------------------------
 constexpr int AK = 32;            // keys per tile
+constexpr float ATTN_TAU = 8.0f;  // lazy-rescale threshold (natural log): p <= e^8 ~ 2981
 static_assert(ATTN_TP_ALIGN % 64 == 0, "query blocks (16 or 64) must tile the padded length");
 // Short sequences use 16-query blocks (more blocks to spread), long ones
 // 64-query blocks (each K/V tile serves 4x the queries).
@@ -157,6 +215,32 @@ constexpr int64_t ATTN_SMALL_T = 1024;
 inline int attn_qs(int64_t T) { return T <= ATTN_SMALL_T ? 1 : 4; }
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
+
+// Lane pairs (l, l ^ 16) and (l, l ^ 32) through gfx950's permlane swaps:
+// v_permlane16_swap / v_permlane32_swap of a value with itself return, in
+// every lane, the lane's own value and its partner's (in either order), all
+// in VALU — no LDS round trip as with ds_bpermute.  max and + over the pair
+// are order-independent, so each equals op(v, v[l ^ 16]) (resp. l ^ 32).
+__device__ __forceinline__ float pair_max16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float pair_max32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float pair_sum16(float v) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float pair_sum32(float v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
 
 // LDS swizzles (16-byte chunk c of row r is stored at chunk c ^ swz(r)); both
 // keep any 8 consecutive lanes of a fragment read on distinct 16-byte bank
@@ -317,11 +401,15 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     // ---- online softmax for query qi
     float mx = fmaxf(fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3])),
                      fmaxf(fmaxf(sacc[1][0], sacc[1][1]), fmaxf(sacc[1][2], sacc[1][3])));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
+    mx = pair_max32(pair_max16(mx));
+    // Lazy rescaling: the reference max m_run moves only when a tile's max
+    // exceeds it by more than ATTN_TAU (the first finite tile always moves
+    // it), so p = e^{s - m_run} <= e^TAU fits f16 with its usual 2^-11
+    // relative rounding, and the O rescale below runs on few tiles.  The
+    // partition's (m, l, O) all refer to m_run; the combine is unchanged.
+    const float m_new = mx > m_run + ATTN_TAU ? mx : m_run;
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __expf(m_run - m_use);
+    const float alpha = __expf(m_run - m_use);   // exactly 1 while m_run holds
     v8h pf;   // P^T B operand: k-slot 4 kt + r = key 8 lq + 4 kt + r
     float ps = 0.0f;
 #pragma unroll
@@ -332,11 +420,9 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
         ps += pv;
         pf[4 * kt + r] = (f16)pv;
       }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = pair_sum32(pair_sum16(ps));
     l_run = l_run * alpha + ps;
     m_run = m_new;
-    // the running max moves on few tiles once the sequence is under way
     if (__any(alpha != 1.0f)) {
 #pragma unroll
       for (int t = 0; t < QKV_HD / 16; t++)
