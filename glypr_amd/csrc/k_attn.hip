@@ -518,6 +518,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
 // Key tiles per partition: enough partitions for ~2 blocks per CU, at least
 // two tiles each, and at most 64 tiles (2 MB of K and V) so one partition's
 // K/V stays in an XCD's L2.
+// Key partitions: enough (query block, partition) items for one round of
+// workgroups (one 96 KB-LDS block per CU on 256 CUs), at most half the key
+// tiles per partition and at most 64 partitions.
+constexpr int64_t ATTN_BLOCKS = 256;
 static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, int* kparts) {
   const int64_t aqb = 16 * attn_qs(T);
   const int64_t tp = attn_padded_len(T);
@@ -527,7 +531,7 @@ static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, 
     int64_t band = (2 * window + aqb + AK - 1) / AK + 1;
     if (band < nkb) nkb = band;
   }
-  int64_t want = (512 + nqb * nkv - 1) / (nqb * nkv);
+  int64_t want = (ATTN_BLOCKS + nqb * nkv - 1) / (nqb * nkv);
   if (want > (nkb + 1) / 2) want = (nkb + 1) / 2;
   if (want < (nkb + 63) / 64) want = (nkb + 63) / 64;
   if (want < 1) want = 1;
