@@ -61,7 +61,9 @@ def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window, f16_qk
 
 
 @pytest.mark.parametrize("t,window,qk_scale", [(70, 0, 1.0), (512, 0, 0.25), (600, 512, 0.25),
-                                               (1100, 256, 1.0), (2048, 512, 0.25)])
+                                               (1100, 256, 1.0), (2048, 512, 0.25),
+                                               (4096, 0, 0.25), (8192, 512, 0.25),
+                                               (8192, 0, 0.25)])
 def test_attention_core_vs_oracle(ctx, oracle, t, window, qk_scale):
     nq, nkv, hd, eps = 3, 1, 256, 1e-6
     say(f"attention core t={t} window={window} qk_norm_scale={qk_scale}")
