@@ -7,7 +7,9 @@ gate/up 768->2x1152 with the tanh-GeGLU epilogue -> down 1152->768.  A step is
 one pass of those 7 projections; value = algorithmic Q8_0 ops / step time.
 
 Also reported (in "extra"): configs[0] (C1, one 512x768x1152 linear) and
-configs[2] (C3, M = 16384 through the same 7 projections) for both variants.
+configs[2] (C3, M = 16384 through the same 7 projections) for both variants,
+and the platform's own GEMM library (hipBLASLt through torch) timed on the C3
+projection shapes as plain bf16 and int8 GEMMs, for reference.
 
     python bench.py [--steps K] [--warmup W] [--variant int8|bf16] [--no-cpu]
 
@@ -255,6 +257,52 @@ def c1_linear(ctx, steps):
                                                    4),
                      "note": f"{copies} operand sets rotated, ~{copies * 5} MB"},
             "note": "one launch: the activation quantization runs as the GEMM prologue"}
+
+
+def vendor_ref(steps):
+    """hipBLASLt (through torch) on the C3 projection shapes, as a reference for
+    what the platform's own GEMM library reaches there: bf16 x bf16 -> bf16
+    (torch.matmul) and int8 x int8 -> int32 (torch._int_mm).  Plain GEMMs: no
+    Q8_0 block scales, no activation quantization, half-width (bf16) outputs."""
+    import torch
+    out = {}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps * 1e3   # us
+
+    step_bf16 = step_i8 = 0.0
+    m = 16384
+    for name, n, k in PROJ:
+        a = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+        b = torch.randn(n, k, device="cuda", generator=gen).to(torch.bfloat16)
+        us_bf = timed(lambda: a @ b.t())
+        ai = torch.randint(-127, 128, (m, k), device="cuda", dtype=torch.int8, generator=gen)
+        bi = torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen)
+        us_i8 = timed(lambda: torch._int_mm(ai, bi))
+        ops_ = 2 * m * n * k
+        out[name] = {"M": m, "N": n, "K": k,
+                     "bf16_us": round(us_bf, 2), "bf16_tflops": round(ops_ / us_bf / 1e6, 1),
+                     "int8_us": round(us_i8, 2), "int8_tops": round(ops_ / us_i8 / 1e6, 1)}
+        step_bf16 += us_bf
+        step_i8 += us_i8
+        del a, b, ai, bi
+    total = LAYER_NK * 2 * m
+    out["c3_step"] = {"bf16_ms": round(step_bf16 / 1e3, 4),
+                      "bf16_tflops": round(total / step_bf16 / 1e6, 1),
+                      "int8_ms": round(step_i8 / 1e3, 4),
+                      "int8_tops": round(total / step_i8 / 1e6, 1)}
+    out["library"] = "hipBLASLt via torch " + torch.__version__
+    return out
 
 
 def vec_search(ctx, steps):
@@ -532,8 +580,9 @@ def main():
     ap.add_argument("--variant", choices=["int8", "bf16"], default="int8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
-    ap.add_argument("--extras", default="c1,cold,c3,c4,c5,vec",
-                    help="comma list of the extra workloads to run (c1, cold, c3, c4, c5, vec)")
+    ap.add_argument("--extras", default="c1,cold,c3,vendor,c4,c5,vec",
+                    help="comma list of the extra workloads to run "
+                         "(c1, cold, c3, vendor, c4, c5, vec)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain device copy of MIB MiB (calibrates rocprof "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -582,6 +631,18 @@ def main():
                     / HBM_PEAK_GBS, 4),
                 "kernels_us": {k: round(vv["us_per_launch"], 2) for k, vv in kx.items()}}
             del Lx
+    if "vendor" in todo:
+        extra["vendor_ref_c3_shapes"] = vendor_ref(max(10, args.steps // 4))
+        if "c3" in todo:
+            # the same C3 step's GEMM launches only (no norm / quantize launches)
+            for vname, gk, geglu in (("int8", "gemm_i8", "gemm_i8_geglu"),
+                                     ("bf16", "gemm_bf16", "gemm_bf16_geglu")):
+                ku = extra[f"c3_{vname}"]["kernels_us"]
+                if gk in ku and geglu in ku:
+                    us = 3 * ku[gk] + ku[geglu]
+                    extra[f"c3_{vname}"]["gemm_ms_per_step"] = round(us / 1e3, 4)
+                    extra[f"c3_{vname}"]["gemm_tops"] = round(
+                        LAYER_NK * 2 * 16384 / us / 1e6, 1)
     if "c1" in todo:
         extra["c1_int8"] = c1_linear(ctx, args.steps)
     if "cold" in todo:
