@@ -413,7 +413,7 @@ def test_matmul_bf16_dequant_within_bf16_bound(ctx, oracle, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 64, 1), (100, 768, 1152), (600, 1152, 257),
-                                   (4100, 768, 1280)])
+                                   (4100, 768, 1280), (8192, 768, 768), (4095, 768, 1024)])
 def test_dense_bf16_weight_matmul_within_bound(ctx, oracle, m, k, n):
     """LinearOp::forward over a dense bf16 weight: x rounded to bf16 (relative
     error <= 2^-9), exact bf16 weights, f32 accumulation:
