@@ -401,23 +401,35 @@ void orc_pool_normalize(const float* tokens, const uint8_t* mask, int64_t t, int
   free(pooled);
 }
 
+/* Rust's `Sum for f32` (core::iter, Rust >= 1.83; the reference is edition
+ * 2024, so Rust >= 1.85) is a sequential fold that starts from -0.0: the sum
+ * of no terms, or of -0.0 terms only, is -0.0. */
+static float rust_sum_start(void) { return -0.0f; }
+
+/* l2_normalize (util.rs:22-29): norm = sqrt(sequential f32 sum of x*x); a
+ * zero norm returns the input unchanged (no clamp); else x / norm. */
 void orc_l2_normalize(const float* x, int64_t n, float* y) {
-  float s = 0.0f;
-  for (int64_t i = 0; i < n; i++) s += x[i] * x[i];
+  float s = rust_sum_start();
+  for (int64_t i = 0; i < n; i++) s = s + x[i] * x[i];
   float nrm = sqrtf(s);
   for (int64_t i = 0; i < n; i++) y[i] = nrm == 0.0f ? x[i] : x[i] / nrm;
 }
 
+/* cosine_similarity (util.rs:32-41): three sequential f32 sums (dot, |a|^2,
+ * |b|^2), sqrt of each norm, 0.0 when either norm is 0, else
+ * (dot / (norm_a * norm_b)) clamped to [-1, 1]. */
 float orc_cosine(const float* a, const float* b, int64_t n) {
-  double dot = 0, na = 0, nb = 0;
-  for (int64_t i = 0; i < n; i++) {
-    dot += (double)a[i] * b[i];
-    na += (double)a[i] * a[i];
-    nb += (double)b[i] * b[i];
-  }
-  if (na == 0 || nb == 0) return 0.0f;
-  double c = dot / sqrt(na * nb);
-  return (float)(c > 1 ? 1 : (c < -1 ? -1 : c));
+  float dot = rust_sum_start(), sa = rust_sum_start(), sb = rust_sum_start();
+  for (int64_t i = 0; i < n; i++) dot = dot + a[i] * b[i];
+  for (int64_t i = 0; i < n; i++) sa = sa + a[i] * a[i];
+  for (int64_t i = 0; i < n; i++) sb = sb + b[i] * b[i];
+  float na = sqrtf(sa), nb = sqrtf(sb);
+  if (na == 0.0f || nb == 0.0f) return 0.0f;
+  float c = dot / (na * nb);
+  /* f32::clamp(-1, 1): NaN stays NaN */
+  if (c < -1.0f) c = -1.0f;
+  if (c > 1.0f) c = 1.0f;
+  return c;
 }
 
 /* ======================================================================== */

@@ -27,6 +27,9 @@
  *  - tanhf / geglu: double-precision tanh (<= 3 ulp), exact special points.
  *  - embed_gather, pool_normalize: dequantized rows; closed-form KAT and the
  *    reference's long-context generator against float64.
+ *  - l2_normalize / cosine: the reference's own known answers (util.rs:258-268),
+ *    numpy's sequential float32 accumulate (np.add.accumulate) bit for bit,
+ *    zero-norm and clamp special cases, float64 within f32 rounding.
  *  - attention: chunked band == dense masked attention in float64.
  *  - rope_tables: closed form (f32 product, float64 cos/sin).
  *  - encoder_layer / model_forward: an independent float64 statement of the
@@ -109,7 +112,9 @@ int orc_embed_gather(const uint8_t* table, int64_t vocab, int64_t d, const uint3
 /* tokens f32 [t,d]; mask (nullable) uint8 [t]; writes out[trunc] (trunc==0 or >=d -> d). */
 void orc_pool_normalize(const float* tokens, const uint8_t* mask, int64_t t, int64_t d,
                         int64_t trunc, float* out);
-/* util.rs:22-29 / 6-19 */
+/* l2_normalize (util.rs:22-29): sequential f32 sum of squares, a zero norm
+ * returns x unchanged.  cosine_similarity (util.rs:32-41): sequential f32
+ * sums, 0 for a zero norm, clamp to [-1, 1]. */
 void orc_l2_normalize(const float* x, int64_t n, float* y);
 float orc_cosine(const float* a, const float* b, int64_t n);
 

@@ -93,6 +93,7 @@ def lib():
             "orc_quantize_int8": (None, [_f32p, _i64, _i8p]),
             "orc_int8_dot": (ctypes.c_int32, [_i8p, _i8p, _i64]),
             "orc_int8_cosine": (ctypes.c_float, [_i8p, _i8p, _i64]),
+            "orc_splitmix64": (ctypes.c_uint64, [ctypes.POINTER(ctypes.c_uint64)]),
             "orc_fill_normal": (None, [_f32p, _i64, ctypes.c_uint64, ctypes.c_float,
                                        ctypes.c_float]),
             "orc_fill_uniform_ids": (None, [_u32p, _i64, ctypes.c_uint64, ctypes.c_uint32]),
@@ -261,6 +262,22 @@ def pool_normalize(tokens: np.ndarray, mask: Optional[np.ndarray] = None,
     mk = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
     lib().orc_pool_normalize(_p(tok, _f32p), _p(mk, _u8p), t, d, trunc, _p(out, _f32p))
     return out
+
+
+def l2_normalize(x: np.ndarray) -> np.ndarray:
+    """util.rs:22-29 (orc_l2_normalize)."""
+    v = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.empty_like(v)
+    lib().orc_l2_normalize(_p(v, _f32p), v.size, _p(out, _f32p))
+    return out
+
+
+def cosine(a: np.ndarray, b: np.ndarray) -> float:
+    """util.rs:32-41 (orc_cosine), as an f32."""
+    va = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+    vb = np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+    assert va.size == vb.size
+    return np.float32(lib().orc_cosine(_p(va, _f32p), _p(vb, _f32p), va.size))
 
 
 # --------------------------------------------------------- vector codecs ----

@@ -297,6 +297,74 @@ def test_pool_long_context_vs_f64(oracle):
         assert m.shape == (256,) and abs(np.linalg.norm(m.astype(np.float64)) - 1) < 1e-6
 
 
+# ------------------------------------------------- l2_normalize / cosine ----
+
+def _seq_sum_f32(terms):
+    """Sequential float32 sum from -0.0 (numpy's add.accumulate is a running
+    float32 sum; np.sum would be pairwise)."""
+    t = np.concatenate([np.array([-0.0], np.float32), np.asarray(terms, np.float32)])
+    return np.add.accumulate(t, dtype=np.float32)[-1]
+
+
+def test_l2_normalize_kat_and_sequential_sum(oracle):
+    # the reference's own known answers (util.rs:258-262)
+    y = oracle.l2_normalize(np.array([3.0, 4.0], np.float32))
+    assert abs(y[0] - 0.6) < 1e-6 and abs(y[1] - 0.8) < 1e-6
+    assert np.array_equal(f32_to_bits(y), f32_to_bits(np.array([3, 4], np.float32) / np.float32(5)))
+    # a zero norm returns the input unchanged, signed zeros included (no 1e-12 clamp)
+    z = np.array([0.0, -0.0, 0.0, -0.0], np.float32)
+    assert np.array_equal(f32_to_bits(oracle.l2_normalize(z)), f32_to_bits(z))
+    # a norm that underflows to 0 (1e-30^2 = 0 in f32) also returns the input
+    tiny = np.full(8, 1e-30, np.float32)
+    assert np.array_equal(f32_to_bits(oracle.l2_normalize(tiny)), f32_to_bits(tiny))
+    # random vectors: bit-identical to the sequential f32 statement, and within
+    # f32 rounding of the float64 normalisation
+    rng = np.random.default_rng(3)
+    for n in (1, 7, 256, 768, 5000):
+        x = rng.standard_normal(n).astype(np.float32) * np.float32(rng.uniform(0.01, 100))
+        got = oracle.l2_normalize(x)
+        nrm = np.sqrt(_seq_sum_f32(x * x), dtype=np.float32)
+        assert np.array_equal(f32_to_bits(got), f32_to_bits(x / nrm)), n
+        ref = x.astype(np.float64) / np.linalg.norm(x.astype(np.float64))
+        assert np.abs(got - ref).max() <= 4e-7 * (1 + np.sqrt(n) * 2**-10)
+
+
+def test_cosine_kat_special_cases_and_sequential_sum(oracle):
+    # util.rs:264-267: truncate_mrl(l2_normalize([1,1,1,1]), 2) has cosine 1 with itself
+    t = oracle.l2_normalize(oracle.l2_normalize(np.ones(4, np.float32))[:2])
+    assert abs(oracle.cosine(t, t) - 1.0) < 1e-6
+    # zero norm -> 0.0, either side
+    assert oracle.cosine(np.zeros(3, np.float32), np.ones(3, np.float32)) == 0.0
+    assert oracle.cosine(np.ones(3, np.float32), np.zeros(3, np.float32)) == 0.0
+    # orthogonal and opposite vectors are exact
+    assert oracle.cosine(np.array([1, 0], np.float32), np.array([0, 2], np.float32)) == 0.0
+    assert oracle.cosine(np.array([3, 4], np.float32), np.array([-6, -8], np.float32)) == -1.0
+    # the clamp: a vector whose rounded cosine with itself exceeds 1 returns 1.0
+    rng = np.random.default_rng(5)
+    over = 0
+    for _ in range(400):
+        a = rng.standard_normal(33).astype(np.float32)
+        d = _seq_sum_f32(a * a)
+        r = np.sqrt(d, dtype=np.float32)
+        raw = np.float32(d / np.float32(r * r))
+        c = oracle.cosine(a, a)
+        assert c == min(raw, np.float32(1.0))
+        over += raw > 1
+    assert over > 0, "no case exercised the clamp"
+    # random pairs: bit-identical to the sequential f32 statement; float64 within rounding
+    for n in (1, 5, 256, 768, 3000):
+        a = rng.standard_normal(n).astype(np.float32)
+        b = (0.3 * a + rng.standard_normal(n)).astype(np.float32)
+        dot, sa, sb = _seq_sum_f32(a * b), _seq_sum_f32(a * a), _seq_sum_f32(b * b)
+        ref = np.float32(dot / (np.sqrt(sa, dtype=np.float32) * np.sqrt(sb, dtype=np.float32)))
+        ref = np.clip(ref, np.float32(-1), np.float32(1))
+        got = oracle.cosine(a, b)
+        assert f32_to_bits(np.float32(got)) == f32_to_bits(ref), n
+        c64 = float(a.astype(np.float64) @ b / np.linalg.norm(a.astype(np.float64))
+                    / np.linalg.norm(b.astype(np.float64)))
+        assert abs(got - c64) < 1e-6 * (1 + n * 2**-8)
+
+
 # ------------------------------------------------------------- attention ----
 
 def test_attention_band_equals_masked_dense(oracle):
@@ -532,3 +600,121 @@ def test_model_forward_vs_float64_statement(oracle):
     with pytest.raises(ValueError):
         oracle.model_forward(tensors, np.array([vocab], np.uint32), 32, hidden=H, ffn=F,
                              n_heads=nh, n_kv_heads=nkv, head_dim=hd, n_layers=L, vocab=vocab)
+
+
+# ------------------------------------------------- synthetic-input makers ----
+
+def test_splitmix64_published_vectors(oracle):
+    """SplitMix64 (Steele, Lea, Flood 2014) from state 0: the published first
+    outputs."""
+    import ctypes
+    st = ctypes.c_uint64(0)
+    got = [oracle.lib().orc_splitmix64(ctypes.byref(st)) for _ in range(3)]
+    assert got == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+
+
+def _splitmix_stream(seed, n):
+    mask = (1 << 64) - 1
+    s, out = seed, []
+    for _ in range(n):
+        s = (s + 0x9E3779B97F4A7C15) & mask
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+        out.append(z ^ (z >> 31))
+    return out
+
+
+def test_generators_restated_in_python(oracle):
+    """fill_normal (Box-Muller on (0,1] uniforms), uniform ids and the Q8_0
+    weight maker, restated in Python from the same SplitMix64 stream."""
+    r = _splitmix_stream(9, 8)
+    u = [((v >> 11) + 1.0) / 9007199254740992.0 for v in r]
+    ref = []
+    for i in range(0, 8, 2):
+        rad = math.sqrt(-2.0 * math.log(u[i]))
+        ref += [np.float32(1.5 + 2.0 * rad * math.cos(2 * math.pi * u[i + 1])),
+                np.float32(1.5 + 2.0 * rad * math.sin(2 * math.pi * u[i + 1]))]
+    assert np.array_equal(oracle.normal(8, seed=9, mean=1.5, std=2.0), np.array(ref, np.float32))
+    ids = oracle.uniform_ids(16, seed=4, vocab=1000)
+    assert ids.tolist() == [v % 1000 for v in _splitmix_stream(4, 16)]
+    w = oracle.q8_0_weight(2, 64, seed=12, sigma=0.02)
+    d, qs = oracle.split_blocks(w, 64)
+    st = _splitmix_stream(12, 4 * 34)
+    pos = 0
+    for blk in range(4):
+        u1 = ((st[pos] >> 11) + 1.0) / 9007199254740992.0
+        u2 = ((st[pos + 1] >> 11) + 1.0) / 9007199254740992.0
+        z = math.sqrt(-2.0 * math.log(u1)) * math.cos(2 * math.pi * u2)
+        dref = np.float32(abs(z) * float(np.float32(0.02)) / 127.0).astype(np.float16).view(np.uint16)
+        assert int(d.reshape(-1)[blk]) == int(dref)
+        qref = [int(v % 255) - 127 for v in st[pos + 2: pos + 34]]
+        assert qs.reshape(-1, 32)[blk].tolist() == qref
+        pos += 34
+    big = oracle.normal(200_000, seed=3)
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 1) < 0.01
+
+
+# The pin of every exported oracle function: a test above (or in the vector
+# codec / rounding modules) that a plausible mistake in it would fail.
+PINS = {
+    "orc_f32_to_f16": ["test_f16_matches_numpy_rne"],
+    "orc_f16_to_f32": ["test_f16_matches_numpy_rne"],
+    "orc_f32_to_f16_array": ["test_f16_matches_numpy_rne"],
+    "orc_f16_to_f32_array": ["test_f16_matches_numpy_rne"],
+    "orc_q8_0_quantize_row": ["test_quantize_kat", "test_quantize_matches_f64_definition"],
+    "orc_q8_0_quantize_rows": ["test_quantize_kat", "test_quantize_matches_f64_definition"],
+    "orc_q8_0_dequantize_row": ["test_dequant_kat"],
+    "orc_q8_0_dequantize_rows": ["test_dequant_kat"],
+    "orc_q8_0_vec_dot": ["test_vec_dot_kat"],
+    "orc_q8_0_matmul": ["test_matmul_vs_f64_bruteforce", "test_matmul_lossless_equals_numpy"],
+    "orc_q8_0_matmul_preq": ["test_matmul_vs_f64_bruteforce"],
+    "orc_q8_0_matmul_f64": ["test_matmul_lossless_equals_numpy"],
+    "orc_q8_0_matmul_dequant_f64": ["test_reference_metal_case_activation_error_bound"],
+    "orc_rmsnorm_row": ["test_rmsnorm_kat", "test_rmsnorm_vs_f64_and_invariants"],
+    "orc_rmsnorm": ["test_rmsnorm_kat", "test_rmsnorm_vs_f64_and_invariants"],
+    "orc_tanhf": ["test_tanh_accuracy"],
+    "orc_geglu_scalar": ["test_geglu_kat_and_formula"],
+    "orc_geglu": ["test_geglu_kat_and_formula"],
+    "orc_geglu_scalar_libm": ["test_geglu_tanh_substitution_is_ulp_level"],
+    "orc_embed_gather": ["test_gather_equals_dequant_rows"],
+    "orc_pool_normalize": ["test_pool_kat", "test_pool_long_context_vs_f64"],
+    "orc_l2_normalize": ["test_l2_normalize_kat_and_sequential_sum"],
+    "orc_cosine": ["test_cosine_kat_special_cases_and_sequential_sum"],
+    "orc_quantize_binary": ["test_reference_known_answers", "test_quantize_binary_matches_packbits"],
+    "orc_hamming": ["test_reference_known_answers", "test_hamming_matches_unpackbits_and_invariants"],
+    "orc_binary_cosine": ["test_reference_known_answers", "test_binary_cosine_against_float64"],
+    "orc_quantize_int8": ["test_reference_known_answers",
+                          "test_quantize_int8_round_half_away_and_saturation"],
+    "orc_int8_dot": ["test_reference_known_answers",
+                     "test_int8_dot_and_cosine_against_int64_and_float64"],
+    "orc_int8_cosine": ["test_reference_known_answers",
+                        "test_int8_dot_and_cosine_against_int64_and_float64"],
+    "orc_splitmix64": ["test_splitmix64_published_vectors"],
+    "orc_fill_normal": ["test_generators_restated_in_python"],
+    "orc_fill_uniform_ids": ["test_generators_restated_in_python"],
+    "orc_make_q8_0_weight": ["test_generators_restated_in_python"],
+    "orc_layer_is_full": ["test_model_forward_vs_float64_statement"],
+    "orc_rope_tables": ["test_rope_tables_closed_form"],
+    "orc_attention": ["test_attention_band_equals_masked_dense"],
+    "orc_encoder_layer": ["test_model_forward_vs_float64_statement"],
+    "orc_model_forward": ["test_model_forward_vs_float64_statement",
+                          "test_model_forward_with_ple_vs_float64_statement"],
+}
+
+
+def test_every_oracle_export_is_pinned():
+    import re
+    hdr = open(os.path.join(os.path.dirname(HERE), "oracle", "glypr_oracle.h")).read()
+    exports = set(re.findall(r"\b(orc_[a-z0-9_]+)\s*\(", hdr))
+    missing = sorted(exports - set(PINS))
+    assert not missing, f"oracle functions with no pin: {missing}"
+    stale = sorted(set(PINS) - exports)
+    assert not stale, f"pins name functions the header no longer exports: {stale}"
+    names = set()
+    for mod in ("test_oracle.py", "test_vec_codecs.py", "test_round.py"):
+        names |= set(re.findall(r"^def (test_[a-z0-9_]+)", open(os.path.join(HERE, mod)).read(),
+                                re.M))
+    for fn, tests in PINS.items():
+        for t in tests:
+            assert t in names, f"{fn}: pin {t} does not exist"
