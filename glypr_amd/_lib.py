@@ -37,6 +37,7 @@ SIGNATURES = {
     "glypr_hip_ctx_create": (_int, [_int, ctypes.POINTER(_vp)]),
     "glypr_hip_ctx_destroy": (_int, [_vp]),
     "glypr_hip_sync": (_int, [_vp, _vp]),
+    "glypr_hip_ctx_reserve": (_int, [_vp, _i64]),
     "glypr_hip_q8_0_weight_create": (_int, [_vp, _vp, _i64, _i64, ctypes.POINTER(_vp)]),
     "glypr_hip_q8_0_weight_concat": (_int, [_vp, ctypes.POINTER(_vp), _int, ctypes.POINTER(_vp),
                                             ctypes.POINTER(_vp)]),

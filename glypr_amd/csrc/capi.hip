@@ -44,7 +44,7 @@ int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const fl
                 float eps, bool norm, float* y, int64_t m, int variant, hipStream_t s) {
   const int64_t n = w->n, k = w->k;
   if (variant == GLYPR_Q8_INT8_EXACT) {
-    if (gemm_i8_pro_ok(m, k, norm)) {
+    if (gemm_i8_pro_ok(m, n, k, norm)) {
       LAUNCH(GLYPR_K_GEMM_I8_PRO, s,
              launch_gemm_i8_pro(x, norm_w, eps, norm, w->qs(), w->dw(), y, m, n, k, n, s),
              "gemm_i8_pro launch");
@@ -173,7 +173,8 @@ int glypr_hip_ctx_destroy(glypr_hip_ctx* ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->ids) (void)hipFree(ctx->ids);
     if (ctx->mask) (void)hipFree(ctx->mask);
-    if (ctx->bcos) (void)hipFree(ctx->bcos);
+    for (auto& kv : ctx->bcos)
+      if (kv.second.dev) (void)hipFree(kv.second.dev);
     for (auto& r : ctx->prof) {
       (void)hipEventDestroy(r.start);
       (void)hipEventDestroy(r.stop);
@@ -190,6 +191,17 @@ int glypr_hip_sync(glypr_hip_ctx* ctx, glypr_stream stream) {
   DeviceScope ds(ctx->device);
   GLYPR_TRY_HIP(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
   return GLYPR_OK;
+}
+
+int glypr_hip_ctx_reserve(glypr_hip_ctx* ctx, int64_t rows) {
+  clear_error();
+  GLYPR_CHECK(rows > 0, GLYPR_ERR_SHAPE, "reserve rows %lld must be positive", (long long)rows);
+  RET_IF(check_ctx(ctx));
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->reserve_rows = rows;
+  return reserve_for_weight(ctx, ctx->max_k);
 }
 
 int glypr_hip_q8_0_weight_create(glypr_hip_ctx* ctx, const uint8_t* gguf_blocks, int64_t n,
@@ -231,6 +243,14 @@ int glypr_hip_q8_0_weight_create(glypr_hip_ctx* ctx, const uint8_t* gguf_blocks,
     (void)hipFree(buf->dw);
     delete buf;
     return set_error(GLYPR_ERR_OOM, "host allocation failed");
+  }
+  {
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const int rc = reserve_for_weight(ctx, k);
+    if (rc != GLYPR_OK) {
+      glypr_hip_q8_0_weight_destroy(w);
+      return rc;
+    }
   }
   *out = w;
   return GLYPR_OK;
@@ -277,6 +297,16 @@ int glypr_hip_q8_0_weight_concat(glypr_hip_ctx* ctx, const glypr_q8w* const* par
     if (buf->dw) (void)hipFree(buf->dw);
     delete buf;
     return hip_error(e, "concat copy");
+  }
+  {
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const int rc = reserve_for_weight(ctx, k);
+    if (rc != GLYPR_OK) {
+      (void)hipFree(buf->qs);
+      (void)hipFree(buf->dw);
+      delete buf;
+      return rc;
+    }
   }
   glypr_q8w* f = new glypr_q8w{buf, 0, rows, k};
   if (views) {
@@ -365,6 +395,14 @@ int glypr_hip_bf16_weight_create(glypr_hip_ctx* ctx, const uint16_t* bf16_rows, 
     if (w->p) (void)hipFree(w->p);
     delete w;
     return hip_error(e, "bf16 weight upload");
+  }
+  {
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const int rc = reserve_for_weight(ctx, k);
+    if (rc != GLYPR_OK) {
+      glypr_hip_bf16_weight_destroy(w);
+      return rc;
+    }
   }
   *out = w;
   return GLYPR_OK;
@@ -647,22 +685,27 @@ int glypr_hip_binary_cosine(glypr_hip_ctx* ctx, const uint64_t* a, int64_t na,
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
   const int64_t dim = words * 64;
-  if (ctx->bcos_dim != dim) {
+  auto it = ctx->bcos.find(dim);
+  if (it == ctx->bcos.end()) {
     // binary_cosine_similarity evaluates (PI * (h as f32 / dim as f32)).cos() in
     // f32 with the platform libm; h is an integer in [0, dim], so the table is
     // that exact expression per h.  dim 0 -> 1.0 (the reference's early return).
-    std::vector<float> host((size_t)dim + 1);
+    // One table per dim, written once by an upload ordered on this stream.
+    glypr_hip_ctx::CosTable tab;
+    tab.host.resize((size_t)dim + 1);
     const float pi = 3.14159265358979323846f;
     for (int64_t h = 0; h <= dim; h++)
-      host[(size_t)h] = dim == 0 ? 1.0f : cosf(pi * ((float)h / (float)dim));
-    RET_IF(ensure_staging(ctx->bcos, ctx->bcos_cap, host.size()));
-    GLYPR_TRY_HIP(hipMemcpy(ctx->bcos, host.data(), host.size() * sizeof(float),
-                            hipMemcpyHostToDevice),
+      tab.host[(size_t)h] = dim == 0 ? 1.0f : cosf(pi * ((float)h / (float)dim));
+    GLYPR_TRY_HIP(hipMalloc((void**)&tab.dev, tab.host.size() * sizeof(float)),
+                  "binary cosine table: hipMalloc");
+    it = ctx->bcos.emplace(dim, std::move(tab)).first;
+    GLYPR_TRY_HIP(hipMemcpyAsync(it->second.dev, it->second.host.data(),
+                                 it->second.host.size() * sizeof(float), hipMemcpyHostToDevice,
+                                 (hipStream_t)stream),
                   "binary cosine table upload");
-    ctx->bcos_dim = dim;
   }
   LAUNCH(GLYPR_K_VEC_SEARCH, (hipStream_t)stream,
-         launch_binary_cosine(a, na, b, nb, words, ctx->bcos, out, (hipStream_t)stream),
+         launch_binary_cosine(a, na, b, nb, words, it->second.dev, out, (hipStream_t)stream),
          "binary_cosine launch");
   return GLYPR_OK;
 }
@@ -696,6 +739,14 @@ int glypr_hip_int8_cosine(glypr_hip_ctx* ctx, const int8_t* a, int64_t na, const
          launch_int8_cosine(a, na, b, nb, dim, (int32_t*)ctx->ws, out, (hipStream_t)stream),
          "int8_cosine launch");
   return GLYPR_OK;
+}
+
+// Not part of the public header: the INT8_EXACT GEMM route (GEMM_ROUTE_*) for a
+// shape, and whether the prologue-fused kernel takes it, so host tests can pin
+// the routing without a GPU.
+int glypr_internal_gemm_i8_route(int64_t m, int64_t n, int64_t k, int prologue) {
+  if (prologue == 1 || prologue == 2) return gemm_i8_pro_ok(m, n, k, prologue == 2) ? 4 : -1;
+  return gemm_i8_route(m, n, k);
 }
 
 static const char* const kKernelNames[GLYPR_K_COUNT] = {

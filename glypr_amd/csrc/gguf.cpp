@@ -39,6 +39,10 @@ enum GgufType : uint32_t {
   T_STR = 8, T_ARR = 9, T_U64 = 10, T_I64 = 11, T_F64 = 12
 };
 
+// A metadata value.  Arrays are not materialised: the parser checks their
+// bounds and keeps the element type, the count and where the elements start,
+// and get_array_u64 decodes one element on demand (string arrays such as the
+// tokenizer's 262144 tokens cost no host memory).
 struct GgufValue {
   uint32_t type = 0;
   uint64_t u = 0;   // unsigned integers and bool
@@ -46,8 +50,20 @@ struct GgufValue {
   double f = 0.0;   // floats
   std::string s;
   uint32_t arr_type = 0;
-  std::vector<GgufValue> arr;
+  uint64_t arr_len = 0;
+  const uint8_t* arr_data = nullptr;
 };
+
+// Byte size of a fixed-size GGUF value type, 0 for strings and arrays.
+size_t scalar_size(uint32_t t) {
+  switch (t) {
+    case T_U8: case T_I8: case T_BOOL: return 1;
+    case T_U16: case T_I16: return 2;
+    case T_U32: case T_I32: case T_F32: return 4;
+    case T_U64: case T_I64: case T_F64: return 8;
+    default: return 0;
+  }
+}
 
 struct GgufTensor {
   std::string name;
@@ -128,10 +144,24 @@ bool read_value(Cursor& c, uint32_t type, GgufValue& v, int depth) {
       if (depth > 0) return false;   // nested arrays do not occur in GGUF files
       v.arr_type = c.get<uint32_t>();
       const uint64_t n = c.get<uint64_t>();
-      if (!c.ok || n > (uint64_t)(c.end - c.p)) return false;   // every element takes >= 1 byte
-      v.arr.resize((size_t)n);
-      for (uint64_t k = 0; k < n; k++)
-        if (!read_value(c, v.arr_type, v.arr[(size_t)k], depth + 1)) return false;
+      if (!c.ok) return false;
+      const size_t remaining = (size_t)(c.end - c.p);
+      v.arr_len = n;
+      v.arr_data = c.p;
+      const size_t es = scalar_size(v.arr_type);
+      if (es > 0) {
+        if (n > remaining / es) return false;
+        c.p += n * es;
+      } else if (v.arr_type == T_STR) {
+        if (n > remaining / 8) return false;   // each string takes >= 8 bytes
+        for (uint64_t k = 0; k < n; k++) {
+          const uint64_t len = c.get<uint64_t>();
+          if (!c.ok || len > (uint64_t)(c.end - c.p)) return false;
+          c.p += len;
+        }
+      } else {
+        return false;
+      }
       break;
     }
     default:
@@ -160,6 +190,14 @@ bool as_f64(const GgufValue& v, double* out) {
   }
   if (as_u64(v, &u)) { *out = (double)u; return true; }
   return false;
+}
+
+// Element i of a fixed-size-typed array (bounds already checked by the parser).
+bool array_elem(const GgufValue& a, uint64_t i, GgufValue* out) {
+  const size_t es = scalar_size(a.arr_type);
+  if (es == 0 || i >= a.arr_len) return false;
+  Cursor c{a.arr_data + i * es, a.arr_data + (i + 1) * es};
+  return read_value(c, a.arr_type, *out, 1);
 }
 
 }  // namespace
@@ -234,12 +272,16 @@ int parse(glypr_gguf* g) {
   for (GgufTensor& t : g->tensors) {
     int64_t blk, bytes;
     ggml_type_size(t.type, &blk, &bytes);
-    const int64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
+    int64_t n = 1;
+    bool ovf = false;
+    for (int d = 0; d < 4; d++) ovf = ovf || __builtin_mul_overflow(n, t.ne[d], &n);
+    GLYPR_CHECK(!ovf, GLYPR_ERR_SHAPE, "tensor '%s': element count overflows", t.name.c_str());
     if (blk > 0) {
       GLYPR_CHECK(t.ne[0] % blk == 0, GLYPR_ERR_SHAPE,
                   "tensor '%s': ne[0] = %lld is not a multiple of the type's block %lld",
                   t.name.c_str(), (long long)t.ne[0], (long long)blk);
-      t.nbytes = n / blk * bytes;
+      GLYPR_CHECK(!__builtin_mul_overflow(n / blk, bytes, &t.nbytes), GLYPR_ERR_SHAPE,
+                  "tensor '%s': byte count overflows", t.name.c_str());
       GLYPR_CHECK(data0 <= g->size && t.offset <= g->size - data0 &&
                       (uint64_t)t.nbytes <= g->size - data0 - t.offset,
                   GLYPR_ERR_SHAPE, "tensor '%s' runs past the end of the file",
@@ -260,8 +302,36 @@ const GgufValue* find_kv(const glypr_gguf* g, const char* key) {
 
 extern "C" {
 
+static int gguf_open_impl(const char* path, glypr_gguf** out);
+static int model_load_gguf_impl(glypr_hip_ctx* ctx, const char* path, glypr_model** out);
+
+// std::bad_alloc (metadata strings, maps) and any other exception end as a
+// status here: none may cross the C ABI.
 int glypr_gguf_open(const char* path, glypr_gguf** out) {
   clear_error();
+  try {
+    return gguf_open_impl(path, out);
+  } catch (const std::bad_alloc&) {
+    return set_error(GLYPR_ERR_OOM, "host allocation failed while parsing the GGUF file");
+  } catch (...) {
+    return set_error(GLYPR_ERR_SHAPE, "GGUF parse failed");
+  }
+}
+
+int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model** out) {
+  clear_error();
+  try {
+    return model_load_gguf_impl(ctx, path, out);
+  } catch (const std::bad_alloc&) {
+    return set_error(GLYPR_ERR_OOM, "host allocation failed while loading the model");
+  } catch (...) {
+    return set_error(GLYPR_ERR_SHAPE, "model load failed");
+  }
+}
+
+}  // extern "C"
+
+static int gguf_open_impl(const char* path, glypr_gguf** out) {
   GLYPR_CHECK(path != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "path or out is NULL");
   *out = nullptr;
   const int fd = open(path, O_RDONLY);
@@ -281,7 +351,14 @@ int glypr_gguf_open(const char* path, glypr_gguf** out) {
   }
   g->map = map;
   g->size = (size_t)st.st_size;
-  const int rc = parse(g);
+  int rc;
+  try {
+    rc = parse(g);
+  } catch (...) {
+    munmap(g->map, g->size);
+    delete g;
+    throw;
+  }
   if (rc != GLYPR_OK) {
     munmap(g->map, g->size);
     delete g;
@@ -290,6 +367,8 @@ int glypr_gguf_open(const char* path, glypr_gguf** out) {
   *out = g;
   return GLYPR_OK;
 }
+
+extern "C" {
 
 int glypr_gguf_close(glypr_gguf* g) {
   clear_error();
@@ -375,7 +454,7 @@ int glypr_gguf_get_array(const glypr_gguf* g, const char* key, int* elem_type, i
   GLYPR_CHECK(v != nullptr, GLYPR_ERR_NOT_FOUND, "no metadata key '%s'", key);
   GLYPR_CHECK(v->type == T_ARR, GLYPR_ERR_UNSUPPORTED, "'%s' is not an array", key);
   *elem_type = (int)v->arr_type;
-  *len = (int64_t)v->arr.size();
+  *len = (int64_t)v->arr_len;
   return GLYPR_OK;
 }
 
@@ -385,18 +464,19 @@ int glypr_gguf_get_array_u64(const glypr_gguf* g, const char* key, int64_t i, ui
   const GgufValue* v = find_kv(g, key);
   GLYPR_CHECK(v != nullptr, GLYPR_ERR_NOT_FOUND, "no metadata key '%s'", key);
   GLYPR_CHECK(v->type == T_ARR, GLYPR_ERR_UNSUPPORTED, "'%s' is not an array", key);
-  GLYPR_CHECK(i >= 0 && i < (int64_t)v->arr.size(), GLYPR_ERR_RANGE,
+  GLYPR_CHECK(i >= 0 && (uint64_t)i < v->arr_len, GLYPR_ERR_RANGE,
               "index %lld out of range for '%s'", (long long)i, key);
-  GLYPR_CHECK(as_u64(v->arr[(size_t)i], out), GLYPR_ERR_UNSUPPORTED,
+  GgufValue e;
+  GLYPR_CHECK(array_elem(*v, (uint64_t)i, &e) && as_u64(e, out), GLYPR_ERR_UNSUPPORTED,
               "'%s'[%lld] is not a non-negative integer", key, (long long)i);
   return GLYPR_OK;
 }
 
 // EmbeddingGemma2Model::from_gguf_content (model.rs:244-488) with the config of
-// TextConfig::from_gguf_metadata (config.rs:79-189), minus the Per-Layer
-// Embedding block, for the uniform-head layout this backend runs.
-int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model** out) {
-  clear_error();
+// TextConfig::from_gguf_metadata (config.rs:79-189): per-layer head dims and kv
+// heads as get_head_dim / get_num_kv_heads give them, the Per-Layer-Embedding
+// block and the embedding projection when the file has their tensors.
+static int model_load_gguf_impl(glypr_hip_ctx* ctx, const char* path, glypr_model** out) {
   GLYPR_CHECK(path != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG, "path or out is NULL");
   *out = nullptr;
   RET_IF(check_ctx(ctx));
@@ -428,18 +508,16 @@ int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model*
   RET_IF(req_u("feed_forward_length", &ffn));
   RET_IF(req_u("attention.head_count", &heads));
   const uint64_t head_dim = opt_u("attention.key_length_swa", 256);
-  const uint64_t full_head_dim = opt_u("attention.key_length", 512);
-  // head_count_kv: an array per layer in EmbeddingGemma-2 files (the first
-  // entry is the sliding layers' value, config.rs:150-157), or a scalar
-  uint64_t kv_heads = 2;
+  const uint64_t full_head_dim = opt_u("attention.key_length", 512);   // config.rs:149-150
+  // head_count_kv (config.rs:142-168): only an array counts.  Its first entry
+  // is every sliding layer's value (2 without one); a full layer i takes entry
+  // i (1 without one).  A scalar is ignored, as in the reference.
   int et;
   int64_t kv_len = 0;
   const std::string kvk = key("attention.head_count_kv");
-  if (glypr_gguf_get_array(g, kvk.c_str(), &et, &kv_len) == GLYPR_OK) {
-    if (kv_len > 0) RET_IF(glypr_gguf_get_array_u64(g, kvk.c_str(), 0, &kv_heads));
-  } else {
-    kv_heads = opt_u("attention.head_count_kv", 2);
-  }
+  const bool kv_arr = glypr_gguf_get_array(g, kvk.c_str(), &et, &kv_len) == GLYPR_OK;
+  uint64_t kv_heads = 2;
+  if (kv_arr && kv_len > 0) RET_IF(glypr_gguf_get_array_u64(g, kvk.c_str(), 0, &kv_heads));
   clear_error();
 
   // layer pattern: the backend runs the default 5 sliding + 1 full layout
@@ -447,10 +525,9 @@ int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model*
   const std::string patk = key("attention.sliding_window_pattern");
   const bool has_pat = glypr_gguf_get_array(g, patk.c_str(), &et, &pat_len) == GLYPR_OK;
   clear_error();
-  bool any_full = false;
+  uint64_t full_kv = 0;   // the full layers' kv heads (0: no full layer)
   for (uint64_t i = 0; i < layers; i++) {
     const bool full = (i + 1) % 6 == 0;
-    any_full = any_full || full;
     if (has_pat) {
       uint64_t sliding = 0;
       GLYPR_CHECK((int64_t)i < pat_len &&
@@ -460,31 +537,30 @@ int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model*
                   "layer %llu: only the 5-sliding / 1-full layer pattern is supported",
                   (unsigned long long)i);
     }
-    if (full && kv_len > (int64_t)i) {
-      uint64_t kvi = 0;
-      RET_IF(glypr_gguf_get_array_u64(g, kvk.c_str(), (int64_t)i, &kvi));
-      GLYPR_CHECK(kvi == kv_heads, GLYPR_ERR_UNSUPPORTED,
-                  "layer %llu has %llu kv heads, the sliding layers %llu (per-layer kv heads "
-                  "are not supported)", (unsigned long long)i, (unsigned long long)kvi,
-                  (unsigned long long)kv_heads);
-    }
+    if (!full) continue;
+    uint64_t kvi = 1;
+    if (kv_arr && kv_len > (int64_t)i) RET_IF(glypr_gguf_get_array_u64(g, kvk.c_str(), (int64_t)i, &kvi));
+    GLYPR_CHECK(full_kv == 0 || kvi == full_kv, GLYPR_ERR_UNSUPPORTED,
+                "full-attention layers with differing kv heads (%llu and %llu) are not "
+                "supported", (unsigned long long)full_kv, (unsigned long long)kvi);
+    full_kv = kvi;
   }
-  GLYPR_CHECK(!any_full || full_head_dim == head_dim ||
-                  find_kv(g, key("attention.key_length").c_str()) == nullptr,
-              GLYPR_ERR_UNSUPPORTED,
-              "full-attention layers use head_dim %llu, sliding ones %llu (only a uniform "
-              "head_dim is supported)", (unsigned long long)full_head_dim,
-              (unsigned long long)head_dim);
+  GLYPR_CHECK(kv_heads > 0 && kv_heads < (1u << 20) && full_kv < (1u << 20) &&
+                  head_dim > 0 && head_dim < (1u << 20) && full_head_dim < (1u << 20),
+              GLYPR_ERR_SHAPE, "attention geometry in the metadata is corrupt");
 
   int64_t ti;
   RET_IF(glypr_gguf_find_tensor(g, "token_embd.weight", &ti));
   const GgufTensor& emb = g->tensors[(size_t)ti];
-  glypr_model_config cfg;
+  glypr_model_config cfg{};
   cfg.hidden = (int64_t)hidden;
   cfg.ffn = (int64_t)ffn;
   cfg.n_heads = (int64_t)heads;
   cfg.n_kv_heads = (int64_t)kv_heads;
   cfg.head_dim = (int64_t)head_dim;
+  cfg.full_head_dim = full_kv ? (int64_t)full_head_dim : 0;
+  cfg.full_n_kv_heads = (int64_t)full_kv;
+  cfg.max_seq_len = 0;   // DEFAULT_MAX_SEQ_LEN
   cfg.n_layers = (int64_t)layers;
   cfg.vocab = emb.ne[1];
   cfg.sliding_window = 512;   // config.rs:191
@@ -508,6 +584,12 @@ int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model*
 
   glypr_model* m = nullptr;
   RET_IF(glypr_hip_model_create(ctx, &cfg, &m));
+  struct Dropper {   // frees the model if a load step throws
+    glypr_model** m;
+    ~Dropper() {
+      if (*m) glypr_hip_model_destroy(*m);
+    }
+  } dropper{&m};
   auto load = [&](const std::string& name) -> int {
     int64_t idx;
     RET_IF(glypr_gguf_find_tensor(g, name.c_str(), &idx));
@@ -543,9 +625,11 @@ int glypr_hip_model_load_gguf(glypr_hip_ctx* ctx, const char* path, glypr_model*
   if (rc != GLYPR_OK) {
     std::string msg = glypr_hip_last_error();
     glypr_hip_model_destroy(m);
+    m = nullptr;
     return set_error(rc, "%s", msg.c_str());
   }
   *out = m;
+  m = nullptr;
   return GLYPR_OK;
 }
 

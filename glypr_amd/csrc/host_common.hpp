@@ -23,6 +23,12 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
     if (!(cond)) return set_error(code, __VA_ARGS__);    \
   } while (0)
 
+#define RET_IF(x)              \
+  do {                         \
+    int rc_ = (x);             \
+    if (rc_ != GLYPR_OK) return rc_; \
+  } while (0)
+
 // Make ctx->device current for the duration of a call.
 struct DeviceScope {
   int prev = -1;
@@ -56,6 +62,29 @@ inline int ensure_ws(glypr_hip_ctx* ctx, size_t bytes) {
   GLYPR_TRY_HIP(hipMalloc(&ctx->ws, cap), "workspace: hipMalloc");
   ctx->ws_cap = cap;
   return GLYPR_OK;
+}
+
+inline size_t q8_act_bytes(int64_t m, int64_t k);
+
+// Workspace that any entry point needs for `rows` rows of a weight with in_dim
+// k: two activation operands (the MLP's x and h; each the larger of the Q8_0
+// planar form and the bf16 form) of up to k columns.
+inline size_t ws_bytes_for(int64_t rows, int64_t k) {
+  const size_t q8 = q8_act_bytes(rows, k);
+  const size_t bf = align_up((size_t)(rows * k) * 2, 256);
+  return 2 * (q8 > bf ? q8 : bf);
+}
+
+// A weight with in_dim k was created: size the workspace for it at the
+// context's reserve rows, so calls within the reserve allocate nothing.
+template <typename T>
+inline int ensure_staging(T*& ptr, size_t& cap, size_t count);
+
+inline int reserve_for_weight(glypr_hip_ctx* ctx, int64_t k) {
+  if (k > ctx->max_k) ctx->max_k = k;
+  RET_IF(ensure_staging(ctx->ids, ctx->ids_cap, (size_t)ctx->reserve_rows));
+  RET_IF(ensure_staging(ctx->mask, ctx->mask_cap, (size_t)ctx->reserve_rows));
+  return ensure_ws(ctx, ws_bytes_for(ctx->reserve_rows, ctx->max_k));
 }
 
 template <typename T>
@@ -108,11 +137,6 @@ inline int check_variant(int variant) {
   return GLYPR_OK;
 }
 
-#define RET_IF(x)              \
-  do {                         \
-    int rc_ = (x);             \
-    if (rc_ != GLYPR_OK) return rc_; \
-  } while (0)
 
 inline hipEvent_t get_event(glypr_hip_ctx* ctx) {
   if (!ctx->event_pool.empty()) {

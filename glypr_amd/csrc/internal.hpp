@@ -5,6 +5,8 @@
 #include <stdint.h>
 
 #include <atomic>
+#include <map>
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -55,9 +57,16 @@ struct glypr_hip_ctx {
   size_t ids_cap = 0;
   uint8_t* mask = nullptr;  // pooling-mask staging
   size_t mask_cap = 0;
-  float* bcos = nullptr;    // binary-cosine table cos(pi * h / dim), h = 0 .. dim
-  size_t bcos_cap = 0;
-  int64_t bcos_dim = -1;    // dim the table holds (-1: none)
+  // Binary-cosine tables cos(pi * h / dim), h = 0 .. dim, one per dim, never
+  // rewritten: the host copy stays alive until the stream-ordered upload has
+  // read it, and a kernel queued earlier never sees its table change.
+  struct CosTable {
+    float* dev = nullptr;
+    std::vector<float> host;
+  };
+  std::map<int64_t, CosTable> bcos;
+  int64_t reserve_rows = 8320;  // rows the workspace is sized for (lib.rs:47)
+  int64_t max_k = 0;            // largest in_dim of a weight created on the context
 };
 
 namespace glypr {
@@ -116,7 +125,10 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
                            int64_t hd, const float* qnw, const float* knw, float eps,
                            const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
                            uint16_t* vt16, hipStream_t s);
-size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t window);
+size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window);
+// Whether launch_attention runs this geometry: head_dim 256, nq / nkv in
+// 1..4, at most 64 key partitions at T (T <= 0: any length).
+bool attention_supported(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window);
 // ctx (f32 [T][nq*hd]), (cq, dc) (Q8_0 planar) and cb (bf16 [T][nq*hd]) may
 // each be null.
 hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
@@ -125,6 +137,11 @@ hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint
                             hipStream_t s, uint16_t* cb = nullptr);
 
 // ---- k_gemm_i8.hip ----
+// Which INT8_EXACT kernel runs an [M x Nrows x K] GEMM (plain or GeGLU):
+// the LDS-ring small-M kernel, the 128 x 128 large-M kernel (both with 32-bit
+// operand offsets) or the register-staged kernel (int64 offsets, any shape).
+enum { GEMM_ROUTE_SMALL = 0, GEMM_ROUTE_BIG = 1, GEMM_ROUTE_REG128 = 2, GEMM_ROUTE_REG64 = 3 };
+int gemm_i8_route(int64_t M, int64_t Nrows, int64_t K);
 // y[m,n] = sum_b ((float)S_b * dw[n,b]) * dx[m,b], sequential over b (exact).
 hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                           float* y, int64_t M, int64_t N, int64_t K, int64_t ldc,
@@ -140,7 +157,7 @@ hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t*
 // nullable), bit-identical to launch_quantize_planar / launch_rmsnorm_quant
 // followed by launch_gemm_i8.  gemm_i8_pro_ok says where it is the faster
 // route (small M).
-bool gemm_i8_pro_ok(int64_t M, int64_t K, bool norm);
+bool gemm_i8_pro_ok(int64_t M, int64_t N, int64_t K, bool norm);
 hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
                               const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
                               int64_t K, int64_t ldc, hipStream_t s);

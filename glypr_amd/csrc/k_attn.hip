@@ -540,11 +540,19 @@ static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, 
   return (int)per;
 }
 
-size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t window) {
+bool attention_supported(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window) {
+  if (hd != QKV_HD || nq <= 0 || nkv <= 0 || nq % nkv != 0 || nq / nkv > 4) return false;
+  if (T <= 0) return true;
+  int kparts;
+  attn_kb_per_part(T, nq, nkv, window, &kparts);
+  return kparts <= 64;   // the combine holds one partition per lane
+}
+
+size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window) {
   int kp;
   attn_kb_per_part(T, nq, nkv, window, &kp);
   const int64_t tp = attn_padded_len(T);
-  return (size_t)(kp * tp * nq * (QKV_HD + 2));
+  return (size_t)(kp * tp * nq * (hd + 2));
 }
 
 hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,

@@ -536,11 +536,13 @@ hipError_t run_small(const int8_t* xq, const float* dx, const int8_t* wq, const 
 }
 
 // Small-M kernels stream K through an LDS ring; the scales of the whole K
-// range stay in LDS ((BM + BN) * K/32 floats).
+// range stay in LDS ((BM + BN) * K/32 floats).  Their DMA offsets into the
+// weight (row * K) are 32-bit: larger weights take the int64-offset kernel.
 constexpr int64_t SMALL_M_MAX = 2048;
 constexpr int64_t SMALL_K_MAX = 32 * SMALL_NB_MAX;
-inline bool small_ok(int64_t M, int64_t K) {
-  return M <= SMALL_M_MAX && K <= SMALL_K_MAX && K % BK == 0;
+inline bool small_ok(int64_t M, int64_t Nrows, int64_t K) {
+  return M <= SMALL_M_MAX && K <= SMALL_K_MAX && K % BK == 0 &&
+         Nrows * K < (int64_t(1) << 31);
 }
 
 // ---------------------------------------------------------------------------
@@ -1053,32 +1055,40 @@ hipError_t run(const int8_t* xq,const float* dx, const int8_t* wq, const float* 
 
 }  // namespace
 
+int gemm_i8_route(int64_t M, int64_t Nrows, int64_t K) {
+  if (small_ok(M, Nrows, K)) return GEMM_ROUTE_SMALL;
+  if (big_ok(M, Nrows, K)) return GEMM_ROUTE_BIG;
+  return ((M + 127) / 128) * ((Nrows + 127) / 128) >= 512 ? GEMM_ROUTE_REG128 : GEMM_ROUTE_REG64;
+}
+
 hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                           float* y, int64_t M, int64_t N, int64_t K, int64_t ldc,
                           hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (small_ok(M, K))
-    return run_small<1, 2, 1, false, 3>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
-  if (big_ok(M, N, K))
-    return run_big<false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
-  int64_t big_tiles = ((M + 127) / 128) * ((N + 127) / 128);
-  if (big_tiles >= 512)
-    return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
-  return run<64, 64, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+  switch (gemm_i8_route(M, N, K)) {
+    case GEMM_ROUTE_SMALL:
+      return run_small<1, 2, 1, false, 3>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+    case GEMM_ROUTE_BIG:
+      return run_big<false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+    case GEMM_ROUTE_REG128:
+      return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+    default:
+      return run<64, 64, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+  }
 }
 
 // The prologue is repeated by every workgroup along N, so fusing pays only
 // while the saved launch outweighs that repetition (measured on MI355X at
 // EmbeddingGemma widths: quantize up to M = 1024, RMSNorm up to M = 256).
-bool gemm_i8_pro_ok(int64_t M, int64_t K, bool norm) {
-  return small_ok(M, K) && M <= (norm ? 256 : 1024);
+bool gemm_i8_pro_ok(int64_t M, int64_t N, int64_t K, bool norm) {
+  return small_ok(M, N, K) && M <= (norm ? 256 : 1024);
 }
 
 hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
                               const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
                               int64_t K, int64_t ldc, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (!small_ok(M, K)) return hipErrorInvalidValue;
+  if (!small_ok(M, N, K)) return hipErrorInvalidValue;
   if (norm) return run_pro<PRO_NORM, 4, 2, 3>(x, nw, eps, wq, dw, y, M, N, K, ldc, s);
   return run_pro<PRO_QUANT, 4, 2, 3>(x, nullptr, 0.0f, wq, dw, y, M, N, K, ldc, s);
 }
@@ -1087,14 +1097,16 @@ hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t*
                                 const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
                                 int64_t K, hipStream_t s) {
   if (M == 0 || F == 0) return hipSuccess;
-  if (small_ok(M, K))
-    return run_small<2, 2, 2, true, 3>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
-  if (big_ok(M, 2 * F, K))
-    return run_big<true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
-  int64_t big_tiles = ((M + 127) / 128) * ((2 * F + 127) / 128);
-  if (big_tiles >= 512)
-    return run<128, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
-  return run<64, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+  switch (gemm_i8_route(M, 2 * F, K)) {
+    case GEMM_ROUTE_SMALL:
+      return run_small<2, 2, 2, true, 3>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+    case GEMM_ROUTE_BIG:
+      return run_big<true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+    case GEMM_ROUTE_REG128:
+      return run<128, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+    default:
+      return run<64, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+  }
 }
 
 }  // namespace glypr

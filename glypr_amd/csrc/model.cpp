@@ -98,6 +98,9 @@ struct EncoderLayer {
       post_feedforward_layernorm;
   PLEBlock ple_block;
   bool full_attention = false;
+  // the layer's attention geometry (TextConfig::get_head_dim /
+  // get_num_kv_heads, config.rs:142-169)
+  int64_t head_dim = 0, n_kv_heads = 0;
 };
 
 }  // namespace host
@@ -117,7 +120,8 @@ struct glypr_model {
   LinearOp embedding_projection;  // output.weight
   bool finalized = false;
   bool dense = false;  // projections are dense bf16 weights (activations run in bf16)
-  // RoPE tables [rope_cap][head_dim] for the sliding and full layer types.
+  // RoPE tables [max_seq_len][head_dim] of the sliding and full layer types
+  // (rope_sliding / rope_full, model.rs:278-279).
   DevBuf cos_s, sin_s, cos_f, sin_f;
   int64_t rope_cap = 0;
   // activations
@@ -157,20 +161,20 @@ int upload_f32(const float* host, int64_t n, float** dev) {
 
 int ensure_rope(glypr_model* m, int64_t t) {
   if (t <= m->rope_cap) return GLYPR_OK;
-  const int64_t cap = t > 8320 ? t : 8320;  // DEFAULT_MAX_SEQ_LEN, lib.rs:47
-  const int64_t hd = m->cfg.head_dim;
+  const int64_t cap = t;
   std::vector<float> c, s;
-  const size_t bytes = (size_t)(cap * hd) * sizeof(float);
-  RET_IF(m->cos_s.ensure(bytes));
-  RET_IF(m->sin_s.ensure(bytes));
-  RET_IF(m->cos_f.ensure(bytes));
-  RET_IF(m->sin_f.ensure(bytes));
-  rope_table(hd, m->cfg.rope_theta_sliding, cap, c, s);
-  GLYPR_TRY_HIP(hipMemcpy(m->cos_s.p, c.data(), bytes, hipMemcpyHostToDevice), "rope upload");
-  GLYPR_TRY_HIP(hipMemcpy(m->sin_s.p, s.data(), bytes, hipMemcpyHostToDevice), "rope upload");
-  rope_table(hd, m->cfg.rope_theta_full, cap, c, s);
-  GLYPR_TRY_HIP(hipMemcpy(m->cos_f.p, c.data(), bytes, hipMemcpyHostToDevice), "rope upload");
-  GLYPR_TRY_HIP(hipMemcpy(m->sin_f.p, s.data(), bytes, hipMemcpyHostToDevice), "rope upload");
+  const int64_t hds = m->cfg.head_dim, hdf = m->cfg.full_head_dim;
+  const size_t bs = (size_t)(cap * hds) * sizeof(float), bf = (size_t)(cap * hdf) * sizeof(float);
+  RET_IF(m->cos_s.ensure(bs));
+  RET_IF(m->sin_s.ensure(bs));
+  RET_IF(m->cos_f.ensure(bf));
+  RET_IF(m->sin_f.ensure(bf));
+  rope_table(hds, m->cfg.rope_theta_sliding, cap, c, s);
+  GLYPR_TRY_HIP(hipMemcpy(m->cos_s.p, c.data(), bs, hipMemcpyHostToDevice), "rope upload");
+  GLYPR_TRY_HIP(hipMemcpy(m->sin_s.p, s.data(), bs, hipMemcpyHostToDevice), "rope upload");
+  rope_table(hdf, m->cfg.rope_theta_full, cap, c, s);
+  GLYPR_TRY_HIP(hipMemcpy(m->cos_f.p, c.data(), bf, hipMemcpyHostToDevice), "rope upload");
+  GLYPR_TRY_HIP(hipMemcpy(m->sin_f.p, s.data(), bf, hipMemcpyHostToDevice), "rope upload");
   m->rope_cap = cap;
   return GLYPR_OK;
 }
@@ -179,18 +183,26 @@ int ensure_activations(glypr_model* m, int64_t t) {
   if (t <= m->cap_t) return GLYPR_OK;
   const glypr_model_config& c = m->cfg;
   const int64_t tp = attn_padded_len(t);
-  const int64_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
+  // the widest attention geometry over the layers
+  int64_t qd = 0, kvd = 0, qkvd = 0;
+  size_t sc = 0;
+  for (const EncoderLayer& L : m->layers) {
+    const int64_t lq = c.n_heads * L.head_dim, lkv = L.n_kv_heads * L.head_dim;
+    qd = lq > qd ? lq : qd;
+    kvd = lkv > kvd ? lkv : kvd;
+    qkvd = lq + 2 * lkv > qkvd ? lq + 2 * lkv : qkvd;
+    const size_t s1 = attention_scratch_floats(t, c.n_heads, L.n_kv_heads, L.head_dim,
+                                               L.full_attention ? 0 : c.sliding_window);
+    sc = s1 > sc ? s1 : sc;
+  }
   const int64_t wide = c.hidden > qd ? c.hidden : qd;
   RET_IF(m->h.ensure((size_t)(t * c.hidden) * 4));
   RET_IF(m->xq.ensure((size_t)(t * wide)));
   RET_IF(m->dx.ensure((size_t)(t * (wide / 32)) * 4));
-  RET_IF(m->qkv.ensure((size_t)(t * (qd + 2 * kvd)) * 4));
+  RET_IF(m->qkv.ensure((size_t)(t * qkvd) * 4));
   RET_IF(m->attn_q.ensure((size_t)(tp * qd) * 2));
   RET_IF(m->attn_k.ensure((size_t)(tp * kvd) * 2));
   RET_IF(m->attn_vt.ensure((size_t)(tp * kvd) * 2));
-  size_t sc = attention_scratch_floats(t, c.n_heads, c.n_kv_heads, 0);
-  const size_t sc2 = attention_scratch_floats(t, c.n_heads, c.n_kv_heads, c.sliding_window);
-  if (sc2 > sc) sc = sc2;
   RET_IF(m->attn_scratch.ensure(sc * 4));
   RET_IF(m->cq.ensure((size_t)(t * qd)));
   RET_IF(m->dc.ensure((size_t)(t * (qd / 32)) * 4));
@@ -316,8 +328,7 @@ int attention_core(glypr_hip_ctx* ctx, const float* qkv, const float* qnw, const
 int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, int64_t t, int64_t trunc, float* out,
                   float* hidden, hipStream_t s) {
   const glypr_model_config& c = m->cfg;
-  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
-  const int64_t qd = nq * hd;
+  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads;
   float* h = dev_f32(m->h);
   uint16_t* xb = m->xb.as<uint16_t>();
   uint16_t* hb = m->hb.as<uint16_t>();
@@ -327,6 +338,7 @@ int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, int64_t t, int64_t trunc, 
   for (size_t li = 0; li < m->layers.size(); li++) {
     EncoderLayer& L = m->layers[li];
     const bool last = li + 1 == m->layers.size();
+    const int64_t hd = L.head_dim, nkv = L.n_kv_heads, qd = nq * hd;
     const glypr_bf16w* wqkv = L.self_attn.fused_qkv.wb;
     LAUNCH(GLYPR_K_GEMM_BF16W, s,
            launch_gemm_bf16w(xb, wqkv->p, dev_f32(m->qkv), t, wqkv->n, H, wqkv->n, s),
@@ -378,11 +390,14 @@ int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_nor
   clear_error();
   GLYPR_CHECK(t >= 0 && n_heads > 0 && n_kv_heads > 0 && window >= 0, GLYPR_ERR_SHAPE,
               "invalid attention shape");
-  GLYPR_CHECK(head_dim == 256, GLYPR_ERR_UNSUPPORTED, "head_dim %lld (only 256 is supported)",
-              (long long)head_dim);
   GLYPR_CHECK(n_heads % n_kv_heads == 0, GLYPR_ERR_SHAPE,
               "n_heads %lld not a multiple of n_kv_heads %lld", (long long)n_heads,
               (long long)n_kv_heads);
+  GLYPR_CHECK(attention_supported(t, n_heads, n_kv_heads, head_dim, window),
+              GLYPR_ERR_UNSUPPORTED,
+              "attention geometry not supported: head_dim %lld (256 is supported), %lld q "
+              "heads per kv head (at most 4), t = %lld", (long long)head_dim,
+              (long long)(n_heads / n_kv_heads), (long long)t);
   GLYPR_CHECK(t == 0 || (qkv && cos_table && sin_table && ctx_out), GLYPR_ERR_INVALID_ARG,
               "qkv, cos/sin tables or ctx_out is NULL");
   GLYPR_CHECK(aligned16(qkv) && aligned16(ctx_out) && aligned16(cos_table) &&
@@ -396,7 +411,7 @@ int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_nor
   const int64_t tp = attn_padded_len(t);
   const size_t qb = align_up((size_t)(tp * n_heads * head_dim) * 2, 256);
   const size_t kb = align_up((size_t)(tp * n_kv_heads * head_dim) * 2, 256);
-  const size_t sb = attention_scratch_floats(t, n_heads, n_kv_heads, window) * 4;
+  const size_t sb = attention_scratch_floats(t, n_heads, n_kv_heads, head_dim, window) * 4;
   RET_IF(ensure_ws(ctx, qb + 2 * kb + sb));
   char* base = (char*)ctx->ws;
   uint16_t* q16 = (uint16_t*)base;
@@ -417,21 +432,44 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
               GLYPR_ERR_SHAPE, "model dimensions must be positive");
   GLYPR_CHECK(cfg->hidden % 32 == 0 && cfg->ffn % 32 == 0 && cfg->hidden <= 1024, GLYPR_ERR_SHAPE,
               "hidden (<= 1024) and ffn must be multiples of 32");
-  GLYPR_CHECK(cfg->head_dim == 256, GLYPR_ERR_UNSUPPORTED, "head_dim %lld (only 256)",
-              (long long)cfg->head_dim);
+  GLYPR_CHECK(cfg->head_dim > 0 && cfg->full_head_dim >= 0 && cfg->full_n_kv_heads >= 0 &&
+                  cfg->max_seq_len >= 0 && cfg->sliding_window >= 0,
+              GLYPR_ERR_SHAPE, "head_dim must be positive; full_head_dim, full_n_kv_heads, "
+              "max_seq_len and sliding_window non-negative");
   GLYPR_CHECK(cfg->n_heads > 0 && cfg->n_kv_heads > 0 && cfg->n_heads % cfg->n_kv_heads == 0,
               GLYPR_ERR_SHAPE, "n_heads must be a positive multiple of n_kv_heads");
+  GLYPR_CHECK(cfg->full_n_kv_heads == 0 || cfg->n_heads % cfg->full_n_kv_heads == 0,
+              GLYPR_ERR_SHAPE, "n_heads must be a multiple of full_n_kv_heads");
   GLYPR_CHECK(cfg->ple_dim >= 0 && cfg->ple_dim % 32 == 0 && cfg->out_dim >= 0, GLYPR_ERR_SHAPE,
               "ple_dim (%lld) must be a non-negative multiple of 32, out_dim (%lld) >= 0",
               (long long)cfg->ple_dim, (long long)cfg->out_dim);
+  glypr_model_config c = *cfg;
+  if (c.full_head_dim == 0) c.full_head_dim = c.head_dim;
+  if (c.full_n_kv_heads == 0) c.full_n_kv_heads = c.n_kv_heads;
+  if (c.max_seq_len == 0) c.max_seq_len = 8320;   // DEFAULT_MAX_SEQ_LEN, lib.rs:47
+  // the attention kernels' geometry, checked for both layer types at the
+  // longest sequence (shorter ones use fewer key partitions)
+  GLYPR_CHECK(attention_supported(c.max_seq_len, c.n_heads, c.n_kv_heads, c.head_dim,
+                                  c.sliding_window) &&
+                  attention_supported(c.max_seq_len, c.n_heads, c.full_n_kv_heads,
+                                      c.full_head_dim, 0),
+              GLYPR_ERR_UNSUPPORTED,
+              "attention geometry not supported: head_dim %lld / %lld (sliding / full; 256 is "
+              "supported), %lld q heads over %lld / %lld kv heads (at most 4 per kv head)",
+              (long long)c.head_dim, (long long)c.full_head_dim, (long long)c.n_heads,
+              (long long)c.n_kv_heads, (long long)c.full_n_kv_heads);
   RET_IF(check_ctx(ctx));
   glypr_model* m = new (std::nothrow) glypr_model();
   GLYPR_CHECK(m != nullptr, GLYPR_ERR_OOM, "host allocation failed");
   m->ctx = ctx;
-  m->cfg = *cfg;
-  m->layers.resize((size_t)cfg->n_layers);
-  for (int64_t i = 0; i < cfg->n_layers; i++)
-    m->layers[(size_t)i].full_attention = ((i + 1) % 6) == 0;  // config.rs:131-140
+  m->cfg = c;
+  m->layers.resize((size_t)c.n_layers);
+  for (int64_t i = 0; i < c.n_layers; i++) {
+    EncoderLayer& L = m->layers[(size_t)i];
+    L.full_attention = ((i + 1) % 6) == 0;  // config.rs:131-140
+    L.head_dim = L.full_attention ? c.full_head_dim : c.head_dim;
+    L.n_kv_heads = L.full_attention ? c.full_n_kv_heads : c.n_kv_heads;
+  }
   *out = m;
   return GLYPR_OK;
 }
@@ -448,7 +486,6 @@ int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* dat
   DeviceScope ds(m->ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   const std::string n(name);
-  const int64_t qd = c.n_heads * c.head_dim, kvd = c.n_kv_heads * c.head_dim;
 
   auto set_q8 = [&](LinearOp& op, int64_t er, int64_t ec) -> int {
     GLYPR_CHECK(dtype == 1, GLYPR_ERR_UNSUPPORTED, "%s must be Q8_0", name);
@@ -494,12 +531,13 @@ int glypr_hip_model_set_tensor(glypr_model* m, const char* name, const void* dat
       name[consumed] == '\0' && layer >= 0 && layer < c.n_layers) {
     EncoderLayer& L = m->layers[(size_t)layer];
     const std::string f(field);
+    const int64_t qd = c.n_heads * L.head_dim, kvd = L.n_kv_heads * L.head_dim;
     if (f == "attn_norm") return set_norm(L.input_layernorm, c.hidden);
     if (f == "post_attention_norm") return set_norm(L.post_attention_layernorm, c.hidden);
     if (f == "ffn_norm") return set_norm(L.pre_feedforward_layernorm, c.hidden);
     if (f == "post_ffw_norm") return set_norm(L.post_feedforward_layernorm, c.hidden);
-    if (f == "attn_q_norm") return set_norm(L.self_attn.q_norm, c.head_dim);
-    if (f == "attn_k_norm") return set_norm(L.self_attn.k_norm, c.head_dim);
+    if (f == "attn_q_norm") return set_norm(L.self_attn.q_norm, L.head_dim);
+    if (f == "attn_k_norm") return set_norm(L.self_attn.k_norm, L.head_dim);
     if (f == "attn_q") return set_lin(L.self_attn.q, qd, c.hidden);
     if (f == "attn_k") return set_lin(L.self_attn.k, kvd, c.hidden);
     if (f == "attn_v") return set_lin(L.self_attn.v, kvd, c.hidden);
@@ -572,6 +610,10 @@ int glypr_hip_model_finalize(glypr_model* m) {
     const glypr_q8w* gu[2] = {L.mlp.gate.w, L.mlp.up.w};
     RET_IF(glypr_hip_q8_0_weight_concat(m->ctx, gu, 2, &L.mlp.fused_gate_up.w, nullptr));
   }
+  // every buffer and table the forward uses, at max_seq_len: model_embed
+  // allocates nothing
+  RET_IF(ensure_rope(m, m->cfg.max_seq_len));
+  RET_IF(ensure_activations(m, m->cfg.max_seq_len));
   m->finalized = true;
   return GLYPR_OK;
 }
@@ -587,6 +629,10 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
   GLYPR_CHECK(aligned16(out) && aligned16(hidden), GLYPR_ERR_ALIGNMENT,
               "out and hidden must be 16-byte aligned");
   const glypr_model_config& c = m->cfg;
+  // the context-length preflight of encode_single_text (lib.rs:970-976)
+  GLYPR_CHECK(t <= c.max_seq_len, GLYPR_ERR_SHAPE,
+              "sequence length (%lld tokens) exceeds the maximum context limit (%lld tokens)",
+              (long long)t, (long long)c.max_seq_len);
   for (int64_t i = 0; i < t; i++)
     GLYPR_CHECK((int64_t)ids[i] < c.vocab, GLYPR_ERR_RANGE,
                 "token id %u at position %lld is out of range for vocab %lld", ids[i],
@@ -595,11 +641,9 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  RET_IF(ensure_rope(m, t));
-  RET_IF(ensure_activations(m, t));
+  // buffers and RoPE tables were sized for max_seq_len at finalize
   hipStream_t s = (hipStream_t)stream;
-  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads, nkv = c.n_kv_heads, hd = c.head_dim;
-  const int64_t qd = nq * hd;
+  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads;
   float* h = dev_f32(m->h);
   int8_t* xq = m->xq.as<int8_t>();
   float* dx = dev_f32(m->dx);
@@ -637,6 +681,7 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
   for (size_t li = 0; li < m->layers.size(); li++) {
     EncoderLayer& L = m->layers[li];
     const bool last = li + 1 == m->layers.size();
+    const int64_t hd = L.head_dim, nkv = L.n_kv_heads, qd = nq * hd;
     // ---- attention block (layer.rs:27-34)
     const glypr_q8w* wqkv = L.self_attn.fused_qkv.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,

@@ -45,6 +45,10 @@ class Context:
     def sync(self):
         check(lib().glypr_hip_sync(self.handle, self.stream))
 
+    def reserve(self, rows: int):
+        """glypr_hip_ctx_reserve: size the workspace for `rows` activation rows."""
+        check(lib().glypr_hip_ctx_reserve(self.handle, rows))
+
     def close(self):
         if self.handle:
             lib().glypr_hip_ctx_destroy(self.handle)
@@ -367,7 +371,9 @@ class ModelConfig(ctypes.Structure):
                 ("n_layers", ctypes.c_int64), ("vocab", ctypes.c_int64),
                 ("sliding_window", ctypes.c_int64), ("eps", ctypes.c_float),
                 ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double),
-                ("ple_dim", ctypes.c_int64), ("out_dim", ctypes.c_int64)]
+                ("ple_dim", ctypes.c_int64), ("out_dim", ctypes.c_int64),
+                ("full_head_dim", ctypes.c_int64), ("full_n_kv_heads", ctypes.c_int64),
+                ("max_seq_len", ctypes.c_int64)]
 
 
 class Gguf:
@@ -474,7 +480,8 @@ class Model:
     def __init__(self, ctx: Context, **cfg):
         defaults = dict(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256, n_layers=24,
                         vocab=262144, sliding_window=512, eps=1e-6, rope_theta_sliding=10000.0,
-                        rope_theta_full=1e6, ple_dim=0, out_dim=0)
+                        rope_theta_full=1e6, ple_dim=0, out_dim=0, full_head_dim=0,
+                        full_n_kv_heads=0, max_seq_len=0)
         defaults.update(cfg)
         self.cfg = defaults
         self.ctx = ctx

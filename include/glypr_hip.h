@@ -16,7 +16,14 @@
  *    f32 unless stated.  Q8_0 weights are library-owned opaque handles.
  *  - Launches are asynchronous on `stream` (a hipStream_t; NULL = the null
  *    stream).  A context's workspace is shared by its calls: calls on one
- *    context must be issued from one thread onto one stream at a time.
+ *    context must be issued from one thread, and all onto one stream (work
+ *    queued on a second stream could still read the workspace while a call on
+ *    the first one overwrites it).  Use one context per stream.
+ *  - Workspace: each weight created on a context sizes the context's activation
+ *    workspace for its in_dim at glypr_hip_ctx_reserve's row count (8320 =
+ *    glypr's DEFAULT_MAX_SEQ_LEN, lib.rs:47, until changed), so calls within
+ *    it allocate nothing and never synchronise.  A call with more rows grows the
+ *    workspace first (a device synchronisation, then hipFree / hipMalloc).
  *  - Q8_0 is the GGUF block format: 34 bytes = { f16 d; int8 qs[32] }, rows
  *    of K/32 blocks; K must be a multiple of 32.
  */
@@ -30,7 +37,7 @@
 extern "C" {
 #endif
 
-#define GLYPR_HIP_ABI_VERSION 4
+#define GLYPR_HIP_ABI_VERSION 5
 
 typedef enum glypr_status {
   GLYPR_OK = 0,
@@ -77,6 +84,12 @@ int glypr_hip_ctx_destroy(glypr_hip_ctx* ctx);
 /* Block until `stream` is idle: the read-back synchronisation of
  * encode_single_text (lib.rs:988-989). */
 int glypr_hip_sync(glypr_hip_ctx* ctx, glypr_stream stream);
+
+/* Row count the workspace is sized for (the max_seq_len of GlyprEmbedder,
+ * lib.rs:47, 267-274, times the batch a caller runs).  Grows the workspace
+ * now for the weights created so far; weights created later are sized for
+ * it too.  rows <= 0 -> GLYPR_ERR_SHAPE. */
+int glypr_hip_ctx_reserve(glypr_hip_ctx* ctx, int64_t rows);
 
 /* ---- Q8_0 weights (LinearOp load path) --------------------------------- */
 
@@ -241,7 +254,9 @@ int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_nor
 /* ---- text backbone (configs 4-5) ---------------------------------------- */
 
 /* EmbeddingGemma layer geometry (TextConfig, config.rs:76-213; BASELINE uses
- * hidden 768, ffn 1152, 3 q heads / 1 kv head, head_dim 256, 24 layers). */
+ * hidden 768, ffn 1152, 3 q heads / 1 kv head, head_dim 256, 24 layers; the
+ * released EmbeddingGemma-2 has hidden 512, ffn 2048, 4 q heads, sliding
+ * layers 2 kv heads of 256, full layers 1 kv head of 512). */
 typedef struct glypr_model_config {
   int64_t hidden;
   int64_t ffn;
@@ -258,6 +273,16 @@ typedef struct glypr_model_config {
                                 * 0 = no Per-Layer-Embedding block (configs 4-5) */
   int64_t out_dim;             /* rows of output.weight, the embedding projection
                                 * (model.rs:472-473, 577); 0 = none */
+  int64_t full_head_dim;       /* head_dim of the full-attention layers
+                                * (attention.key_length, config.rs:149-150,
+                                * 158-166); 0 = head_dim */
+  int64_t full_n_kv_heads;     /* kv heads of the full-attention layers
+                                * (head_count_kv[i], config.rs:151-157); 0 =
+                                * n_kv_heads */
+  int64_t max_seq_len;         /* longest sequence model_embed accepts
+                                * (GlyprEmbedder::max_seq_len, lib.rs:47, 425);
+                                * every activation buffer is sized for it at
+                                * finalize; 0 = 8320 */
 } glypr_model_config;
 
 typedef struct glypr_model glypr_model;

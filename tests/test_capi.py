@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_symbols():
         assert hasattr(L, name), name
-    assert L.glypr_hip_abi_version() == 4
+    assert L.glypr_hip_abi_version() == 5
 
 
 def _has_gpu():
@@ -161,3 +161,124 @@ def test_product_has_no_oracle_dependency():
             if f.endswith((".py", ".hip", ".cpp", ".hpp", ".h")):
                 text = open(os.path.join(root, f)).read()
                 assert "pyoracle" not in text and "liboracle" not in text, f
+
+
+def test_reserve_validation():
+    L = _lib.lib()
+    assert L.glypr_hip_ctx_reserve(NULL, 0) == _lib.GLYPR_ERR_SHAPE
+    assert L.glypr_hip_ctx_reserve(NULL, -5) == _lib.GLYPR_ERR_SHAPE
+    assert L.glypr_hip_ctx_reserve(NULL, 8320) == _lib.GLYPR_ERR_INVALID_ARG   # ctx NULL
+
+
+def _cfg(**kw):
+    from glypr_amd.ops import ModelConfig
+    base = dict(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256, n_layers=24,
+                vocab=262144, sliding_window=512, eps=1e-6, rope_theta_sliding=1e4,
+                rope_theta_full=1e6, ple_dim=0, out_dim=0, full_head_dim=0, full_n_kv_heads=0,
+                max_seq_len=0)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
+def test_attention_geometry_validation():
+    """Geometries the attention kernels do not run are refused before anything
+    is launched or allocated: more than 4 q heads per kv head, or head dims
+    other than 256."""
+    L = _lib.lib()
+    out = ctypes.c_void_p()
+    # the BASELINE geometry passes validation (then fails on the NULL ctx)
+    assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg()), ctypes.byref(out)) == \
+        _lib.GLYPR_ERR_INVALID_ARG
+    assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(n_heads=5, n_kv_heads=1)),
+                                    ctypes.byref(out)) == _lib.GLYPR_ERR_UNSUPPORTED
+    assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(n_heads=4, full_n_kv_heads=3)),
+                                    ctypes.byref(out)) == _lib.GLYPR_ERR_SHAPE
+    assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(head_dim=128)),
+                                    ctypes.byref(out)) == _lib.GLYPR_ERR_UNSUPPORTED
+    assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(max_seq_len=-1)),
+                                    ctypes.byref(out)) == _lib.GLYPR_ERR_SHAPE
+    # glypr_hip_attention: the same geometry rule, checked before the pointers
+    args = lambda nq, nkv, hd: (NULL, FAKE, FAKE, FAKE, 1e-6, FAKE, FAKE, 512, nq, nkv, hd, 0,
+                                FAKE, NULL)
+    assert L.glypr_hip_attention(*args(5, 1, 256)) == _lib.GLYPR_ERR_UNSUPPORTED
+    assert L.glypr_hip_attention(*args(3, 1, 128)) == _lib.GLYPR_ERR_UNSUPPORTED
+    assert L.glypr_hip_attention(*args(3, 2, 256)) == _lib.GLYPR_ERR_SHAPE
+    assert L.glypr_hip_attention(*args(4, 1, 256)) == _lib.GLYPR_ERR_INVALID_ARG   # ctx NULL
+
+
+def test_gemm_routing():
+    """The INT8_EXACT GEMM routes (k_gemm_i8.hip): the LDS-ring small-M kernel
+    and the 128 x 128 large-M kernel address operands with 32-bit offsets, so a
+    weight of 2^31 or more bytes (N * K) takes the int64-offset kernel."""
+    L = _lib.lib()
+    route = L.glypr_internal_gemm_i8_route
+    route.restype = ctypes.c_int
+    route.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int]
+    SMALL, BIG, REG128, REG64, PRO = 0, 1, 2, 3, 4
+    assert route(512, 1280, 768, 0) == SMALL           # C2 qkv
+    assert route(512, 2304, 768, 0) == SMALL           # C2 gate|up
+    assert route(2048, 768, 1152, 0) == SMALL
+    assert route(2049, 768, 1152, 0) == BIG
+    assert route(16384, 1280, 768, 0) == BIG           # C3
+    big_n = (1 << 31) // 1024                          # N * K = 2^31
+    assert route(512, big_n, 1024, 0) == REG128
+    assert route(512, big_n - 1, 1024, 0) == SMALL
+    assert route(4096, big_n, 1024, 0) == REG128
+    assert route(4096, big_n - 1, 1024, 0) == BIG
+    assert route(64, 64, 1024, 0) == SMALL
+    assert route(4096, 64, 96, 0) in (REG128, REG64)   # K % 128 != 0
+    # the fused prologue: quantize up to M = 1024, RMSNorm up to M = 256
+    assert route(1024, 768, 768, 1) == PRO and route(1025, 768, 768, 1) == -1
+    assert route(256, 1280, 768, 2) == PRO and route(257, 1280, 768, 2) == -1
+    assert route(256, big_n, 1024, 2) == -1
+
+
+# ---- the model-config struct: C header, ctypes mirror and the Rust binding ----
+
+_C_FIELDS = re.compile(r"^\s*(int64_t|float|double)\s+(\w+);", re.M)
+
+
+def _header_struct_fields():
+    text = open(HEADER).read()
+    body = text[text.index("typedef struct glypr_model_config {"):]
+    body = body[:body.index("} glypr_model_config;")]
+    return [(t, n) for t, n in _C_FIELDS.findall(body)]
+
+
+def test_model_config_layout_probe():
+    """sizeof / offsetof of glypr_model_config compiled by the C compiler
+    against include/glypr_hip.h equal the ctypes mirror (ops.ModelConfig)."""
+    import subprocess
+    import tempfile
+    from glypr_amd.ops import ModelConfig
+    fields = _header_struct_fields()
+    assert [n for _, n in fields] == [f[0] for f in ModelConfig._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "glypr_hip.h"',
+           "int main(void) {", 'printf("size %zu\\n", sizeof(glypr_model_config));']
+    for _, n in fields:
+        src.append(f'printf("{n} %zu %zu\\n", offsetof(glypr_model_config, {n}), '
+                   f'sizeof(((glypr_model_config*)0)->{n}));')
+    src.append("return 0; }")
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "probe.c")
+        open(c, "w").write("\n".join(src))
+        exe = os.path.join(d, "probe")
+        subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), c,
+                        "-o", exe], check=True)
+        out = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = dict((l.split()[0], tuple(int(v) for v in l.split()[1:])) for l in out if l)
+    assert got["size"] == (ctypes.sizeof(ModelConfig),)
+    for name, ctype in ModelConfig._fields_:
+        assert got[name] == (getattr(ModelConfig, name).offset, ctypes.sizeof(ctype)), name
+
+
+def test_integration_rust_struct_matches_header():
+    """The Rust #[repr(C)] glypr_model_config in INTEGRATION.md lists the C
+    struct's fields in order with matching types, so a Rust caller's struct is
+    exactly as large as the one glypr_hip_model_create reads."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    body = text[text.index("pub struct glypr_model_config {"):]
+    body = body[len("pub struct glypr_model_config {"):body.index("}")]
+    rust = re.findall(r"pub\s+(\w+)\s*:\s*(\w+)", body)
+    rmap = {"int64_t": "i64", "float": "f32", "double": "f64"}
+    assert [(n, t) for n, t in rust] == [(n, rmap[t]) for t, n in _header_struct_fields()]
