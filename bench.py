@@ -1,21 +1,26 @@
 """Benchmark of the MI355X Q8_0 hot path (one JSON line on stdout).
 
-Workload ("C2"): one EmbeddingGemma layer's quantized
-projections at T = 512, hidden 768 — RMSNorm(eps 1e-6) -> q/k/v (fused
-768->1280), o 768->768 on a fixed synthetic attention output, RMSNorm ->
-gate/up 768->2x1152 with the tanh-GeGLU epilogue -> down 1152->768.  A step is
-one pass of those 7 projections; value = algorithmic Q8_0 ops / step time.
+Headline workload ("C4", the "512-tok embeddings/sec"
+half of the metric): the 24-layer EmbeddingGemma text backbone (hidden 768,
+3 q heads / 1 kv head, head_dim 256, FFN 1152, Q8_0 projections run as
+INT8_EXACT) on one 512-token sequence, batch 1: Q8_0 gather of uniform-random
+ids from the 262144 x 768 table, 24 layers, final norm, mean pool, L2, MRL-256.
+A step is one embedding (glypr_hip_model_embed); value = embeddings/s.
 
-Also reported (in "extra"): configs[0] (C1, one 512x768x1152 linear) and
-configs[2] (C3, M = 16384 through the same 7 projections) for both variants,
-and the platform's own GEMM library (hipBLASLt through torch) timed on the C3
-projection shapes as plain bf16 and int8 GEMMs, for reference.
+Also reported (in "extra"): C2 (one layer's 7 projections at T = 512, the
+previous headline, with its own roofline), C1 (one 512 x 768 x 1152 linear),
+C3 (M = 16384 through the 7 projections, TOPS and % of MFMA peak, both
+variants, BF16_DEQUANT's per-row cosine to INT8_EXACT), C5 (T = 8192, Q8_0 and
+bf16 weights, GEMM vs attention split), the Q8_0 gather on its own at 1M ids,
+the output-vector codecs, and hipBLASLt on the C3 shapes for reference.
 
-    python bench.py [--steps K] [--warmup W] [--variant int8|bf16] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--extras LIST]
 
 Inputs are synthetic (seeded numpy), resident in HBM before the timed region.
-The roofline entry is measured live: the library brackets every kernel of the
-timed region with HIP events on its launch stream (glypr_hip_profile_*).
+The roofline entry is measured live: a second pass of the same steps runs with
+the library's per-kernel HIP events on the launch stream
+(glypr_hip_profile_*); the per-launch event cost, measured as the difference
+between that pass and the event-free timed pass, is subtracted.
 """
 from __future__ import annotations
 
@@ -418,7 +423,7 @@ def model_tensors(rng, n_layers, vocab, hidden=H, ffn=F, nq=3, nkv=1, hd=256, de
 
 def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1):
     """Embeddings/s of the full backbone for one t-token sequence (config 4/5), plus
-    the per-op split from a second, profiled pass."""
+    the per-op split from a second pass of the same steps with per-kernel events."""
     import torch
     from glypr_amd import _lib
     from glypr_amd.ops import Model
@@ -430,25 +435,35 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1):
     out = torch.empty(256, dtype=torch.float32, device="cuda")
     for _ in range(warmup):
         m.embed(ids, trunc=256, out=out)
-    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
+    torch.cuda.synchronize()
+    e0.record(stream)
     for _ in range(steps):
         m.embed(ids, trunc=256, out=out)
-    e1.record()
+    e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 1))
+    torch.cuda.synchronize()
+    e0.record(stream)
     for _ in range(steps):
         m.embed(ids, trunc=256, out=out)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_prof = e0.elapsed_time(e1) / steps
     tot = (ctypes.c_double * _lib.KERNEL_COUNT)()
     cnt = (ctypes.c_int64 * _lib.KERNEL_COUNT)()
     _lib.check(_lib.lib().glypr_hip_profile_read(ctx.handle, tot, cnt))
     _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 0))
-    split = {}
+    split, kern = {}, {}
     for i in range(_lib.KERNEL_COUNT):
         if cnt[i]:
-            split[_lib.lib().glypr_hip_kernel_name(i).decode()] = round(tot[i] / steps, 4)
+            name = _lib.lib().glypr_hip_kernel_name(i).decode()
+            split[name] = round(tot[i] / steps, 4)
+            kern[name] = {"ms_total": tot[i], "launches": int(cnt[i]),
+                          "us_per_launch": 1000.0 * tot[i] / cnt[i]}
+    launches = sum(v["launches"] for v in kern.values()) / steps
     gemm = sum(v for k, v in split.items() if k.startswith("gemm"))
     att = split.get("attention", 0.0) + split.get("qkv_post", 0.0)
     m.close()
@@ -456,7 +471,116 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1):
             "tokens_per_s": round(t * 1000.0 / ms, 1),
             "gemm_ops_per_embedding": 2 * t * n_layers * LAYER_NK,
             "gemm_tops": round(2 * t * n_layers * LAYER_NK / (ms / 1e3) / 1e12, 2),
-            "split_ms_profiled": split, "gemm_ms": round(gemm, 4), "attention_ms": round(att, 4)}
+            "split_ms_profiled": split, "gemm_ms": round(gemm, 4), "attention_ms": round(att, 4),
+            "launches_per_embedding": int(round(launches)),
+            "event_cost_us_per_launch": round(1000.0 * (ms_prof - ms) / max(1.0, launches), 3),
+            "_kernels": kern, "_steps": steps}
+
+
+# Projections of one backbone layer as the model driver launches them (all
+# INT8_EXACT, Q8_0 operands from the fused prologues): (kernel, N, K).
+MODEL_GEMMS = [("gemm_i8", NQ + 2 * NKV, H), ("gemm_i8", H, NQ), ("gemm_i8_geglu", 2 * F, H),
+               ("gemm_i8", H, F)]
+
+
+def model_kernel_work(kernel, t, n_layers=24, window=512, nq=3, hd=256):
+    """Algorithmic work of every launch of `kernel` in one backbone embedding:
+    (bound, amount per embedding, unit).  GEMMs and norms are HBM-bound byte
+    work (each operand read once, each result written once); attention is MFMA
+    work, 4 T^2 hd flop per q head for full layers (QK^T and PV), the band
+    |i - j| <= window for sliding ones."""
+    nb = lambda k: k // 32
+    if kernel in ("gemm_i8", "gemm_i8_geglu"):
+        b = 0
+        for name, n, k in MODEL_GEMMS:
+            if name != kernel:
+                continue
+            w = n * k + 4 * n * nb(k)
+            if name == "gemm_i8_geglu":
+                b += t * k + 4 * t * nb(k) + w + t * F + 4 * t * nb(F)
+            else:
+                b += t * k + 4 * t * nb(k) + w + 4 * t * n
+        return "hbm", b * n_layers, "B"
+    if kernel == "residual_norm":   # x, h read; h written; Q8_0 of the next input written
+        return "hbm", 2 * n_layers * (4 * t * H * 3 + 8 * H + t * H + 4 * t * nb(H)), "B"
+    if kernel == "attention":
+        flop = 0
+        for l in range(n_layers):
+            full = (l + 1) % 6 == 0
+            keys = t * t if full or window >= t - 1 else \
+                sum(min(t, i + window + 1) - max(0, i - window) for i in range(t))
+            flop += 4 * keys * hd * nq
+        return "mfma", flop, "flop"
+    return None, 0, None
+
+
+def model_roofline(res, t):
+    """Roofline entry of the dominant kernel (by profiled time) of a backbone run."""
+    kern, steps = res["_kernels"], res["_steps"]
+    dom = max(kern, key=lambda k: kern[k]["ms_total"])
+    k = kern[dom]
+    bound, work, unit = model_kernel_work(dom, t)
+    per_launch = work / (k["launches"] / steps)
+    secs = k["us_per_launch"] * 1e-6
+    if bound == "mfma":
+        ach = per_launch / secs / 1e12
+        peak, u = 2500.0, "TFLOP/s"
+    else:
+        ach = per_launch / secs / 1e9
+        peak, u = HBM_PEAK_GBS, "GB/s"
+    return {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": u,
+            "frac": round(ach / peak, 4), "traffic": measured_traffic("C4", dom, 0),
+            "kernel": dom, "us_per_launch": round(k["us_per_launch"], 3),
+            "launches_per_step": k["launches"] // steps,
+            "algorithmic_per_launch": int(per_launch), "algorithmic_unit": unit,
+            "event_cost_us_per_launch": res["event_cost_us_per_launch"],
+            "timing": "per-launch HIP events on the launch stream over a second pass of the "
+                      "timed steps (event cost included)"}
+
+
+def gather_line(ctx, steps, n_ids=1 << 20, vocab=262144, d=768):
+    """The Q8_0 token-row gather on its own (Embedding::forward x embed_scale,
+    model.rs:254-255, 507-508) at a size that is not launch-bound: 1M uniform
+    ids over the 262144 x 768 table.  Algorithmic bytes per id: the Q8_0 row
+    (816 B as GGUF blocks) read and the f32 row (3072 B) written."""
+    import torch
+    from glypr_amd import ops
+    from glypr_amd.ops import Q8Weight
+    rng = np.random.default_rng(21)
+    table = Q8Weight.from_gguf(ctx, q8_0_weight(rng, vocab, d), vocab, d)
+    ids = rng.integers(0, vocab, size=n_ids).astype(np.uint32)
+    out = torch.empty((n_ids, d), dtype=torch.float32, device="cuda")
+    scale = float(np.float32(np.sqrt(float(d))))
+    for _ in range(3):
+        ops.embed_gather(ctx, table, ids, scale, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ops.embed_gather(ctx, table, ids, scale, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_call = e0.elapsed_time(e1) / steps
+    from glypr_amd import _lib
+    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 1))
+    for _ in range(steps):
+        ops.embed_gather(ctx, table, ids, scale, out=out)
+    tot = (ctypes.c_double * _lib.KERNEL_COUNT)()
+    cnt = (ctypes.c_int64 * _lib.KERNEL_COUNT)()
+    _lib.check(_lib.lib().glypr_hip_profile_read(ctx.handle, tot, cnt))
+    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 0))
+    kid = [i for i in range(_lib.KERNEL_COUNT)
+           if _lib.lib().glypr_hip_kernel_name(i).decode() == "gather"][0]
+    us = 1000.0 * tot[kid] / cnt[kid]
+    nbytes = n_ids * (d // 32 * 34 + 4 * d)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    table.close()
+    del out
+    return {"ids": n_ids, "table": f"{vocab} x {d} Q8_0", "us_per_launch": round(us, 2),
+            "us_per_call": round(ms_call * 1e3, 2),
+            "algorithmic_bytes": nbytes, "gb_per_s": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "note": "per call also uploads the 4 MB of host ids (PCIe) before the kernel"}
 
 
 def cpu_backbone_baseline(tensors, n_layers, vocab, t, seconds=10.0):
@@ -488,18 +612,34 @@ def cpu_backbone_baseline(tensors, n_layers, vocab, t, seconds=10.0):
                                                 "post_ffw_norm", "attn_q_norm", "attn_k_norm")])
     ids = np.ascontiguousarray(np.random.default_rng(1).integers(0, vocab, size=t), np.uint32)
     out = np.empty(256, np.float32)
-    t0 = time.perf_counter()
-    n = 0
-    while n == 0 or time.perf_counter() - t0 < seconds:
+
+    def one():
         rc = po.lib().orc_model_forward(ctypes.byref(cfg), u8("token_embd.weight"), layers,
                                         f32("output_norm.weight"), None, None, None,
                                         ids.ctypes.data_as(po._u32p),
                                         t, 256, out.ctypes.data_as(po._f32p), None, cores)
         assert rc == 0
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    return {"value": round(1.0 / dt, 4), "unit": "embeddings/s", "cores": cores, "kind": "port",
-            "sample": f"config 4 full forward (24 layers, T={t}), {n} embeddings"}
+
+    one()   # warm-up
+    times = []
+    t0 = time.perf_counter()
+    while len(times) < 3 or time.perf_counter() - t0 < seconds:
+        t1 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t1)
+    times = np.array(times)
+    med = float(np.median(times))
+    return {"value": round(1.0 / med, 4), "unit": "embeddings/s", "cores": cores,
+            "kind": "port", "ms_per_embedding": round(med * 1e3, 1),
+            "ms_per_embedding_p95": round(float(np.percentile(times, 95)) * 1e3, 1),
+            "ms_per_embedding_min": round(float(times.min()) * 1e3, 1),
+            "host": host_cpu(),
+            "sample": f"config 4 full forward (24 layers, T={t}, the same weights and a "
+                      f"512-id sequence), {len(times)} embeddings over {seconds:.0f}s on "
+                      f"{cores} threads after one warm-up (median; p95 and min beside it); "
+                      "glypr's CPU Q8_0 path restated (oracle/glypr_oracle.c, candle-default-"
+                      "x86 scalar vec_dot semantics, gcc -O3 x86-64-v3, OpenMP over output "
+                      "columns)"}
 
 
 def cpu_baseline(seconds=10.0):
@@ -577,12 +717,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--variant", choices=["int8", "bf16"], default="int8")
+    ap.add_argument("--variant", choices=["int8", "bf16"], default="int8",
+                    help="Q8_0 variant of the C2 / cold-C2 extra lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
-    ap.add_argument("--extras", default="c1,cold,c3,vendor,c4,c5,vec",
+    ap.add_argument("--extras", default="c2,c1,cold,c3,vendor,c5,gather,vec",
                     help="comma list of the extra workloads to run "
-                         "(c1, cold, c3, vendor, c4, c5, vec)")
+                         "(c2, c1, cold, c3, vendor, c5, gather, vec)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain device copy of MIB MiB (calibrates rocprof "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -607,18 +748,35 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    m = 512
-    L, ms, kern = run_workload(ctx, m, variant, args.steps, args.warmup)
-    tops = L.ops_per_step() / (ms / 1e3) / 1e12
-    dom, roof = roofline_for(kern, m, variant, args.steps)
-    peak = INT8_PEAK_TOPS if variant == INT8_EXACT else BF16_PEAK_TFLOPS
+    # ---- headline: config 4, one 512-token embedding per step
+    t_c4, n_layers, vocab = 512, 24, 262144
+    tensors = model_tensors(np.random.default_rng(7), n_layers, vocab)
+    c4 = run_backbone(ctx, tensors, n_layers, vocab, t_c4, args.steps, args.warmup)
+    roof = model_roofline(c4, t_c4)
+    extra = {"c4": {k: v for k, v in c4.items() if not k.startswith("_")}}
+    extra["c4"]["kernels_us_per_launch"] = {k: round(v["us_per_launch"], 3)
+                                            for k, v in c4["_kernels"].items()}
 
-    extra = {"kernels_c2": {k: {"us_per_launch": round(v["us_per_launch"], 3),
-                                "launches_per_step": v["launches"] // args.steps}
-                            for k, v in kern.items()},
-             "pct_mfma_peak_c2": round(100 * tops / peak, 3)}
     todo = set() if args.no_extra else {e.strip() for e in args.extras.split(",") if e.strip()}
+    if "c2" in todo:
+        m = 512
+        L, ms, kern = run_workload(ctx, m, variant, args.steps, args.warmup)
+        tops = L.ops_per_step() / (ms / 1e3) / 1e12
+        _, roof_c2 = roofline_for(kern, m, variant, args.steps)
+        peak = INT8_PEAK_TOPS if variant == INT8_EXACT else BF16_PEAK_TFLOPS
+        extra["c2"] = {"tops": round(tops, 3), "ms_per_step": round(ms, 5),
+                       "pct_mfma_peak": round(100 * tops / peak, 3), "roofline": roof_c2,
+                       "kernels": {k: {"us_per_launch": round(v["us_per_launch"], 3),
+                                       "launches_per_step": v["launches"] // args.steps}
+                                   for k, v in kern.items()},
+                       "workload": "one layer's 7 Q8_0 projections at T=512 (RMSNorm->qkv, o, "
+                                   "RMSNorm->gate/up+GeGLU->down)"}
+        if not args.no_cpu:
+            extra["c2"]["cpu_baseline"] = cpu_baseline(seconds=6.0)
+        del L
     if "c3" in todo:
+        import torch
+        keep = {}
         for vname, v in (("int8", INT8_EXACT), ("bf16", BF16_DEQUANT)):
             Lx, msx, kx = run_workload(ctx, 16384, v, max(10, args.steps // 10), 3)
             t = Lx.ops_per_step() / (msx / 1e3) / 1e12
@@ -630,62 +788,75 @@ def main():
                     sum(kernel_bytes(k, 16384, v) for k in kx) / (msx / 1e3) / 1e9
                     / HBM_PEAK_GBS, 4),
                 "kernels_us": {k: round(vv["us_per_launch"], 2) for k, vv in kx.items()}}
-            del Lx
+            keep[vname] = Lx
+        # A5': BF16_DEQUANT's outputs against INT8_EXACT's (bit-identical to glypr's
+        # CPU Q8_0 path), per row, on the same inputs
+        cos = {}
+        for out_name in ("y_qkv", "y_o", "y_mlp"):
+            a = getattr(keep["bf16"], out_name).double()
+            b = getattr(keep["int8"], out_name).double()
+            c = (a * b).sum(1) / a.norm(dim=1) / b.norm(dim=1)
+            cos[out_name[2:]] = {"min": round(float(c.min()), 7), "mean": round(float(c.mean()), 7)}
+        extra["c3_bf16"]["cosine_to_int8_exact_per_row"] = cos
+        del keep
+        torch.cuda.synchronize()
     if "vendor" in todo:
         try:
             extra["vendor_ref_c3_shapes"] = vendor_ref(max(10, args.steps // 4))
         except (RuntimeError, AttributeError, TypeError) as e:   # a reference only
             extra["vendor_ref_c3_shapes"] = {"error": f"{type(e).__name__}: {e}"[:200]}
-        if "c3" in todo:
-            # the same C3 step's GEMM launches only (no norm / quantize launches)
-            for vname, gk, geglu in (("int8", "gemm_i8", "gemm_i8_geglu"),
-                                     ("bf16", "gemm_bf16", "gemm_bf16_geglu")):
-                ku = extra[f"c3_{vname}"]["kernels_us"]
-                if gk in ku and geglu in ku:
-                    us = 3 * ku[gk] + ku[geglu]
-                    extra[f"c3_{vname}"]["gemm_ms_per_step"] = round(us / 1e3, 4)
-                    extra[f"c3_{vname}"]["gemm_tops"] = round(
-                        LAYER_NK * 2 * 16384 / us / 1e6, 1)
+    if "c3" in todo:
+        # the same C3 step's GEMM launches only (no norm / quantize launches)
+        for vname, gk, geglu in (("int8", "gemm_i8", "gemm_i8_geglu"),
+                                 ("bf16", "gemm_bf16", "gemm_bf16_geglu")):
+            ku = extra[f"c3_{vname}"]["kernels_us"]
+            if gk in ku and geglu in ku:
+                us = 3 * ku[gk] + ku[geglu]
+                extra[f"c3_{vname}"]["gemm_ms_per_step"] = round(us / 1e3, 4)
+                extra[f"c3_{vname}"]["gemm_tops"] = round(LAYER_NK * 2 * 16384 / us / 1e6, 1)
     if "c1" in todo:
         extra["c1_int8"] = c1_linear(ctx, args.steps)
     if "cold" in todo:
         extra["c2_cold"] = c2_cold(ctx, variant)
+    if "gather" in todo:
+        extra["gather"] = gather_line(ctx, 20)
     if "vec" in todo:
         extra["vec_codecs"] = vec_search(ctx, 20)
-    if "c4" in todo or "c5" in todo:
-        rng = np.random.default_rng(7)
-        tensors = model_tensors(rng, 24, 262144)
-        if "c4" in todo:
-            extra["c4"] = run_backbone(ctx, tensors, 24, 262144, 512,
-                                       max(10, args.steps // 10), 3)
-            if not args.no_cpu:
-                extra["c4"]["cpu_baseline"] = cpu_backbone_baseline(tensors, 24, 262144, 512)
-        if "c5" in todo:
-            extra["c5"] = run_backbone(ctx, tensors, 24, 262144, 8192, 3, 1)
-            extra["c5"]["attention_layers"] = ("4 full + 20 sliding (window 512) layers, "
-                                               "1.341 TFLOP per embedding")
-        del tensors
-        if "c5" in todo:
-            dense = model_tensors(np.random.default_rng(8), 24, 262144, dense=True)
-            extra["c5_bf16w"] = run_backbone(ctx, dense, 24, 262144, 8192, 3, 1)
-            extra["c5_bf16w"]["weights"] = "dense bf16 projections (8,454,144 B per layer)"
-            del dense
+    if "c5" in todo:
+        extra["c5"] = {k: v for k, v in run_backbone(ctx, tensors, n_layers, vocab, 8192, 3,
+                                                     1).items() if not k.startswith("_")}
+        extra["c5"]["attention_layers"] = ("4 full + 20 sliding (window 512) layers, "
+                                           "1.341 TFLOP per embedding")
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_backbone_baseline(tensors, n_layers, vocab, t_c4)
+    del tensors
+    if "c5" in todo:
+        dense = model_tensors(np.random.default_rng(8), n_layers, vocab, dense=True)
+        extra["c5_bf16w"] = {k: v for k, v in run_backbone(ctx, dense, n_layers, vocab, 8192, 3,
+                                                           1).items() if not k.startswith("_")}
+        extra["c5_bf16w"]["weights"] = "dense bf16 projections (8,454,144 B per layer)"
+        del dense
 
     line = {
         "metric": "Q8_0 matmul TOPS (% MFMA peak); 512-tok embeddings/sec on 1 MI355X",
-        "value": round(tops, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8" if variant == INT8_EXACT else "bf16", "data": "synthetic",
-        "config": {"workload": "C2: one EmbeddingGemma layer's 7 Q8_0 projections at T=512 "
-                               "(RMSNorm->qkv, o, RMSNorm->gate/up+GeGLU->down)",
-                   "T": m, "hidden": H, "ffn": F, "q_dim": NQ, "kv_dim": NKV,
-                   "variant": "INT8_EXACT" if variant == INT8_EXACT else "BF16_DEQUANT",
-                   "ops_per_step": L.ops_per_step()},
+        "value": c4["embeddings_per_s"], "unit": "embeddings/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": c4["ms_per_embedding"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic (seeded random-init Q8_0 weights, uniform ids)",
+        "config": {"workload": "C4: 24-layer EmbeddingGemma text backbone, one 512-token "
+                               "sequence (batch 1): Q8_0 gather from the 262144 x 768 table, "
+                               "24 layers (hidden 768, 3 q / 1 kv heads, head_dim 256, FFN "
+                               "1152, 5 sliding (window 512) + 1 full pattern), mean pool, "
+                               "L2, MRL-256; projections INT8_EXACT",
+                   "T": t_c4, "batch": 1, "layers": n_layers, "vocab": vocab,
+                   "gemm_ops_per_step": c4["gemm_ops_per_embedding"],
+                   "gemm_tops": c4["gemm_tops"],
+                   "pct_int8_mfma_peak_gemm": round(100 * c4["gemm_tops"] / INT8_PEAK_TOPS, 3)},
         "roofline": roof,
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline()
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
     line["extra"] = extra
     print(json.dumps(line), flush=True)
     ctx.close()

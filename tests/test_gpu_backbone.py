@@ -327,3 +327,79 @@ def test_model_from_gguf_matches_set_tensor(ctx, oracle, tmp_path):
     assert a.shape == (200,) and np.array_equal(a.view(np.uint32), b.view(np.uint32))
     g.close()
     m.close()
+
+
+# ------------------------------------------------------- config 5 (T = 8192) --
+
+def test_config5_vs_oracle_six_layers(ctx, oracle):
+    """Config 5's sequence length through glypr_hip_model_embed against the CPU
+    oracle, at the depth the oracle finishes in seconds: 6 layers at T = 8192
+    (layers 0-4 sliding with window 512, layer 5 full attention over all 8192
+    keys), the 262144-row Q8_0 table."""
+    n_layers, t, vocab = 6, 8192, 262144
+    say(f"config 5 length: backbone layers={n_layers} t={t} vs oracle")
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=50)
+    ids = oracle.uniform_ids(t, seed=51, vocab=vocab)
+    hidden = torch.empty((t, 768), dtype=torch.float32, device="cuda")
+    got = host(m.embed(ids, trunc=256, hidden=hidden))
+    ref, ref_hidden = oracle_forward(oracle, tensors, n_layers, vocab, ids, 256)
+    cos = float(got @ ref / np.linalg.norm(got) / np.linalg.norm(ref))
+    gh = host(hidden)
+    row_cos = (gh * ref_hidden).sum(1) / np.linalg.norm(gh, axis=1) / \
+        np.linalg.norm(ref_hidden, axis=1)
+    say(f"  final embedding cosine {cos:.8f}, token-state cosine min {row_cos.min():.8f}")
+    assert cos >= 0.9999 and row_cos.min() >= 0.999
+    m.close()
+
+
+def test_config5_full_backbone_both_weight_kinds(ctx, oracle):
+    """Config 5 exactly: the 24-layer backbone at one 8192-token sequence, with
+    Q8_0 weights and with the same weights as dense bf16.  Size-independent
+    checks: finite outputs, unit L2 norm, bit-identical repeats, and the two
+    weight kinds' embeddings within the activation-quantization bound.
+
+    The bound: INT8_EXACT quantizes every GEMM input per 32-block (relative
+    error ~ amax / (127 sqrt 12) ~ 0.6 % for Gaussian blocks, where
+    amax ~ 2.5 sigma), the bf16 variant rounds it to bf16 (~0.1 %).  Taking
+    each of the 24 x 7 GEMMs' errors as independent and undamped gives a
+    relative error energy of 168 x (0.006)^2 ~ 6e-3 at most, so
+    cos >= 1 - 6e-3 / 2 = 0.997."""
+    n_layers, t, vocab = 24, 8192, 262144
+    ids = oracle.uniform_ids(t, seed=53, vocab=vocab)
+    outs = {}
+    for dense in (False, True):
+        say(f"config 5: 24 layers t={t} {'dense bf16' if dense else 'Q8_0'} weights")
+        m, _ = make_model(ctx, oracle, n_layers, vocab, seed=52, dense=dense)
+        a = host(m.embed(ids, trunc=0))
+        b = host(m.embed(ids, trunc=0))
+        assert np.isfinite(a).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert abs(np.linalg.norm(a.astype(np.float64)) - 1.0) < 1e-5
+        mrl = host(m.embed(ids, trunc=256))
+        ref = a[:256].astype(np.float64) / np.linalg.norm(a[:256].astype(np.float64))
+        assert np.abs(mrl - ref).max() < 1e-6
+        outs[dense] = a.astype(np.float64)
+        m.close()
+    cos = float(outs[False] @ outs[True])
+    say(f"  Q8_0 vs bf16-weight embedding cosine {cos:.8f}")
+    assert cos >= 0.997
+
+
+def test_model_embed_length_preflight(ctx, oracle):
+    """max_seq_len is the longest input (the preflight of lib.rs:970-976):
+    buffers are sized for it at finalize, a longer sequence is refused with
+    GLYPR_ERR_SHAPE before anything is launched."""
+    from glypr_amd._lib import GlyprError
+    m = Model(ctx, n_layers=1, vocab=300, max_seq_len=700)
+    m0, tensors = make_model(ctx, oracle, 1, 300, seed=54)
+    m0.close()
+    for name, (data, r, c, q8) in tensors.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    ids = oracle.uniform_ids(701, seed=55, vocab=300)
+    ok = host(m.embed(ids[:700], trunc=256))
+    assert np.isfinite(ok).all()
+    with pytest.raises(GlyprError) as e:
+        m.embed(ids, trunc=256)
+    assert e.value.code == _lib.GLYPR_ERR_SHAPE
+    m.close()

@@ -410,6 +410,15 @@ def test_matmul_bf16_dequant_within_bf16_bound(ctx, oracle, m, k, n):
     assert np.all(np.abs(y - y64) <= bound)
     cos = (y * y64).sum(1) / np.linalg.norm(y, axis=1) / np.linalg.norm(y64, axis=1)
     assert cos.min() > 0.9999
+    # A5': the same output against glypr's CPU Q8_0 path (INT8_EXACT oracle,
+    # activations quantized per 32-block).  The gap is the oracle's own
+    # activation-quantization error, ~0.5 % relative per element, so the
+    # per-row cosine sits near 1 - (0.005)^2 / 2.
+    rows = np.arange(m) if m <= 512 else np.random.default_rng(m).choice(m, 256, replace=False)
+    y8 = oracle.matmul(x[rows], wb, n).astype(np.float64)
+    c8 = (y[rows] * y8).sum(1) / np.linalg.norm(y[rows], axis=1) / np.linalg.norm(y8, axis=1)
+    say(f"  cosine to the INT8_EXACT oracle: min {c8.min():.7f} mean {c8.mean():.7f}")
+    assert c8.min() > 0.999
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 64, 1), (100, 768, 1152), (600, 1152, 257),
@@ -470,3 +479,72 @@ def test_zero_rows_and_shape_errors(ctx, oracle):
     with pytest.raises(_lib.GlyprError) as e:
         ops.mlp(ctx, w, other, torch.zeros((4, 64), device="cuda"))
     assert e.value.code == _lib.GLYPR_ERR_SHAPE
+
+
+# ------------------------------------------------------ C3 (M = 16384) ------
+
+C3_M, C3_H, C3_F = 16384, 768, 1152
+
+
+def _c3_weights(ctx, oracle):
+    qb = oracle.q8_0_weight(1280, C3_H, seed=501)        # q | k | v of one layer
+    gb, ub = oracle.q8_0_weight(C3_F, C3_H, seed=502), oracle.q8_0_weight(C3_F, C3_H, seed=503)
+    db = oracle.q8_0_weight(C3_H, C3_F, seed=504)
+    wq = Q8Weight.from_gguf(ctx, qb, 1280, C3_H)
+    g, u = Q8Weight.from_gguf(ctx, gb, C3_F, C3_H), Q8Weight.from_gguf(ctx, ub, C3_F, C3_H)
+    d = Q8Weight.from_gguf(ctx, db, C3_H, C3_F)
+    gu, _ = Q8Weight.concat(ctx, [g, u])
+    return (qb, gb, ub, db), (wq, gu, d)
+
+
+def test_c3_int8_rmsnorm_geglu_mlp(ctx, oracle):
+    """C3's RMSNorm -> gate/up GeGLU -> down at M = 16384 (the large-M GeGLU
+    epilogue kernel): two runs bit-identical, 64 sampled rows bit-exact."""
+    say(f"C3 INT8_EXACT rmsnorm_mlp m={C3_M}")
+    x = oracle.normal(C3_M * C3_H, seed=505).reshape(C3_M, C3_H)
+    nw = 1 + 0.1 * oracle.normal(C3_H, seed=506)
+    (qb, gb, ub, db), (wq, gu, d) = _c3_weights(ctx, oracle)
+    xd, nwd = dev(x), dev(nw)
+    y1 = host(ops.rmsnorm_mlp(ctx, gu, d, xd, nwd, 1e-6, INT8_EXACT))
+    y2 = host(ops.rmsnorm_mlp(ctx, gu, d, xd, nwd, 1e-6, INT8_EXACT))
+    assert np.array_equal(bits(y1), bits(y2))
+    rows = np.random.default_rng(5).choice(C3_M, 64, replace=False)
+    rows[:2] = [0, C3_M - 1]
+    xn = oracle.rmsnorm(x[rows], nw, 1e-6)
+    assert_bits_equal(y1[rows], _mlp_ref(oracle, xn, gb, ub, db, C3_H, C3_F), "C3 mlp rows")
+
+
+def test_c3_bf16_dequant_qkv_and_mlp(ctx, oracle):
+    """C3's BF16_DEQUANT launches at M = 16384 (RMSNorm -> bf16 prologue, the
+    128 x 256 large-M kernels, the bf16 GeGLU epilogue): sampled rows against
+    the float64 dequant oracle within the bf16 bound, and the per-row cosine to
+    glypr's CPU Q8_0 path (INT8_EXACT oracle) reported (A5')."""
+    say(f"C3 BF16_DEQUANT qkv + mlp m={C3_M}")
+    x = oracle.normal(C3_M * C3_H, seed=507).reshape(C3_M, C3_H)
+    nw = 1 + 0.1 * oracle.normal(C3_H, seed=508)
+    (qb, gb, ub, db), (wq, gu, d) = _c3_weights(ctx, oracle)
+    xd, nwd = dev(x), dev(nw)
+    y = host(ops.rmsnorm_q8_0_matmul(ctx, wq, xd, nwd, 1e-6, BF16_DEQUANT))
+    z = host(ops.rmsnorm_mlp(ctx, gu, d, xd, nwd, 1e-6, BF16_DEQUANT))
+    again = host(ops.rmsnorm_q8_0_matmul(ctx, wq, xd, nwd, 1e-6, BF16_DEQUANT))
+    assert np.array_equal(bits(y), bits(again))
+    rows = np.random.default_rng(6).choice(C3_M, 96, replace=False)
+    rows[:2] = [0, C3_M - 1]
+    xn = oracle.rmsnorm(x[rows], nw, 1e-6)
+    y64 = oracle.matmul_dequant_f64(xn, qb, 1280)
+    wd = np.abs(oracle.dequantize_rows(qb, C3_H).astype(np.float64))
+    bound = 2.0 ** -7 * (np.abs(xn).astype(np.float64) @ wd.T) * (1 + 1e-3) + 1e-6
+    assert np.all(np.abs(y[rows] - y64) <= bound)
+    y8 = oracle.matmul(xn, qb, 1280).astype(np.float64)
+    c8 = (y[rows] * y8).sum(1) / np.linalg.norm(y[rows], axis=1) / np.linalg.norm(y8, axis=1)
+    say(f"  qkv cosine to the INT8_EXACT oracle: min {c8.min():.7f} mean {c8.mean():.7f}")
+    assert c8.min() > 0.999
+    gate = oracle.matmul_dequant_f64(xn, gb, C3_F).astype(np.float32)
+    up = oracle.matmul_dequant_f64(xn, ub, C3_F).astype(np.float32)
+    ref = oracle.matmul_dequant_f64(oracle.geglu(gate, up), db, C3_H)
+    cz = (z[rows] * ref).sum(1) / np.linalg.norm(z[rows], axis=1) / np.linalg.norm(ref, axis=1)
+    assert cz.min() > 0.999, cz.min()
+    z8 = _mlp_ref(oracle, xn, gb, ub, db, C3_H, C3_F).astype(np.float64)
+    c8 = (z[rows] * z8).sum(1) / np.linalg.norm(z[rows], axis=1) / np.linalg.norm(z8, axis=1)
+    say(f"  mlp cosine to the INT8_EXACT oracle: min {c8.min():.7f} mean {c8.mean():.7f}")
+    assert c8.min() > 0.998
