@@ -40,6 +40,11 @@ __device__ __forceinline__ float dpp_mov(float old, float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
                                                     ROW_MASK, 0xF, false));
 }
+// max over each aligned group of 4 lanes; every lane of the group gets it
+__device__ __forceinline__ float max4(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v, v));    // quad_perm [1,0,3,2]
+  return fmaxf(v, dpp_mov<0x4E>(v, v));  // quad_perm [2,3,0,1]
+}
 // max over each aligned group of 8 lanes; every lane of the group gets it
 __device__ __forceinline__ float max8(float v) {
   v = fmaxf(v, dpp_mov<0xB1>(v, v));    // quad_perm [1,0,3,2]

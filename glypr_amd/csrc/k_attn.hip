@@ -27,54 +27,70 @@ typedef _Float16 f16;
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// qkv_post.  q and k: one wave per (token, head slot); slots 0..nq-1 are q
-// heads, nq..nq+nkv-1 k heads.  hd == 256: lane l holds dims 4l..4l+3 and
-// writes them as one 8-byte store.  v (the blocks after the q/k blocks): one
-// wave per 4 consecutive tokens of a head, so each lane writes its 4 dims of
-// the transposed vt as four 8-byte runs of 4 tokens; the same eight chains and
-// horizontal sum per token, run by lanes 8 i + j (token i, chain j).  RMSNorm follows simd_rmsnorm_row_f32's order (eight FMA chains,
-// lane j = dims j, j+8, ...; see k_norm.hip) so it is bit-exact with the CPU
-// path; RoPE is x*cos + rot*sin with both products rounded (no FMA), rot =
-// -x[i+128] for i < 128 and x[i-128] otherwise: lane l's partner is l ^ 32.
+// qkv_post, for head dims HD = 256 and 512 (DPL = HD / 64 dims per lane).
+// q and k: one wave per (token, head slot); slots 0..nq-1 are q heads,
+// nq..nq+nkv-1 k heads.  Lane l holds dims DPL l .. DPL l + DPL-1 and writes
+// them as one 8- (HD 256) or 16-byte (HD 512) store.  v (the blocks after the
+// q/k blocks): one wave per 4 consecutive tokens of a head, so each lane
+// writes its DPL dims of the transposed vt as DPL 8-byte runs of 4 tokens; the
+// same eight chains and horizontal sum per token, run by lanes 8 i + j (token
+// i, chain j).  RMSNorm follows simd_rmsnorm_row_f32's order (eight FMA
+// chains, chain j = dims j, j+8, ...; see k_norm.hip) so it is bit-exact with
+// the CPU path; RoPE is x*cos + rot*sin with both products rounded (no FMA),
+// rot = -x[i+HD/2] for i < HD/2 and x[i-HD/2] otherwise: lane l's partner is
+// l ^ 32 for either HD.
 // Outputs (token rows padded to Tp, padding zero-filled):
-//   q [nq][Tp][hd], k [nkv][Tp][hd], vt [nkv][hd][Tp] (f16).
+//   q [nq][Tp][HD], k [nkv][Tp][HD], vt [nkv][HD][Tp] (f16).
 // ---------------------------------------------------------------------------
-constexpr int QKV_HD = 256;
-
 constexpr int QKV_V_TOK = 4;   // tokens per v wave (8 lanes each)
-constexpr int QKV_V_LDS = QKV_V_TOK * 8 * (QKV_HD / 8 + 4);   // floats per v wave
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
+template <int HD>
+struct QkvGeom {
+  static constexpr int DPL = HD / 64;                        // dims per lane
+  static constexpr int S = HD / 8 + 4;                       // chain stride (k_norm.hip)
+  static constexpr int V_LDS = QKV_V_TOK * 8 * S;            // floats per v wave
+  static constexpr int LDS = V_LDS > HD ? V_LDS : HD;        // per-wave staging
+};
+
+template <int HD>
 __global__ void __launch_bounds__(256) qkv_post_kernel(
     const float* __restrict__ qkv, int T, int Tp, int nq, int nkv, const float* __restrict__ qnw,
     const float* __restrict__ knw, float eps, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, f16* __restrict__ q16,
     f16* __restrict__ k16, f16* __restrict__ vt16, int qk_blocks) {
-  // per wave: a q/k row (QKV_HD floats) or the chain-major v rows (QKV_V_LDS)
-  static_assert(QKV_V_LDS >= QKV_HD, "shared staging sized by the v rows");
-  __shared__ __attribute__((aligned(16))) float lds_rows[4][QKV_V_LDS];
+  using Gm = QkvGeom<HD>;
+  constexpr int DPL = Gm::DPL;
+  constexpr int NV4 = DPL / 4;   // float4s per lane
+  __shared__ __attribute__((aligned(16))) float lds_rows[4][Gm::LDS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slots = nq + 2 * nkv;
   if ((int)blockIdx.x >= qk_blocks) {
     // v: wave = QKV_V_TOK consecutive tokens of one head; lane 8 i + j runs
     // chain j of token i from the chain-major LDS copy, then lane l stores dims
-    // 4l .. 4l+3 of the tokens as four runs of vt rows.
+    // DPL l .. DPL l + DPL-1 of the tokens as DPL runs of vt rows.
     const int64_t vtask = (int64_t)((int)blockIdx.x - qk_blocks) * 4 + wave;
     const int per_head = Tp / QKV_V_TOK;
     if (vtask >= (int64_t)nkv * per_head) return;
     const int head = (int)(vtask / per_head), t0 = (int)(vtask % per_head) * QKV_V_TOK;
-    constexpr int S = QKV_HD / 8 + 4;   // chain stride, as chain_stride() in k_norm.hip
+    constexpr int S = Gm::S;
     float* lv = lds_rows[wave];
-    v4f x[QKV_V_TOK];
+    v4f x[QKV_V_TOK][NV4];
 #pragma unroll
     for (int i = 0; i < QKV_V_TOK; i++) {
       const int t = t0 + i;
-      x[i] = t < T ? *reinterpret_cast<const v4f*>(qkv + (int64_t)t * slots * QKV_HD +
-                                                   (int64_t)(nq + nkv + head) * QKV_HD + 4 * lane)
-                   : v4f{0, 0, 0, 0};
-      const int j0 = 4 * (lane & 1), idx = lane >> 1;
 #pragma unroll
-      for (int k = 0; k < 4; k++) lv[i * 8 * S + (j0 + k) * S + idx] = x[i][k];
+      for (int c = 0; c < NV4; c++) {
+        x[i][c] = t < T ? *reinterpret_cast<const v4f*>(
+                              qkv + (int64_t)t * slots * HD + (int64_t)(nq + nkv + head) * HD +
+                              DPL * lane + 4 * c)
+                        : v4f{0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const int d = DPL * lane + 4 * c + k;   // chain d & 7, position d >> 3
+          lv[i * 8 * S + (d & 7) * S + (d >> 3)] = x[i][c][k];
+        }
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
@@ -83,7 +99,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     const v4f* src = reinterpret_cast<const v4f*>(lv + ti * 8 * S + (lane & 7) * S);
     float acc = 0.0f;
 #pragma unroll
-    for (int c = 0; c < QKV_HD / 32; c++) {
+    for (int c = 0; c < HD / 32; c++) {
       const v4f e = src[c];
       acc = fmaf(e[0], e[0], acc);
       acc = fmaf(e[1], e[1], acc);
@@ -93,17 +109,17 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     const float s4 = acc + __shfl_down(acc, 4, 8);
     const float s2 = s4 + __shfl_down(s4, 2, 8);
     const float sum = s2 + __shfl_down(s2, 1, 8);
-    const float inv = 1.0f / sqrtf(sum / (float)QKV_HD + eps);   // valid on lanes 8 i
-    v4h yh[4];
+    const float inv = 1.0f / sqrtf(sum / (float)HD + eps);   // valid on lanes 8 i
+    v4h yh[DPL];
 #pragma unroll
     for (int i = 0; i < QKV_V_TOK; i++) {
       const float inv_i = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), 8 * i));
 #pragma unroll
-      for (int e = 0; e < 4; e++) yh[e][i] = (f16)(x[i][e] * inv_i);
+      for (int e = 0; e < DPL; e++) yh[e][i] = (f16)(x[i][e / 4][e % 4] * inv_i);
     }
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-      *reinterpret_cast<v4h*>(vt16 + ((int64_t)head * QKV_HD + 4 * lane + e) * Tp + t0) = yh[e];
+    for (int e = 0; e < DPL; e++)
+      *reinterpret_cast<v4h*>(vt16 + ((int64_t)head * HD + DPL * lane + e) * Tp + t0) = yh[e];
     return;
   }
   const int qk_slots = nq + nkv;
@@ -113,19 +129,25 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
   const int kind = slot < nq ? 0 : 1;
   const int head = kind == 0 ? slot : slot - nq;
 
-  v4f y = {0, 0, 0, 0};
+  float y[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; e++) y[e] = 0.0f;
   if (t < T) {
-    const float* src = qkv + (int64_t)t * (nq + 2 * nkv) * QKV_HD + (int64_t)slot * QKV_HD;
-    v4f x = *reinterpret_cast<const v4f*>(src + 4 * lane);
+    const float* src = qkv + (int64_t)t * (nq + 2 * nkv) * HD + (int64_t)slot * HD;
+    v4f x[NV4];
     float* lrow = lds_rows[wave];
-    *reinterpret_cast<v4f*>(lrow + 4 * lane) = x;
+#pragma unroll
+    for (int c = 0; c < NV4; c++) {
+      x[c] = *reinterpret_cast<const v4f*>(src + DPL * lane + 4 * c);
+      *reinterpret_cast<v4f*>(lrow + DPL * lane + 4 * c) = x[c];
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
     float sum = 0.0f;
     if (lane < 8) {
       float acc = 0.0f;
 #pragma unroll
-      for (int c = 0; c < QKV_HD / 8; c++) {
+      for (int c = 0; c < HD / 8; c++) {
         float e = lrow[8 * c + lane];
         acc = fmaf(e, e, acc);
       }
@@ -134,48 +156,60 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
       sum = u + __shfl_down(u, 1, 8);
     }
     sum = __shfl(sum, 0);
-    const float inv = 1.0f / sqrtf(sum / (float)QKV_HD + eps);
+    const float inv = 1.0f / sqrtf(sum / (float)HD + eps);
     const float* w = kind == 0 ? qnw : knw;
-    v4f wv = w ? *reinterpret_cast<const v4f*>(w + 4 * lane) : v4f{1, 1, 1, 1};
 #pragma unroll
-    for (int e = 0; e < 4; e++) y[e] = w ? (x[e] * inv) * wv[e] : x[e] * inv;
-    {
-      v4f c = *reinterpret_cast<const v4f*>(cos_t + (int64_t)t * QKV_HD + 4 * lane);
-      v4f s = *reinterpret_cast<const v4f*>(sin_t + (int64_t)t * QKV_HD + 4 * lane);
-      v4f r;
+    for (int c = 0; c < NV4; c++) {
+      const v4f wv = w ? *reinterpret_cast<const v4f*>(w + DPL * lane + 4 * c) : v4f{1, 1, 1, 1};
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[4 * c + e] = w ? (x[c][e] * inv) * wv[e] : x[c][e] * inv;
+    }
+#pragma unroll
+    for (int c = 0; c < NV4; c++) {
+      const v4f cv = *reinterpret_cast<const v4f*>(cos_t + (int64_t)t * HD + DPL * lane + 4 * c);
+      const v4f sv = *reinterpret_cast<const v4f*>(sin_t + (int64_t)t * HD + DPL * lane + 4 * c);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         // v_permlane32_swap of y with itself: lanes < 32 get (own, lane + 32),
         // lanes >= 32 get (lane - 32, own)
-        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(y[e]),
-                                                        __float_as_uint(y[e]), false, false);
-        r[e] = lane < 32 ? -__uint_as_float(p[1]) : __uint_as_float(p[0]);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        float a = y[e] * c[e];
-        float b = r[e] * s[e];
-        y[e] = a + b;
+        const float ye = y[4 * c + e];
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(ye), __float_as_uint(ye),
+                                                        false, false);
+        const float r = lane < 32 ? -__uint_as_float(p[1]) : __uint_as_float(p[0]);
+        const float a = ye * cv[e];
+        const float b = r * sv[e];
+        y[4 * c + e] = a + b;
       }
     }
   }
-  const v4h yh = {(f16)y[0], (f16)y[1], (f16)y[2], (f16)y[3]};
-  f16* out = kind == 0 ? q16 : k16;
-  *reinterpret_cast<v4h*>(out + ((int64_t)head * Tp + t) * QKV_HD + 4 * lane) = yh;
+  f16* out = (kind == 0 ? q16 : k16) + ((int64_t)head * Tp + t) * HD + DPL * lane;
+#pragma unroll
+  for (int c = 0; c < NV4; c++) {
+    const v4h yh = {(f16)y[4 * c], (f16)y[4 * c + 1], (f16)y[4 * c + 2], (f16)y[4 * c + 3]};
+    *reinterpret_cast<v4h*>(out + 4 * c) = yh;
+  }
 }
 
 hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
                            int64_t hd, const float* qnw, const float* knw, float eps,
                            const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
                            uint16_t* vt16, hipStream_t s) {
-  if (hd != QKV_HD) return hipErrorInvalidValue;
   if (Tp % 64 != 0) return hipErrorInvalidValue;
   const int64_t qk_blocks = (Tp * (nq + nkv) + 3) / 4;
   const int64_t v_blocks = (nkv * (Tp / QKV_V_TOK) + 3) / 4;
-  qkv_post_kernel<<<(unsigned)(qk_blocks + v_blocks), 256, 0, s>>>(
-      qkv, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
-      reinterpret_cast<f16*>(q16), reinterpret_cast<f16*>(k16),
-      reinterpret_cast<f16*>(vt16), (int)qk_blocks);
+  const unsigned grid = (unsigned)(qk_blocks + v_blocks);
+  if (hd == 256)
+    qkv_post_kernel<256><<<grid, 256, 0, s>>>(
+        qkv, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
+        reinterpret_cast<f16*>(q16), reinterpret_cast<f16*>(k16), reinterpret_cast<f16*>(vt16),
+        (int)qk_blocks);
+  else if (hd == 512)
+    qkv_post_kernel<512><<<grid, 256, 0, s>>>(
+        qkv, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
+        reinterpret_cast<f16*>(q16), reinterpret_cast<f16*>(k16), reinterpret_cast<f16*>(vt16),
+        (int)qk_blocks);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
@@ -210,9 +244,8 @@ constexpr int AK = 32;            // keys per tile
 constexpr float ATTN_TAU = 8.0f;  // lazy-rescale threshold (natural log): p <= e^8 ~ 2981
 static_assert(ATTN_TP_ALIGN % 64 == 0, "query blocks (16 or 64) must tile the padded length");
 // Short sequences use 16-query blocks (more blocks to spread), long ones
-// 64-query blocks (each K/V tile serves 4x the queries).
+// 64-query blocks (each K/V tile serves 4x the queries; head_dim 256).
 constexpr int64_t ATTN_SMALL_T = 1024;
-inline int attn_qs(int64_t T) { return T <= ATTN_SMALL_T ? 1 : 4; }
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
 
@@ -250,15 +283,23 @@ __device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
 // V^T rows are 64 B (4 chunks); the O^T tiles read rows 16 t + l16.
 __device__ __forceinline__ int vswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-template <int G, int AQS>
+// HD = 512: the K and V^T tiles are 32 KB each, so the ring has two slots
+// (128 KB) and each block is one 16-query row of waves (AQS = 1): the next
+// tile's DMA overlaps the current tile's S^T, softmax and PV.
+template <int HD, int G, int AQS>
 __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     const f16* __restrict__ q16, const f16* __restrict__ kk, const f16* __restrict__ vt,
     float* __restrict__ part_o, float* __restrict__ part_ml, int T, int Tp, int nq, int nkv,
     int window, int kb_per_part, int kparts) {
+  static_assert(HD == 256 || HD == 512, "head dims 256 and 512");
   constexpr int NWV = G * AQS;
   constexpr int AQB = 16 * AQS;
-  constexpr int RING = 3;
-  constexpr int TILE_H = AK * QKV_HD;   // halves per K (or V^T) tile: 16 KB
+  constexpr int RING = HD == 256 ? 3 : 2;
+  constexpr int TILE_H = AK * HD;        // halves per K (or V^T) tile: 16 or 32 KB
+  constexpr int KU = HD / 16;            // 1 KB DMA units per K tile (= per V^T tile)
+  constexpr int UNITS = 2 * KU;
+  constexpr int KLPR = HD / 8;           // lanes (16-byte chunks) per K row
+  constexpr int KRPU = 64 / KLPR;        // K rows per unit
   __shared__ __attribute__((aligned(16))) f16 Ks[RING][TILE_H];
   __shared__ __attribute__((aligned(16))) f16 Vs[RING][TILE_H];
 
@@ -291,52 +332,50 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
   const int kb1 = kb0 + kb_per_part < kb_hi ? kb0 + kb_per_part : kb_hi;
 
   // Q fragments (B operand of S^T = K Q^T): query qi, dims 32 s + 8 lq .. +7
-  v8h qf[QKV_HD / 32];
+  v8h qf[HD / 32];
   {
-    const int64_t off = ((int64_t)h * Tp + qi) * QKV_HD + 8 * lq;
+    const int64_t off = ((int64_t)h * Tp + qi) * HD + 8 * lq;
 #pragma unroll
-    for (int s = 0; s < QKV_HD / 32; s++) qf[s] = *reinterpret_cast<const v8h*>(q16 + off + 32 * s);
+    for (int s = 0; s < HD / 32; s++) qf[s] = *reinterpret_cast<const v8h*>(q16 + off + 32 * s);
   }
 
-  const f16* kbase = kk + (int64_t)g * Tp * QKV_HD;
-  const f16* vbase = vt + (int64_t)g * QKV_HD * Tp;
-  // A tile is 16 K units (2 key rows each) + 16 V^T units (16 dim rows each),
-  // 1 KB per unit; wave w issues units w, w + NWV, ...  Per-lane byte offsets
-  // are fixed; the tile moves the (uniform) base.
-  constexpr int UPWA = (32 + NWV - 1) / NWV;
+  const f16* kbase = kk + (int64_t)g * Tp * HD;
+  const f16* vbase = vt + (int64_t)g * HD * Tp;
+  // A tile is KU K units (KRPU key rows each) + KU V^T units (16 dim rows
+  // each), 1 KB per unit; wave w issues units w, w + NWV, ...  Per-lane byte
+  // offsets are fixed; the tile moves the (uniform) base.
+  constexpr int UPWA = (UNITS + NWV - 1) / NWV;
   int uoff[UPWA];
 #pragma unroll
   for (int j = 0; j < UPWA; j++) {
     const int u = w + NWV * j;
-    if (u < 16) {
-      const int row = 2 * u + (lane >> 5), pc = lane & 31;
-      uoff[j] = (row * QKV_HD + ((pc ^ kswz(row)) << 3)) * 2;
+    if (u < KU) {
+      const int row = KRPU * u + lane / KLPR, pc = lane % KLPR;
+      uoff[j] = (row * HD + ((pc ^ kswz(row)) << 3)) * 2;
     } else {
-      const int row = 16 * (u - 16) + (lane >> 2), pc = lane & 3;
+      const int row = 16 * (u - KU) + (lane >> 2), pc = lane & 3;
       uoff[j] = (row * Tp + ((pc ^ vswz(row)) << 3)) * 2;
     }
   }
   auto issue = [&](int kb, int sl) {
     const int k0 = kb * AK;
-    const f16* kb_base = kbase + (int64_t)k0 * QKV_HD;
+    const f16* kb_base = kbase + (int64_t)k0 * HD;
     const f16* vb_base = vbase + k0;
 #pragma unroll
     for (int j = 0; j < UPWA; j++) {
       const int u = w + NWV * j;
-      if (u < 32) {
-        const f16* dst = u < 16 ? &Ks[sl][u * 512] : &Vs[sl][(u - 16) * 512];
-        dma16(reinterpret_cast<const int8_t*>(u < 16 ? kb_base : vb_base), uoff[j],
+      if (u < UNITS) {
+        const f16* dst = u < KU ? &Ks[sl][u * 512] : &Vs[sl][(u - KU) * 512];
+        dma16(reinterpret_cast<const int8_t*>(u < KU ? kb_base : vb_base), uoff[j],
               lds_u32(dst));
       }
     }
   };
-  if (kb0 < kb1) issue(kb0, 0);
-  if (kb0 + 1 < kb1) issue(kb0 + 1, 1);
 
   float m_run = -INFINITY, l_run = 0.0f;
-  v4f_ o[QKV_HD / 16];   // O^T: dims 16 t + 4 lq + r of query qi
+  v4f_ o[HD / 16];   // O^T: dims 16 t + 4 lq + r of query qi
 #pragma unroll
-  for (int t = 0; t < QKV_HD / 16; t++) o[t] = v4f_{0, 0, 0, 0};
+  for (int t = 0; t < HD / 16; t++) o[t] = v4f_{0, 0, 0, 0};
 
   // S^T of the tile in slot sl: sacc[kt][r] = S[qi][k0 + 8 lq + 4 kt + r]
   auto scores = [&](int sl, v4f_ (&sacc)[2]) {
@@ -344,41 +383,20 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     sacc[0] = v4f_{0, 0, 0, 0};
     sacc[1] = v4f_{0, 0, 0, 0};
 #pragma unroll
-    for (int s = 0; s < QKV_HD / 32; s++) {
+    for (int s = 0; s < HD / 32; s++) {
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
         const int row = 8 * (l16 >> 2) + 4 * kt + (l16 & 3);
-        const v8h kf = *reinterpret_cast<const v8h*>(Kt + row * QKV_HD +
+        const v8h kf = *reinterpret_cast<const v8h*>(Kt + row * HD +
                                                      (((4 * s + lq) ^ kswz(row)) << 3));
         sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[s], sacc[kt], 0, 0, 0);
       }
     }
   };
 
-  // Software pipeline over key tiles, slot = (kb - kb0) % 3: iteration kb
-  // issues S^T of tile kb+1, runs the softmax of tile kb, then O^T += V^T P^T
-  // for tile kb; tile kb+2 is in flight meanwhile.
-  const int my_units = (32 - w + NWV - 1) / NWV;   // this wave's DMAs per tile
-  v4f_ sacc[2];
-  if (kb0 < kb1) {
-    if (kb0 + 1 >= kb1)
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    else if (my_units == (32 + NWV - 1) / NWV)
-      asm volatile("s_waitcnt vmcnt(%0)" :: "n"((32 + NWV - 1) / NWV) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(%0)" :: "n"(32 / NWV) : "memory");
-    __syncthreads();
-    scores(0, sacc);
-  }
-  for (int kb = kb0, sl = 0; kb < kb1; kb++, sl = sl == RING - 1 ? 0 : sl + 1) {
-    const int sl1 = sl == RING - 1 ? 0 : sl + 1;
-    v4f_ snext[2];
-    if (kb + 1 < kb1) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kb+1 has landed
-      __syncthreads();   // ... for every wave; tile kb-1's slot is free
-      if (kb + 2 < kb1) issue(kb + 2, sl == 0 ? RING - 1 : sl - 1);
-      scores(sl1, snext);
-    }
+  // Softmax of one S^T tile (mask, lazy-rescaled online statistics) and
+  // O^T += V^T P^T with the tile's V^T in slot sl.
+  auto softmax_pv = [&](int kb, int sl, v4f_ (&sacc)[2]) {
     const f16* Vt = Vs[sl];
     const int k0 = kb * AK;
     // ---- mask (only where a key of the tile can be out of range or band)
@@ -425,27 +443,70 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     m_run = m_new;
     if (__any(alpha != 1.0f)) {
 #pragma unroll
-      for (int t = 0; t < QKV_HD / 16; t++)
+      for (int t = 0; t < HD / 16; t++)
 #pragma unroll
         for (int r = 0; r < 4; r++) o[t][r] *= alpha;
     }
     // ---- O^T += V^T P^T: A = V^T[16 t + l16][keys 8 lq .. +7]
 #pragma unroll
-    for (int t = 0; t < QKV_HD / 16; t++) {
+    for (int t = 0; t < HD / 16; t++) {
       const int row = 16 * t + l16;
       const v8h vf = *reinterpret_cast<const v8h*>(Vt + row * AK + ((lq ^ vswz(row)) << 3));
       o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[t], 0, 0, 0);
     }
-    sacc[0] = snext[0];
-    sacc[1] = snext[1];
+  };
+
+  v4f_ sacc[2];
+  if constexpr (RING == 3) {
+    // Software pipeline over key tiles, slot = (kb - kb0) % 3: iteration kb
+    // issues S^T of tile kb+1, runs the softmax of tile kb, then O^T += V^T P^T
+    // for tile kb; tile kb+2 is in flight meanwhile.
+    if (kb0 < kb1) issue(kb0, 0);
+    if (kb0 + 1 < kb1) issue(kb0 + 1, 1);
+    const int my_units = (UNITS - w + NWV - 1) / NWV;   // this wave's DMAs per tile
+    if (kb0 < kb1) {
+      if (kb0 + 1 >= kb1)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      else if (my_units == (UNITS + NWV - 1) / NWV)
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"((UNITS + NWV - 1) / NWV) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%0)" :: "n"(UNITS / NWV) : "memory");
+      __syncthreads();
+      scores(0, sacc);
+    }
+    for (int kb = kb0, sl = 0; kb < kb1; kb++, sl = sl == RING - 1 ? 0 : sl + 1) {
+      const int sl1 = sl == RING - 1 ? 0 : sl + 1;
+      v4f_ snext[2];
+      if (kb + 1 < kb1) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kb+1 has landed
+        __syncthreads();   // ... for every wave; tile kb-1's slot is free
+        if (kb + 2 < kb1) issue(kb + 2, sl == 0 ? RING - 1 : sl - 1);
+        scores(sl1, snext);
+      }
+      softmax_pv(kb, sl, sacc);
+      sacc[0] = snext[0];
+      sacc[1] = snext[1];
+    }
+  } else {
+    // Two slots: iteration kb waits for tile kb, then issues tile kb+1 into the
+    // other slot (free: every wave has passed tile kb-1's PV, the barrier
+    // says) and runs S^T, softmax and PV of tile kb under that DMA.
+    if (kb0 < kb1) issue(kb0, 0);
+    for (int kb = kb0, sl = 0; kb < kb1; kb++, sl ^= 1) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // tile kb has landed
+      __syncthreads();
+      if (kb + 1 < kb1) issue(kb + 1, sl ^ 1);
+      scores(sl, sacc);
+      softmax_pv(kb, sl, sacc);
+    }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- partial results: query qi, dims 16 t + 4 lq .. +3
   const int64_t prow = (int64_t)kp * Tp + qi;
 #pragma unroll
-  for (int t = 0; t < QKV_HD / 16; t++)
-    *reinterpret_cast<v4f_*>(part_o + prow * nq * QKV_HD + (int64_t)h * QKV_HD + 16 * t + 4 * lq) =
+  for (int t = 0; t < HD / 16; t++)
+    *reinterpret_cast<v4f_*>(part_o + prow * nq * HD + (int64_t)h * HD + 16 * t + 4 * lq) =
         o[t];
   if (lq == 0) {
     part_ml[(prow * nq + h) * 2] = m_run;
@@ -454,18 +515,21 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
 }
 
 // One wave per (token, head): merge the partitions in order p = 0, 1, ...;
-// emit f32 ctx and/or the head's 256 columns of the Q8_0 operand.  Lane p
-// holds partition p's (m, l); readlane broadcasts them.
+// emit f32 ctx and/or the head's HD columns of the Q8_0 operand.  Lane p
+// holds partition p's (m, l); readlane broadcasts them.  Lane l owns dims
+// DPL l .. DPL l + DPL-1 (DPL = HD / 64), so a Q8_0 block is 32 / DPL lanes.
+template <int HD>
 __global__ void __launch_bounds__(256) attn_combine_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml, int T, int Tp, int nq,
     int kparts, float* __restrict__ ctx, int8_t* __restrict__ cq, float* __restrict__ dc,
     uint16_t* __restrict__ cb) {
+  constexpr int DPL = HD / 64;
   const int lane = threadIdx.x & 63;
   const int64_t task = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (task >= (int64_t)T * nq) return;
   const int64_t q = task / nq;
   const int h = (int)(task % nq);
-  const int width = nq * QKV_HD;
+  const int width = nq * HD;
   float mp = -INFINITY, lp = 0.0f;
   if (lane < kparts) {
     const int64_t r = ((int64_t)lane * Tp + q) * nq + h;
@@ -477,53 +541,72 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
     M = fmaxf(M, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mp), p)));
   const float wl = mp == -INFINITY ? 0.0f : __expf(mp - M);
   float L = 0.0f;
-  v4f acc = {0, 0, 0, 0};
-  const float* src = part_o + q * width + h * QKV_HD + 4 * lane;
+  float acc[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; e++) acc[e] = 0.0f;
+  const float* src = part_o + q * width + h * HD + DPL * lane;
   for (int p = 0; p < kparts; p++) {
     const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), p));
     L += wgt * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lp), p));
-    const v4f v = *reinterpret_cast<const v4f*>(src + (int64_t)p * Tp * width);
 #pragma unroll
-    for (int e = 0; e < 4; e++) acc[e] += wgt * v[e];
+    for (int c = 0; c < DPL / 4; c++) {
+      const v4f v = *reinterpret_cast<const v4f*>(src + (int64_t)p * Tp * width + 4 * c);
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[4 * c + e] += wgt * v[e];
+    }
   }
   const float inv = 1.0f / L;
-  v4f y;
+  float y[DPL];
 #pragma unroll
-  for (int e = 0; e < 4; e++) y[e] = acc[e] * inv;
-  const int64_t col = (int64_t)h * QKV_HD + 4 * lane;
-  if (ctx) *reinterpret_cast<v4f*>(ctx + q * width + col) = y;
+  for (int e = 0; e < DPL; e++) y[e] = acc[e] * inv;
+  const int64_t col = (int64_t)h * HD + DPL * lane;
+  if (ctx) {
+#pragma unroll
+    for (int c = 0; c < DPL / 4; c++)
+      *reinterpret_cast<v4f*>(ctx + q * width + col + 4 * c) =
+          v4f{y[4 * c], y[4 * c + 1], y[4 * c + 2], y[4 * c + 3]};
+  }
   if (cb) {
     // bf16, round to nearest even (the dense-bf16 o projection's operand)
     uint32_t* dst = reinterpret_cast<uint32_t*>(cb + q * width + col);
-    dst[0] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[0]) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[1]) << 16);
-    dst[1] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[2]) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[3]) << 16);
+#pragma unroll
+    for (int e = 0; e < DPL / 2; e++)
+      dst[e] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[2 * e]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y[2 * e + 1]) << 16);
   }
   if (cq) {
     float a = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(y[e]));
-    a = max8(a);
+    for (int e = 0; e < DPL; e++) a = fmaxf(a, fabsf(y[e]));
+    a = DPL == 4 ? max8(a) : max4(a);
     QScale sc = q8_scale(a);
-    uint32_t packed = 0;
+    uint32_t packed[DPL / 4];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-      packed |= ((uint32_t)(quant_round(y[e] * sc.id) & 0xFF)) << (8 * e);
-    *reinterpret_cast<uint32_t*>(cq + q * width + col) = packed;
-    if ((lane & 7) == 0) dc[q * (width / QK) + (col >> 5)] = sc.dq;
+    for (int c = 0; c < DPL / 4; c++) {
+      packed[c] = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        packed[c] |= ((uint32_t)(quant_round(y[4 * c + e] * sc.id) & 0xFF)) << (8 * e);
+    }
+#pragma unroll
+    for (int c = 0; c < DPL / 4; c++)
+      *reinterpret_cast<uint32_t*>(cq + q * width + col + 4 * c) = packed[c];
+    if ((lane & (32 / DPL - 1)) == 0) dc[q * (width / QK) + (col >> 5)] = sc.dq;
   }
 }
 
-// Key tiles per partition: enough partitions for ~2 blocks per CU, at least
-// two tiles each, and at most 64 tiles (2 MB of K and V) so one partition's
-// K/V stays in an XCD's L2.
 // Key partitions: enough (query block, partition) items for one round of
-// workgroups (one 96 KB-LDS block per CU on 256 CUs), at most half the key
-// tiles per partition and at most 64 partitions.
+// workgroups (256 CUs), at most half the key tiles per partition and at most
+// 64 partitions (the combine holds one partition per lane).
 constexpr int64_t ATTN_BLOCKS = 256;
-static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, int* kparts) {
-  const int64_t aqb = 16 * attn_qs(T);
+// Queries per block: 16 AQS.  HD 512 runs one row of 16 queries (its two
+// 32 KB tile slots and 192 accumulator registers per lane leave no room for
+// more waves).
+inline int attn_qs(int64_t T, int64_t hd) { return hd == 512 ? 1 : (T <= ATTN_SMALL_T ? 1 : 4); }
+
+static int attn_kb_per_part(int64_t T, int64_t hd, int64_t nq, int64_t nkv, int64_t window,
+                            int* kparts) {
+  const int64_t aqb = 16 * attn_qs(T, hd);
   const int64_t tp = attn_padded_len(T);
   const int64_t nqb = tp / aqb;
   int64_t nkb = (T + AK - 1) / AK;
@@ -541,54 +624,71 @@ static int attn_kb_per_part(int64_t T, int64_t nq, int64_t nkv, int64_t window, 
 }
 
 bool attention_supported(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window) {
-  if (hd != QKV_HD || nq <= 0 || nkv <= 0 || nq % nkv != 0 || nq / nkv > 4) return false;
+  if ((hd != 256 && hd != 512) || nq <= 0 || nkv <= 0 || nq % nkv != 0 || nq / nkv > 4)
+    return false;
   if (T <= 0) return true;
   int kparts;
-  attn_kb_per_part(T, nq, nkv, window, &kparts);
+  attn_kb_per_part(T, hd, nq, nkv, window, &kparts);
   return kparts <= 64;   // the combine holds one partition per lane
 }
 
 size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window) {
   int kp;
-  attn_kb_per_part(T, nq, nkv, window, &kp);
+  attn_kb_per_part(T, hd, nq, nkv, window, &kp);
   const int64_t tp = attn_padded_len(T);
   return (size_t)(kp * tp * nq * (hd + 2));
+}
+
+template <int HD>
+static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float* scratch,
+                                float* ctx, int8_t* cq, float* dc, int64_t T, int64_t Tp,
+                                int64_t nq, int64_t nkv, int64_t window, hipStream_t s,
+                                uint16_t* cb) {
+  const int64_t G = nq / nkv;
+  const int aqs = attn_qs(T, HD);
+  int kparts;
+  const int per = attn_kb_per_part(T, HD, nq, nkv, window, &kparts);
+  if (kparts > 64) return hipErrorInvalidValue;   // the combine holds one partition per lane
+  float* part_o = scratch;
+  float* part_ml = scratch + (int64_t)kparts * Tp * nq * HD;
+  const int64_t items = nkv * kparts * (Tp / (16 * aqs));
+  const unsigned grid = (unsigned)((items + 7) / 8 * 8);
+#define GLYPR_ATTN_CASE(GG, QS)                                                                  \
+  if (G == GG && aqs == QS)                                                                      \
+    attn_partial_kernel<HD, GG, QS><<<grid, GG * QS * 64, 0, s>>>(                               \
+        q, k, v, part_o, part_ml, (int)T, (int)Tp, (int)nq, (int)nkv, (int)window, per, kparts);
+  if constexpr (HD == 256) {
+    GLYPR_ATTN_CASE(1, 1) else GLYPR_ATTN_CASE(1, 4)
+    else GLYPR_ATTN_CASE(2, 1) else GLYPR_ATTN_CASE(2, 4)
+    else GLYPR_ATTN_CASE(3, 1) else GLYPR_ATTN_CASE(3, 4)
+    else GLYPR_ATTN_CASE(4, 1) else GLYPR_ATTN_CASE(4, 4)
+    else return hipErrorInvalidValue;
+  } else {
+    GLYPR_ATTN_CASE(1, 1) else GLYPR_ATTN_CASE(2, 1)
+    else GLYPR_ATTN_CASE(3, 1) else GLYPR_ATTN_CASE(4, 1)
+    else return hipErrorInvalidValue;
+  }
+#undef GLYPR_ATTN_CASE
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  attn_combine_kernel<HD><<<(unsigned)((T * nq + 3) / 4), 256, 0, s>>>(
+      part_o, part_ml, (int)T, (int)Tp, (int)nq, kparts, ctx, cq, dc, cb);
+  return hipGetLastError();
 }
 
 hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
                             float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
                             int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
                             hipStream_t s, uint16_t* cb) {
-  if (hd != QKV_HD || Tp % ATTN_TP_ALIGN != 0 || Tp < T || nq % nkv != 0)
-    return hipErrorInvalidValue;
-  const int64_t G = nq / nkv;
-  const int aqs = attn_qs(T);
-  int kparts;
-  const int per = attn_kb_per_part(T, nq, nkv, window, &kparts);
-  if (kparts > 64) return hipErrorInvalidValue;   // the combine holds one partition per lane
-  float* part_o = scratch;
-  float* part_ml = scratch + (int64_t)kparts * Tp * nq * QKV_HD;
-  const int64_t items = nkv * kparts * (Tp / (16 * aqs));
-  const unsigned grid = (unsigned)((items + 7) / 8 * 8);
+  if (Tp % ATTN_TP_ALIGN != 0 || Tp < T || nq % nkv != 0) return hipErrorInvalidValue;
   const f16* q = reinterpret_cast<const f16*>(q16);
   const f16* k = reinterpret_cast<const f16*>(k16);
   const f16* v = reinterpret_cast<const f16*>(vt16);
-#define GLYPR_ATTN_CASE(GG, QS)                                                              \
-  if (G == GG && aqs == QS)                                                                  \
-    attn_partial_kernel<GG, QS><<<grid, GG * QS * 64, 0, s>>>(q, k, v, part_o, part_ml, (int)T, \
-                                                             (int)Tp, (int)nq, (int)nkv,       \
-                                                             (int)window, per, kparts);
-  GLYPR_ATTN_CASE(1, 1) else GLYPR_ATTN_CASE(1, 4)
-  else GLYPR_ATTN_CASE(2, 1) else GLYPR_ATTN_CASE(2, 4)
-  else GLYPR_ATTN_CASE(3, 1) else GLYPR_ATTN_CASE(3, 4)
-  else GLYPR_ATTN_CASE(4, 1) else GLYPR_ATTN_CASE(4, 4)
-  else return hipErrorInvalidValue;
-#undef GLYPR_ATTN_CASE
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  attn_combine_kernel<<<(unsigned)((T * nq + 3) / 4), 256, 0, s>>>(
-      part_o, part_ml, (int)T, (int)Tp, (int)nq, kparts, ctx, cq, dc, cb);
-  return hipGetLastError();
+  if (hd == 256)
+    return run_attention<256>(q, k, v, scratch, ctx, cq, dc, T, Tp, nq, nkv, window, s, cb);
+  if (hd == 512)
+    return run_attention<512>(q, k, v, scratch, ctx, cq, dc, T, Tp, nq, nkv, window, s, cb);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace glypr

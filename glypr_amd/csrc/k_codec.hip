@@ -101,10 +101,64 @@ hipError_t launch_dequant(const int8_t* qs, const float* dw, int64_t rows, int64
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Token-row gather (Embedding::forward x embed_scale): out[r] =
+// ((float)q * f32(d)) * scale + 0 for table row ids[r], the dequant kernel's
+// arithmetic.  The write of the f32 rows is 80 % of the bytes, so every store
+// instruction covers 1 KB of contiguous output: lane l of a wave handles 4
+// int8 values (one 32-bit load) and writes them as one 16-byte store, and a
+// block of k/4 lanes covers a row.  Each block walks GATHER_ROWS rows with all
+// their loads issued before the stores, so several rows are in flight per
+// wave; the row ids are block-uniform scalar loads.
+// ---------------------------------------------------------------------------
+constexpr int GATHER_ROWS = 8;
+
+__global__ void __launch_bounds__(256) gather_rows_kernel(const int8_t* __restrict__ qs,
+                                                          const float* __restrict__ dw, int k,
+                                                          const uint32_t* __restrict__ ids,
+                                                          int64_t rows, float scale,
+                                                          float* __restrict__ out) {
+  const int lanes_per_row = k >> 2;
+  const int c = threadIdx.x;   // 4-value column group
+  if (c >= lanes_per_row) return;
+  const int64_t r0 = (int64_t)blockIdx.x * GATHER_ROWS;
+  const int nb = k >> 5;
+  int q[GATHER_ROWS];
+  float d[GATHER_ROWS];
+#pragma unroll
+  for (int i = 0; i < GATHER_ROWS; i++) {
+    const int64_t r = r0 + i;
+    if (r < rows) {
+      const int64_t src = (int64_t)ids[r];
+      q[i] = *reinterpret_cast<const int*>(qs + src * k + 4 * c);
+      d[i] = dw[src * nb + (c >> 3)];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < GATHER_ROWS; i++) {
+    const int64_t r = r0 + i;
+    if (r >= rows) break;
+    v4f o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float y = (float)(int8_t)((q[i] >> (8 * e)) & 0xFF) * d[i];
+      o[e] = y * scale + 0.0f;
+    }
+    *reinterpret_cast<v4f*>(out + r * k + 4 * c) = o;
+  }
+}
+
 hipError_t launch_gather(const int8_t* qs, const float* dw, int64_t k, const uint32_t* ids,
                          int64_t n_ids, float scale, float* out, hipStream_t s) {
-  int64_t work = n_ids * (k / 16);
-  if (work == 0) return hipSuccess;
+  if (n_ids == 0) return hipSuccess;
+  if (k % 32 == 0 && k / 4 <= 256) {
+    const int threads = (int)((k / 4 + 63) / 64 * 64);
+    const int64_t blocks = (n_ids + GATHER_ROWS - 1) / GATHER_ROWS;
+    gather_rows_kernel<<<(unsigned)blocks, threads, 0, s>>>(qs, dw, (int)k, ids, n_ids, scale,
+                                                            out);
+    return hipGetLastError();
+  }
+  const int64_t work = n_ids * (k / 16);
   dequant_rows_kernel<true><<<grid_for(work, 256, 65536), 256, 0, s>>>(qs, dw, k, ids, n_ids,
                                                                        scale, out);
   return hipGetLastError();

@@ -300,7 +300,7 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 // chunk (i%8) ^ (row & 7).  Rows past M/N are clamped to a valid row (their
 // outputs are never stored).
 // ---------------------------------------------------------------------------
-constexpr int SMALL_NB_MAX = 36;   // K <= 1152
+constexpr int SMALL_NB_MAX = 64;   // K <= 2048
 
 // WM x WN waves; wave (wm, wn) owns rows 16 wm.. and TNW 16-row B tiles.
 // GEGLU: TNW == 2 (gate tile, up tile of the same 16 h columns) and WN == 2:
@@ -324,7 +324,7 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   constexpr int UA = BM / 8, UB = BN / 8;   // 1 KB DMA units per stage
   constexpr int UPW = (UA + UB) / NW;
   constexpr int SA = NB * BM, SB = NB * BN;
-  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 1152");
+  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 2048");
   static_assert((UA + UB) % NW == 0, "stage units must split evenly over the waves");
   static_assert(RING >= 2, "ring needs >= 2 slots");
   static_assert(!GEGLU || (TNW == 2 && WN == 2), "GeGLU tile: 2 waves x (gate, up)");
@@ -510,7 +510,9 @@ hipError_t run_small_nb(const int8_t* xq, const float* dx, const int8_t* wq, con
   return hipGetLastError();
 }
 
-// K is a multiple of 128 and <= 1152 (small_ok).
+// K is a multiple of 128 and <= 2048 (small_ok): the BASELINE widths (768,
+// 1152) and the released EmbeddingGemma-2's (512; 2048 for its down and
+// full-layer o projections).
 template <int WM, int WN, int TNW, bool GEGLU, int RING>
 hipError_t run_small(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                      float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K,
@@ -529,6 +531,8 @@ hipError_t run_small(const int8_t* xq, const float* dx, const int8_t* wq, const 
     GLYPR_SMALL_NB(28)
     GLYPR_SMALL_NB(32)
     GLYPR_SMALL_NB(36)
+    GLYPR_SMALL_NB(48)
+    GLYPR_SMALL_NB(64)
     default:
       return hipErrorInvalidValue;
   }
@@ -541,8 +545,9 @@ hipError_t run_small(const int8_t* xq, const float* dx, const int8_t* wq, const 
 constexpr int64_t SMALL_M_MAX = 2048;
 constexpr int64_t SMALL_K_MAX = 32 * SMALL_NB_MAX;
 inline bool small_ok(int64_t M, int64_t Nrows, int64_t K) {
+  const int64_t nb = K / QK;
   return M <= SMALL_M_MAX && K <= SMALL_K_MAX && K % BK == 0 &&
-         Nrows * K < (int64_t(1) << 31);
+         (nb <= 36 || nb == 48 || nb == 64) && Nrows * K < (int64_t(1) << 31);
 }
 
 // ---------------------------------------------------------------------------
@@ -582,7 +587,7 @@ gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, fl
   constexpr int LPR = NW * 64 / BM;        // lanes per row in the prologue
   constexpr int PARTS = LPR / 8;           // 8-lane groups per row
   constexpr int BPP = NB / PARTS;          // blocks per group
-  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 1152");
+  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 2048");
   static_assert(UB % NW == 0 && RING >= 2, "stage units must split evenly over the waves");
   static_assert(LPR >= 8 && LPR <= 64 && NB % PARTS == 0, "prologue lane layout");
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
@@ -1081,14 +1086,14 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
 // while the saved launch outweighs that repetition (measured on MI355X at
 // EmbeddingGemma widths: quantize up to M = 1024, RMSNorm up to M = 256).
 bool gemm_i8_pro_ok(int64_t M, int64_t N, int64_t K, bool norm) {
-  return small_ok(M, N, K) && M <= (norm ? 256 : 1024);
+  return small_ok(M, N, K) && K <= 1152 && M <= (norm ? 256 : 1024);
 }
 
 hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
                               const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
                               int64_t K, int64_t ldc, hipStream_t s) {
   if (M == 0 || N == 0) return hipSuccess;
-  if (!small_ok(M, N, K)) return hipErrorInvalidValue;
+  if (!gemm_i8_pro_ok(M, N, K, norm)) return hipErrorInvalidValue;
   if (norm) return run_pro<PRO_NORM, 4, 2, 3>(x, nw, eps, wq, dw, y, M, N, K, ldc, s);
   return run_pro<PRO_QUANT, 4, 2, 3>(x, nullptr, 0.0f, wq, dw, y, M, N, K, ldc, s);
 }

@@ -395,7 +395,7 @@ int glypr_hip_attention(glypr_hip_ctx* ctx, const float* qkv, const float* q_nor
               (long long)n_kv_heads);
   GLYPR_CHECK(attention_supported(t, n_heads, n_kv_heads, head_dim, window),
               GLYPR_ERR_UNSUPPORTED,
-              "attention geometry not supported: head_dim %lld (256 is supported), %lld q "
+              "attention geometry not supported: head_dim %lld (256 and 512 are supported), %lld q "
               "heads per kv head (at most 4), t = %lld", (long long)head_dim,
               (long long)(n_heads / n_kv_heads), (long long)t);
   GLYPR_CHECK(t == 0 || (qkv && cos_table && sin_table && ctx_out), GLYPR_ERR_INVALID_ARG,
@@ -454,8 +454,9 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
                   attention_supported(c.max_seq_len, c.n_heads, c.full_n_kv_heads,
                                       c.full_head_dim, 0),
               GLYPR_ERR_UNSUPPORTED,
-              "attention geometry not supported: head_dim %lld / %lld (sliding / full; 256 is "
-              "supported), %lld q heads over %lld / %lld kv heads (at most 4 per kv head)",
+              "attention geometry not supported: head_dim %lld / %lld (sliding / full; 256 and "
+              "512 are supported), %lld q heads over %lld / %lld kv heads (at most 4 per kv "
+              "head)",
               (long long)c.head_dim, (long long)c.full_head_dim, (long long)c.n_heads,
               (long long)c.n_kv_heads, (long long)c.full_n_kv_heads);
   RET_IF(check_ctx(ctx));

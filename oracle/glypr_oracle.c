@@ -642,9 +642,13 @@ static void orc_linear(const uint8_t* w, int64_t n, int64_t k, const float* x, i
 
 void orc_encoder_layer(const orc_model_config* cfg, const orc_layer_weights* w, int64_t layer_idx,
                        float* hidden, const float* per_layer_input, int64_t t, int threads) {
-  int64_t H = cfg->hidden, F = cfg->ffn, nh = cfg->n_heads, nkv = cfg->n_kv_heads,
-          hd = cfg->head_dim;
   int full = orc_layer_is_full(layer_idx);
+  /* per-layer geometry: full-attention layers take their own head_dim and kv
+   * head count (TextConfig::get_head_dim / get_num_kv_heads, config.rs:142-169,
+   * 208-230; model.rs:286-287), the RoPE table of their head_dim */
+  int64_t H = cfg->hidden, F = cfg->ffn, nh = cfg->n_heads,
+          nkv = full && cfg->full_n_kv_heads ? cfg->full_n_kv_heads : cfg->n_kv_heads,
+          hd = full && cfg->full_head_dim ? cfg->full_head_dim : cfg->head_dim;
   float* normed = (float*)malloc((size_t)(t * H) * sizeof(float));
   float* qb = (float*)malloc((size_t)(t * nh * hd) * sizeof(float));
   float* kb = (float*)malloc((size_t)(t * nkv * hd) * sizeof(float));

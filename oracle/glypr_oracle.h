@@ -148,10 +148,14 @@ typedef struct {
   double rope_theta_full;    /* 1e6 */
   int64_t ple_dim;      /* hidden_size_per_layer_input; 0 = no PLE (configs 4-5) */
   int64_t out_dim;      /* rows of output.weight; 0 = no embedding projection */
+  int64_t full_head_dim;   /* full-attention layers' head_dim (config.rs:149-166); 0 = head_dim */
+  int64_t full_n_kv_heads; /* full-attention layers' kv heads (config.rs:151-157); 0 = n_kv_heads */
 } orc_model_config;
 
 /* Per-layer weights, host memory.  Q8_0 tensors are GGUF blocks. */
 typedef struct {
+  /* head_dim / n_kv of the layer's type (TextConfig::get_head_dim /
+   * get_num_kv_heads, config.rs:208-230) */
   const uint8_t* q;     /* [n_heads*head_dim][hidden] */
   const uint8_t* k;     /* [n_kv*head_dim][hidden] */
   const uint8_t* v;     /* [n_kv*head_dim][hidden] */

@@ -46,7 +46,8 @@ class ModelConfig(ctypes.Structure):
                 ("head_dim", _i64), ("n_layers", _i64), ("vocab", _i64),
                 ("sliding_window", _i64), ("eps", ctypes.c_float),
                 ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double),
-                ("ple_dim", _i64), ("out_dim", _i64)]
+                ("ple_dim", _i64), ("out_dim", _i64), ("full_head_dim", _i64),
+                ("full_n_kv_heads", _i64)]
 
 
 class LayerWeights(ctypes.Structure):
@@ -389,7 +390,8 @@ def attention(q, k, v, window: int, threads: int = 0):
 def model_forward(tensors: dict, ids: np.ndarray, trunc: int, *, hidden: int, ffn: int,
                   n_heads: int, n_kv_heads: int, head_dim: int, n_layers: int, vocab: int,
                   sliding_window: int = 512, eps: float = 1e-6, theta_sliding: float = 1e4,
-                  theta_full: float = 1e6, threads: int = 0):
+                  theta_full: float = 1e6, full_head_dim: int = 0, full_n_kv_heads: int = 0,
+                  threads: int = 0):
     """orc_model_forward over GGUF-named tensors {name: array} (Q8_0 tensors as
     block bytes, norms as f32).  The PLE block runs when
     `per_layer_model_proj.weight` is present (ple_dim = its rows / n_layers),
@@ -402,7 +404,8 @@ def model_forward(tensors: dict, ids: np.ndarray, trunc: int, *, hidden: int, ff
     cfg = ModelConfig(hidden=hidden, ffn=ffn, n_heads=n_heads, n_kv_heads=n_kv_heads,
                       head_dim=head_dim, n_layers=n_layers, vocab=vocab,
                       sliding_window=sliding_window, eps=eps, rope_theta_sliding=theta_sliding,
-                      rope_theta_full=theta_full, ple_dim=ple_dim, out_dim=out_dim)
+                      rope_theta_full=theta_full, ple_dim=ple_dim, out_dim=out_dim,
+                      full_head_dim=full_head_dim, full_n_kv_heads=full_n_kv_heads)
     keep = []
 
     def arr(name, dt, ptype):

@@ -195,6 +195,13 @@ def test_attention_geometry_validation():
                                     ctypes.byref(out)) == _lib.GLYPR_ERR_SHAPE
     assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(head_dim=128)),
                                     ctypes.byref(out)) == _lib.GLYPR_ERR_UNSUPPORTED
+    # the released geometry: full layers with head_dim 512 and one kv head pass
+    real = _cfg(hidden=512, ffn=2048, n_heads=4, n_kv_heads=2, full_head_dim=512,
+                full_n_kv_heads=1)
+    assert L.glypr_hip_model_create(NULL, ctypes.byref(real), ctypes.byref(out)) == \
+        _lib.GLYPR_ERR_INVALID_ARG
+    assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(full_head_dim=384)),
+                                    ctypes.byref(out)) == _lib.GLYPR_ERR_UNSUPPORTED
     assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(max_seq_len=-1)),
                                     ctypes.byref(out)) == _lib.GLYPR_ERR_SHAPE
     # glypr_hip_attention: the same geometry rule, checked before the pointers
@@ -204,6 +211,7 @@ def test_attention_geometry_validation():
     assert L.glypr_hip_attention(*args(3, 1, 128)) == _lib.GLYPR_ERR_UNSUPPORTED
     assert L.glypr_hip_attention(*args(3, 2, 256)) == _lib.GLYPR_ERR_SHAPE
     assert L.glypr_hip_attention(*args(4, 1, 256)) == _lib.GLYPR_ERR_INVALID_ARG   # ctx NULL
+    assert L.glypr_hip_attention(*args(4, 1, 512)) == _lib.GLYPR_ERR_INVALID_ARG
 
 
 def test_gemm_routing():
@@ -227,6 +235,10 @@ def test_gemm_routing():
     assert route(4096, big_n - 1, 1024, 0) == BIG
     assert route(64, 64, 1024, 0) == SMALL
     assert route(4096, 64, 96, 0) in (REG128, REG64)   # K % 128 != 0
+    # the released EmbeddingGemma-2 widths: K = 2048 (down, full-layer o) stays small-M
+    assert route(512, 512, 2048, 0) == SMALL and route(512, 512, 1536, 0) == SMALL
+    assert route(512, 512, 1280, 0) == BIG               # no 40-block small instantiation
+    assert route(512, 512, 2048, 1) == -1                 # the fused prologue stops at 1152
     # the fused prologue: quantize up to M = 1024, RMSNorm up to M = 256
     assert route(1024, 768, 768, 1) == PRO and route(1025, 768, 768, 1) == -1
     assert route(256, 1280, 768, 2) == PRO and route(257, 1280, 768, 2) == -1

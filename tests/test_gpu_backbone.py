@@ -403,3 +403,125 @@ def test_model_embed_length_preflight(ctx, oracle):
         m.embed(ids, trunc=256)
     assert e.value.code == _lib.GLYPR_ERR_SHAPE
     m.close()
+
+
+# ------------------------------------- head_dim 512 and per-layer geometry ----
+
+@pytest.mark.parametrize("t,window,nq,nkv", [(70, 0, 4, 1), (600, 0, 4, 1), (2048, 0, 4, 1),
+                                             (8192, 0, 4, 1), (1100, 256, 4, 2), (300, 0, 3, 1)])
+def test_attention_core_head_dim_512(ctx, oracle, t, window, nq, nkv):
+    """The full-attention layers of the released EmbeddingGemma-2 (head_dim 512,
+    one kv head for 4 q heads, RoPE table of 512 dims), through
+    glypr_hip_attention, against the oracle; the same bounds as head_dim 256."""
+    hd, eps = 512, 1e-6
+    say(f"attention core hd=512 t={t} window={window} nq={nq} nkv={nkv}")
+    qkv = oracle.normal(t * (nq + 2 * nkv) * hd, seed=t + 7).reshape(t, -1) * np.float32(0.7)
+    qnw = (1 + 0.1 * oracle.normal(hd, seed=3)) * QK_NORM_SCALE
+    knw = (1 + 0.1 * oracle.normal(hd, seed=4)) * QK_NORM_SCALE
+    ref16, c, s = attention_ref(oracle, qkv, qnw, knw, eps, 1e6, nq, nkv, hd, window, True)
+    ref, _, _ = attention_ref(oracle, qkv, qnw, knw, eps, 1e6, nq, nkv, hd, window)
+    got = host(ops.attention(ctx, dev(qkv), dev(qnw), dev(knw), eps, dev(c), dev(s), nq, nkv, hd,
+                             window)).astype(np.float64)
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref16).max() <= 5e-4 * scale, np.abs(got - ref16).max() / scale
+    assert np.abs(got - ref).max() <= 1e-3 * scale, np.abs(got - ref).max() / scale
+
+
+# The released EmbeddingGemma-2 text geometry (config.rs:142-169): hidden 512,
+# FFN 2048, 4 q heads; sliding layers 2 kv heads of 256, full layers 1 kv head
+# of 512; Per-Layer Embeddings and the 512 -> 768 embedding projection.
+REAL = dict(hidden=512, ffn=2048, n_heads=4, n_kv_heads=2, head_dim=256, full_head_dim=512,
+            full_n_kv_heads=1)
+
+
+def real_geometry_tensors(oracle, n_layers, vocab, ple_dim, out_dim, seed):
+    from test_oracle import _small_model
+    rng = np.random.default_rng(seed)
+    t = _small_model(oracle, REAL["hidden"], REAL["ffn"], REAL["n_heads"], REAL["n_kv_heads"],
+                     REAL["head_dim"], n_layers, vocab, rng, ple_dim=ple_dim, out_dim=out_dim,
+                     full_hd=REAL["full_head_dim"], full_nkv=REAL["full_n_kv_heads"])
+    H = REAL["hidden"]
+    shaped = {}
+    for name, a in t.items():
+        if a.dtype == np.uint8:
+            shaped[name] = (a, a.shape[0], a.shape[1] // 34 * 32, True)
+        else:
+            shaped[name] = (a, 1, a.size, False)
+    assert shaped["blk.5.attn_q.weight"][1:3] == (4 * 512, H)
+    assert shaped["blk.0.attn_k.weight"][1:3] == (2 * 256, H)
+    return t, shaped
+
+
+def test_real_geometry_model_vs_oracle(ctx, oracle):
+    """Six layers of the released geometry (layer 5 full attention with head_dim
+    512 and 1 kv head, layers 0-4 sliding with 2 kv heads of 256), with PLE and
+    the embedding projection, at T = 600 (the window is active), against the
+    oracle at BASELINE's cosine bar."""
+    n_layers, vocab, t, P, D = 6, 2000, 600, 256, 768
+    say(f"real EmbeddingGemma-2 geometry layers={n_layers} t={t} ple={P} out={D}")
+    raw, shaped = real_geometry_tensors(oracle, n_layers, vocab, P, D, seed=31)
+    m = Model(ctx, n_layers=n_layers, vocab=vocab, ple_dim=P, out_dim=D, **REAL)
+    for name, (data, r, c, q8) in shaped.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    ids = oracle.uniform_ids(t, seed=32, vocab=vocab)
+    tokens = torch.empty((t, D), dtype=torch.float32, device="cuda")
+    got = host(m.embed(ids, trunc=256, hidden=tokens))
+    ref, ref_tokens = oracle.model_forward(raw, ids, 256, hidden=REAL["hidden"], ffn=REAL["ffn"],
+                                           n_heads=4, n_kv_heads=2, head_dim=256,
+                                           n_layers=n_layers, vocab=vocab,
+                                           full_head_dim=512, full_n_kv_heads=1)
+    cos = float(got @ ref / np.linalg.norm(got) / np.linalg.norm(ref))
+    gt = host(tokens)
+    row_cos = (gt * ref_tokens).sum(1) / np.linalg.norm(gt, axis=1) / \
+        np.linalg.norm(ref_tokens, axis=1)
+    say(f"  final embedding cosine {cos:.8f}, token cosine min {row_cos.min():.8f}")
+    assert cos >= 0.9999 and row_cos.min() >= 0.999
+    again = host(m.embed(ids, trunc=256))
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+    m.close()
+
+
+def test_real_geometry_gguf_load(ctx, oracle, tmp_path):
+    """A GGUF file laid out like embeddinggemma-2 (head_count_kv per layer with
+    2 for sliding and 1 for the full layer, key_length 512, key_length_swa 256,
+    the sliding_window_pattern, PLE and output.weight) loads through
+    glypr_hip_model_load_gguf into the same model set_tensor builds:
+    bit-identical embeddings."""
+    import gguf_util as gu
+    n_layers, vocab, t, P, D = 6, 2000, 300, 256, 768
+    say("real-geometry GGUF load vs set_tensor")
+    raw, shaped = real_geometry_tensors(oracle, n_layers, vocab, P, D, seed=33)
+    m = Model(ctx, n_layers=n_layers, vocab=vocab, ple_dim=P, out_dim=D, **REAL)
+    for name, (data, r, c, q8) in shaped.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    meta = [("general.architecture", gu.STR, "gemma-embedding2"),
+            ("gemma-embedding2.block_count", gu.U32, n_layers),
+            ("gemma-embedding2.embedding_length", gu.U32, 512),
+            ("gemma-embedding2.feed_forward_length", gu.U32, 2048),
+            ("gemma-embedding2.attention.head_count", gu.U32, 4),
+            ("gemma-embedding2.attention.head_count_kv", gu.ARR,
+             (gu.U32, [1 if (i + 1) % 6 == 0 else 2 for i in range(n_layers)])),
+            ("gemma-embedding2.attention.key_length", gu.U32, 512),
+            ("gemma-embedding2.attention.key_length_swa", gu.U32, 256),
+            ("gemma-embedding2.attention.layer_norm_rms_epsilon", gu.F32, 1e-6),
+            ("gemma-embedding2.rope.freq_base", gu.F32, 1000000.0),
+            ("gemma-embedding2.rope.freq_base_swa", gu.F32, 10000.0),
+            ("gemma-embedding2.embedding_length_per_layer_input", gu.U32, P),
+            ("gemma-embedding2.attention.sliding_window_pattern", gu.ARR,
+             (gu.BOOL, [(i + 1) % 6 != 0 for i in range(n_layers)]))]
+    tens = []
+    for name, (a, rows, cols, q8) in shaped.items():
+        arr = np.ascontiguousarray(a)
+        tens.append((name, gu.GGML_Q8_0 if q8 else gu.GGML_F32,
+                     (cols, rows) if rows > 1 else (cols,), arr.view(np.uint8).tobytes()))
+    path = tmp_path / "eg2.gguf"
+    gu.write_gguf(path, meta, tens)
+    g = Model.from_gguf(ctx, str(path))
+    ids = oracle.uniform_ids(t, seed=34, vocab=vocab)
+    a = host(m.embed(ids, trunc=256))
+    b = host(g.embed(ids, trunc=256))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    g.close()
+    m.close()

@@ -408,7 +408,8 @@ def test_rope_tables_closed_form(oracle, hd, theta):
 
 # -------------------------------------------------------- whole forward ----
 
-def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, window, eps=1e-6):
+def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, window, eps=1e-6,
+                 full_hd=0, full_nkv=0):
     """Independent float64 statement of forward_embeds (model.rs:498-578) over the
     layer order of layer.rs:20-50: the same Q8_0 quantization of every GEMM input
     (oracle quantizer, pinned above), everything else in float64.  With
@@ -416,7 +417,9 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
     layer's TextPLEBlock with the layer scalar (ple.rs:118-145, norm.rs:65-95);
     with `output.weight` the embedding projection (model.rs:577).  A projection
     given as a uint16 [n, k] array is a dense bf16 weight (linear.rs:48-54): its
-    exact values, and no quantization of its input."""
+    exact values, and no quantization of its input.  full_hd / full_nkv (0: the
+    sliding values) give the full-attention layers their own head_dim and kv
+    head count (config.rs:142-169)."""
     def deq(name, n, k):
         w = tensors[name]
         if w.dtype == np.uint16:
@@ -434,7 +437,7 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
         return y if w is None else y * w.astype(np.float64)
 
     def rope(x, theta):     # x [t, hd]
-        t = x.shape[0]
+        t, hd = x.shape
         inv = (1.0 / np.power(theta, 2.0 * np.arange(hd // 2) / hd)).astype(np.float32)
         f = np.arange(t, dtype=np.float32)[:, None] * inv[None, :]
         e = np.concatenate([f, f], 1).astype(np.float64)
@@ -453,9 +456,12 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
         raw = lin(h, "per_layer_model_proj.weight", n_layers * P, H) * float(H) ** -0.5
         ple = rms(raw.reshape(t, n_layers, P), tensors["per_layer_proj_norm.weight"])
     idx = np.arange(t)
+    sliding_hd, sliding_nkv = hd, nkv
     for l in range(n_layers):
         p = f"blk.{l}."
         full = (l + 1) % 6 == 0
+        hd = (full_hd or sliding_hd) if full else sliding_hd
+        nkv = (full_nkv or sliding_nkv) if full else sliding_nkv
         theta = 1e6 if full else 1e4
         mask = np.zeros((t, t)) if full else \
             np.where(np.abs(idx[:, None] - idx[None, :]) > window, -np.inf, 0.0)
@@ -493,11 +499,16 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
     return m / max(np.linalg.norm(m), 1e-12), states
 
 
-def _small_model(oracle, H, F, nh, nkv, hd, L, vocab, rng, ple_dim=0, out_dim=0):
+def _small_model(oracle, H, F, nh, nkv, hd, L, vocab, rng, ple_dim=0, out_dim=0, full_hd=0,
+                 full_nkv=0):
     tensors = {"token_embd.weight": oracle.q8_0_weight(vocab, H, 100, 0.02),
                "output_norm.weight": (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)}
     seed = 200
+    sliding_hd, sliding_nkv = hd, nkv
     for l in range(L):
+        full = (l + 1) % 6 == 0
+        hd = (full_hd or sliding_hd) if full else sliding_hd
+        nkv = (full_nkv or sliding_nkv) if full else sliding_nkv
         for name, n, k in [("attn_q", nh * hd, H), ("attn_k", nkv * hd, H),
                            ("attn_v", nkv * hd, H), ("attn_output", H, nh * hd),
                            ("ffn_gate", F, H), ("ffn_up", F, H), ("ffn_down", H, F)]:
@@ -697,7 +708,8 @@ PINS = {
     "orc_layer_is_full": ["test_model_forward_vs_float64_statement"],
     "orc_rope_tables": ["test_rope_tables_closed_form"],
     "orc_attention": ["test_attention_band_equals_masked_dense"],
-    "orc_encoder_layer": ["test_model_forward_vs_float64_statement"],
+    "orc_encoder_layer": ["test_model_forward_vs_float64_statement",
+                          "test_model_forward_per_layer_geometry_vs_float64_statement"],
     "orc_model_forward": ["test_model_forward_vs_float64_statement",
                           "test_model_forward_with_ple_vs_float64_statement"],
 }
@@ -718,3 +730,43 @@ def test_every_oracle_export_is_pinned():
     for fn, tests in PINS.items():
         for t in tests:
             assert t in names, f"{fn}: pin {t} does not exist"
+
+
+def test_model_forward_per_layer_geometry_vs_float64_statement(oracle):
+    """The released EmbeddingGemma-2 layout in miniature: sliding layers with 2
+    kv heads of head_dim 32, the full layer (5) with 1 kv head of head_dim 64
+    and its own RoPE table (config.rs:142-169, model.rs:278-287): the oracle
+    against the float64 statement.  Using the sliding geometry for the full
+    layer is a shape error, and a uniform-geometry model embeds differently."""
+    H, F, nh, nkv, hd, fhd, fnkv, L, vocab, t, W = 128, 192, 4, 2, 32, 64, 1, 6, 1000, 40, 8
+    rng = np.random.default_rng(21)
+    tensors = _small_model(oracle, H, F, nh, nkv, hd, L, vocab, rng, full_hd=fhd, full_nkv=fnkv)
+    assert tensors["blk.5.attn_q.weight"].shape[0] == nh * fhd
+    assert tensors["blk.5.attn_k.weight"].shape[0] == fnkv * fhd
+    ids = rng.integers(0, vocab, t).astype(np.uint32)
+    kw = dict(hidden=H, ffn=F, n_heads=nh, n_kv_heads=nkv, head_dim=hd, n_layers=L, vocab=vocab,
+              sliding_window=W, full_head_dim=fhd, full_n_kv_heads=fnkv)
+    out, states = oracle.model_forward(tensors, ids, 32, **kw)
+    ref_out, ref_states = _forward_f64(oracle, tensors, ids, 32, H, F, nh, nkv, hd, L, W,
+                                       full_hd=fhd, full_nkv=fnkv)
+    row_cos = (states * ref_states).sum(1) / np.linalg.norm(states, axis=1) / \
+        np.linalg.norm(ref_states, axis=1)
+    assert row_cos.min() > 0.9995 and row_cos.mean() > 0.9999, (row_cos.min(), row_cos.mean())
+    assert float(out @ ref_out) > 0.99999
+    # the full layer's geometry matters: the same tensors with the full layer's
+    # q/k/v/o cut to the sliding geometry give another embedding
+    cut = dict(tensors)
+    cut["blk.5.attn_q.weight"] = tensors["blk.5.attn_q.weight"].reshape(nh, fhd, -1)[:, :hd] \
+        .reshape(nh * hd, -1).copy()
+    cut["blk.5.attn_k.weight"] = np.concatenate([tensors["blk.5.attn_k.weight"][:hd]] * nkv)
+    cut["blk.5.attn_v.weight"] = np.concatenate([tensors["blk.5.attn_v.weight"][:hd]] * nkv)
+    o = tensors["blk.5.attn_output.weight"]
+    nbk = o.shape[1] // 34
+    cut["blk.5.attn_output.weight"] = o.reshape(H, nh, fhd // 32, 34)[:, :, :hd // 32] \
+        .reshape(H, -1).copy()
+    cut["blk.5.attn_q_norm.weight"] = tensors["blk.5.attn_q_norm.weight"][:hd].copy()
+    cut["blk.5.attn_k_norm.weight"] = tensors["blk.5.attn_k_norm.weight"][:hd].copy()
+    del nbk
+    uni = dict(kw, full_head_dim=0, full_n_kv_heads=0)
+    o2, _ = oracle.model_forward(cut, ids, 32, **uni)
+    assert float(o2 @ out) < 0.9999
