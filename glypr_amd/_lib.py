@@ -47,6 +47,7 @@ SIGNATURES = {
     "glypr_hip_q8_0_dequantize": (_int, [_vp, _vp, _vp, _vp]),
     "glypr_hip_q8_0_quantize": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "glypr_hip_q8_0_matmul": (_int, [_vp, _vp, _vp, _vp, _i64, _int, _vp]),
+    "glypr_hip_q8_0_matmul_noalloc": (_int, [_vp, _vp, _vp, _vp, _i64, _int, _vp]),
     "glypr_hip_bf16_weight_create": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "glypr_hip_bf16_weight_destroy": (_int, [_vp]),
     "glypr_hip_bf16_matmul": (_int, [_vp, _vp, _vp, _vp, _i64, _vp]),

@@ -39,9 +39,19 @@ int hip_error(hipError_t e, const char* what) {
 
 namespace {
 
-// Shared body of the plain and RMSNorm-prologue matmuls.
+// Workspace bytes matmul_impl needs for [m, k] activations in `variant`
+// (0 when the prologue-fused GEMM runs and needs none).
+size_t matmul_ws_bytes(int64_t m, int64_t n, int64_t k, bool norm, int variant) {
+  if (variant == GLYPR_Q8_INT8_EXACT)
+    return gemm_i8_pro_ok(m, n, k, norm) ? 0 : q8_act_bytes(m, k);
+  return align_up((size_t)(m * k) * 2, 256);
+}
+
+// Shared body of the plain, RMSNorm-prologue and no-allocation matmuls: the
+// activation operand goes to `ws`, which holds matmul_ws_bytes.
 int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const float* norm_w,
-                float eps, bool norm, float* y, int64_t m, int variant, hipStream_t s) {
+                float eps, bool norm, float* y, int64_t m, int variant, void* ws,
+                hipStream_t s) {
   const int64_t n = w->n, k = w->k;
   if (variant == GLYPR_Q8_INT8_EXACT) {
     if (gemm_i8_pro_ok(m, n, k, norm)) {
@@ -50,8 +60,7 @@ int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const fl
              "gemm_i8_pro launch");
       return GLYPR_OK;
     }
-    RET_IF(ensure_ws(ctx, q8_act_bytes(m, k)));
-    Carve c(ctx->ws);
+    Carve c(ws);
     int8_t* xq = c.take<int8_t>((size_t)(m * k));
     float* dx = c.take<float>((size_t)(m * (k / 32)));
     if (norm)
@@ -63,8 +72,7 @@ int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const fl
            "gemm_i8 launch");
     return GLYPR_OK;
   }
-  RET_IF(ensure_ws(ctx, align_up((size_t)(m * k) * 2, 256)));
-  Carve c(ctx->ws);
+  Carve c(ws);
   uint16_t* xb = c.take<uint16_t>((size_t)(m * k));
   if (norm)
     LAUNCH(GLYPR_K_RMSNORM_BF16, s, launch_rmsnorm_bf16(x, norm_w, eps, m, k, xb, s),
@@ -74,6 +82,14 @@ int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const fl
   LAUNCH(GLYPR_K_GEMM_BF16, s, launch_gemm_bf16(xb, w->qs(), w->dw(), y, m, n, k, n, s),
          "gemm_bf16 launch");
   return GLYPR_OK;
+}
+
+// matmul_impl on the context's workspace, grown first if needed.
+int matmul_ws(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const float* norm_w,
+              float eps, bool norm, float* y, int64_t m, int variant, hipStream_t s) {
+  const size_t need = matmul_ws_bytes(m, w->n, w->k, norm, variant);
+  if (need) RET_IF(ensure_ws(ctx, need));
+  return matmul_impl(ctx, w, x, norm_w, eps, norm, y, m, variant, ctx->ws, s);
 }
 
 int mlp_impl(glypr_hip_ctx* ctx, const glypr_q8w* gu, const glypr_q8w* down, const float* x,
@@ -156,10 +172,16 @@ int glypr_hip_ctx_create(int device, glypr_hip_ctx** out) {
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   hipDeviceProp_t prop;
   GLYPR_TRY_HIP(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  // this device's no-allocation scratch array (scratch.hip), with the device
+  // current; if it cannot be resolved only glypr_hip_q8_0_matmul_noalloc fails
+  void* scratch_ptr = nullptr;
+  const hipError_t se = resolve_scratch(&scratch_ptr);
   glypr_hip_ctx* ctx = new (std::nothrow) glypr_hip_ctx();
   GLYPR_CHECK(ctx != nullptr, GLYPR_ERR_OOM, "host allocation failed");
   ctx->device = device;
   ctx->cu_count = prop.multiProcessorCount;
+  ctx->scratch = scratch_ptr;
+  ctx->scratch_err = se;
   *out = ctx;
   return GLYPR_OK;
 }
@@ -476,7 +498,37 @@ int glypr_hip_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  return matmul_impl(ctx, w, x, nullptr, 0.0f, false, y, m, variant, (hipStream_t)stream);
+  return matmul_ws(ctx, w, x, nullptr, 0.0f, false, y, m, variant, (hipStream_t)stream);
+}
+
+int glypr_hip_q8_0_matmul_noalloc(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x,
+                                  float* y, int64_t m, int variant, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
+  RET_IF(check_variant(variant));
+  GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
+  const size_t need = matmul_ws_bytes(m, w->n, w->k, false, variant);
+  GLYPR_CHECK(need <= GLYPR_NOALLOC_SCRATCH_BYTES, GLYPR_ERR_SHAPE,
+              "m = %lld, k = %lld needs %zu bytes of activation scratch; the no-allocation "
+              "matmul has %zu",
+              (long long)m, (long long)w->k, need, (size_t)GLYPR_NOALLOC_SCRATCH_BYTES);
+  GLYPR_CHECK(m == 0 || (x != nullptr && y != nullptr), GLYPR_ERR_INVALID_ARG, "x or y is NULL");
+  GLYPR_CHECK(aligned16(x) && aligned16(y), GLYPR_ERR_ALIGNMENT,
+              "x and y must be 16-byte aligned");
+  RET_IF(check_ctx(ctx));
+  RET_IF(check_weight_device(ctx, w, "w"));
+  GLYPR_CHECK(ctx->scratch != nullptr, GLYPR_ERR_DEVICE,
+              "no scratch address for device %d (hipGetSymbolAddress: %s)", ctx->device,
+              hipGetErrorString(ctx->scratch_err));
+  if (m == 0) return GLYPR_OK;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  ctx->no_events = true;
+  const int rc = matmul_impl(ctx, w, x, nullptr, 0.0f, false, y, m, variant, ctx->scratch,
+                             (hipStream_t)stream);
+  ctx->no_events = false;
+  return rc;
 }
 
 int glypr_hip_rmsnorm(glypr_hip_ctx* ctx, const float* x, const float* weight, float eps,
@@ -509,7 +561,7 @@ int glypr_hip_rmsnorm_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const 
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  return matmul_impl(ctx, w, x, norm_weight, eps, true, y, m, variant, (hipStream_t)stream);
+  return matmul_ws(ctx, w, x, norm_weight, eps, true, y, m, variant, (hipStream_t)stream);
 }
 
 int glypr_hip_geglu(glypr_hip_ctx* ctx, const float* gate, const float* up, float* out,

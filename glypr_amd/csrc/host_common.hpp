@@ -158,7 +158,7 @@ struct ProfScope {
   hipStream_t s;
   hipEvent_t a = nullptr, b = nullptr;
   ProfScope(glypr_hip_ctx* c, int k, hipStream_t st) : ctx(c), kernel(k), s(st) {
-    if (!ctx->profiling) return;
+    if (!ctx->profiling || ctx->no_events) return;   // events may be created on demand
     a = get_event(ctx);
     b = get_event(ctx);
     if (a && b) (void)hipEventRecord(a, s);

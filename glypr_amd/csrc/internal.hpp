@@ -66,10 +66,20 @@ struct glypr_hip_ctx {
   };
   std::map<int64_t, CosTable> bcos;
   int64_t reserve_rows = 8320;  // rows the workspace is sized for (lib.rs:47)
+  // device address of this device's no-allocation scratch array (capi.hip),
+  // resolved once at context creation
+  void* scratch = nullptr;
+  hipError_t scratch_err = hipSuccess;
+  bool no_events = false;       // a no-allocation call is running: no profile events
   int64_t max_k = 0;            // largest in_dim of a weight created on the context
 };
 
 namespace glypr {
+
+// ---- scratch.hip ----
+// This device's address of the no-allocation scratch array (the device must be
+// current); on failure *ptr is NULL and the HIP error is returned.
+hipError_t resolve_scratch(void** ptr);
 
 // error.cpp-style helpers (defined in capi.hip)
 int set_error(int code, const char* fmt, ...);

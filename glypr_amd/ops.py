@@ -183,6 +183,18 @@ def q8_0_matmul(ctx: Context, w: Q8Weight, x: torch.Tensor, variant: int = INT8_
     return y
 
 
+def q8_0_matmul_noalloc(ctx: Context, w: Q8Weight, x: torch.Tensor, variant: int = INT8_EXACT,
+                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """glypr_hip_q8_0_matmul_noalloc: the same GEMM with its activation operand
+    in the library's fixed per-device scratch array (no device allocation)."""
+    ctx._check_tensor(x, "x")
+    m = x.numel() // w.k
+    y = _out(x, (*x.shape[:-1], w.n), out)
+    check(lib().glypr_hip_q8_0_matmul_noalloc(ctx.handle, w.handle, _ptr(x), _ptr(y), m, variant,
+                                              ctx.stream))
+    return y
+
+
 def rmsnorm_q8_0_matmul(ctx: Context, w: Q8Weight, x: torch.Tensor,
                         norm_weight: Optional[torch.Tensor], eps: float = 1e-6,
                         variant: int = INT8_EXACT,

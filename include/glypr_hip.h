@@ -156,6 +156,20 @@ int glypr_hip_q8_0_quantize(glypr_hip_ctx* ctx, const float* x, int64_t m, int64
 int glypr_hip_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, float* y,
                           int64_t m, int variant, glypr_stream stream);
 
+/* No counterpart in the reference: glypr_hip_q8_0_matmul for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, kernels and bits
+ * as glypr_hip_q8_0_matmul, but the activation operand (Q8_0 or bf16 copy of
+ * x) lives in a file-scope device array of GLYPR_NOALLOC_SCRATCH_BYTES that
+ * each device holds until the process ends; the call allocates nothing.
+ * Calls whose operand needs more (INT8_EXACT: m*k + 4*m*k/32 bytes, rounded
+ * up to 256 each; BF16_DEQUANT: 2*m*k) fail with GLYPR_ERR_SHAPE.  Every call
+ * on a device shares that device's array, across contexts: calls that overlap
+ * on one device (other streams, other threads) race. */
+#define GLYPR_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int glypr_hip_q8_0_matmul_noalloc(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x,
+                                  float* y, int64_t m, int variant, glypr_stream stream);
+
 /* RMSNorm::forward (norm.rs:22-63) -> cpu_rmsnorm (cpu_simd/mod.rs:10-32;
  * simd_rmsnorm_row_f32, cpu_simd/rmsnorm.rs:6-47).  weight may be NULL (the
  * weightless v_norm).  x,y [rows,dim]; x == y allowed. */

@@ -91,6 +91,18 @@ def test_matmul_validation_order():
                                    NULL) == _lib.GLYPR_ERR_ALIGNMENT
 
 
+def test_noalloc_matmul_validation():
+    """glypr_hip_q8_0_matmul_noalloc validates like glypr_hip_q8_0_matmul (its
+    scratch-size check needs the weight handle, so it runs on the GPU)."""
+    L = _lib.lib()
+    assert L.glypr_hip_q8_0_matmul_noalloc(NULL, NULL, NULL, NULL, -1, 0, NULL) == \
+        _lib.GLYPR_ERR_SHAPE
+    assert L.glypr_hip_q8_0_matmul_noalloc(NULL, NULL, NULL, NULL, 4, 7, NULL) == \
+        _lib.GLYPR_ERR_UNSUPPORTED
+    assert L.glypr_hip_q8_0_matmul_noalloc(NULL, NULL, FAKE, FAKE, 4, 0, NULL) == \
+        _lib.GLYPR_ERR_INVALID_ARG
+
+
 def test_elementwise_validation():
     L = _lib.lib()
     assert L.glypr_hip_rmsnorm(NULL, FAKE, NULL, 1e-6, FAKE, -1, 768, NULL) == \

@@ -1,0 +1,81 @@
+"""glypr_hip_q8_0_matmul_noalloc, the matmul for callers that cannot allocate:
+through the C ABI, its output equals glypr_hip_q8_0_matmul's bit for bit (both
+variants), on two calls in a row with the second input smaller (the shared
+per-device scratch keeps the first call's contents), on a second context of the
+same device (which shares the array) and with profiling on; sizes beyond the
+scratch are refused with GLYPR_ERR_SHAPE before anything runs."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from glypr_amd import _lib, ops
+from glypr_amd.ops import BF16_DEQUANT, INT8_EXACT, Q8Weight
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def bits(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("variant", [INT8_EXACT, BF16_DEQUANT])
+def test_noalloc_matmul_equals_matmul(variant):
+    from oracle import pyoracle as po
+    ctx = ops.Context(0)
+    n, k = 1280, 768
+    wb = po.q8_0_weight(n, k, seed=71)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    # M = 3000 runs the separate quantize (or bf16) launch into the scratch;
+    # M = 700 then the prologue-fused GEMM (INT8_EXACT) on a smaller input
+    for m in (3000, 700):
+        say(f"no-alloc matmul variant={variant} m={m}")
+        x = torch.from_numpy(po.normal(m * k, seed=m).reshape(m, k)).cuda()
+        ref = ops.q8_0_matmul(ctx, w, x, variant)
+        got = ops.q8_0_matmul_noalloc(ctx, w, x, variant)
+        assert np.array_equal(bits(got), bits(ref)), f"m={m}"
+    # a smaller call after a larger one on the separate-launch route too
+    x2 = torch.from_numpy(po.normal(2100 * k, seed=5).reshape(2100, k)).cuda()
+    assert np.array_equal(bits(ops.q8_0_matmul_noalloc(ctx, w, x2, variant)),
+                          bits(ops.q8_0_matmul(ctx, w, x2, variant)))
+    # a second context on the device shares the array; profiling records nothing
+    ctx2 = ops.Context(0)
+    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx2.handle, 1))
+    w2 = Q8Weight.from_gguf(ctx2, wb, n, k)
+    got2 = ops.q8_0_matmul_noalloc(ctx2, w2, x2, variant)
+    assert np.array_equal(bits(got2), bits(ops.q8_0_matmul(ctx, w, x2, variant)))
+    tot = (ctypes.c_double * _lib.KERNEL_COUNT)()
+    cnt = (ctypes.c_int64 * _lib.KERNEL_COUNT)()
+    _lib.check(_lib.lib().glypr_hip_profile_read(ctx2.handle, tot, cnt))
+    assert sum(cnt) == 0
+    w2.close()
+    ctx2.close()
+    w.close()
+    ctx.close()
+
+
+def test_noalloc_matmul_rejects_oversized():
+    from oracle import pyoracle as po
+    ctx = ops.Context(0)
+    k = 2048
+    w = Q8Weight.from_gguf(ctx, po.q8_0_weight(64, k, seed=72), 64, k)
+    # BF16_DEQUANT needs 2 m k bytes: m = 16384 fits 64 MiB exactly, one more row does not
+    m_ok = (64 << 20) // (2 * k)
+    x = torch.zeros((m_ok + 1, k), dtype=torch.float32, device="cuda")
+    y = torch.empty((m_ok + 1, 64), dtype=torch.float32, device="cuda")
+    L = _lib.lib()
+    rc = L.glypr_hip_q8_0_matmul_noalloc(ctx.handle, w.handle, ops._ptr(x), ops._ptr(y),
+                                         m_ok + 1, BF16_DEQUANT, ctx.stream)
+    assert rc == _lib.GLYPR_ERR_SHAPE and "scratch" in _lib.last_error()
+    rc = L.glypr_hip_q8_0_matmul_noalloc(ctx.handle, w.handle, ops._ptr(x), ops._ptr(y), m_ok,
+                                         BF16_DEQUANT, ctx.stream)
+    assert rc == _lib.GLYPR_OK
+    torch.cuda.synchronize()
+    w.close()
+    ctx.close()
