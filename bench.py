@@ -583,6 +583,39 @@ def gather_line(ctx, steps, n_ids=1 << 20, vocab=262144, d=768):
             "note": "per call also uploads the 4 MB of host ids (PCIe) before the kernel"}
 
 
+def run_backbone_batch(ctx, tensors, n_layers, vocab, n_seqs, t, steps, warmup, seed=2):
+    """Embeddings/s of the full backbone on a batch of n_seqs t-token sequences in
+    one glypr_hip_model_embed_batch call (C3's 32 x 512 regime through the whole
+    model: every projection at M = n_seqs * t)."""
+    import torch
+    from glypr_amd.ops import Model
+    m = Model(ctx, n_layers=n_layers, vocab=vocab, max_batch_tokens=n_seqs * t)
+    for name, (data, r, c, q8) in tensors.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    rng = np.random.default_rng(seed)
+    seqs = [rng.integers(0, vocab, size=t).astype(np.uint32) for _ in range(n_seqs)]
+    out = torch.empty((n_seqs, 256), dtype=torch.float32, device="cuda")
+    for _ in range(warmup):
+        m.embed_batch(seqs, trunc=256, out=out)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        m.embed_batch(seqs, trunc=256, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    m.close()
+    gemm_ops = 2 * n_seqs * t * n_layers * LAYER_NK
+    return {"sequences": n_seqs, "T": t, "ms_per_batch": round(ms, 4),
+            "embeddings_per_s": round(n_seqs * 1000.0 / ms, 1),
+            "tokens_per_s": round(n_seqs * t * 1000.0 / ms, 1),
+            "gemm_tops": round(gemm_ops / (ms / 1e3) / 1e12, 2),
+            "note": "one embed_batch call per step; every projection at M = "
+                    f"{n_seqs * t}, attention and pooling per sequence"}
+
+
 def cpu_backbone_baseline(tensors, n_layers, vocab, t, seconds=10.0):
     """The oracle's full forward (glypr's CPU path restated) on this host."""
     from oracle import pyoracle as po
@@ -721,9 +754,9 @@ def main():
                     help="Q8_0 variant of the C2 / cold-C2 extra lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
-    ap.add_argument("--extras", default="c2,c1,cold,c3,vendor,c5,gather,vec",
+    ap.add_argument("--extras", default="c2,c1,cold,c3,vendor,c5,c3model,gather,vec",
                     help="comma list of the extra workloads to run "
-                         "(c2, c1, cold, c3, vendor, c5, gather, vec)")
+                         "(c2, c1, cold, c3, vendor, c5, c3model, gather, vec)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain device copy of MIB MiB (calibrates rocprof "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -827,6 +860,8 @@ def main():
                                                      1).items() if not k.startswith("_")}
         extra["c5"]["attention_layers"] = ("4 full + 20 sliding (window 512) layers, "
                                            "1.341 TFLOP per embedding")
+    if "c3model" in todo:
+        extra["c3_model_batch"] = run_backbone_batch(ctx, tensors, n_layers, vocab, 32, 512, 5, 1)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_backbone_baseline(tensors, n_layers, vocab, t_c4)

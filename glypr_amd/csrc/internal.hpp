@@ -110,6 +110,13 @@ hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, h
 size_t pool_scratch_floats(int64_t t, int64_t d);
 hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t d, int64_t trunc,
                        float* out, float* scratch, hipStream_t s);
+// Several sequences at 64-aligned row offsets of tok [rows][d] (rows % 64 ==
+// 0): seg is the per-row segment table (launch_qkv_post), seqs {offset,
+// length} per sequence; out [n_seqs][trunc or d].
+size_t pool_segments_scratch_floats(int64_t rows, int64_t n_seqs, int64_t d);
+hipError_t launch_pool_segments(const float* tok, int64_t rows, const int32_t* seg,
+                                const int32_t* seqs, int64_t n_seqs, int64_t d, int64_t trunc,
+                                float* out, float* scratch, hipStream_t s);
 
 // h = h + rmsnorm(x; w_post); if xq: (xq, dx) = Q8_0(rmsnorm(h; w_next)).  dim % 32 == 0.
 // scalar (device, nullable): h = (h + RMSNorm(x)) * scalar.  plain_q: xq/dx
@@ -131,20 +138,30 @@ hipError_t launch_geglu_quant(const float* g, const float* u, int64_t u_stride, 
 constexpr int64_t ATTN_TP_ALIGN = 64;
 inline int64_t attn_padded_len(int64_t t) { return (t + ATTN_TP_ALIGN - 1) / ATTN_TP_ALIGN * ATTN_TP_ALIGN; }
 // q16 [nq][Tp][hd], k16 [nkv][Tp][hd], vt16 [nkv][hd][Tp] (f16).  hd == 256.
+// seg (nullable, device int32 pairs [Tp][2]): row t holds position t - seg[t][0]
+// of a sequence of seg[t][1] tokens starting at row seg[t][0] (sequences at
+// 64-aligned row offsets); rows past a sequence's length are padding.
+// Without it the rows are one sequence of T tokens.
 hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
                            int64_t hd, const float* qnw, const float* knw, float eps,
                            const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
-                           uint16_t* vt16, hipStream_t s);
-size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window);
+                           uint16_t* vt16, hipStream_t s, const int32_t* seg = nullptr);
+// T: the (longest) sequence length; rows: the padded row count when several
+// sequences share the buffers (0: attn_padded_len(T)).
+size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
+                                int64_t rows = 0);
 // Whether launch_attention runs this geometry: head_dim 256, nq / nkv in
 // 1..4, at most 64 key partitions at T (T <= 0: any length).
 bool attention_supported(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window);
 // ctx (f32 [T][nq*hd]), (cq, dc) (Q8_0 planar) and cb (bf16 [T][nq*hd]) may
 // each be null.
+// seg / seg_max: the segment table of launch_qkv_post and the longest sequence;
+// each query block attends to its own sequence's keys only.
 hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
                             float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
                             int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
-                            hipStream_t s, uint16_t* cb = nullptr);
+                            hipStream_t s, uint16_t* cb = nullptr, const int32_t* seg = nullptr,
+                            int64_t seg_max = 0);
 
 // ---- k_gemm_i8.hip ----
 // Which INT8_EXACT kernel runs an [M x Nrows x K] GEMM (plain or GeGLU):

@@ -53,12 +53,28 @@ struct QkvGeom {
   static constexpr int LDS = V_LDS > HD ? V_LDS : HD;        // per-wave staging
 };
 
+// Row t's RoPE position and whether it holds a token: with a segment table
+// (several sequences at 64-aligned row offsets, seg[t] = {start, length} of
+// row t's sequence) the position restarts at each sequence and the rows past
+// a sequence's length are padding; without one, row t is position t of one
+// sequence of T tokens.
+__device__ __forceinline__ int row_pos(const int2* __restrict__ seg, int t, int T, bool* valid) {
+  if (!seg) {
+    *valid = t < T;
+    return t;
+  }
+  const int2 sg = seg[t];
+  const int p = t - sg.x;
+  *valid = p < sg.y;
+  return p;
+}
+
 template <int HD>
 __global__ void __launch_bounds__(256) qkv_post_kernel(
     const float* __restrict__ qkv, int T, int Tp, int nq, int nkv, const float* __restrict__ qnw,
     const float* __restrict__ knw, float eps, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, f16* __restrict__ q16,
-    f16* __restrict__ k16, f16* __restrict__ vt16, int qk_blocks) {
+    f16* __restrict__ k16, f16* __restrict__ vt16, int qk_blocks, const int2* __restrict__ seg) {
   using Gm = QkvGeom<HD>;
   constexpr int DPL = Gm::DPL;
   constexpr int NV4 = DPL / 4;   // float4s per lane
@@ -79,9 +95,11 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
 #pragma unroll
     for (int i = 0; i < QKV_V_TOK; i++) {
       const int t = t0 + i;
+      bool valid;
+      (void)row_pos(seg, t, T, &valid);
 #pragma unroll
       for (int c = 0; c < NV4; c++) {
-        x[i][c] = t < T ? *reinterpret_cast<const v4f*>(
+        x[i][c] = valid ? *reinterpret_cast<const v4f*>(
                               qkv + (int64_t)t * slots * HD + (int64_t)(nq + nkv + head) * HD +
                               DPL * lane + 4 * c)
                         : v4f{0, 0, 0, 0};
@@ -132,7 +150,9 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
   float y[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; e++) y[e] = 0.0f;
-  if (t < T) {
+  bool valid;
+  const int pos = row_pos(seg, t, T, &valid);
+  if (valid) {
     const float* src = qkv + (int64_t)t * (nq + 2 * nkv) * HD + (int64_t)slot * HD;
     v4f x[NV4];
     float* lrow = lds_rows[wave];
@@ -166,8 +186,8 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     }
 #pragma unroll
     for (int c = 0; c < NV4; c++) {
-      const v4f cv = *reinterpret_cast<const v4f*>(cos_t + (int64_t)t * HD + DPL * lane + 4 * c);
-      const v4f sv = *reinterpret_cast<const v4f*>(sin_t + (int64_t)t * HD + DPL * lane + 4 * c);
+      const v4f cv = *reinterpret_cast<const v4f*>(cos_t + (int64_t)pos * HD + DPL * lane + 4 * c);
+      const v4f sv = *reinterpret_cast<const v4f*>(sin_t + (int64_t)pos * HD + DPL * lane + 4 * c);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         // v_permlane32_swap of y with itself: lanes < 32 get (own, lane + 32),
@@ -193,7 +213,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
 hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
                            int64_t hd, const float* qnw, const float* knw, float eps,
                            const float* cos_t, const float* sin_t, uint16_t* q16, uint16_t* k16,
-                           uint16_t* vt16, hipStream_t s) {
+                           uint16_t* vt16, hipStream_t s, const int32_t* seg) {
   if (Tp % 64 != 0) return hipErrorInvalidValue;
   const int64_t qk_blocks = (Tp * (nq + nkv) + 3) / 4;
   const int64_t v_blocks = (nkv * (Tp / QKV_V_TOK) + 3) / 4;
@@ -202,12 +222,12 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
     qkv_post_kernel<256><<<grid, 256, 0, s>>>(
         qkv, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
         reinterpret_cast<f16*>(q16), reinterpret_cast<f16*>(k16), reinterpret_cast<f16*>(vt16),
-        (int)qk_blocks);
+        (int)qk_blocks, reinterpret_cast<const int2*>(seg));
   else if (hd == 512)
     qkv_post_kernel<512><<<grid, 256, 0, s>>>(
         qkv, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
         reinterpret_cast<f16*>(q16), reinterpret_cast<f16*>(k16), reinterpret_cast<f16*>(vt16),
-        (int)qk_blocks);
+        (int)qk_blocks, reinterpret_cast<const int2*>(seg));
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -290,7 +310,7 @@ template <int HD, int G, int AQS>
 __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     const f16* __restrict__ q16, const f16* __restrict__ kk, const f16* __restrict__ vt,
     float* __restrict__ part_o, float* __restrict__ part_ml, int T, int Tp, int nq, int nkv,
-    int window, int kb_per_part, int kparts) {
+    int window, int kb_per_part, int kparts, const int2* __restrict__ seg) {
   static_assert(HD == 256 || HD == 512, "head dims 256 and 512");
   constexpr int NWV = G * AQS;
   constexpr int AQB = 16 * AQS;
@@ -320,13 +340,22 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
   const int h = g * G + hh;
   const int qw = q0 + 16 * qs;   // this wave's first query
   const int qi = qw + l16;       // this lane's query
-  const bool banded = window > 0 && T > window;
+  // keys of this query block's sequence: [kstart, kend) (a segment table
+  // places each sequence at a 64-aligned row offset; query blocks never
+  // straddle two sequences)
+  int kstart = 0, kend = T;
+  if (seg) {
+    const int2 sg = seg[q0];
+    kstart = sg.x;
+    kend = sg.x + sg.y;
+  }
+  const bool banded = window > 0 && kend - kstart > window;
 
-  int kb_lo = 0, kb_hi = (T + AK - 1) / AK;
+  int kb_lo = kstart / AK, kb_hi = (kend + AK - 1) / AK;
   if (banded) {
-    int lo_key = q0 - window, hi_key = q0 + AQB - 1 + window;
-    kb_lo = lo_key > 0 ? lo_key / AK : 0;
-    kb_hi = (hi_key < T - 1 ? hi_key : T - 1) / AK + 1;
+    const int lo_key = q0 - window, hi_key = q0 + AQB - 1 + window;
+    kb_lo = (lo_key > kstart ? lo_key : kstart) / AK;
+    kb_hi = (hi_key < kend - 1 ? hi_key : kend - 1) / AK + 1;
   }
   const int kb0 = kb_lo + kp * kb_per_part;
   const int kb1 = kb0 + kb_per_part < kb_hi ? kb0 + kb_per_part : kb_hi;
@@ -400,7 +429,7 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     const f16* Vt = Vs[sl];
     const int k0 = kb * AK;
     // ---- mask (only where a key of the tile can be out of range or band)
-    const bool edge = k0 + AK > T ||
+    const bool edge = k0 + AK > kend ||
                       (banded && (k0 < q0 + AQB - 1 - window || k0 + AK - 1 > q0 + window));
     if (edge) {
 #pragma unroll
@@ -408,7 +437,7 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const int key = k0 + 8 * lq + 4 * kt + r;
-          bool ok = key < T;
+          bool ok = key < kend;
           if (banded) {
             const int d = qi - key;
             ok = ok && d <= window && -d <= window;
@@ -604,13 +633,14 @@ constexpr int64_t ATTN_BLOCKS = 256;
 // more waves).
 inline int attn_qs(int64_t T, int64_t hd) { return hd == 512 ? 1 : (T <= ATTN_SMALL_T ? 1 : 4); }
 
-static int attn_kb_per_part(int64_t T, int64_t hd, int64_t nq, int64_t nkv, int64_t window,
-                            int* kparts) {
-  const int64_t aqb = 16 * attn_qs(T, hd);
-  const int64_t tp = attn_padded_len(T);
-  const int64_t nqb = tp / aqb;
-  int64_t nkb = (T + AK - 1) / AK;
-  if (window > 0 && T > window) {
+// Tseg: the longest sequence (its key range sets the tile count); rows: the
+// padded rows of all sequences (they set the query blocks).
+static int attn_kb_per_part(int64_t Tseg, int64_t rows, int64_t hd, int64_t nq, int64_t nkv,
+                            int64_t window, int* kparts) {
+  const int64_t aqb = 16 * attn_qs(Tseg, hd);
+  const int64_t nqb = rows / aqb;
+  int64_t nkb = (Tseg + AK - 1) / AK;
+  if (window > 0 && Tseg > window) {
     int64_t band = (2 * window + aqb + AK - 1) / AK + 1;
     if (band < nkb) nkb = band;
   }
@@ -628,14 +658,15 @@ bool attention_supported(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t
     return false;
   if (T <= 0) return true;
   int kparts;
-  attn_kb_per_part(T, hd, nq, nkv, window, &kparts);
+  attn_kb_per_part(T, attn_padded_len(T), hd, nq, nkv, window, &kparts);
   return kparts <= 64;   // the combine holds one partition per lane
 }
 
-size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window) {
+size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
+                                int64_t rows) {
+  const int64_t tp = rows > 0 ? rows : attn_padded_len(T);
   int kp;
-  attn_kb_per_part(T, hd, nq, nkv, window, &kp);
-  const int64_t tp = attn_padded_len(T);
+  attn_kb_per_part(T, tp, hd, nq, nkv, window, &kp);
   return (size_t)(kp * tp * nq * (hd + 2));
 }
 
@@ -643,11 +674,12 @@ template <int HD>
 static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float* scratch,
                                 float* ctx, int8_t* cq, float* dc, int64_t T, int64_t Tp,
                                 int64_t nq, int64_t nkv, int64_t window, hipStream_t s,
-                                uint16_t* cb) {
+                                uint16_t* cb, const int2* seg, int64_t seg_max) {
   const int64_t G = nq / nkv;
-  const int aqs = attn_qs(T, HD);
+  const int64_t Tk = seg ? seg_max : T;   // the longest key range
+  const int aqs = attn_qs(Tk, HD);
   int kparts;
-  const int per = attn_kb_per_part(T, HD, nq, nkv, window, &kparts);
+  const int per = attn_kb_per_part(Tk, Tp, HD, nq, nkv, window, &kparts);
   if (kparts > 64) return hipErrorInvalidValue;   // the combine holds one partition per lane
   float* part_o = scratch;
   float* part_ml = scratch + (int64_t)kparts * Tp * nq * HD;
@@ -656,7 +688,8 @@ static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float*
 #define GLYPR_ATTN_CASE(GG, QS)                                                                  \
   if (G == GG && aqs == QS)                                                                      \
     attn_partial_kernel<HD, GG, QS><<<grid, GG * QS * 64, 0, s>>>(                               \
-        q, k, v, part_o, part_ml, (int)T, (int)Tp, (int)nq, (int)nkv, (int)window, per, kparts);
+        q, k, v, part_o, part_ml, (int)T, (int)Tp, (int)nq, (int)nkv, (int)window, per, kparts, \
+        seg);
   if constexpr (HD == 256) {
     GLYPR_ATTN_CASE(1, 1) else GLYPR_ATTN_CASE(1, 4)
     else GLYPR_ATTN_CASE(2, 1) else GLYPR_ATTN_CASE(2, 4)
@@ -679,15 +712,19 @@ static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float*
 hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint16_t* vt16,
                             float* scratch, float* ctx, int8_t* cq, float* dc, int64_t T,
                             int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
-                            hipStream_t s, uint16_t* cb) {
+                            hipStream_t s, uint16_t* cb, const int32_t* seg, int64_t seg_max) {
   if (Tp % ATTN_TP_ALIGN != 0 || Tp < T || nq % nkv != 0) return hipErrorInvalidValue;
+  if (seg && (seg_max <= 0 || seg_max > Tp)) return hipErrorInvalidValue;
   const f16* q = reinterpret_cast<const f16*>(q16);
   const f16* k = reinterpret_cast<const f16*>(k16);
   const f16* v = reinterpret_cast<const f16*>(vt16);
+  const int2* sg = reinterpret_cast<const int2*>(seg);
   if (hd == 256)
-    return run_attention<256>(q, k, v, scratch, ctx, cq, dc, T, Tp, nq, nkv, window, s, cb);
+    return run_attention<256>(q, k, v, scratch, ctx, cq, dc, T, Tp, nq, nkv, window, s, cb, sg,
+                              seg_max);
   if (hd == 512)
-    return run_attention<512>(q, k, v, scratch, ctx, cq, dc, T, Tp, nq, nkv, window, s, cb);
+    return run_attention<512>(q, k, v, scratch, ctx, cq, dc, T, Tp, nq, nkv, window, s, cb, sg,
+                              seg_max);
   return hipErrorInvalidValue;
 }
 

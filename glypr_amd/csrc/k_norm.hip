@@ -475,15 +475,24 @@ hipError_t launch_geglu_quant(const float* g, const float* u, int64_t u_stride, 
 // ---------------------------------------------------------------------------
 constexpr int POOL_CHUNK = 64;
 
+// seg (nullable): the segment table of several sequences at 64-aligned row
+// offsets ({start, length} per row, see launch_qkv_post); a chunk then ends at
+// its sequence's last token, and chunks of padding rows sum to 0.
 __global__ void __launch_bounds__(256) pool_partial_kernel(const float* __restrict__ tok,
                                                            const uint8_t* __restrict__ mask,
                                                            int64_t t, int64_t d,
-                                                           float* __restrict__ partial) {
+                                                           float* __restrict__ partial,
+                                                           const int2* __restrict__ seg) {
   const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t chunk = blockIdx.y;
   if (col >= d) return;
   const int64_t r0 = chunk * POOL_CHUNK;
-  const int64_t r1 = r0 + POOL_CHUNK < t ? r0 + POOL_CHUNK : t;
+  int64_t end = t;
+  if (seg) {
+    const int2 sg = seg[r0];
+    end = (int64_t)sg.x + sg.y;
+  }
+  const int64_t r1 = r0 + POOL_CHUNK < end ? r0 + POOL_CHUNK : end;
   float s = 0.0f;
   if (mask) {
     for (int64_t j = r0; j < r1; j++) s += tok[j * d + col] * (mask[j] ? 1.0f : 0.0f);
@@ -509,12 +518,25 @@ __device__ __forceinline__ float block_sum_1024(float v, float* red) {
   return t;
 }
 
+// seqs (nullable): {row offset, length} per sequence; block b then pools
+// sequence b from its own chunks into out[b][td] (pooled: d floats per block).
 __global__ void __launch_bounds__(1024) pool_finalize_kernel(const float* __restrict__ partial,
                                                              const uint8_t* __restrict__ mask,
                                                              int64_t t, int64_t d, int64_t trunc,
                                                              float* __restrict__ out,
-                                                             float* __restrict__ pooled) {
+                                                             float* __restrict__ pooled,
+                                                             const int32_t* __restrict__ seqs) {
   __shared__ float red[16];
+  const int64_t td_out = (trunc > 0 && trunc < d) ? trunc : d;
+  if (seqs) {
+    const int64_t b = blockIdx.x;
+    const int64_t off = seqs[2 * b];
+    t = seqs[2 * b + 1];
+    partial += (off / POOL_CHUNK) * d;
+    out += b * td_out;
+    pooled += b * d;
+    mask = nullptr;
+  }
   const int64_t nchunk = (t + POOL_CHUNK - 1) / POOL_CHUNK;
   float cnt = 0.0f;
   if (mask) {
@@ -561,8 +583,27 @@ hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t
   float* partial = scratch;
   float* pooled = scratch + nchunk * d;
   dim3 g1((unsigned)((d + 255) / 256), (unsigned)nchunk);
-  pool_partial_kernel<<<g1, 256, 0, s>>>(tok, mask, t, d, partial);
-  pool_finalize_kernel<<<1, 1024, 0, s>>>(partial, mask, t, d, trunc, out, pooled);
+  pool_partial_kernel<<<g1, 256, 0, s>>>(tok, mask, t, d, partial, nullptr);
+  pool_finalize_kernel<<<1, 1024, 0, s>>>(partial, mask, t, d, trunc, out, pooled, nullptr);
+  return hipGetLastError();
+}
+
+size_t pool_segments_scratch_floats(int64_t rows, int64_t n_seqs, int64_t d) {
+  return (size_t)(((rows + POOL_CHUNK - 1) / POOL_CHUNK) * d + n_seqs * d);
+}
+
+hipError_t launch_pool_segments(const float* tok, int64_t rows, const int32_t* seg,
+                                const int32_t* seqs, int64_t n_seqs, int64_t d, int64_t trunc,
+                                float* out, float* scratch, hipStream_t s) {
+  if (rows % POOL_CHUNK != 0) return hipErrorInvalidValue;
+  const int64_t nchunk = rows / POOL_CHUNK;
+  float* partial = scratch;
+  float* pooled = scratch + nchunk * d;
+  dim3 g1((unsigned)((d + 255) / 256), (unsigned)nchunk);
+  pool_partial_kernel<<<g1, 256, 0, s>>>(tok, nullptr, rows, d, partial,
+                                         reinterpret_cast<const int2*>(seg));
+  pool_finalize_kernel<<<(unsigned)n_seqs, 1024, 0, s>>>(partial, nullptr, rows, d, trunc, out,
+                                                          pooled, seqs);
   return hipGetLastError();
 }
 

@@ -127,7 +127,13 @@ struct glypr_model {
   // activations
   DevBuf h, xq, dx, qkv, attn_q, attn_k, attn_vt, attn_scratch, cq, dc, proj, hq,
       dh, normed, pooled, ids, ple, ple_gate, tokens, xb, hb;
-  int64_t cap_t = 0;
+  // several sequences in one forward: the per-row segment table ({start,
+  // length} of the row's sequence, int32 pairs) and {offset, length} per
+  // sequence; host staging of both and of the padded ids
+  DevBuf seg, seqs;
+  std::vector<int32_t> h_seg, h_seqs;
+  std::vector<uint32_t> h_ids;
+  int64_t cap_t = 0;   // rows every buffer holds: max(max_seq_len, max_batch_tokens), 64-aligned
 };
 
 namespace {
@@ -179,22 +185,43 @@ int ensure_rope(glypr_model* m, int64_t t) {
   return GLYPR_OK;
 }
 
+// Attention scratch for the largest case the model can meet: any (longest)
+// sequence length up to max_seq_len with any padded row count up to the
+// capacity (key partitions shrink as rows grow, so the product is checked at
+// every 64-row step), for each layer's geometry.
+size_t model_attention_scratch(const glypr_model* m, int64_t cap) {
+  const glypr_model_config& c = m->cfg;
+  size_t best = 0;
+  for (int full = 0; full < 2; full++) {
+    const int64_t hd = full ? c.full_head_dim : c.head_dim;
+    const int64_t nkv = full ? c.full_n_kv_heads : c.n_kv_heads;
+    const int64_t w = full ? 0 : c.sliding_window;
+    for (int64_t tk = 32;; tk += 32) {
+      if (tk > c.max_seq_len) tk = c.max_seq_len;
+      for (int64_t rows = attn_padded_len(tk); rows <= cap; rows += 64) {
+        const size_t sc = attention_scratch_floats(tk, c.n_heads, nkv, hd, w, rows);
+        best = sc > best ? sc : best;
+      }
+      if (tk == c.max_seq_len) break;
+    }
+  }
+  return best;
+}
+
+// Every activation buffer for `t` rows (a 64-aligned capacity).
 int ensure_activations(glypr_model* m, int64_t t) {
   if (t <= m->cap_t) return GLYPR_OK;
   const glypr_model_config& c = m->cfg;
   const int64_t tp = attn_padded_len(t);
   // the widest attention geometry over the layers
   int64_t qd = 0, kvd = 0, qkvd = 0;
-  size_t sc = 0;
   for (const EncoderLayer& L : m->layers) {
     const int64_t lq = c.n_heads * L.head_dim, lkv = L.n_kv_heads * L.head_dim;
     qd = lq > qd ? lq : qd;
     kvd = lkv > kvd ? lkv : kvd;
     qkvd = lq + 2 * lkv > qkvd ? lq + 2 * lkv : qkvd;
-    const size_t s1 = attention_scratch_floats(t, c.n_heads, L.n_kv_heads, L.head_dim,
-                                               L.full_attention ? 0 : c.sliding_window);
-    sc = s1 > sc ? s1 : sc;
   }
+  const size_t sc = model_attention_scratch(m, tp);
   const int64_t wide = c.hidden > qd ? c.hidden : qd;
   RET_IF(m->h.ensure((size_t)(t * c.hidden) * 4));
   RET_IF(m->xq.ensure((size_t)(t * wide)));
@@ -212,7 +239,9 @@ int ensure_activations(glypr_model* m, int64_t t) {
   RET_IF(m->dh.ensure((size_t)(t * (hw / 32)) * 4));
   RET_IF(m->normed.ensure((size_t)(t * c.hidden) * 4));
   const int64_t width = c.out_dim > 0 ? c.out_dim : c.hidden;
-  RET_IF(m->pooled.ensure(pool_scratch_floats(t, width) * 4));
+  const size_t p1 = pool_scratch_floats(t, width);
+  const size_t p2 = pool_segments_scratch_floats(tp, tp / 64, width);
+  RET_IF(m->pooled.ensure((p1 > p2 ? p1 : p2) * 4));
   if (c.ple_dim > 0) {
     RET_IF(m->ple.ensure((size_t)(t * c.n_layers * c.ple_dim) * 4));
     RET_IF(m->ple_gate.ensure((size_t)(t * c.ple_dim) * 4));
@@ -223,6 +252,11 @@ int ensure_activations(glypr_model* m, int64_t t) {
     RET_IF(m->hb.ensure((size_t)(t * c.ffn) * 2));
   }
   RET_IF(m->ids.ensure((size_t)t * 4));
+  RET_IF(m->seg.ensure((size_t)tp * 8));
+  RET_IF(m->seqs.ensure((size_t)(tp / 64) * 8));
+  m->h_seg.reserve((size_t)tp * 2);
+  m->h_seqs.reserve((size_t)(tp / 64) * 2);
+  m->h_ids.reserve((size_t)tp);
   m->cap_t = t;
   return GLYPR_OK;
 }
@@ -268,7 +302,7 @@ void free_model(glypr_model* m) {
   for (DevBuf* b : {&m->cos_s, &m->sin_s, &m->cos_f, &m->sin_f, &m->h, &m->xq, &m->dx, &m->qkv,
                     &m->attn_q, &m->attn_k, &m->attn_vt, &m->attn_scratch,
                     &m->cq, &m->dc, &m->proj, &m->hq, &m->dh, &m->normed, &m->pooled, &m->ids,
-                    &m->ple, &m->ple_gate, &m->tokens, &m->xb, &m->hb})
+                    &m->ple, &m->ple_gate, &m->tokens, &m->xb, &m->hb, &m->seg, &m->seqs})
     b->release();
 }
 
@@ -310,23 +344,35 @@ int attention_core(glypr_hip_ctx* ctx, const float* qkv, const float* qnw, const
                    float eps, const float* cos_t, const float* sin_t, int64_t t, int64_t nq,
                    int64_t nkv, int64_t hd, int64_t window, uint16_t* q16, uint16_t* k16,
                    uint16_t* vt16, float* scratch, float* out, int8_t* cq, float* dc,
-                   hipStream_t s, uint16_t* cb = nullptr) {
+                   hipStream_t s, uint16_t* cb = nullptr, const int32_t* seg = nullptr,
+                   int64_t seg_max = 0) {
   const int64_t tp = attn_padded_len(t);
   LAUNCH(GLYPR_K_QKV_POST, s,
-         launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q16, k16, vt16, s),
+         launch_qkv_post(qkv, t, tp, nq, nkv, hd, qnw, knw, eps, cos_t, sin_t, q16, k16, vt16, s,
+                         seg),
          "qkv_post launch");
   LAUNCH(GLYPR_K_ATTENTION, s,
-         launch_attention(q16, k16, vt16, scratch, out, cq, dc, t, tp, nq, nkv, hd, window, s, cb),
+         launch_attention(q16, k16, vt16, scratch, out, cq, dc, t, tp, nq, nkv, hd, window, s, cb,
+                          seg, seg_max),
          "attention launch");
   return GLYPR_OK;
 }
+
+// The rows of one forward: t rows of one sequence (seg NULL), or several
+// sequences at 64-aligned offsets of t padded rows with their segment table.
+struct Rows {
+  int64_t t;
+  const int32_t* seg;
+  int64_t seg_max;
+};
 
 // The layers, final norm and pooling with dense bf16 projections (the
 // bf16-weight variant of configs 4-5): each GEMM takes bf16 activations
 // (nearest even) from the norm kernels and the attention combine, the
 // residual stream h stays f32, GeGLU leaves the gate/up GEMM as bf16.
-int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, int64_t t, int64_t trunc, float* out,
-                  float* hidden, hipStream_t s) {
+int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hidden,
+                  float** tokens_out, hipStream_t s) {
+  const int64_t t = rows.t;
   const glypr_model_config& c = m->cfg;
   const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads;
   float* h = dev_f32(m->h);
@@ -349,7 +395,8 @@ int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, int64_t t, int64_t trunc, 
                           L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
                           L.full_attention ? 0 : c.sliding_window, m->attn_q.as<uint16_t>(),
                           m->attn_k.as<uint16_t>(), m->attn_vt.as<uint16_t>(),
-                          dev_f32(m->attn_scratch), nullptr, nullptr, nullptr, s, xb));
+                          dev_f32(m->attn_scratch), nullptr, nullptr, nullptr, s, xb, rows.seg,
+                          rows.seg_max));
     const glypr_bf16w* wo = L.self_attn.o.wb;
     LAUNCH(GLYPR_K_GEMM_BF16W, s,
            launch_gemm_bf16w(xb, wo->p, dev_f32(m->proj), t, H, qd, H, s), "o gemm launch");
@@ -374,8 +421,145 @@ int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, int64_t t, int64_t trunc, 
   float* tokens = hidden ? hidden : dev_f32(m->normed);
   LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, tokens, t, H, s),
          "final rmsnorm launch");
-  LAUNCH(GLYPR_K_POOL, s, launch_pool(tokens, nullptr, t, H, trunc, out, dev_f32(m->pooled), s),
-         "pool launch");
+  *tokens_out = tokens;
+  return GLYPR_OK;
+}
+
+// forward_embeds (model.rs:498-578) over the rows whose ids are in m->ids:
+// gather x embed_scale, the Per-Layer-Embedding inputs, the layers, the final
+// norm and the embedding projection.  The token embeddings (width out_dim or
+// hidden) are left in *tokens_out (`hidden` when given).
+int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hidden,
+                 float** tokens_out, hipStream_t s) {
+  const glypr_model_config& c = m->cfg;
+  const int64_t t = rows.t;
+  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads;
+  float* h = dev_f32(m->h);
+  int8_t* xq = m->xq.as<int8_t>();
+  float* dx = dev_f32(m->dx);
+
+  // model.rs:507-508: Embedding::forward, then * embed_scale (f64 sqrt(hidden) as f32)
+  const float embed_scale = (float)sqrt((double)H);
+  LAUNCH(GLYPR_K_GATHER, s,
+         launch_gather(m->token_embd.w->qs(), m->token_embd.w->dw(), H, m->ids.as<uint32_t>(), t,
+                       embed_scale, h, s),
+         "gather launch");
+  // TextPLE::project_and_norm_per_layer (ple.rs:48-85): per_layer_model_proj of
+  // the scaled embeddings, * hidden^-0.5 (f64 powf, applied as candle's f32
+  // affine), RMSNorm over ple_dim.  Layer l's input is row t*NL + l of [t*NL][P].
+  const int64_t P = c.ple_dim, NL = c.n_layers;
+  float* ple = dev_f32(m->ple);
+  if (P > 0) {
+    LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(h, t, H, xq, dx, s), "quantize launch");
+    const glypr_q8w* wpl = m->ple_projection.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, wpl->qs(), wpl->dw(), ple, t, NL * P, H, NL * P, s),
+           "per-layer projection launch");
+    LAUNCH(GLYPR_K_RMSNORM, s, launch_affine(ple, t * NL * P, (float)pow((double)H, -0.5), s),
+           "per-layer scale launch");
+    LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(ple, m->ple_norm.weight, c.eps, ple, t * NL, P, s),
+           "per-layer norm launch");
+  }
+  if (m->dense) return forward_dense(m, ctx, rows, hidden, tokens_out, s);
+  // layer 0 input_layernorm as the qkv GEMM's prologue
+  LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
+         launch_rmsnorm_quant(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xq, dx, s),
+         "rmsnorm_quant launch");
+
+  for (size_t li = 0; li < m->layers.size(); li++) {
+    EncoderLayer& L = m->layers[li];
+    const bool last = li + 1 == m->layers.size();
+    const int64_t hd = L.head_dim, nkv = L.n_kv_heads, qd = nq * hd;
+    // ---- attention block (layer.rs:27-34)
+    const glypr_q8w* wqkv = L.self_attn.fused_qkv.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, wqkv->qs(), wqkv->dw(), dev_f32(m->qkv), t, wqkv->n, H, wqkv->n,
+                          s),
+           "qkv gemm launch");
+    const float* cos_t = dev_f32(L.full_attention ? m->cos_f : m->cos_s);
+    const float* sin_t = dev_f32(L.full_attention ? m->sin_f : m->sin_s);
+    RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
+                          L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
+                          L.full_attention ? 0 : c.sliding_window, m->attn_q.as<uint16_t>(),
+                          m->attn_k.as<uint16_t>(), m->attn_vt.as<uint16_t>(),
+                          dev_f32(m->attn_scratch), nullptr,
+                          m->cq.as<int8_t>(), dev_f32(m->dc), s, nullptr, rows.seg,
+                          rows.seg_max));
+    const glypr_q8w* wo = L.self_attn.o.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(m->cq.as<int8_t>(), dev_f32(m->dc), wo->qs(), wo->dw(),
+                          dev_f32(m->proj), t, H, qd, H, s),
+           "o gemm launch");
+    // post_attention_layernorm.forward_residual_add + pre_feedforward_layernorm prologue
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.post_attention_layernorm.weight, h,
+                                L.pre_feedforward_layernorm.weight, c.eps, t, H, xq, dx, s),
+           "residual_norm launch");
+    // ---- feed-forward block (layer.rs:36-42): gate/up + GeGLU epilogue, down
+    const glypr_q8w* wgu = L.mlp.fused_gate_up.w;
+    LAUNCH(GLYPR_K_GEMM_I8_GEGLU, s,
+           launch_gemm_i8_geglu(xq, dx, wgu->qs(), wgu->dw(), m->hq.as<int8_t>(), dev_f32(m->dh),
+                                t, F, H, s),
+           "gate/up GeGLU launch");
+    const glypr_q8w* wd = L.mlp.down.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wd->qs(), wd->dw(),
+                          dev_f32(m->proj), t, H, F, H, s),
+           "down gemm launch");
+    const float* w_next = last ? nullptr : m->layers[li + 1].input_layernorm.weight;
+    if (P == 0) {
+      // post_feedforward_layernorm.forward_residual_add + next layer's input norm
+      LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+             launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h,
+                                  w_next, c.eps, t, H, last ? nullptr : xq, last ? nullptr : dx,
+                                  s),
+             "residual_norm launch");
+      continue;
+    }
+    // post_feedforward_layernorm.forward_residual_add, then Q8_0 of h itself
+    // for the PLE block's inp_gate (no norm in front of it)
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h, nullptr,
+                                c.eps, t, H, xq, dx, s, nullptr, true),
+           "residual_norm launch");
+    // ---- TextPLEBlock::forward_with_scalar (ple.rs:118-145)
+    const glypr_q8w* wg = L.ple_block.gate.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, wg->qs(), wg->dw(), dev_f32(m->ple_gate), t, P, H, P, s),
+           "per-layer gate launch");
+    LAUNCH(GLYPR_K_GEGLU, s,
+           launch_geglu_quant(dev_f32(m->ple_gate), ple + (int64_t)li * P, NL * P, t, P,
+                              m->hq.as<int8_t>(), dev_f32(m->dh), s),
+           "per-layer geglu launch");
+    const glypr_q8w* wpj = L.ple_block.projection.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wpj->qs(), wpj->dw(),
+                          dev_f32(m->proj), t, H, P, H, s),
+           "per-layer proj launch");
+    // post_norm.forward_residual_add(.., layer_scalar) + next layer's input norm
+    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
+           launch_residual_norm(dev_f32(m->proj), L.ple_block.norm.weight, h, w_next, c.eps, t, H,
+                                last ? nullptr : xq, last ? nullptr : dx, s,
+                                L.ple_block.layer_scalar, false),
+           "residual_norm launch");
+  }
+  // model.rs:576-577: final norm, then the embedding projection when present
+  float* tokens = hidden;
+  if (c.out_dim > 0) {
+    if (!tokens) tokens = dev_f32(m->tokens);
+    LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
+           launch_rmsnorm_quant(h, m->norm.weight, c.eps, t, H, xq, dx, s),
+           "rmsnorm_quant launch");
+    const glypr_q8w* we = m->embedding_projection.w;
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(xq, dx, we->qs(), we->dw(), tokens, t, c.out_dim, H, c.out_dim, s),
+           "embedding projection launch");
+  } else {
+    if (!tokens) tokens = dev_f32(m->normed);
+    LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, tokens, t, H, s),
+           "final rmsnorm launch");
+  }
+  *tokens_out = tokens;
   return GLYPR_OK;
 }
 
@@ -447,6 +631,9 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
   if (c.full_head_dim == 0) c.full_head_dim = c.head_dim;
   if (c.full_n_kv_heads == 0) c.full_n_kv_heads = c.n_kv_heads;
   if (c.max_seq_len == 0) c.max_seq_len = 8320;   // DEFAULT_MAX_SEQ_LEN, lib.rs:47
+  GLYPR_CHECK(c.max_batch_tokens >= 0 && c.max_batch_tokens <= (int64_t(1) << 24),
+              GLYPR_ERR_SHAPE, "max_batch_tokens %lld outside [0, 2^24]",
+              (long long)c.max_batch_tokens);
   // the attention kernels' geometry, checked for both layer types at the
   // longest sequence (shorter ones use fewer key partitions)
   GLYPR_CHECK(attention_supported(c.max_seq_len, c.n_heads, c.n_kv_heads, c.head_dim,
@@ -614,7 +801,9 @@ int glypr_hip_model_finalize(glypr_model* m) {
   // every buffer and table the forward uses, at max_seq_len: model_embed
   // allocates nothing
   RET_IF(ensure_rope(m, m->cfg.max_seq_len));
-  RET_IF(ensure_activations(m, m->cfg.max_seq_len));
+  const int64_t cap = m->cfg.max_batch_tokens > m->cfg.max_seq_len ? m->cfg.max_batch_tokens
+                                                                  : m->cfg.max_seq_len;
+  RET_IF(ensure_activations(m, attn_padded_len(cap)));
   m->finalized = true;
   return GLYPR_OK;
 }
@@ -642,138 +831,86 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
-  // buffers and RoPE tables were sized for max_seq_len at finalize
+  // buffers and RoPE tables were sized at finalize
   hipStream_t s = (hipStream_t)stream;
-  const int64_t H = c.hidden, F = c.ffn, nq = c.n_heads;
-  float* h = dev_f32(m->h);
-  int8_t* xq = m->xq.as<int8_t>();
-  float* dx = dev_f32(m->dx);
-
-  // model.rs:507-508: Embedding::forward, then * embed_scale (f64 sqrt(hidden) as f32)
   GLYPR_TRY_HIP(hipMemcpyAsync(m->ids.p, ids, (size_t)t * 4, hipMemcpyHostToDevice, s),
                 "ids upload");
-  const float embed_scale = (float)sqrt((double)H);
-  LAUNCH(GLYPR_K_GATHER, s,
-         launch_gather(m->token_embd.w->qs(), m->token_embd.w->dw(), H, m->ids.as<uint32_t>(), t,
-                       embed_scale, h, s),
-         "gather launch");
-  // TextPLE::project_and_norm_per_layer (ple.rs:48-85): per_layer_model_proj of
-  // the scaled embeddings, * hidden^-0.5 (f64 powf, applied as candle's f32
-  // affine), RMSNorm over ple_dim.  Layer l's input is row t*NL + l of [t*NL][P].
-  const int64_t P = c.ple_dim, NL = c.n_layers;
-  float* ple = dev_f32(m->ple);
-  if (P > 0) {
-    LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(h, t, H, xq, dx, s), "quantize launch");
-    const glypr_q8w* wpl = m->ple_projection.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, wpl->qs(), wpl->dw(), ple, t, NL * P, H, NL * P, s),
-           "per-layer projection launch");
-    LAUNCH(GLYPR_K_RMSNORM, s, launch_affine(ple, t * NL * P, (float)pow((double)H, -0.5), s),
-           "per-layer scale launch");
-    LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(ple, m->ple_norm.weight, c.eps, ple, t * NL, P, s),
-           "per-layer norm launch");
-  }
-  if (m->dense) return forward_dense(m, ctx, t, trunc, out, hidden, s);
-  // layer 0 input_layernorm as the qkv GEMM's prologue
-  LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
-         launch_rmsnorm_quant(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xq, dx, s),
-         "rmsnorm_quant launch");
-
-  for (size_t li = 0; li < m->layers.size(); li++) {
-    EncoderLayer& L = m->layers[li];
-    const bool last = li + 1 == m->layers.size();
-    const int64_t hd = L.head_dim, nkv = L.n_kv_heads, qd = nq * hd;
-    // ---- attention block (layer.rs:27-34)
-    const glypr_q8w* wqkv = L.self_attn.fused_qkv.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, wqkv->qs(), wqkv->dw(), dev_f32(m->qkv), t, wqkv->n, H, wqkv->n,
-                          s),
-           "qkv gemm launch");
-    const float* cos_t = dev_f32(L.full_attention ? m->cos_f : m->cos_s);
-    const float* sin_t = dev_f32(L.full_attention ? m->sin_f : m->sin_s);
-    RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
-                          L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
-                          L.full_attention ? 0 : c.sliding_window, m->attn_q.as<uint16_t>(),
-                          m->attn_k.as<uint16_t>(), m->attn_vt.as<uint16_t>(),
-                          dev_f32(m->attn_scratch), nullptr,
-                          m->cq.as<int8_t>(), dev_f32(m->dc), s));
-    const glypr_q8w* wo = L.self_attn.o.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(m->cq.as<int8_t>(), dev_f32(m->dc), wo->qs(), wo->dw(),
-                          dev_f32(m->proj), t, H, qd, H, s),
-           "o gemm launch");
-    // post_attention_layernorm.forward_residual_add + pre_feedforward_layernorm prologue
-    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
-           launch_residual_norm(dev_f32(m->proj), L.post_attention_layernorm.weight, h,
-                                L.pre_feedforward_layernorm.weight, c.eps, t, H, xq, dx, s),
-           "residual_norm launch");
-    // ---- feed-forward block (layer.rs:36-42): gate/up + GeGLU epilogue, down
-    const glypr_q8w* wgu = L.mlp.fused_gate_up.w;
-    LAUNCH(GLYPR_K_GEMM_I8_GEGLU, s,
-           launch_gemm_i8_geglu(xq, dx, wgu->qs(), wgu->dw(), m->hq.as<int8_t>(), dev_f32(m->dh),
-                                t, F, H, s),
-           "gate/up GeGLU launch");
-    const glypr_q8w* wd = L.mlp.down.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wd->qs(), wd->dw(),
-                          dev_f32(m->proj), t, H, F, H, s),
-           "down gemm launch");
-    const float* w_next = last ? nullptr : m->layers[li + 1].input_layernorm.weight;
-    if (P == 0) {
-      // post_feedforward_layernorm.forward_residual_add + next layer's input norm
-      LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
-             launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h,
-                                  w_next, c.eps, t, H, last ? nullptr : xq, last ? nullptr : dx,
-                                  s),
-             "residual_norm launch");
-      continue;
-    }
-    // post_feedforward_layernorm.forward_residual_add, then Q8_0 of h itself
-    // for the PLE block's inp_gate (no norm in front of it)
-    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
-           launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h, nullptr,
-                                c.eps, t, H, xq, dx, s, nullptr, true),
-           "residual_norm launch");
-    // ---- TextPLEBlock::forward_with_scalar (ple.rs:118-145)
-    const glypr_q8w* wg = L.ple_block.gate.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, wg->qs(), wg->dw(), dev_f32(m->ple_gate), t, P, H, P, s),
-           "per-layer gate launch");
-    LAUNCH(GLYPR_K_GEGLU, s,
-           launch_geglu_quant(dev_f32(m->ple_gate), ple + (int64_t)li * P, NL * P, t, P,
-                              m->hq.as<int8_t>(), dev_f32(m->dh), s),
-           "per-layer geglu launch");
-    const glypr_q8w* wpj = L.ple_block.projection.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wpj->qs(), wpj->dw(),
-                          dev_f32(m->proj), t, H, P, H, s),
-           "per-layer proj launch");
-    // post_norm.forward_residual_add(.., layer_scalar) + next layer's input norm
-    LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
-           launch_residual_norm(dev_f32(m->proj), L.ple_block.norm.weight, h, w_next, c.eps, t, H,
-                                last ? nullptr : xq, last ? nullptr : dx, s,
-                                L.ple_block.layer_scalar, false),
-           "residual_norm launch");
-  }
-  // model.rs:576-577: final norm, then the embedding projection when present
-  const int64_t width = c.out_dim > 0 ? c.out_dim : H;
-  float* tokens = hidden;
-  if (c.out_dim > 0) {
-    if (!tokens) tokens = dev_f32(m->tokens);
-    LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
-           launch_rmsnorm_quant(h, m->norm.weight, c.eps, t, H, xq, dx, s),
-           "rmsnorm_quant launch");
-    const glypr_q8w* we = m->embedding_projection.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, we->qs(), we->dw(), tokens, t, c.out_dim, H, c.out_dim, s),
-           "embedding projection launch");
-  } else {
-    if (!tokens) tokens = dev_f32(m->normed);
-    LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, tokens, t, H, s),
-           "final rmsnorm launch");
-  }
+  float* tokens = nullptr;
+  RET_IF(forward_rows(m, ctx, Rows{t, nullptr, 0}, hidden, &tokens, s));
+  const int64_t width = c.out_dim > 0 ? c.out_dim : c.hidden;
   LAUNCH(GLYPR_K_POOL, s,
          launch_pool(tokens, nullptr, t, width, trunc, out, dev_f32(m->pooled), s),
+         "pool launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_model_embed_batch(glypr_model* m, const uint32_t* ids, const int64_t* lens,
+                                int64_t n_seqs, int64_t trunc, float* out, glypr_stream stream) {
+  clear_error();
+  GLYPR_CHECK(m != nullptr, GLYPR_ERR_INVALID_ARG, "model is NULL");
+  GLYPR_CHECK(m->finalized, GLYPR_ERR_INVALID_ARG, "call glypr_hip_model_finalize first");
+  GLYPR_CHECK(n_seqs > 0 && trunc >= 0, GLYPR_ERR_SHAPE, "n_seqs = %lld, trunc = %lld",
+              (long long)n_seqs, (long long)trunc);
+  GLYPR_CHECK(ids != nullptr && lens != nullptr && out != nullptr, GLYPR_ERR_INVALID_ARG,
+              "ids, lens or out is NULL");
+  GLYPR_CHECK(aligned16(out), GLYPR_ERR_ALIGNMENT, "out must be 16-byte aligned");
+  const glypr_model_config& c = m->cfg;
+  // embed_batch_inner's preflight per item (lib.rs:838-845), then the layout:
+  // sequence i at rows [off_i, off_i + lens[i]), offsets 64-aligned
+  int64_t rows = 0, total = 0, longest = 0;
+  for (int64_t i = 0; i < n_seqs; i++) {
+    GLYPR_CHECK(lens[i] > 0 && lens[i] <= c.max_seq_len, GLYPR_ERR_SHAPE,
+                "batch item %lld sequence length (%lld) is outside [1, %lld]", (long long)i,
+                (long long)lens[i], (long long)c.max_seq_len);
+    rows += attn_padded_len(lens[i]);
+    total += lens[i];
+    longest = lens[i] > longest ? lens[i] : longest;
+  }
+  GLYPR_CHECK(rows <= m->cap_t, GLYPR_ERR_SHAPE,
+              "batch of %lld sequences takes %lld padded rows; the model holds %lld "
+              "(max_batch_tokens)", (long long)n_seqs, (long long)rows, (long long)m->cap_t);
+  for (int64_t i = 0; i < total; i++)
+    GLYPR_CHECK((int64_t)ids[i] < c.vocab, GLYPR_ERR_RANGE,
+                "token id %u at position %lld is out of range for vocab %lld", ids[i],
+                (long long)i, (long long)c.vocab);
+  glypr_hip_ctx* ctx = m->ctx;
+  DeviceScope ds(ctx->device);
+  if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  hipStream_t s = (hipStream_t)stream;
+  // host staging (capacity reserved at finalize): padded ids (padding rows take
+  // id 0; they never reach a valid token's attention or its pooled mean),
+  // the per-row segment table and the per-sequence {offset, length}
+  m->h_ids.assign((size_t)rows, 0u);
+  m->h_seg.resize((size_t)rows * 2);
+  m->h_seqs.resize((size_t)n_seqs * 2);
+  int64_t off = 0, src = 0;
+  for (int64_t i = 0; i < n_seqs; i++) {
+    const int64_t len = lens[i], span = attn_padded_len(len);
+    memcpy(m->h_ids.data() + off, ids + src, (size_t)len * 4);
+    for (int64_t r = off; r < off + span; r++) {
+      m->h_seg[(size_t)r * 2] = (int32_t)off;
+      m->h_seg[(size_t)r * 2 + 1] = (int32_t)len;
+    }
+    m->h_seqs[(size_t)i * 2] = (int32_t)off;
+    m->h_seqs[(size_t)i * 2 + 1] = (int32_t)len;
+    off += span;
+    src += len;
+  }
+  // pageable-memory uploads are staged before hipMemcpyAsync returns, so the
+  // host vectors may be refilled by the next call
+  GLYPR_TRY_HIP(hipMemcpyAsync(m->ids.p, m->h_ids.data(), (size_t)rows * 4,
+                               hipMemcpyHostToDevice, s), "ids upload");
+  GLYPR_TRY_HIP(hipMemcpyAsync(m->seg.p, m->h_seg.data(), (size_t)rows * 8,
+                               hipMemcpyHostToDevice, s), "segment table upload");
+  GLYPR_TRY_HIP(hipMemcpyAsync(m->seqs.p, m->h_seqs.data(), (size_t)n_seqs * 8,
+                               hipMemcpyHostToDevice, s), "sequence table upload");
+  float* tokens = nullptr;
+  RET_IF(forward_rows(m, ctx, Rows{rows, m->seg.as<int32_t>(), longest}, nullptr, &tokens, s));
+  const int64_t width = c.out_dim > 0 ? c.out_dim : c.hidden;
+  LAUNCH(GLYPR_K_POOL, s,
+         launch_pool_segments(tokens, rows, m->seg.as<int32_t>(), m->seqs.as<int32_t>(), n_seqs,
+                              width, trunc, out, dev_f32(m->pooled), s),
          "pool launch");
   return GLYPR_OK;
 }

@@ -385,7 +385,7 @@ class ModelConfig(ctypes.Structure):
                 ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double),
                 ("ple_dim", ctypes.c_int64), ("out_dim", ctypes.c_int64),
                 ("full_head_dim", ctypes.c_int64), ("full_n_kv_heads", ctypes.c_int64),
-                ("max_seq_len", ctypes.c_int64)]
+                ("max_seq_len", ctypes.c_int64), ("max_batch_tokens", ctypes.c_int64)]
 
 
 class Gguf:
@@ -493,7 +493,7 @@ class Model:
         defaults = dict(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256, n_layers=24,
                         vocab=262144, sliding_window=512, eps=1e-6, rope_theta_sliding=10000.0,
                         rope_theta_full=1e6, ple_dim=0, out_dim=0, full_head_dim=0,
-                        full_n_kv_heads=0, max_seq_len=0)
+                        full_n_kv_heads=0, max_seq_len=0, max_batch_tokens=0)
         defaults.update(cfg)
         self.cfg = defaults
         self.ctx = ctx
@@ -526,6 +526,21 @@ class Model:
         check(lib().glypr_hip_model_embed(self.handle, ids.ctypes.data_as(ctypes.c_void_p),
                                           ids.size, trunc, _ptr(out), _ptr(hidden),
                                           self.ctx.stream))
+        return out
+
+    def embed_batch(self, seqs, trunc: int = 0, out: Optional[torch.Tensor] = None):
+        """glypr_hip_model_embed_batch: a list of id arrays -> [n, width]."""
+        lens = np.array([len(q) for q in seqs], dtype=np.int64)
+        ids = np.ascontiguousarray(np.concatenate([np.asarray(q, np.uint32) for q in seqs]),
+                                   dtype=np.uint32)
+        H = self.cfg.get("out_dim") or self.cfg["hidden"]
+        td = trunc if 0 < trunc < H else H
+        if out is None:
+            out = torch.empty((len(seqs), td), dtype=torch.float32,
+                              device=f"cuda:{self.ctx.device}")
+        check(lib().glypr_hip_model_embed_batch(self.handle, ids.ctypes.data_as(ctypes.c_void_p),
+                                                lens.ctypes.data_as(ctypes.c_void_p), len(seqs),
+                                                trunc, _ptr(out), self.ctx.stream))
         return out
 
     def close(self):

@@ -297,6 +297,9 @@ typedef struct glypr_model_config {
                                 * (GlyprEmbedder::max_seq_len, lib.rs:47, 425);
                                 * every activation buffer is sized for it at
                                 * finalize; 0 = 8320 */
+  int64_t max_batch_tokens;    /* padded rows one glypr_hip_model_embed_batch
+                                * call may take (each sequence rounded up to 64);
+                                * buffers are sized for max(max_seq_len, this) */
 } glypr_model_config;
 
 typedef struct glypr_model glypr_model;
@@ -340,6 +343,19 @@ int glypr_hip_model_finalize(glypr_model* model);
  * take bf16 activations (nearest even) with f32 accumulation. */
 int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, int64_t trunc,
                           float* out, float* hidden, glypr_stream stream);
+
+/* embed_batch_inner (lib.rs:752-952) for text: n_seqs sequences of lens[i]
+ * tokens (ids concatenated, host memory) in one forward pass.  Each sequence's
+ * embedding equals the one the reference computes from its padded batch (pad
+ * keys masked out of attention, pads left out of the mean, model.rs:580-705),
+ * which is the sequence's own single-sequence embedding.  The sequences sit at
+ * 64-aligned row offsets, so every projection runs once over all of their rows
+ * and attention and pooling stay within each sequence.  out [n_seqs][trunc,
+ * or the embedding width].  Each len must be in [1, max_seq_len] (the
+ * preflight of lib.rs:838-845) and the padded total <= max(max_seq_len,
+ * max_batch_tokens) (GLYPR_ERR_SHAPE otherwise). */
+int glypr_hip_model_embed_batch(glypr_model* model, const uint32_t* ids, const int64_t* lens,
+                                int64_t n_seqs, int64_t trunc, float* out, glypr_stream stream);
 
 int glypr_hip_model_destroy(glypr_model* model);
 

@@ -149,6 +149,13 @@ def test_vector_codec_validation():
         _lib.GLYPR_ERR_SHAPE
 
 
+def test_embed_batch_validation():
+    L = _lib.lib()
+    lens = (ctypes.c_int64 * 2)(3, 4)
+    assert L.glypr_hip_model_embed_batch(NULL, FAKE, lens, 2, 256, FAKE, NULL) == \
+        _lib.GLYPR_ERR_INVALID_ARG
+
+
 def test_handle_lifecycle_validation():
     L = _lib.lib()
     assert L.glypr_hip_q8_0_weight_destroy(NULL) == _lib.GLYPR_OK

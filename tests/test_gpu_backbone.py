@@ -525,3 +525,89 @@ def test_real_geometry_gguf_load(ctx, oracle, tmp_path):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     g.close()
     m.close()
+
+
+# ------------------------------------------------ several sequences at once --
+
+def _cos(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(a @ b / np.linalg.norm(a) / np.linalg.norm(b))
+
+
+def test_embed_batch_vs_single_and_oracle(ctx, oracle):
+    """glypr_hip_model_embed_batch (embed_batch_inner, lib.rs:752-952): a
+    heterogeneous batch (lengths 512, 37, 600, 64, 1, 1000: padding inside the
+    64-row slots, sequences longer and shorter than the 512 window, the full
+    layer over 1000 keys) gives each sequence its single-sequence embedding,
+    and each meets BASELINE's cosine against the oracle."""
+    n_layers, vocab = 6, 2000
+    lens = [512, 37, 600, 64, 1, 1000]
+    say(f"embed_batch lens={lens} layers={n_layers}")
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=60)
+    seqs = [oracle.uniform_ids(n, seed=61 + i, vocab=vocab) for i, n in enumerate(lens)]
+    got = host(m.embed_batch(seqs, trunc=256))
+    again = host(m.embed_batch(seqs, trunc=256))
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+    for i, q in enumerate(seqs):
+        single = host(m.embed(q, trunc=256))
+        ref, _ = oracle_forward(oracle, tensors, n_layers, vocab, q, 256)
+        c1, c2 = _cos(got[i], single), _cos(got[i], ref)
+        say(f"  seq {i} len {lens[i]}: cos vs single {c1:.9f}, vs oracle {c2:.8f}")
+        assert c1 >= 0.99999 and c2 >= 0.9999
+        assert abs(np.linalg.norm(got[i].astype(np.float64)) - 1) < 1e-5
+    # a batch of one is the single-sequence embedding
+    one = host(m.embed_batch([seqs[2]], trunc=256))
+    assert _cos(one[0], host(m.embed(seqs[2], trunc=256))) >= 0.99999
+    from glypr_amd._lib import GlyprError
+    with pytest.raises(GlyprError) as e:     # over the model's row capacity (8320)
+        m.embed_batch([seqs[5]] * 9, trunc=256)
+    assert e.value.code == _lib.GLYPR_ERR_SHAPE
+    m.close()
+
+
+def test_embed_batch_real_geometry_and_dense(ctx, oracle):
+    """The batch path with the released geometry (head_dim 512 full layer, 2 kv
+    heads, PLE, projection) and with dense bf16 projections: each sequence
+    against its single-sequence embedding."""
+    lens = [300, 70, 650]
+    say(f"embed_batch real geometry + dense bf16, lens={lens}")
+    raw, shaped = real_geometry_tensors(oracle, 6, 2000, 256, 768, seed=62)
+    m = Model(ctx, n_layers=6, vocab=2000, ple_dim=256, out_dim=768, **REAL)
+    for name, (data, r, c, q8) in shaped.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    seqs = [oracle.uniform_ids(n, seed=70 + i, vocab=2000) for i, n in enumerate(lens)]
+    got = host(m.embed_batch(seqs, trunc=128))
+    for i, q in enumerate(seqs):
+        c1 = _cos(got[i], host(m.embed(q, trunc=128)))
+        say(f"  real geometry seq {i}: cos vs single {c1:.9f}")
+        assert c1 >= 0.99999
+    m.close()
+    d, _ = make_model(ctx, oracle, 2, 2000, seed=63, dense=True)
+    got = host(d.embed_batch(seqs, trunc=0))
+    for i, q in enumerate(seqs):
+        c1 = _cos(got[i], host(d.embed(q, trunc=0)))
+        say(f"  dense bf16 seq {i}: cos vs single {c1:.9f}")
+        assert c1 >= 0.99999
+    d.close()
+
+
+def test_embed_batch_c3_regime(ctx, oracle):
+    """C3's batch, 32 sequences x 512 tokens (M = 16384 through every
+    projection), on 2 layers with max_batch_tokens 16384: sampled sequences
+    against their single-sequence embeddings."""
+    vocab = 5000
+    say("embed_batch 32 x 512 (M = 16384)")
+    m = Model(ctx, n_layers=2, vocab=vocab, max_batch_tokens=16384)
+    m0, tensors = make_model(ctx, oracle, 2, vocab, seed=64)
+    m0.close()
+    for name, (data, r, c, q8) in tensors.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    seqs = [oracle.uniform_ids(512, seed=80 + i, vocab=vocab) for i in range(32)]
+    got = host(m.embed_batch(seqs, trunc=256))
+    assert np.isfinite(got).all()
+    for i in (0, 13, 31):
+        c1 = _cos(got[i], host(m.embed(seqs[i], trunc=256)))
+        assert c1 >= 0.99999, (i, c1)
+    m.close()
