@@ -1,8 +1,10 @@
 // k_attn.hip — the attention side of one encoder layer (backbone configs):
 //   qkv_post: q/k/v RMSNorm per head (q_norm, k_norm, weightless v_norm), RoPE,
-//             and the f16 hi/lo split the MFMA attention consumes;
+//             and the f16 Q / K / V^T operands the MFMA attention consumes;
 //   attention: bidirectional GQA flash attention, scale 1.0, f32 softmax,
 //             optional band mask |i - j| <= W (sliding layers).
+// Head dims 256 and 512 (the released model's full-attention layers), one
+// sequence or several at 64-aligned row offsets (a segment table).
 //
 // Reference semantics: SelfAttention::forward (attention/mod.rs:166-277):
 // q/k/v projections -> per-head RMSNorm on [T, heads, hd] -> transpose ->
