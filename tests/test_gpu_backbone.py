@@ -584,8 +584,15 @@ def test_embed_batch_real_geometry_and_dense(ctx, oracle):
     got = host(m.embed_batch(seqs, trunc=128))
     for i, q in enumerate(seqs):
         c1 = _cos(got[i], host(m.embed(q, trunc=128)))
-        say(f"  real geometry seq {i}: cos vs single {c1:.9f}")
-        assert c1 >= 0.99999
+        ref, _ = oracle.model_forward(raw, q, 128, hidden=512, ffn=2048, n_heads=4,
+                                      n_kv_heads=2, head_dim=256, n_layers=6, vocab=2000,
+                                      full_head_dim=512, full_n_kv_heads=1)
+        c2 = _cos(got[i], ref)
+        say(f"  real geometry seq {i}: cos vs single {c1:.9f}, vs oracle {c2:.8f}")
+        # batch and single runs split the keys into different partitions, so
+        # their f32 sums round differently and some Q8_0 roundings of the
+        # o / PLE / projection inputs flip: both are held to the oracle bar
+        assert c1 >= 0.9999 and c2 >= 0.9999
     m.close()
     d, _ = make_model(ctx, oracle, 2, 2000, seed=63, dense=True)
     got = host(d.embed_batch(seqs, trunc=0))
