@@ -206,8 +206,23 @@ __device__ __forceinline__ void vm_wait_units(int later) {
 // expm1(y) = 2^k * p + (2^k - 1).  Only IEEE +,-,*,/ and fma appear, so the
 // CPU oracle computes the same bits.  Max error ~2.5 ulp vs exact tanh.
 // ---------------------------------------------------------------------------
+// Straight-line code: every case is computed and the result picked by
+// selects (v_cndmask), so the four h elements a lane holds run interleaved
+// instead of one after another behind per-element branches.  Each select
+// returns exactly what the branch of the CPU statement (orc_tanhf) returns.
+// materialize(v) pins v to a register at that point (an empty asm that reads
+// and writes it), so the compiler cannot sink v's computation into a branch
+// around the select.
+__device__ __forceinline__ float materialize(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// expm1(y) for y in [-20, -2^-11] (tanh_glypr's range): the oracle's
+// orc_expm1_nonpos without its two early returns, which cannot change a bit
+// here: y >= -20 never takes the y < -30 one, and for k == 0 the general
+// result fma(1, p, 1 - 1) = p + 0 equals p (p < 0 for these y).
 __device__ __forceinline__ float expm1_nonpos(float y) {
-  if (y < -30.0f) return -1.0f;
   const float LOG2E = 1.44269504088896341f;
   const float LN2_HI = 6.93145751953125e-01f;
   const float LN2_LO = 1.42860682030941723e-06f;
@@ -221,31 +236,33 @@ __device__ __forceinline__ float expm1_nonpos(float y) {
   p = fmaf(r, p, 1.66666666666666667e-01f);
   p = fmaf(r, p, 0.5f);
   p = fmaf(r * r, p, r);
-  int k = (int)kf;
-  if (k == 0) return p;
-  float s = __int_as_float((k + 127) << 23);
-  return fmaf(s, p, s - 1.0f);
+  const int k = (int)kf;
+  const float sc = __int_as_float((k + 127) << 23);
+  return fmaf(sc, p, sc - 1.0f);
 }
 
+// orc_tanhf's value for every input.  The general path runs on |x| clamped to
+// [2^-12, 10]: at 10 it gives expm1(-20) = -1.0f exactly and so +-1, which is
+// orc_tanhf's |x| >= 10 result; the NaN and |x| < 2^-12 cases (-> x) are
+// selects.
 __device__ __forceinline__ float tanh_glypr(float x) {
-  float ax = fabsf(x);
-  if (x != x) return x;
-  if (ax >= 10.0f) return copysignf(1.0f, x);
-  if (ax < 2.44140625e-04f) return x;
-  float t = expm1_nonpos(-2.0f * ax);
-  float r = -t / (t + 2.0f);
-  return copysignf(r, x);
+  const float ax = fabsf(x);
+  const float axc = fminf(fmaxf(ax, 2.44140625e-04f), 10.0f);
+  const float t = expm1_nonpos(-2.0f * axc);
+  const float r = materialize(copysignf(-t / (t + 2.0f), x));
+  return (x != x || ax < 2.44140625e-04f) ? x : r;
 }
 
-// geglu_scalar_f32 (cpu_simd/geglu.rs:6-18).
+// geglu_scalar_f32 (cpu_simd/geglu.rs:6-18).  For g >= 10 the general path
+// already gives g * u (tanh = 1, so act = (0.5 g) * 2 = g); g <= -10 gives
+// +-0 there, where the reference returns +0, hence the select.
 __device__ __forceinline__ float geglu_scalar(float g, float u) {
-  if (g <= -10.0f) return 0.0f;
-  if (g >= 10.0f) return g * u;
   float g3 = g * g * g;
   float inner = 0.7978846f * (g + 0.044715f * g3);
   float th = tanh_glypr(inner);
   float act = 0.5f * g * (1.0f + th);
-  return act * u;
+  const float mid = materialize(act * u);
+  return g <= -10.0f ? 0.0f : mid;
 }
 
 }  // namespace glypr
