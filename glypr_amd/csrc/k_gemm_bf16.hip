@@ -32,13 +32,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // error up to 2^-9): tanh(z) = 1 - 2 / (exp2(2 z log2 e) + 1) on the
 // hardware exp2 and reciprocal (~1e-6 relative), the same tanh-GELU
 // constants and the +-10 clamp of geglu_scalar_f32 (cpu_simd/geglu.rs:6-18).
+// Straight-line: the formula is evaluated for every g (it cannot trap) and
+// the clamps select, so a wave's lanes need no divergent branches.
 __device__ __forceinline__ float geglu_bf16(float g, float u) {
-  if (g <= -10.0f) return 0.0f;
-  if (g >= 10.0f) return g * u;
   const float inner = 0.7978846f * (g + 0.044715f * (g * g * g));
   const float e = __builtin_amdgcn_exp2f(2.0f * 1.44269504f * inner);
   const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-  return 0.5f * g * (1.0f + th) * u;
+  const float mid = materialize(0.5f * g * (1.0f + th) * u);
+  return g <= -10.0f ? 0.0f : (g >= 10.0f ? g * u : mid);
 }
 
 // 16 int8 -> 16 bf16 (32 bytes) scaled by d.
@@ -219,31 +220,37 @@ hipError_t run(const uint16_t* xb, const int8_t* wq, const float* dw, float* y, 
 }
 
 // ---------------------------------------------------------------------------
-// Large-M variant (M > 2048, K % 64 == 0).  128 x 256 tiles on 4 waves side
-// by side along N, 128 x 64 outputs each (4 x 2 v_mfma_f32_32x32x16_bf16
-// tiles), so every B column is dequantized by exactly one wave; every
-// 64-K stage arrives by LDS DMA into a two-slot ring:
+// Large-M variant (M > 2048, K % 64 == 0).  128 x 128 tiles on 4 waves side
+// by side along N, 128 x 32 outputs each (4 v_mfma_f32_32x32x16_bf16 tiles
+// stacked along M), so every B column is dequantized by exactly one wave;
+// every 64-K stage arrives by LDS DMA into a two-slot ring:
 //   A  [128 rows][128 B] bf16, 16-byte chunk c of row r at c ^ ((r >> 1) & 7);
-//   B  [256 rows][64 B]  int8, chunk c of row r at c ^ ((r >> 2) & 3);
-//   dB [2 blocks][256 rows] f32.
+//   B  [128 rows][64 B]  int8, chunk c of row r at c ^ ((r >> 2) & 3);
+//   dB [2 blocks][128 rows] f32.
 // Per 32-K block a lane reads 16 consecutive K of its A row (two b128) and
 // of its B column (one b128 of int8), dequantizes the latter in registers
 // (dequant16: the exact q*d, then bf16 round-to-nearest-even, as the staged
 // path) and runs two MFMA k-steps on K {0..7, 16..23} and {8..15, 24..31} of
 // the block; A and B use the same order, so every product is formed once.
-// XCD-aware tile order as in the int8 large-M kernel; 68 KB of LDS, so two
-// workgroups share a CU.
+// XCD-aware tile order as in the int8 large-M kernel; 50 KB of LDS and ~120
+// VGPRs, so three workgroups share a CU.  The 128-column tile (rather than
+// 256) keeps the grids of the C3 projections near whole rounds of 768
+// workgroup slots.
+// GEGLU: the 32 B rows of wave w are gate columns hc0 + 16 w .. + 15, then
+// the up columns of the same h columns, so lanes l and l + 16 hold gate and
+// up of one h element; one v_permlane16_swap per register pair brings them
+// together, and each lane evaluates half of its 16 rows per MFMA tile.
 // ---------------------------------------------------------------------------
-constexpr int BFB_BN = 256, BFB_BK = 64;
+constexpr int BFB_BN = 128, BFB_BK = 64;
 
 // TM 32-row MFMA tiles per wave (BM = 32 TM rows per workgroup).
 template <bool GEGLU, int TM>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TM == 2 ? 3 : 2)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ B,
                      const float* __restrict__ dB, float* __restrict__ C,
                      uint16_t* __restrict__ Hb, int M, int N, int K, int ldc, int F,
                      int tiles_n) {
-  constexpr int NW = 4, TN = 2, BFB_BM = 32 * TM;
+  constexpr int NW = 4, BFB_BM = 32 * TM;
   constexpr int UA = BFB_BM / 8;         // 1 KB units: 8 A rows of 128 B
   constexpr int UB = BFB_BN / 16;        // 1 KB units: 16 B rows of 64 B
   constexpr int USB = 2 * BFB_BN / 64;   // 256 B units: 64 scales of one block
@@ -266,18 +273,17 @@ gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ 
   const int hc0 = n0 >> 1;
   const int nb = K / QK, nst = K / BFB_BK;
 
-  // GEGLU: 32-row tiles alternate gate and up of the same 32 h columns.
+  // GEGLU: 32-row group t holds gate then up of h columns hc0 + 16 t .. + 15.
   auto b_row = [&](int nl) -> int {
     if (!GEGLU) return n0 + nl < N ? n0 + nl : N - 1;
-    const int t = nl >> 5;
-    int c = hc0 + (t >> 1) * 32 + (nl & 31);
+    int c = hc0 + 16 * (nl >> 5) + (nl & 15);
     if (c >= F) c = F - 1;
-    return (t & 1) ? F + c : c;
+    return (nl & 16) ? F + c : c;
   };
   auto a_row = [&](int ml) -> int { return m0 + ml < M ? m0 + ml : M - 1; };
 
   // this wave's DMA units, unit u = 4 j + wave: [0, UA) A, [UA, UA + UB) B,
-  // then the B scales of block u / 4 of the stage, 64 rows each.
+  // then the B scales of block u / 2 of the stage, 64 rows each.
   const int8_t* ubase[UPW];
   int uvoff[UPW];
 #pragma unroll
@@ -315,7 +321,7 @@ gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ 
   // fragment offsets; the swizzles depend on lrow only (tile rows are
   // multiples of 32)
   const int lrow = lane & 31, lhalf = lane >> 5;
-  int offA[TM][2][2], offB[TN][2], offS[TN][2];
+  int offA[TM][2][2], offB[2], offS[2];
 #pragma unroll
   for (int p = 0; p < 2; p++) {
 #pragma unroll
@@ -325,20 +331,15 @@ gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ 
         const int row = 32 * tm + lrow, q = 4 * p + 2 * lhalf + h;
         offA[tm][p][h] = row * 128 + ((q ^ ((row >> 1) & 7)) << 4);
       }
-#pragma unroll
-    for (int tn = 0; tn < TN; tn++) {
-      const int row = 64 * wn + 32 * tn + lrow, c = 2 * p + lhalf;
-      offB[tn][p] = OFF_B + row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
-      offS[tn][p] = OFF_SB + (p * BFB_BN + row) * 4;
-    }
+    const int row = 32 * wn + lrow, c = 2 * p + lhalf;
+    offB[p] = OFF_B + row * 64 + ((c ^ ((row >> 2) & 3)) << 4);
+    offS[p] = OFF_SB + (p * BFB_BN + row) * 4;
   }
-  v16f acc[TM][TN];
+  v16f acc[TM];
 #pragma unroll
   for (int tm = 0; tm < TM; tm++)
 #pragma unroll
-    for (int tn = 0; tn < TN; tn++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
+    for (int r = 0; r < 16; r++) acc[tm][r] = 0.0f;
 
 #pragma unroll 1
   for (int st = 0; st < nst; st++) {
@@ -355,47 +356,73 @@ gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ 
 #pragma unroll
         for (int h = 0; h < 2; h++)
           a[tm][h] = *reinterpret_cast<const v8bf*>(slot + offA[tm][p][h]);
+      const v4i q = *reinterpret_cast<const v4i*>(slot + offB[p]);
+      const float d = *reinterpret_cast<const float*>(slot + offS[p]);
+      v4i lo, hi;
+      dequant16(q, d, lo, hi);
+      const v8bf b0 = __builtin_bit_cast(v8bf, lo), b1 = __builtin_bit_cast(v8bf, hi);
 #pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        const v4i q = *reinterpret_cast<const v4i*>(slot + offB[tn][p]);
-        const float d = *reinterpret_cast<const float*>(slot + offS[tn][p]);
-        v4i lo, hi;
-        dequant16(q, d, lo, hi);
-        const v8bf b0 = __builtin_bit_cast(v8bf, lo), b1 = __builtin_bit_cast(v8bf, hi);
-#pragma unroll
-        for (int tm = 0; tm < TM; tm++) {
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][0], b0, acc[tm][tn], 0, 0, 0);
-          acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][1], b1, acc[tm][tn], 0, 0, 0);
-        }
+      for (int tm = 0; tm < TM; tm++) {
+        acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][0], b0, acc[tm], 0, 0, 0);
+        acc[tm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][1], b1, acc[tm], 0, 0, 0);
       }
     }
   }
 
   // output rows of register r: 8 (r >> 2) + 4 lhalf + (r & 3) of the 32-row tile
   if constexpr (!GEGLU) {
+    const int gn = n0 + 32 * wn + lrow;
+    float* crow = C + (int64_t)(m0 + 4 * lhalf) * ldc + gn;
+    if (m0 + BFB_BM <= M && n0 + BFB_BN <= N) {  // whole tile in range (uniform)
 #pragma unroll
-    for (int tm = 0; tm < TM; tm++)
+      for (int tm = 0; tm < TM; tm++)
 #pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        const int gn = n0 + 64 * wn + 32 * tn + lrow;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int gm = m0 + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-          if (gm < M && gn < N) C[(int64_t)gm * ldc + gn] = acc[tm][tn][r];
-        }
-      }
-  } else {
-    // tiles 0 and 1 of the wave are gate and up of h columns hc0 + 32 wn ..
-    const int hc = hc0 + 32 * wn + lrow;
-#pragma unroll
-    for (int qp = 0; qp < TN / 2; qp++) {
+        for (int r = 0; r < 16; r++)
+          crow[(int64_t)(32 * tm + 8 * (r >> 2) + (r & 3)) * ldc] = acc[tm][r];
+    } else {
 #pragma unroll
       for (int tm = 0; tm < TM; tm++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int gm = m0 + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-          const float h = geglu_bf16(acc[tm][2 * qp][r], acc[tm][2 * qp + 1][r]);
-          if (gm < M && hc < F) Hb[(int64_t)gm * F + hc] = __builtin_bit_cast(uint16_t, (__bf16)h);
+          if (gm < M && gn < N) crow[(int64_t)(32 * tm + 8 * (r >> 2) + (r & 3)) * ldc] = acc[tm][r];
+        }
+    }
+  } else {
+    // Lane l < 16 (of each 16-lane row pair) holds gate, lane l + 16 up, of
+    // h column hc.  v_permlane16_swap on registers (i, 8 + i) swaps the odd
+    // 16-lane rows of the first with the even rows of the second, leaving
+    // gate in the first and up in the second, for tile row 8 (i >> 2) +
+    // 4 lhalf + (i & 3) in lanes l < 16 and that row + 16 in lanes l + 16.
+    const int hc = hc0 + 16 * wn + (lrow & 15);
+    uint16_t hv[TM][8];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        // (copied to scalars first: __builtin_bit_cast of an ext_vector
+        // element reads element 0 with this compiler)
+        const float x = acc[tm][i], y = acc[tm][8 + i];
+        const auto gu = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                         __builtin_bit_cast(uint32_t, y), false, false);
+        const float h = geglu_bf16(__builtin_bit_cast(float, (uint32_t)gu[0]),
+                                   __builtin_bit_cast(float, (uint32_t)gu[1]));
+        hv[tm][i] = __builtin_bit_cast(uint16_t, (__bf16)h);
+      }
+    uint16_t* hrow = Hb + (int64_t)(m0 + (lrow & 16) + 4 * lhalf) * F + hc;
+    if (m0 + BFB_BM <= M && hc0 + BFB_BN / 2 <= F) {  // whole tile in range (uniform)
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          hrow[(int64_t)(32 * tm + 8 * (i >> 2) + (i & 3)) * F] = hv[tm][i];
+    } else {
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const int gm = m0 + 32 * tm + 8 * (i >> 2) + (lrow & 16) + 4 * lhalf + (i & 3);
+          if (gm < M && hc < F) hrow[(int64_t)(32 * tm + 8 * (i >> 2) + (i & 3)) * F] = hv[tm][i];
         }
     }
   }
