@@ -5,9 +5,9 @@
 // unquantized activations, f32 accumulate; fused_ops.metal:574-581, 649-758)
 // and of candle's CANDLE_DEQUANTIZE_ALL path, at bf16 operand precision.
 // Weights stay Q8_0 in HBM (1.125 B/value); each 16-byte int8 chunk is turned
-// into 16 bf16 values on the way into LDS: q ^ 0x80 as an unsigned byte
-// (v_cvt_f32_ubyteN) then fma(q+128, d, -128 d) = q*d exactly, then
-// v_cvt_pk_bf16_f32 (round to nearest even).  Activations arrive as bf16 from
+// into 16 bf16 values in registers: the signed byte to f32 (an SDWA byte
+// select of v_cvt_f32_i32), q*d (exact), then v_cvt_pk_bf16_f32 (round to
+// nearest even).  Activations arrive as bf16 from
 // the RMSNorm prologue (or a conversion pass).
 #include "device_common.hpp"
 #include "internal.hpp"
@@ -29,30 +29,33 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 }
 
 // GeGLU of the BF16_DEQUANT path, whose h is rounded to bf16 (relative
-// error up to 2^-9): tanh(z) = 1 - 2 / (exp2(2 z log2 e) + 1) on the
-// hardware exp2 and reciprocal (~1e-6 relative), the same tanh-GELU
-// constants and the +-10 clamp of geglu_scalar_f32 (cpu_simd/geglu.rs:6-18).
-// Straight-line: the formula is evaluated for every g (it cannot trap) and
-// the clamps select, so a wave's lanes need no divergent branches.
+// error up to 2^-9): 0.5 g (1 + tanh(z)) = g sigmoid(2 z), evaluated as
+// g u / (1 + exp2(-2 log2(e) z)) on the hardware exp2 and reciprocal (~1e-6
+// relative, and no cancellation for negative z, where 1 + tanh(z) would
+// lose its low bits); the tanh-GELU constants and the +-10 clamps of
+// geglu_scalar_f32 (cpu_simd/geglu.rs:6-18).  Straight-line: the formula is
+// evaluated for every g (it cannot trap) and the clamps select, so a wave's
+// lanes need no divergent branches.
 __device__ __forceinline__ float geglu_bf16(float g, float u) {
-  const float inner = 0.7978846f * (g + 0.044715f * (g * g * g));
-  const float e = __builtin_amdgcn_exp2f(2.0f * 1.44269504f * inner);
-  const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
-  const float mid = materialize(0.5f * g * (1.0f + th) * u);
+  // -2 log2(e) * 0.7978846
+  const float z2 = -2.3022083f * (g + 0.044715f * (g * g * g));
+  const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z2));
+  const float mid = materialize((g * u) * s);
   return g <= -10.0f ? 0.0f : (g >= 10.0f ? g * u : mid);
 }
 
-// 16 int8 -> 16 bf16 (32 bytes) scaled by d.
+// 16 int8 -> 16 bf16 (32 bytes) scaled by d: the sign-extending byte select of
+// v_cvt_f32_i32 (SDWA), the exact product q*d (8 x 11 significant bits), then
+// v_cvt_pk_bf16_f32 (round to nearest even).
 __device__ __forceinline__ void dequant16(v4i q, float d, v4i& lo, v4i& hi) {
-  const float c = -128.0f * d;
   uint32_t w[8];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    uint32_t u = (uint32_t)q[i] ^ 0x80808080u;
-    float f0 = fmaf((float)(u & 0xFFu), d, c);
-    float f1 = fmaf((float)((u >> 8) & 0xFFu), d, c);
-    float f2 = fmaf((float)((u >> 16) & 0xFFu), d, c);
-    float f3 = fmaf((float)(u >> 24), d, c);
+    const uint32_t u = (uint32_t)q[i];
+    const float f0 = (float)(int)(signed char)(u & 0xFFu) * d;
+    const float f1 = (float)(int)(signed char)((u >> 8) & 0xFFu) * d;
+    const float f2 = (float)(int)(signed char)((u >> 16) & 0xFFu) * d;
+    const float f3 = (float)(int)(signed char)(u >> 24) * d;
     w[2 * i] = pack_bf16x2(f0, f1);
     w[2 * i + 1] = pack_bf16x2(f2, f3);
   }
