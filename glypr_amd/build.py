@@ -3,7 +3,9 @@
     python -m glypr_amd.build          # compile every source, link the library
 
 Each .hip/.cpp source under csrc/ is compiled to an object in parallel and
-linked into glypr_amd/libglypr_hip.so, which travels with the source tree.
+linked into glypr_amd/libglypr_hip.so, which travels with the source tree;
+glypr_amd/capi_bench (capi_bench.cpp, the C3 projections through the C ABI
+alone) is linked against it.
 """
 from __future__ import annotations
 
@@ -19,6 +21,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libglypr_hip.so")
+BENCH_BIN = os.path.join(PKG, "capi_bench")
 ARCH = os.environ.get("GLYPR_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -75,6 +78,14 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    # the C-ABI benchmark driver (no Python): links the library just built
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", f"-I{INCLUDE}",
+           os.path.join(PKG, "capi_bench.cpp"), f"-L{PKG}", "-lglypr_hip",
+           "-Wl,-rpath,$ORIGIN", "-o", BENCH_BIN + ".tmp"]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"capi_bench build failed:\n{r.stdout}")
+    os.replace(BENCH_BIN + ".tmp", BENCH_BIN)
     return LIB
 
 

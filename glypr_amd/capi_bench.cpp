@@ -1,0 +1,198 @@
+// capi_bench.cpp — the C2/C3 layer-projection workload through the C ABI
+// alone (no Python, no torch): the program to put under rocprofv3 when the
+// counters of one projection kernel are wanted, and an example of driving
+// libglypr_hip.so from C++.
+//
+// One step is the C2/C3 layer's seven Q8_0 projections as the library fuses
+// them (qkv as one concatenated weight, gate|up as one):
+//   glypr_hip_rmsnorm_q8_0_matmul  x -> RMSNorm -> qkv   768 -> 1280
+//   glypr_hip_q8_0_matmul          attn -> o             768 -> 768
+//   glypr_hip_rmsnorm_mlp          x -> RMSNorm -> gate|up + GeGLU -> down
+// on synthetic Q8_0 weights (BASELINE's N(0, 0.02) quantized as
+// BlockQ8_0::from_float does: d = amax / 127 as f16) and N(0, 1) activations.
+//
+//   capi_bench [--m 16384] [--variant int8|bf16] [--steps 20] [--warmup 3]
+//              [--copy-probe MB]
+//
+// Prints one JSON line: ms per step and TOPS (2 * m * 7-projection MACs).
+// --copy-probe MB ends the run with one device-to-device copy of MB MiB: the
+// known-size launch that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <random>
+#include <vector>
+
+#include "glypr_hip.h"
+
+namespace {
+
+constexpr int64_t H = 768, NQ = 768, NKV = 256, F = 1152;
+
+void die(const char* what, int rc) {
+  fprintf(stderr, "%s failed (%d): %s\n", what, rc, glypr_hip_last_error());
+  exit(1);
+}
+#define CK(call)                      \
+  do {                                \
+    int rc_ = (call);                 \
+    if (rc_ != 0) die(#call, rc_);    \
+  } while (0)
+#define HK(call)                                                              \
+  do {                                                                        \
+    hipError_t e_ = (call);                                                   \
+    if (e_ != hipSuccess) {                                                   \
+      fprintf(stderr, "%s failed: %s\n", #call, hipGetErrorString(e_));       \
+      exit(1);                                                                \
+    }                                                                         \
+  } while (0)
+
+uint16_t f32_to_f16(float f) {
+  // round to nearest even; the scales here are normal f16 values
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  int32_t e = (int32_t)((u >> 23) & 0xFF) - 127 + 15;
+  uint32_t m = u & 0x7FFFFFu;
+  if (e <= 0) return (uint16_t)sign;   // never reached for these scales
+  uint32_t r = (uint32_t)(e << 10) | (m >> 13);
+  const uint32_t rem = m & 0x1FFFu;
+  if (rem > 0x1000u || (rem == 0x1000u && (r & 1u))) r++;
+  return (uint16_t)(sign | r);
+}
+
+// GGUF Q8_0 blocks [n][k/32][34 B] of N(0, sigma) values quantized as
+// BlockQ8_0::from_float: d = amax / 127 (stored as f16), q = round(x / d).
+std::vector<uint8_t> q8_0_weight(std::mt19937_64& rng, int64_t n, int64_t k, float sigma) {
+  std::normal_distribution<float> nd(0.0f, sigma);
+  std::vector<uint8_t> out((size_t)(n * (k / 32) * 34));
+  float x[32];
+  for (int64_t b = 0; b < n * (k / 32); b++) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+      x[i] = nd(rng);
+      amax = fmaxf(amax, fabsf(x[i]));
+    }
+    const float d = amax / 127.0f;
+    const uint16_t dh = f32_to_f16(d);
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t* blk = out.data() + b * 34;
+    memcpy(blk, &dh, 2);
+    for (int i = 0; i < 32; i++) {
+      const float q = roundf(x[i] * id);
+      blk[2 + i] = (uint8_t)(int8_t)(q > 127.0f ? 127.0f : (q < -128.0f ? -128.0f : q));
+    }
+  }
+  return out;
+}
+
+float* device_normal(std::mt19937_64& rng, int64_t n, float mean, float sigma) {
+  std::normal_distribution<float> nd(mean, sigma);
+  std::vector<float> h((size_t)n);
+  for (auto& v : h) v = nd(rng);
+  float* d = nullptr;
+  HK(hipMalloc(&d, (size_t)n * 4));
+  HK(hipMemcpy(d, h.data(), (size_t)n * 4, hipMemcpyHostToDevice));
+  return d;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  int64_t m = 16384;
+  int variant = GLYPR_Q8_BF16_DEQUANT, steps = 20, warmup = 3;
+  int64_t probe_mb = 0;
+  for (int i = 1; i < argc; i++) {
+    if (!strcmp(argv[i], "--m") && i + 1 < argc) m = atoll(argv[++i]);
+    else if (!strcmp(argv[i], "--variant") && i + 1 < argc) {
+      ++i;
+      variant = !strcmp(argv[i], "int8") ? GLYPR_Q8_INT8_EXACT : GLYPR_Q8_BF16_DEQUANT;
+    } else if (!strcmp(argv[i], "--steps") && i + 1 < argc) steps = atoi(argv[++i]);
+    else if (!strcmp(argv[i], "--warmup") && i + 1 < argc) warmup = atoi(argv[++i]);
+    else if (!strcmp(argv[i], "--copy-probe") && i + 1 < argc) probe_mb = atoll(argv[++i]);
+    else {
+      fprintf(stderr,
+              "usage: %s [--m M] [--variant int8|bf16] [--steps K] [--warmup W] "
+              "[--copy-probe MB]\n", argv[0]);
+      return 2;
+    }
+  }
+  if (m <= 0 || steps <= 0 || warmup < 0 || probe_mb < 0 || probe_mb > 4096) {
+    fprintf(stderr, "m, steps must be > 0, warmup >= 0, copy-probe in [0, 4096]\n");
+    return 2;
+  }
+  glypr_hip_ctx* ctx = nullptr;
+  CK(glypr_hip_ctx_create(0, &ctx));
+  CK(glypr_hip_ctx_reserve(ctx, m));
+  std::mt19937_64 rng(12345);
+  const struct { const char* name; int64_t n, k; } shapes[] = {
+      {"q", NQ, H}, {"k", NKV, H}, {"v", NKV, H}, {"o", H, NQ},
+      {"gate", F, H}, {"up", F, H}, {"down", H, F}};
+  glypr_q8w* w[7] = {};
+  for (int i = 0; i < 7; i++) {
+    const std::vector<uint8_t> b = q8_0_weight(rng, shapes[i].n, shapes[i].k, 0.02f);
+    CK(glypr_hip_q8_0_weight_create(ctx, b.data(), shapes[i].n, shapes[i].k, &w[i]));
+  }
+  glypr_q8w *qkv = nullptr, *gate_up = nullptr;
+  const glypr_q8w* p3[3] = {w[0], w[1], w[2]};
+  const glypr_q8w* p2[2] = {w[4], w[5]};
+  CK(glypr_hip_q8_0_weight_concat(ctx, p3, 3, &qkv, nullptr));
+  CK(glypr_hip_q8_0_weight_concat(ctx, p2, 2, &gate_up, nullptr));
+  float* x = device_normal(rng, m * H, 0.0f, 1.0f);
+  float* attn = device_normal(rng, m * NQ, 0.0f, 1.0f);
+  float* n1 = device_normal(rng, H, 1.0f, 0.1f);
+  float* n2 = device_normal(rng, H, 1.0f, 0.1f);
+  float *y_qkv = nullptr, *y_o = nullptr, *y_mlp = nullptr;
+  HK(hipMalloc(&y_qkv, (size_t)(m * (NQ + 2 * NKV)) * 4));
+  HK(hipMalloc(&y_o, (size_t)(m * H) * 4));
+  HK(hipMalloc(&y_mlp, (size_t)(m * H) * 4));
+  hipStream_t s;
+  HK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  auto step = [&]() {
+    CK(glypr_hip_rmsnorm_q8_0_matmul(ctx, qkv, x, n1, 1e-6f, y_qkv, m, variant, s));
+    CK(glypr_hip_q8_0_matmul(ctx, w[3], attn, y_o, m, variant, s));
+    CK(glypr_hip_rmsnorm_mlp(ctx, gate_up, w[6], x, n2, 1e-6f, y_mlp, m, variant, s));
+  };
+  for (int i = 0; i < warmup; i++) step();
+  HK(hipStreamSynchronize(s));
+  hipEvent_t e0, e1;
+  HK(hipEventCreate(&e0));
+  HK(hipEventCreate(&e1));
+  HK(hipEventRecord(e0, s));
+  for (int i = 0; i < steps; i++) step();
+  HK(hipEventRecord(e1, s));
+  HK(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HK(hipEventElapsedTime(&ms, e0, e1));
+  const double per = ms / steps;
+  const double macs = (double)m * (double)(H * (NQ + 2 * NKV) + NQ * H + H * 2 * F + F * H);
+  printf("{\"workload\": \"c3-layer-projections\", \"m\": %lld, \"variant\": \"%s\", "
+         "\"steps\": %d, \"ms_per_step\": %.4f, \"tops\": %.2f}\n",
+         (long long)m, variant == GLYPR_Q8_INT8_EXACT ? "int8" : "bf16", steps, per,
+         2.0 * macs / (per / 1e3) / 1e12);
+  fflush(stdout);
+  if (probe_mb > 0) {
+    const size_t bytes = (size_t)probe_mb << 20;
+    void *a = nullptr, *b = nullptr;
+    HK(hipMalloc(&a, bytes));
+    HK(hipMalloc(&b, bytes));
+    HK(hipMemsetAsync(a, 1, bytes, s));
+    HK(hipMemcpyAsync(b, a, bytes, hipMemcpyDeviceToDevice, s));
+    HK(hipStreamSynchronize(s));
+    HK(hipFree(a));
+    HK(hipFree(b));
+    printf("{\"copy_probe_bytes\": %zu}\n", bytes);
+  }
+  for (auto* p : w) CK(glypr_hip_q8_0_weight_destroy(p));
+  CK(glypr_hip_q8_0_weight_destroy(qkv));
+  CK(glypr_hip_q8_0_weight_destroy(gate_up));
+  for (float* p : {x, attn, n1, n2, y_qkv, y_o, y_mlp}) HK(hipFree(p));
+  HK(hipStreamDestroy(s));
+  CK(glypr_hip_ctx_destroy(ctx));
+  return 0;
+}
