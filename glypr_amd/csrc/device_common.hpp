@@ -179,6 +179,25 @@ __device__ __forceinline__ void dma4(const int8_t* base, int voff, uint32_t lds_
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
                :: "v"(voff), "s"(base), "s"(lds_base) : "memory", "m0");
 }
+// Tile (mi, ni) of this workgroup in a 1D grid of tm x tn tiles.  Workgroup
+// i runs on XCD i % 8 (eight XCDs, each with its own L2), so the tiles are
+// dealt out as one contiguous run per XCD: nmajor runs cover whole columns of
+// N tiles (an XCD reads its slice of B once and all of A: 8*A + B bytes from
+// memory), otherwise whole rows of M tiles (A + 8*B).  The caller picks the
+// order that re-reads the smaller operand.
+__device__ __forceinline__ void xcd_tile(int tm, int tn, bool nmajor, int& mi, int& ni) {
+  const int nblk = gridDim.x, id = blockIdx.x;
+  const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
+  const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
+  if (nmajor) {
+    ni = W / tm;
+    mi = W - ni * tm;
+  } else {
+    mi = W / tn;
+    ni = W - mi * tn;
+  }
+}
+
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
