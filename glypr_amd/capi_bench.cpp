@@ -13,8 +13,13 @@
 //
 //   capi_bench [--m 16384] [--variant int8|bf16] [--steps 20] [--warmup 3]
 //              [--copy-probe MB]
+//   capi_bench --model [--t 512] [--steps 20] [--warmup 3] [--copy-probe MB]
 //
 // Prints one JSON line: ms per step and TOPS (2 * m * 7-projection MACs).
+// --model instead runs config 4: glypr_hip_model_embed of one t-token
+// sequence through the 24-layer backbone (hidden 768, 3 q / 1 kv heads of
+// 256, FFN 1152, the 262144 x 768 Q8_0 token table, MRL-256), synthetic
+// weights as above and norm weights 1 + N(0, 0.1) (q/k norms x 0.25).
 // --copy-probe MB ends the run with one device-to-device copy of MB MiB: the
 // known-size launch that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE.
 #include <hip/hip_runtime.h>
@@ -91,6 +96,105 @@ std::vector<uint8_t> q8_0_weight(std::mt19937_64& rng, int64_t n, int64_t k, flo
   return out;
 }
 
+std::vector<float> host_normal(std::mt19937_64& rng, int64_t n, float mean, float sigma,
+                              float scale = 1.0f) {
+  std::normal_distribution<float> nd(mean, sigma);
+  std::vector<float> h((size_t)n);
+  for (auto& v : h) v = nd(rng) * scale;
+  return h;
+}
+
+// Config 4 through glypr_hip_model_*: ms per embedding.
+int run_model(int64_t t, int steps, int warmup) {
+  constexpr int64_t L = 24, V = 262144, HD = 256;
+  glypr_hip_ctx* ctx = nullptr;
+  CK(glypr_hip_ctx_create(0, &ctx));
+  glypr_model_config cfg{};
+  cfg.hidden = H;
+  cfg.ffn = F;
+  cfg.n_heads = 3;
+  cfg.n_kv_heads = 1;
+  cfg.head_dim = HD;
+  cfg.n_layers = L;
+  cfg.vocab = V;
+  cfg.sliding_window = 512;
+  cfg.eps = 1e-6f;
+  cfg.rope_theta_sliding = 10000.0;
+  cfg.rope_theta_full = 1e6;
+  glypr_model* m = nullptr;
+  CK(glypr_hip_model_create(ctx, &cfg, &m));
+  std::mt19937_64 rng(7);
+  auto set_q8 = [&](const char* name, int64_t n, int64_t k) {
+    const std::vector<uint8_t> b = q8_0_weight(rng, n, k, 0.02f);
+    CK(glypr_hip_model_set_tensor(m, name, b.data(), n, k, 1));
+  };
+  auto set_f32 = [&](const char* name, int64_t n, float scale) {
+    const std::vector<float> w = host_normal(rng, n, 1.0f, 0.1f, scale);
+    CK(glypr_hip_model_set_tensor(m, name, w.data(), 1, n, 0));
+  };
+  set_q8("token_embd.weight", V, H);
+  set_f32("output_norm.weight", H, 1.0f);
+  char name[96];
+  const struct { const char* n; int64_t rows, cols; } proj[] = {
+      {"attn_q", NQ, H}, {"attn_k", NKV, H}, {"attn_v", NKV, H}, {"attn_output", H, NQ},
+      {"ffn_gate", F, H}, {"ffn_up", F, H}, {"ffn_down", H, F}};
+  const struct { const char* n; int64_t dim; float scale; } norms[] = {
+      {"attn_norm", H, 1.0f}, {"post_attention_norm", H, 1.0f}, {"ffn_norm", H, 1.0f},
+      {"post_ffw_norm", H, 1.0f}, {"attn_q_norm", HD, 0.25f}, {"attn_k_norm", HD, 0.25f}};
+  for (int64_t i = 0; i < L; i++) {
+    for (const auto& p : proj) {
+      snprintf(name, sizeof name, "blk.%lld.%s.weight", (long long)i, p.n);
+      set_q8(name, p.rows, p.cols);
+    }
+    for (const auto& nw : norms) {
+      snprintf(name, sizeof name, "blk.%lld.%s.weight", (long long)i, nw.n);
+      set_f32(name, nw.dim, nw.scale);
+    }
+  }
+  CK(glypr_hip_model_finalize(m));
+  std::vector<uint32_t> ids((size_t)t);
+  std::uniform_int_distribution<uint32_t> ud(0, (uint32_t)V - 1);
+  for (auto& v : ids) v = ud(rng);
+  float* out = nullptr;
+  HK(hipMalloc(&out, 256 * 4));
+  hipStream_t s;
+  HK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  for (int i = 0; i < warmup; i++) CK(glypr_hip_model_embed(m, ids.data(), t, 256, out, nullptr, s));
+  HK(hipStreamSynchronize(s));
+  hipEvent_t e0, e1;
+  HK(hipEventCreate(&e0));
+  HK(hipEventCreate(&e1));
+  HK(hipEventRecord(e0, s));
+  for (int i = 0; i < steps; i++) CK(glypr_hip_model_embed(m, ids.data(), t, 256, out, nullptr, s));
+  HK(hipEventRecord(e1, s));
+  HK(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HK(hipEventElapsedTime(&ms, e0, e1));
+  printf("{\"workload\": \"c4-embed\", \"t\": %lld, \"layers\": %lld, \"steps\": %d, "
+         "\"ms_per_embedding\": %.4f, \"embeddings_per_s\": %.2f}\n",
+         (long long)t, (long long)L, steps, ms / steps, 1000.0 * steps / ms);
+  fflush(stdout);
+  HK(hipFree(out));
+  HK(hipStreamDestroy(s));
+  CK(glypr_hip_model_destroy(m));
+  CK(glypr_hip_ctx_destroy(ctx));
+  return 0;
+}
+
+void copy_probe(int64_t probe_mb) {
+  if (probe_mb <= 0) return;
+  const size_t bytes = (size_t)probe_mb << 20;
+  void *a = nullptr, *b = nullptr;
+  HK(hipMalloc(&a, bytes));
+  HK(hipMalloc(&b, bytes));
+  HK(hipMemset(a, 1, bytes));
+  HK(hipMemcpy(b, a, bytes, hipMemcpyDeviceToDevice));
+  HK(hipDeviceSynchronize());
+  HK(hipFree(a));
+  HK(hipFree(b));
+  printf("{\"copy_probe_bytes\": %zu}\n", bytes);
+}
+
 float* device_normal(std::mt19937_64& rng, int64_t n, float mean, float sigma) {
   std::normal_distribution<float> nd(mean, sigma);
   std::vector<float> h((size_t)n);
@@ -106,9 +210,12 @@ float* device_normal(std::mt19937_64& rng, int64_t n, float mean, float sigma) {
 int main(int argc, char** argv) {
   int64_t m = 16384;
   int variant = GLYPR_Q8_BF16_DEQUANT, steps = 20, warmup = 3;
-  int64_t probe_mb = 0;
+  int64_t probe_mb = 0, t = 512;
+  bool model = false;
   for (int i = 1; i < argc; i++) {
     if (!strcmp(argv[i], "--m") && i + 1 < argc) m = atoll(argv[++i]);
+    else if (!strcmp(argv[i], "--model")) model = true;
+    else if (!strcmp(argv[i], "--t") && i + 1 < argc) t = atoll(argv[++i]);
     else if (!strcmp(argv[i], "--variant") && i + 1 < argc) {
       ++i;
       variant = !strcmp(argv[i], "int8") ? GLYPR_Q8_INT8_EXACT : GLYPR_Q8_BF16_DEQUANT;
@@ -118,13 +225,21 @@ int main(int argc, char** argv) {
     else {
       fprintf(stderr,
               "usage: %s [--m M] [--variant int8|bf16] [--steps K] [--warmup W] "
-              "[--copy-probe MB]\n", argv[0]);
+              "[--copy-probe MB]\n       %s --model [--t T] [--steps K] [--warmup W] "
+              "[--copy-probe MB]\n", argv[0], argv[0]);
       return 2;
     }
   }
-  if (m <= 0 || steps <= 0 || warmup < 0 || probe_mb < 0 || probe_mb > 4096) {
-    fprintf(stderr, "m, steps must be > 0, warmup >= 0, copy-probe in [0, 4096]\n");
+  if (m <= 0 || t <= 0 || t > 8192 || steps <= 0 || warmup < 0 || probe_mb < 0 ||
+      probe_mb > 4096) {
+    fprintf(stderr, "m, steps must be > 0, t in [1, 8192], warmup >= 0, copy-probe in "
+                    "[0, 4096]\n");
     return 2;
+  }
+  if (model) {
+    const int rc = run_model(t, steps, warmup);
+    copy_probe(probe_mb);
+    return rc;
   }
   glypr_hip_ctx* ctx = nullptr;
   CK(glypr_hip_ctx_create(0, &ctx));
@@ -176,18 +291,7 @@ int main(int argc, char** argv) {
          (long long)m, variant == GLYPR_Q8_INT8_EXACT ? "int8" : "bf16", steps, per,
          2.0 * macs / (per / 1e3) / 1e12);
   fflush(stdout);
-  if (probe_mb > 0) {
-    const size_t bytes = (size_t)probe_mb << 20;
-    void *a = nullptr, *b = nullptr;
-    HK(hipMalloc(&a, bytes));
-    HK(hipMalloc(&b, bytes));
-    HK(hipMemsetAsync(a, 1, bytes, s));
-    HK(hipMemcpyAsync(b, a, bytes, hipMemcpyDeviceToDevice, s));
-    HK(hipStreamSynchronize(s));
-    HK(hipFree(a));
-    HK(hipFree(b));
-    printf("{\"copy_probe_bytes\": %zu}\n", bytes);
-  }
+  copy_probe(probe_mb);
   for (auto* p : w) CK(glypr_hip_q8_0_weight_destroy(p));
   CK(glypr_hip_q8_0_weight_destroy(qkv));
   CK(glypr_hip_q8_0_weight_destroy(gate_up));
