@@ -2,14 +2,17 @@
 // 52-197): 1-bit and symmetric int8 quantization of embeddings, and all-pairs
 // similarity between a query set and a database of encoded vectors.
 //
-//  - quantize_binary: bit i of word i/64 is (x[i] > 0).  Lane i holds element
-//    64 w + i, so the wave's ballot IS word w; a wave handles 8 words per
-//    iteration (8 loads in flight) in a grid-stride loop.
+//  - quantize_binary: bit i of word i/64 is (x[i] > 0).  With dim % 256 == 0
+//    a lane loads 4 consecutive elements (one 16-byte load, 1 KB per wave),
+//    forms their nibble, and 16 lanes' nibbles shift-or into one word;
+//    otherwise lane i holds element 64 w + i and the wave's ballot IS word w.
+//    Grid-stride loops, 4 (8) loads in flight per wave.
 //  - quantize_int8: (x * 127).round().clamp(-127, 127) as i8, NaN -> 0.
 //  - hamming / binary cosine: one thread per database row, the row's words in
 //    registers, the query words read wave-uniformly (scalar loads); every
 //    database byte is read once from HBM.  The binary cosine looks up
-//    cos(pi * h / dim) in a host-built table (h takes only dim + 1 values).
+//    cos(pi * h / dim) in a host-built table (h takes only dim + 1 values),
+//    staged in LDS per workgroup.
 //  - int8 dot / int8 cosine: the all-pairs product is an int8 GEMM with exact
 //    i32 sums, so it runs on v_mfma_i32_16x16x64_i8: a wave holds 16 database
 //    rows against up to 64 queries, streaming K in 64-byte steps (16 bytes per
@@ -24,11 +27,43 @@ namespace glypr {
 namespace {
 
 
-constexpr int BIN_WPW = 8;   // words per wave per iteration
+constexpr int BIN_CPW = 4;   // 256-element chunks per wave per iteration (4 words each)
 
+// Lane l loads elements 4 l .. 4 l + 3 of a 256-element chunk as one float4
+// (1 KB per wave load) and forms their 4-bit nibble; word j of the chunk is
+// the nibbles of lanes 16 j .. 16 j + 15 in lane order, gathered by three
+// shift-or steps down each 16-lane group into lane 16 j.
 __global__ void __launch_bounds__(256) quantize_binary_kernel(const float* __restrict__ x,
                                                               int64_t words,
                                                               unsigned long long* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t chunks = words >> 2;   // words % 4 == 0 (dim % 256 == 0)
+  const int64_t nwaves = (int64_t)gridDim.x * 4;
+  for (int64_t c0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * BIN_CPW; c0 < chunks;
+       c0 += nwaves * BIN_CPW) {
+    v4f v[BIN_CPW];
+#pragma unroll
+    for (int t = 0; t < BIN_CPW; t++)
+      v[t] = c0 + t < chunks ? *reinterpret_cast<const v4f*>(x + (c0 + t) * 256 + 4 * lane)
+                             : v4f{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < BIN_CPW; t++) {
+      const uint32_t n = (uint32_t)(v[t][0] > 0.0f) | ((uint32_t)(v[t][1] > 0.0f) << 1) |
+                         ((uint32_t)(v[t][2] > 0.0f) << 2) | ((uint32_t)(v[t][3] > 0.0f) << 3);
+      const uint32_t n2 = n | ((uint32_t)__shfl_down((int)n, 1, 16) << 4);      // 8 bits
+      const uint32_t n4 = n2 | ((uint32_t)__shfl_down((int)n2, 2, 16) << 8);    // 16 bits
+      const uint32_t n8 = n4 | ((uint32_t)__shfl_down((int)n4, 4, 16) << 16);   // 32 bits
+      const uint32_t hi = (uint32_t)__shfl_down((int)n8, 8, 16);               // next 32
+      if ((lane & 15) == 0 && c0 + t < chunks)
+        out[(c0 + t) * 4 + (lane >> 4)] = (unsigned long long)n8 | ((unsigned long long)hi << 32);
+    }
+  }
+}
+
+// Any dim % 64 == 0: lane i holds element 64 w + i, so the ballot IS word w.
+constexpr int BIN_WPW = 8;   // words per wave per iteration
+__global__ void __launch_bounds__(256) quantize_binary_word_kernel(
+    const float* __restrict__ x, int64_t words, unsigned long long* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t nwaves = (int64_t)gridDim.x * 4;
   for (int64_t w0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * BIN_WPW; w0 < words;
@@ -67,6 +102,8 @@ __global__ void __launch_bounds__(256) quantize_int8_kernel(const float* __restr
 }
 
 // out[i][j] = popcount(a_i ^ b_j) (u32) or table[that] (f32).  W words per row.
+// The cosine table (64 W + 1 floats) is staged in LDS: every output looks it
+// up at a lane-dependent index.
 template <int W, bool COS>
 __global__ void __launch_bounds__(256) hamming_kernel(const unsigned long long* __restrict__ a,
                                                       int64_t na,
@@ -74,6 +111,11 @@ __global__ void __launch_bounds__(256) hamming_kernel(const unsigned long long* 
                                                       int64_t nb, uint32_t* __restrict__ out_h,
                                                       const float* __restrict__ table,
                                                       float* __restrict__ out_c) {
+  __shared__ float tab[COS ? 64 * W + 1 : 1];
+  if constexpr (COS) {
+    for (int i = threadIdx.x; i <= 64 * W; i += 256) tab[i] = table[i];
+    __syncthreads();
+  }
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= nb) return;
   unsigned long long row[W];
@@ -83,7 +125,7 @@ __global__ void __launch_bounds__(256) hamming_kernel(const unsigned long long* 
     uint32_t h = 0;
 #pragma unroll
     for (int w = 0; w < W; w++) h += (uint32_t)__popcll(a[i * W + w] ^ row[w]);
-    if (COS) out_c[i * nb + j] = table[h];
+    if (COS) out_c[i * nb + j] = tab[h];
     else out_h[i * nb + j] = h;
   }
 }
@@ -256,9 +298,15 @@ hipError_t launch_quantize_binary(const float* x, int64_t n, int64_t dim, uint64
                                   hipStream_t s) {
   const int64_t words = n * (dim / 64);
   if (words == 0) return hipSuccess;
-  const int64_t blocks = (words + 4 * BIN_WPW - 1) / (4 * BIN_WPW);
-  quantize_binary_kernel<<<(unsigned)(blocks < 16384 ? blocks : 16384), 256, 0, s>>>(
-      x, words, reinterpret_cast<unsigned long long*>(out));
+  if (dim % 256 == 0) {
+    const int64_t blocks = (words / 4 + 4 * BIN_CPW - 1) / (4 * BIN_CPW);
+    quantize_binary_kernel<<<(unsigned)(blocks < 16384 ? blocks : 16384), 256, 0, s>>>(
+        x, words, reinterpret_cast<unsigned long long*>(out));
+  } else {
+    const int64_t blocks = (words + 4 * BIN_WPW - 1) / (4 * BIN_WPW);
+    quantize_binary_word_kernel<<<(unsigned)(blocks < 16384 ? blocks : 16384), 256, 0, s>>>(
+        x, words, reinterpret_cast<unsigned long long*>(out));
+  }
   return hipGetLastError();
 }
 

@@ -41,6 +41,13 @@ def test_quantize_binary_and_int8(ctx, oracle):
         x[0, :6] = [0.0, -0.0, np.nan, np.inf, -np.inf, 1e-45]
         got = host(ops.quantize_binary(ctx, dev(x))).view(np.uint64)
         assert np.array_equal(got, oracle.quantize_binary(x))
+    # more 256-element chunks than one pass of the capped grid (16384 blocks x
+    # 4 waves x 4 chunks = 262144): the grid-stride loop runs a second round
+    n = 262144 + 300
+    say(f"quantize_binary n={n} dim=256 (grid-stride)")
+    x = rng.standard_normal((n, 256)).astype(np.float32)
+    got = host(ops.quantize_binary(ctx, dev(x))).view(np.uint64)
+    assert np.array_equal(got, oracle.quantize_binary(x))
     with pytest.raises(Exception):
         ops.quantize_binary(ctx, dev(np.ones((1, 65), np.float32)))
     for count in (5, 1001, 768 * 33):
