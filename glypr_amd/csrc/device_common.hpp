@@ -113,6 +113,24 @@ __device__ __forceinline__ void quad_transpose4(float (&v)[4]) {
   v[2] = h2 ? a2 : q0;
   v[3] = h2 ? a3 : q1;
 }
+// v of lane i + N within each row of 16 lanes (DPP row_shl:N); lanes whose
+// source lies past the end of the row keep their own v.
+template <int N>
+__device__ __forceinline__ float dpp_row_shl(float v) {
+  static_assert(N >= 1 && N <= 15, "row shift");
+  return dpp_mov<0x100 + N>(v, v);
+}
+// The AVX2 horizontal sum of simd_rmsnorm_row_f32 over eight chain
+// accumulators held by lanes 8g + j (j = 0..7):
+//   ((l0 + l4) + (l2 + l6)) + ((l1 + l5) + (l3 + l7)),
+// valid in lane 8g.  Lane j < 4 first adds l(j+4), lanes 0 and 1 then add
+// lanes 2 and 3, lane 0 adds lane 1: the same three levels of f32 adds, in
+// VALU with DPP row shifts (no LDS round trips).
+__device__ __forceinline__ float hsum8_avx2(float acc) {
+  const float s = acc + dpp_row_shl<4>(acc);
+  const float t = s + dpp_row_shl<2>(s);
+  return t + dpp_row_shl<1>(t);
+}
 // max over each row of 16 lanes; every lane of the row gets it
 __device__ __forceinline__ float max16(float v) {
   v = max8(v);

@@ -126,9 +126,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
       acc = fmaf(e[2], e[2], acc);
       acc = fmaf(e[3], e[3], acc);
     }
-    const float s4 = acc + __shfl_down(acc, 4, 8);
-    const float s2 = s4 + __shfl_down(s4, 2, 8);
-    const float sum = s2 + __shfl_down(s2, 1, 8);
+    const float sum = hsum8_avx2(acc);
     const float inv = 1.0f / sqrtf(sum / (float)HD + eps);   // valid on lanes 8 i
     v4h yh[DPL];
 #pragma unroll
@@ -165,19 +163,19 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
+    // lanes 0..7 run the eight chains, every read issued before the chain
     float sum = 0.0f;
     if (lane < 8) {
+      float e[HD / 8];
+#pragma unroll
+      for (int c = 0; c < HD / 8; c++) e[c] = lrow[8 * c + lane];
+      __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the chain
       float acc = 0.0f;
 #pragma unroll
-      for (int c = 0; c < HD / 8; c++) {
-        float e = lrow[8 * c + lane];
-        acc = fmaf(e, e, acc);
-      }
-      float s = acc + __shfl_down(acc, 4, 8);
-      float u = s + __shfl_down(s, 2, 8);
-      sum = u + __shfl_down(u, 1, 8);
+      for (int c = 0; c < HD / 8; c++) acc = fmaf(e[c], e[c], acc);
+      sum = hsum8_avx2(acc);
     }
-    sum = __shfl(sum, 0);
+    sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), 0));
     const float inv = 1.0f / sqrtf(sum / (float)HD + eps);
     const float* w = kind == 0 ? qnw : knw;
 #pragma unroll

@@ -73,25 +73,55 @@ __device__ __forceinline__ void stage_chains(float* lrow, int S, int c4, const v
 #pragma unroll
   for (int k = 0; k < 4; k++) lrow[(j0 + k) * S + idx] = v[k];
 }
+// 1/rms of a chain-major staged row (dim % 32 == 0, dim <= 256 NV) in the
+// reference's order.  Lanes 0..7 run the chains with every ds_read_b128 of
+// the chain issued before its first FMA: chunks past dim / 32 are read
+// clamped and replaced by zeros.  The horizontal sum runs through DPP and
+// lane 0's total is broadcast with readlane.
+template <int NV>
 __device__ __forceinline__ float chain_row_inv(const float* lrow, int dim, int lane, float eps) {
+  // reads in batches of up to 12 chunks (48 registers): the row-per-wave
+  // kernels also stream large row counts, where occupancy hides latency
+  constexpr int NC = 8 * NV, BATCH = NC < 12 ? NC : 12;
   float sum = 0.0f;
   if (lane < 8) {
     const v4f* src = reinterpret_cast<const v4f*>(lrow + lane * chain_stride(dim));
     const int n = dim / 32;
     float acc = 0.0f;
-#pragma unroll 6
-    for (int t = 0; t < n; t++) {
-      const v4f e = src[t];
-      acc = fmaf(e[0], e[0], acc);
-      acc = fmaf(e[1], e[1], acc);
-      acc = fmaf(e[2], e[2], acc);
-      acc = fmaf(e[3], e[3], acc);
+#pragma unroll
+    for (int b0 = 0; b0 < NC; b0 += BATCH) {
+      constexpr int LAST = NC % BATCH == 0 ? BATCH : NC % BATCH;
+      const int nb = b0 + BATCH <= NC ? BATCH : LAST;   // chunks of this batch
+      v4f e[BATCH];
+#pragma unroll
+      for (int t = 0; t < BATCH; t++)
+        if (t < nb) e[t] = src[b0 + t < n ? b0 + t : n - 1];
+      __builtin_amdgcn_sched_barrier(0);   // keep the reads ahead of the chain
+      if (n == NC) {   // uniform: dim = 256 NV, every chunk is the row's
+#pragma unroll
+        for (int t = 0; t < BATCH; t++) {
+          if (t >= nb) break;
+          acc = fmaf(e[t][0], e[t][0], acc);
+          acc = fmaf(e[t][1], e[t][1], acc);
+          acc = fmaf(e[t][2], e[t][2], acc);
+          acc = fmaf(e[t][3], e[t][3], acc);
+        }
+      } else {
+        // chunks past n become zeros: fma(0, 0, acc) = acc exactly (acc >= +0)
+#pragma unroll
+        for (int t = 0; t < BATCH; t++) {
+          if (t >= nb) break;
+          const v4f z = b0 + t < n ? e[t] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+          acc = fmaf(z[0], z[0], acc);
+          acc = fmaf(z[1], z[1], acc);
+          acc = fmaf(z[2], z[2], acc);
+          acc = fmaf(z[3], z[3], acc);
+        }
+      }
     }
-    float s = acc + __shfl_down(acc, 4, 8);
-    float t = s + __shfl_down(s, 2, 8);
-    sum = t + __shfl_down(t, 1, 8);
+    sum = hsum8_avx2(acc);
   }
-  sum = __shfl(sum, 0);
+  sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sum), 0));
   return 1.0f / sqrtf(sum / (float)dim + eps);
 }
 
@@ -128,7 +158,7 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
-    inv = chain_row_inv(lrow, dim, lane, eps);
+    inv = chain_row_inv<NV>(lrow, dim, lane, eps);
   } else {
 #pragma unroll
     for (int i = 0; i < NV; i++) {
@@ -156,37 +186,52 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
     inv = 1.0f / sqrtf(sum / (float)dim + eps);
   }
 
+  v4f yv[NV];
 #pragma unroll
-  for (int i = 0; i < NV; i++) {
-    const int c4 = lane + 64 * i;
-    const bool ok = c4 < n4;
-    v4f yv;
+  for (int i = 0; i < NV; i++)
 #pragma unroll
-    for (int e = 0; e < 4; e++) yv[e] = w ? (v[i][e] * inv) * wv[i][e] : v[i][e] * inv;
-    if constexpr (MODE == OUT_F32) {
-      if (ok) *reinterpret_cast<v4f*>(y + row * dim + 4 * c4) = yv;
-    } else if constexpr (MODE == OUT_BF16) {
-      if (ok) {
+    for (int e = 0; e < 4; e++) yv[i][e] = w ? (v[i][e] * inv) * wv[i][e] : v[i][e] * inv;
+  if constexpr (MODE == OUT_F32) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int c4 = lane + 64 * i;
+      if (c4 < n4) *reinterpret_cast<v4f*>(y + row * dim + 4 * c4) = yv[i];
+    }
+  } else if constexpr (MODE == OUT_BF16) {
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int c4 = lane + 64 * i;
+      if (c4 < n4) {
         uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
-        dst[0] = bf16_rne(yv[0]) | (bf16_rne(yv[1]) << 16);
-        dst[1] = bf16_rne(yv[2]) | (bf16_rne(yv[3]) << 16);
+        dst[0] = bf16_rne(yv[i][0]) | (bf16_rne(yv[i][1]) << 16);
+        dst[1] = bf16_rne(yv[i][2]) | (bf16_rne(yv[i][3]) << 16);
       }
-    } else {
-      // 8 consecutive lanes hold one 32-block (dim % 32 == 0 keeps blocks whole).
+    }
+  } else {
+    // 8 consecutive lanes hold one 32-block (dim % 32 == 0 keeps blocks
+    // whole); every chunk's scale first, then the stores.
+    QScale sc[NV];
+    uint32_t packed[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
       float a = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(yv[e]));
-      a = fmaxf(a, __shfl_xor(a, 1, 8));
-      a = fmaxf(a, __shfl_xor(a, 2, 8));
-      a = fmaxf(a, __shfl_xor(a, 4, 8));
-      QScale sc = q8_scale(a);
-      uint32_t packed = 0;
+      for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(yv[i][e]));
+      sc[i] = q8_scale(max8(a));
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      packed[i] = 0;
 #pragma unroll
       for (int e = 0; e < 4; e++)
-        packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
-      if (ok) {
-        *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed;
-        if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc.dq;
+        packed[i] |= ((uint32_t)(quant_round(yv[i][e] * sc[i].id) & 0xFF)) << (8 * e);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+      const int c4 = lane + 64 * i;
+      if (c4 < n4) {
+        *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed[i];
+        if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc[i].dq;
       }
     }
   }
@@ -288,7 +333,7 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  const float inv = chain_row_inv(lrow, dim, lane, eps);
+  const float inv = chain_row_inv<NV>(lrow, dim, lane, eps);
   __builtin_amdgcn_wave_barrier();
   const float sv = scalar ? *scalar : 1.0f;
 #pragma unroll
@@ -307,39 +352,54 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   if constexpr (QNEXT) {
     float inv2 = 1.0f;
     if constexpr (CHAIN2) {
-      __builtin_amdgcn_s_waitcnt(0);
+      // the staging writes must land; the h stores need not
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_wave_barrier();
-      inv2 = chain_row_inv(lrow, dim, lane, eps);
+      inv2 = chain_row_inv<NV>(lrow, dim, lane, eps);
     }
+    // all NV chunks' scales first (independent chains the scheduler can
+    // interleave), then the stores
+    v4f yv[NV];
+    float am[NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-      const int c4 = lane + 64 * i;
-      const bool ok = c4 < n4;
-      v4f yv;
-      float a = 0.0f;
+      am[i] = 0.0f;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        if (NEXT == 2) yv[e] = v[i][e];
-        else yv[e] = w_next ? (v[i][e] * inv2) * wn[i][e] : v[i][e] * inv2;
-        a = fmaxf(a, fabsf(yv[e]));
+        if (NEXT == 2) yv[i][e] = v[i][e];
+        else yv[i][e] = w_next ? (v[i][e] * inv2) * wn[i][e] : v[i][e] * inv2;
+        am[i] = fmaxf(am[i], fabsf(yv[i][e]));
       }
-      if constexpr (NEXT == 3) {
-        if (ok) {
-          uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
-          dst[0] = bf16_rne(yv[0]) | (bf16_rne(yv[1]) << 16);
-          dst[1] = bf16_rne(yv[2]) | (bf16_rne(yv[3]) << 16);
-        }
-        continue;
-      }
-      a = max8(a);
-      QScale sc = q8_scale(a);
-      uint32_t packed = 0;
+    }
+    if constexpr (NEXT == 3) {
 #pragma unroll
-      for (int e = 0; e < 4; e++)
-        packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
-      if (ok) {
-        *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed;
-        if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc.dq;
+      for (int i = 0; i < NV; i++) {
+        const int c4 = lane + 64 * i;
+        if (c4 < n4) {
+          uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
+          dst[0] = bf16_rne(yv[i][0]) | (bf16_rne(yv[i][1]) << 16);
+          dst[1] = bf16_rne(yv[i][2]) | (bf16_rne(yv[i][3]) << 16);
+        }
+      }
+    } else {
+      QScale sc[NV];
+      uint32_t packed[NV];
+#pragma unroll
+      for (int i = 0; i < NV; i++) sc[i] = q8_scale(max8(am[i]));
+#pragma unroll
+      for (int i = 0; i < NV; i++) {
+        packed[i] = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          packed[i] |= ((uint32_t)(quant_round(yv[i][e] * sc[i].id) & 0xFF)) << (8 * e);
+      }
+#pragma unroll
+      for (int i = 0; i < NV; i++) {
+        const int c4 = lane + 64 * i;
+        if (c4 < n4) {
+          *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed[i];
+          if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc[i].dq;
+        }
       }
     }
   }

@@ -192,6 +192,36 @@ def ctypes_byref(oracle, cfg):
     return ctypes.byref(cfg)
 
 
+@pytest.mark.parametrize("n_layers,t", [(3, 130), (2, 512)])
+def test_model_attention_silenced_bit_exact(ctx, oracle, n_layers, t):
+    """With every o projection zero (Q8_0 blocks of d = 0), attention adds
+    exactly +0 to the residual stream on both sides (0 * inv * w = 0), so the
+    whole rest of the layer chain is exact integer/f32 work in the reference's
+    order: gather * embed_scale, the input RMSNorm's Q8_0, the qkv, gate/up +
+    GeGLU and down GEMMs, and both residual_norm launches per layer (post-norm,
+    residual add and the next norm's Q8_0).  The final normed token states must
+    equal the oracle's bit for bit (layer.rs:20-50, norm.rs:65-95)."""
+    say(f"attention-silenced backbone layers={n_layers} t={t}: bit-exact token states")
+    m0, tensors = make_model(ctx, oracle, n_layers, 2000, seed=40 + n_layers)
+    m0.close()
+    for i in range(n_layers):
+        data, r, c, q8 = tensors[f"blk.{i}.attn_output.weight"]
+        tensors[f"blk.{i}.attn_output.weight"] = (np.zeros_like(data), r, c, q8)
+    m = Model(ctx, n_layers=n_layers, vocab=2000)
+    for name, (data, r, c, q8) in tensors.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    ids = oracle.uniform_ids(t, seed=t + 1, vocab=2000)
+    hidden = torch.empty((t, 768), dtype=torch.float32, device="cuda")
+    m.embed(ids, trunc=256, hidden=hidden)
+    _, ref_hidden = oracle_forward(oracle, tensors, n_layers, 2000, ids, 256)
+    gh = host(hidden)
+    diff = int((gh.view(np.uint32) != ref_hidden.view(np.uint32)).sum())
+    say(f"  token-state values differing from the oracle: {diff} of {gh.size}")
+    assert diff == 0
+    m.close()
+
+
 @pytest.mark.parametrize("n_layers,t,vocab", [(2, 64, 2000), (6, 600, 2000), (24, 512, 262144)])
 def test_model_forward_vs_oracle(ctx, oracle, n_layers, t, vocab):
     """(24, 512, 262144) is BASELINE config 4 exactly: 24 layers, T = 512, the

@@ -158,8 +158,12 @@ def test_matmul_deterministic_and_c3_rows(ctx, oracle):
 
 
 def test_rmsnorm_bit_exact(ctx, oracle):
+    # dims 256 NV (every staged chunk used) and between (the chain's zero-padded
+    # tail), with one to six read batches of the chain
     for rows, dim, with_w in [(37, 768, True), (512, 768, True), (96, 256, True), (40, 256, False),
-                              (5, 1152, True), (3, 20, True), (6, 21, True), (4, 3000, False)]:
+                              (5, 1152, True), (33, 512, True), (17, 640, True), (9, 1024, True),
+                              (7, 2048, True), (11, 1792, False), (5, 1312, True),
+                              (3, 20, True), (6, 21, True), (4, 3000, False)]:
         say(f"rmsnorm rows={rows} dim={dim} weight={with_w}")
         x = oracle.normal(rows * dim, seed=rows + dim).reshape(rows, dim) * np.float32(2.5)
         w = (1 + 0.1 * oracle.normal(dim, seed=9)) if with_w else None
