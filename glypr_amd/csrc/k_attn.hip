@@ -574,14 +574,27 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
 #pragma unroll
   for (int e = 0; e < DPL; e++) acc[e] = 0.0f;
   const float* src = part_o + q * width + h * HD + DPL * lane;
-  for (int p = 0; p < kparts; p++) {
-    const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), p));
-    L += wgt * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lp), p));
+  // partitions in batches of 8: the batch's loads are all in flight before
+  // the first is used (one memory latency per batch, not per partition);
+  // the sums still run in partition order
+  constexpr int PB = 8;
+  for (int p0 = 0; p0 < kparts; p0 += PB) {
+    v4f v[PB][DPL / 4];
 #pragma unroll
-    for (int c = 0; c < DPL / 4; c++) {
-      const v4f v = *reinterpret_cast<const v4f*>(src + (int64_t)p * Tp * width + 4 * c);
+    for (int j = 0; j < PB; j++)
+      if (p0 + j < kparts)
 #pragma unroll
-      for (int e = 0; e < 4; e++) acc[4 * c + e] += wgt * v[e];
+        for (int c = 0; c < DPL / 4; c++)
+          v[j][c] = *reinterpret_cast<const v4f*>(src + (int64_t)(p0 + j) * Tp * width + 4 * c);
+#pragma unroll
+    for (int j = 0; j < PB; j++) {
+      if (p0 + j >= kparts) break;
+      const float wgt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), p0 + j));
+      L += wgt * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lp), p0 + j));
+#pragma unroll
+      for (int c = 0; c < DPL / 4; c++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc[4 * c + e] += wgt * v[j][c][e];
     }
   }
   const float inv = 1.0f / L;
