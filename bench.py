@@ -433,25 +433,30 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1):
     m.finalize()
     ids = np.random.default_rng(seed).integers(0, vocab, size=t).astype(np.uint32)
     out = torch.empty(256, dtype=torch.float32, device="cuda")
-    for _ in range(warmup):
-        m.embed(ids, trunc=256, out=out)
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(steps):
-        m.embed(ids, trunc=256, out=out)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
-    _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 1))
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(steps):
-        m.embed(ids, trunc=256, out=out)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_prof = e0.elapsed_time(e1) / steps
+    # The embeddings run on a stream of their own (default priority, not the
+    # legacy null stream, whose launches carry implicit cross-stream
+    # synchronisation in the runtime), as a serving caller would; the C ABI
+    # takes the stream per call.
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            m.embed(ids, trunc=256, out=out)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            m.embed(ids, trunc=256, out=out)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        _lib.check(_lib.lib().glypr_hip_profile_enable(ctx.handle, 1))
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            m.embed(ids, trunc=256, out=out)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_prof = e0.elapsed_time(e1) / steps
     tot = (ctypes.c_double * _lib.KERNEL_COUNT)()
     cnt = (ctypes.c_int64 * _lib.KERNEL_COUNT)()
     _lib.check(_lib.lib().glypr_hip_profile_read(ctx.handle, tot, cnt))
@@ -479,7 +484,7 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1):
 
 # Projections of one backbone layer as the model driver launches them (all
 # INT8_EXACT, Q8_0 operands from the fused prologues): (kernel, N, K).
-MODEL_GEMMS = [("gemm_i8", NQ + 2 * NKV, H), ("gemm_i8", H, NQ), ("gemm_i8_geglu", 2 * F, H),
+MODEL_GEMMS = [("gemm_i8_qkv", NQ + 2 * NKV, H), ("gemm_i8", H, NQ), ("gemm_i8_geglu", 2 * F, H),
                ("gemm_i8", H, F)]
 
 
@@ -490,7 +495,7 @@ def model_kernel_work(kernel, t, n_layers=24, window=512, nq=3, hd=256):
     work, 4 T^2 hd flop per q head for full layers (QK^T and PV), the band
     |i - j| <= window for sliding ones."""
     nb = lambda k: k // 32
-    if kernel in ("gemm_i8", "gemm_i8_geglu"):
+    if kernel in ("gemm_i8", "gemm_i8_geglu", "gemm_i8_qkv"):
         b = 0
         for name, n, k in MODEL_GEMMS:
             if name != kernel:
@@ -498,6 +503,8 @@ def model_kernel_work(kernel, t, n_layers=24, window=512, nq=3, hd=256):
             w = n * k + 4 * n * nb(k)
             if name == "gemm_i8_geglu":
                 b += t * k + 4 * t * nb(k) + w + t * F + 4 * t * nb(F)
+            elif name == "gemm_i8_qkv":   # f16 q/k/vt out, the RoPE tables and norm weights in
+                b += t * k + 4 * t * nb(k) + w + 2 * t * n + 8 * t * hd + 8 * hd
             else:
                 b += t * k + 4 * t * nb(k) + w + 4 * t * n
         return "hbm", b * n_layers, "B"

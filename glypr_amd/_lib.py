@@ -96,7 +96,7 @@ SIGNATURES = {
     "glypr_hip_kernel_name": (ctypes.c_char_p, [_int]),
 }
 
-KERNEL_COUNT = 20
+KERNEL_COUNT = 21
 
 
 class GlyprError(RuntimeError):

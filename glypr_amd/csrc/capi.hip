@@ -628,6 +628,13 @@ int glypr_hip_q8_0_embed_gather(glypr_hip_ctx* ctx, const glypr_q8w* table, cons
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
   std::lock_guard<std::mutex> lk(ctx->mu);
+  if (gather_host_ids_ok(table->k, n_ids)) {   // the ids travel in the kernel arguments
+    LAUNCH(GLYPR_K_GATHER, (hipStream_t)stream,
+           launch_gather_host_ids(table->qs(), table->dw(), table->k, ids, n_ids, scale, out,
+                                  (hipStream_t)stream),
+           "gather launch");
+    return GLYPR_OK;
+  }
   RET_IF(ensure_staging(ctx->ids, ctx->ids_cap, (size_t)n_ids));
   GLYPR_TRY_HIP(hipMemcpyAsync(ctx->ids, ids, (size_t)n_ids * 4, hipMemcpyHostToDevice,
                                (hipStream_t)stream),
@@ -805,7 +812,7 @@ static const char* const kKernelNames[GLYPR_K_COUNT] = {
     "quantize",   "rmsnorm_quant",  "gemm_i8", "gemm_i8_geglu", "to_bf16", "rmsnorm_bf16",
     "gemm_bf16",  "gemm_bf16_geglu", "rmsnorm", "geglu",         "gather",  "dequant",
     "pool",       "qkv_post",       "attention", "residual_norm", "vec_encode", "vec_search",
-    "gemm_i8_pro", "gemm_bf16w"};
+    "gemm_i8_pro", "gemm_bf16w",   "gemm_i8_qkv"};
 
 const char* glypr_hip_kernel_name(int id) {
   return (id >= 0 && id < GLYPR_K_COUNT) ? kKernelNames[id] : "";

@@ -234,6 +234,23 @@ __device__ __forceinline__ void vm_wait_units(int later) {
   }
 }
 
+// Row t's RoPE position and whether it holds a token: with a segment table
+// (several sequences at 64-aligned row offsets, seg[t] = {start, length} of
+// row t's sequence) the position restarts at each sequence and the rows past
+// a sequence's length are padding; without one, row t is position t of one
+// sequence of T tokens.
+__device__ __forceinline__ int seg_row_pos(const int2* __restrict__ seg, int t, int T,
+                                           bool* valid) {
+  if (!seg) {
+    *valid = t < T;
+    return t;
+  }
+  const int2 sg = seg[t];
+  const int p = t - sg.x;
+  *valid = p < sg.y;
+  return p;
+}
+
 // ---------------------------------------------------------------------------
 // tanh for GeGLU.  glypr's geglu_scalar_f32 calls the platform libm tanh, so
 // its bits differ between glibc and Apple libm.  The backend defines tanh as

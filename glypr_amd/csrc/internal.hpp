@@ -92,6 +92,14 @@ hipError_t launch_dequant(const int8_t* qs, const float* dw, int64_t rows, int64
                           hipStream_t s);
 hipError_t launch_gather(const int8_t* qs, const float* dw, int64_t k, const uint32_t* ids,
                          int64_t n_ids, float scale, float* out, hipStream_t s);
+// The same gather with the ids read from host memory at launch (they travel in
+// the kernel arguments, so the ids need no device copy): rows of width k with
+// k % 32 == 0 and k <= 1024, at most GATHER_ARG_IDS ids.
+constexpr int GATHER_ARG_IDS = 768;
+bool gather_host_ids_ok(int64_t k, int64_t n_ids);
+hipError_t launch_gather_host_ids(const int8_t* qs, const float* dw, int64_t k,
+                                  const uint32_t* host_ids, int64_t n_ids, float scale, float* out,
+                                  hipStream_t s);
 hipError_t launch_quantize_planar(const float* x, int64_t m, int64_t k, int8_t* xq, float* dx,
                                   hipStream_t s);
 hipError_t launch_quantize_gguf(const float* x, int64_t m, int64_t k, uint8_t* out,
@@ -178,6 +186,17 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
 hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t* wq,
                                 const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
                                 int64_t K, hipStream_t s);
+
+// The q|k|v projection (INT8_EXACT, Q8_0 activations) with qkv_post's work
+// as its epilogue: writes the attention operands q / k / vt (f16, rows padded
+// to Tp, invalid rows zero) straight from the GEMM.  head_dim 256, Tp <= 2048,
+// K in {512, 768, 1024, 1152}.
+bool gemm_i8_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd);
+hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* wq,
+                              const float* dw, int64_t T, int64_t Tp, int64_t K, int64_t nq,
+                              int64_t nkv, int64_t hd, const float* qnw, const float* knw,
+                              float eps, const float* cos_t, const float* sin_t, uint16_t* q16,
+                              uint16_t* k16, uint16_t* vt16, const int32_t* seg, hipStream_t s);
 
 // The int8 GEMM with the activation prologue fused: x is f32 [M][K],
 // quantized to Q8_0 inside the GEMM (norm: of RMSNorm(x; nw, eps), nw

@@ -55,22 +55,6 @@ struct QkvGeom {
   static constexpr int LDS = V_LDS > HD ? V_LDS : HD;        // per-wave staging
 };
 
-// Row t's RoPE position and whether it holds a token: with a segment table
-// (several sequences at 64-aligned row offsets, seg[t] = {start, length} of
-// row t's sequence) the position restarts at each sequence and the rows past
-// a sequence's length are padding; without one, row t is position t of one
-// sequence of T tokens.
-__device__ __forceinline__ int row_pos(const int2* __restrict__ seg, int t, int T, bool* valid) {
-  if (!seg) {
-    *valid = t < T;
-    return t;
-  }
-  const int2 sg = seg[t];
-  const int p = t - sg.x;
-  *valid = p < sg.y;
-  return p;
-}
-
 template <int HD>
 __global__ void __launch_bounds__(256) qkv_post_kernel(
     const float* __restrict__ qkv, int T, int Tp, int nq, int nkv, const float* __restrict__ qnw,
@@ -98,7 +82,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
     for (int i = 0; i < QKV_V_TOK; i++) {
       const int t = t0 + i;
       bool valid;
-      (void)row_pos(seg, t, T, &valid);
+      (void)seg_row_pos(seg, t, T, &valid);
 #pragma unroll
       for (int c = 0; c < NV4; c++) {
         x[i][c] = valid ? *reinterpret_cast<const v4f*>(
@@ -151,7 +135,7 @@ __global__ void __launch_bounds__(256) qkv_post_kernel(
 #pragma unroll
   for (int e = 0; e < DPL; e++) y[e] = 0.0f;
   bool valid;
-  const int pos = row_pos(seg, t, T, &valid);
+  const int pos = seg_row_pos(seg, t, T, &valid);
   if (valid) {
     const float* src = qkv + (int64_t)t * (nq + 2 * nkv) * HD + (int64_t)slot * HD;
     v4f x[NV4];

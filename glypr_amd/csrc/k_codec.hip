@@ -1,6 +1,8 @@
 // k_codec.hip — Q8_0 codec kernels: load-time repack, dequantize, token-row
 // gather, activation quantization.  All are HBM-bound byte/integer work:
 // 16-byte vector loads/stores, no LDS.
+#include <cstring>
+
 #include "device_common.hpp"
 #include "internal.hpp"
 
@@ -113,10 +115,18 @@ hipError_t launch_dequant(const int8_t* qs, const float* dw, int64_t rows, int64
 // ---------------------------------------------------------------------------
 constexpr int GATHER_ROWS = 8;
 
+// Ids carried by value in the kernel arguments (up to GATHER_ARG_IDS of
+// them, 3 KB): the launch needs no device copy of the ids, so the caller's
+// host array is read when the launch is enqueued and nothing waits on it.
+struct GatherIds {
+  uint32_t v[GATHER_ARG_IDS];
+  __device__ uint32_t operator[](int64_t i) const { return v[i]; }
+};
+
+template <class Ids>
 __global__ void __launch_bounds__(256) gather_rows_kernel(const int8_t* __restrict__ qs,
                                                           const float* __restrict__ dw, int k,
-                                                          const uint32_t* __restrict__ ids,
-                                                          int64_t rows, float scale,
+                                                          Ids ids, int64_t rows, float scale,
                                                           float* __restrict__ out) {
   const int lanes_per_row = k >> 2;
   const int c = threadIdx.x;   // 4-value column group
@@ -148,19 +158,38 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const int8_t* __restri
   }
 }
 
+static bool gather_rows_ok(int64_t k) { return k % 32 == 0 && k / 4 <= 256; }
+
 hipError_t launch_gather(const int8_t* qs, const float* dw, int64_t k, const uint32_t* ids,
                          int64_t n_ids, float scale, float* out, hipStream_t s) {
   if (n_ids == 0) return hipSuccess;
-  if (k % 32 == 0 && k / 4 <= 256) {
+  if (gather_rows_ok(k)) {
     const int threads = (int)((k / 4 + 63) / 64 * 64);
     const int64_t blocks = (n_ids + GATHER_ROWS - 1) / GATHER_ROWS;
-    gather_rows_kernel<<<(unsigned)blocks, threads, 0, s>>>(qs, dw, (int)k, ids, n_ids, scale,
-                                                            out);
+    gather_rows_kernel<const uint32_t*><<<(unsigned)blocks, threads, 0, s>>>(
+        qs, dw, (int)k, ids, n_ids, scale, out);
     return hipGetLastError();
   }
   const int64_t work = n_ids * (k / 16);
   dequant_rows_kernel<true><<<grid_for(work, 256, 65536), 256, 0, s>>>(qs, dw, k, ids, n_ids,
                                                                        scale, out);
+  return hipGetLastError();
+}
+
+bool gather_host_ids_ok(int64_t k, int64_t n_ids) {
+  return gather_rows_ok(k) && n_ids > 0 && n_ids <= GATHER_ARG_IDS;
+}
+
+hipError_t launch_gather_host_ids(const int8_t* qs, const float* dw, int64_t k,
+                                  const uint32_t* host_ids, int64_t n_ids, float scale, float* out,
+                                  hipStream_t s) {
+  if (!gather_host_ids_ok(k, n_ids)) return hipErrorInvalidValue;
+  GatherIds ids;
+  memcpy(ids.v, host_ids, (size_t)n_ids * 4);
+  const int threads = (int)((k / 4 + 63) / 64 * 64);
+  const int64_t blocks = (n_ids + GATHER_ROWS - 1) / GATHER_ROWS;
+  gather_rows_kernel<GatherIds><<<(unsigned)blocks, threads, 0, s>>>(qs, dw, (int)k, ids, n_ids,
+                                                                     scale, out);
   return hipGetLastError();
 }
 

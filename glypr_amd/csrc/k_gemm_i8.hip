@@ -1072,6 +1072,269 @@ hipError_t run(const int8_t* xq,const float* dx, const int8_t* wq, const float* 
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// The fused q|k|v projection with the attention prologue as its epilogue
+// (SelfAttention::forward up to the attention itself, attention/mod.rs:
+// 192-214 with the per-head RMSNorm and rope.rs:99-106): the small-M GEMM
+// above, one workgroup per (16 tokens, head slot of 256 columns), 8 waves of
+// 16 x 32 outputs, then the head's f32 tile is staged in LDS and turned into
+// the attention operands exactly as qkv_post_kernel (k_attn.hip) does it:
+//   q / k slots: RMSNorm over the head (eight FMA chains in the reference's
+//     order), times q_norm / k_norm, RoPE x*cos + rot*sin with both products
+//     rounded, f16 -> q [nq][Tp][256] / k [nkv][Tp][256];
+//   v slots: weightless RMSNorm, f16 -> vt [nkv][256][Tp] (transposed);
+//   rows that hold no token (past T, or past their sequence in a segment
+//   table) are written as zeros.
+// The f32 q|k|v rows never reach HBM and qkv_post's launch goes away.  Grid:
+// x = head slot (q heads, k heads, v heads), y = 16-row block of the Tp
+// padded rows.  Stage DMA: 2 A units and 32 B units per 128-byte K stage;
+// wave w issues B units 4 w .. 4 w + 3 and waves 0 and 1 one A unit each.
+// ---------------------------------------------------------------------------
+constexpr int QKV_HD = 256;
+constexpr int QKV_NW = 8;
+constexpr int QKV_RING = 3;
+constexpr int QKV_SP = QKV_HD + 4;   // staged row stride (floats)
+
+template <int NB>
+__global__ void __launch_bounds__(QKV_NW * 64)
+gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
+                   const int8_t* __restrict__ B, const float* __restrict__ dB, int T, int Tp,
+                   int nq, int nkv, const float* __restrict__ qnw, const float* __restrict__ knw,
+                   float eps, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                   _Float16* __restrict__ q16, _Float16* __restrict__ k16,
+                   _Float16* __restrict__ vt16, const int2* __restrict__ seg) {
+  constexpr int K = NB * QK, NST = NB / KB;
+  constexpr int BM = 16, BN = QKV_HD, TNW = 2;
+  constexpr int UA = BM / 8, UB = BN / 8;   // 2 and 32 units of 1 KB per stage
+  constexpr int UBW = UB / QKV_NW;          // B units per wave
+  constexpr int SA = NB * BM, SB = NB * BN;
+  constexpr int SLOT = (BM + BN) * BK;
+  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 2048");
+  static_assert(UB % QKV_NW == 0 && UA <= QKV_NW && BM * QKV_SP * 4 <= SLOT, "layout");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[QKV_RING * SLOT];
+  __shared__ __attribute__((aligned(16))) float sc[SA + SB + 256];
+  __shared__ float sinv[BM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave;
+  const int slot = blockIdx.x;            // head slot
+  const int m0 = blockIdx.y * BM;         // first row (token) of the block
+  const int n0 = slot * BN;
+  const int M = T;                        // rows with activations
+
+  // ---- scales: dA rows [BM][NB], then dB rows [BN][NB]
+  constexpr int NQ = NB / 4;
+  constexpr int SCH = (SA + SB) / 4;
+  for (int c0 = wave * 64; c0 < SCH; c0 += QKV_NW * 64) {
+    const int c = c0 + lane < SCH ? c0 + lane : SCH - 1;
+    const float* src;
+    if (c < SA / 4) {
+      const int r = c / NQ, q = c - r * NQ;
+      const int gm = m0 + r < M ? m0 + r : M - 1;
+      src = dA + (int64_t)gm * NB + 4 * q;
+    } else {
+      const int f = c - SA / 4, r = f / NQ, q = f - r * NQ;
+      src = dB + (int64_t)(n0 + r) * NB + 4 * q;
+    }
+    dma16_flat(src, lds_u32(sc + 4 * c0));
+  }
+  // ---- this wave's stage units: B units UA + UBW w .. (+ A unit w for w < UA)
+  const int rsub = lane >> 3, pch = lane & 7;
+  int boff[UBW];
+#pragma unroll
+  for (int j = 0; j < UBW; j++) {
+    const int row = (UBW * wave + j) * 8 + rsub;
+    boff[j] = (n0 + row) * K + ((pch ^ (row & 7)) << 4);
+  }
+  const bool has_a = wave < UA;
+  int aoff;
+  {
+    const int row = (has_a ? wave : 0) * 8 + rsub;
+    const int gm = m0 + row < M ? m0 + row : M - 1;
+    aoff = gm * K + ((pch ^ (row & 7)) << 4);
+  }
+  auto issue = [&](int st, int sl) {
+    uint8_t* base = ring + sl * SLOT;
+    if (has_a) dma16(A + st * BK, aoff, lds_u32(base + wave * 1024));
+#pragma unroll
+    for (int j = 0; j < UBW; j++)
+      dma16(B + st * BK, boff[j], lds_u32(base + (UA + UBW * wave + j) * 1024));
+  };
+#pragma unroll
+  for (int st = 0; st < QKV_RING - 1; st++)
+    if (st < NST) issue(st, st);
+
+  const int l16 = lane & 15, lq = lane >> 4;
+  int offA[KB], offB[TNW][KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    const int ch = 2 * kb + (lq >> 1);
+    offA[kb] = l16 * BK + ((ch ^ (l16 & 7)) << 4) + ((lq & 1) << 3);
+#pragma unroll
+    for (int t = 0; t < TNW; t++) {
+      const int brow = wn * 16 * TNW + t * 16 + l16;
+      offB[t][kb] = (BM + brow) * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+    }
+  }
+  const float* xrow = sc + (4 * lq) * NB;
+  const float* wrow = sc + SA + (wn * 16 * TNW + l16) * NB;
+  const v4i magic = {MAGIC, MAGIC, MAGIC, MAGIC};
+  float acc[TNW][4];
+#pragma unroll
+  for (int t = 0; t < TNW; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
+
+#pragma unroll 1
+  for (int g = 0; g < NST; g += QKV_RING) {
+#pragma unroll
+    for (int r = 0; r < QKV_RING; r++) {
+      const int st = g + r;
+      if (st < NST) {
+        const int later = (st + QKV_RING - 2 < NST - 1 ? st + QKV_RING - 2 : NST - 1) - st;
+        if (has_a)
+          vm_wait_units<UBW + 1, QKV_RING - 2>(later);
+        else
+          vm_wait_units<UBW, QKV_RING - 2>(later);
+        __syncthreads();
+        if (st + QKV_RING - 1 < NST) issue(st + QKV_RING - 1, (r + QKV_RING - 1) % QKV_RING);
+        const uint8_t* sl = ring + r * SLOT;
+        v4i d[KB][TNW];
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+          const v1l af = *reinterpret_cast<const v1l*>(sl + offA[kb]);
+#pragma unroll
+          for (int t = 0; t < TNW; t++) {
+            const v1l bf = *reinterpret_cast<const v1l*>(sl + offB[t][kb]);
+            d[kb][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, magic, 0, 0, 0);
+          }
+        }
+        v4f xq[4], wq[TNW];
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++)
+          xq[rr] = *reinterpret_cast<const v4f*>(xrow + rr * NB + st * KB);
+#pragma unroll
+        for (int t = 0; t < TNW; t++)
+          wq[t] = *reinterpret_cast<const v4f*>(wrow + t * 16 * NB + st * KB);
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+          for (int t = 0; t < TNW; t++) {
+            const float wd = wq[t][kb];
+            const float wc = wd * NEG_MAGIC;
+#pragma unroll
+            for (int rr = 0; rr < 4; rr++) {
+              float tt = fmaf(__int_as_float(d[kb][t][rr]), wd, wc);  // round(S * d_w)
+              float u = tt * xq[rr][kb];                              // round(. * d_x)
+              acc[t][rr] = acc[t][rr] + u;                            // round(acc + .)
+            }
+          }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();   // every wave is past its last ring read
+
+  // ---- the head's f32 tile [16 rows][256] into LDS (ring slot 0)
+  float* stg = reinterpret_cast<float*>(ring);
+#pragma unroll
+  for (int t = 0; t < TNW; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      stg[(4 * lq + r) * QKV_SP + wn * 16 * TNW + t * 16 + l16] = acc[t][r];
+  __syncthreads();
+
+  // Reference-order 1/rms of staged row i, on lanes 8 c + j (chain j of the
+  // row held by lane group c): every read ahead of the chain, DPP sum.
+  auto row_inv = [&](int i) -> float {
+    float e[QKV_HD / 8];
+#pragma unroll
+    for (int c = 0; c < QKV_HD / 8; c++) e[c] = stg[i * QKV_SP + 8 * c + (lane & 7)];
+    __builtin_amdgcn_sched_barrier(0);
+    float a = 0.0f;
+#pragma unroll
+    for (int c = 0; c < QKV_HD / 8; c++) a = fmaf(e[c], e[c], a);
+    const float sum = hsum8_avx2(a);
+    return 1.0f / sqrtf(sum / (float)QKV_HD + eps);   // valid on lanes 8 c
+  };
+
+  if (slot < nq + nkv) {
+    // q / k: wave w handles rows 2 w and 2 w + 1; lane l holds dims 4 l .. 4 l + 3
+    const bool is_q = slot < nq;
+    const int head = is_q ? slot : slot - nq;
+    const float* w = is_q ? qnw : knw;
+    _Float16* outp = is_q ? q16 : k16;
+    // lanes 0..7 run row 2 w's chains, lanes 8..15 row 2 w + 1's
+    const float invp = row_inv(2 * wave + ((lane >> 3) & 1));
+    const float inv0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(invp), 0));
+    const float inv1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(invp), 8));
+    const v4f wv = w ? *reinterpret_cast<const v4f*>(w + 4 * lane) : v4f{1, 1, 1, 1};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int i = 2 * wave + k;
+      const int t = m0 + i;
+      bool valid;
+      const int pos = seg_row_pos(seg, t, T, &valid);
+      const float inv = k == 0 ? inv0 : inv1;
+      const v4f x = *reinterpret_cast<const v4f*>(stg + i * QKV_SP + 4 * lane);
+      float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (valid) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = w ? (x[e] * inv) * wv[e] : x[e] * inv;
+        const v4f cv = *reinterpret_cast<const v4f*>(cos_t + (int64_t)pos * QKV_HD + 4 * lane);
+        const v4f sv = *reinterpret_cast<const v4f*>(sin_t + (int64_t)pos * QKV_HD + 4 * lane);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          // lanes l and l ^ 32 hold dims d and d +- 128 (rotate_half's pairs)
+          const float ye = y[e];
+          const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(ye), __float_as_uint(ye),
+                                                          false, false);
+          const float rt = lane < 32 ? -__uint_as_float(p[1]) : __uint_as_float(p[0]);
+          const float a = ye * cv[e];
+          const float b = rt * sv[e];
+          y[e] = a + b;
+        }
+      }
+      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+      const h4 yh = {(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+      *reinterpret_cast<h4*>(outp + ((int64_t)head * Tp + t) * QKV_HD + 4 * lane) = yh;
+    }
+  } else {
+    // v: the 16 rows' 1/rms first, then thread (dim d, token half) writes 8
+    // consecutive tokens of vt row d as one 16-byte store
+    const int head = slot - nq - nkv;
+    const float invp = row_inv(2 * wave + ((lane >> 3) & 1));
+    if (lane == 0) sinv[2 * wave] = invp;
+    if (lane == 8) sinv[2 * wave + 1] = invp;
+    __syncthreads();
+    const int d = tid >> 1, th = tid & 1;
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 yh;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int i = 8 * th + j;
+      bool valid;
+      (void)seg_row_pos(seg, m0 + i, T, &valid);
+      yh[j] = valid ? (_Float16)(stg[i * QKV_SP + d] * sinv[i]) : (_Float16)0.0f;
+    }
+    *reinterpret_cast<h8*>(vt16 + ((int64_t)head * QKV_HD + d) * Tp + m0 + 8 * th) = yh;
+  }
+}
+
+template <int NB>
+hipError_t run_qkv_nb(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                      int64_t T, int64_t Tp, int64_t nq, int64_t nkv, const float* qnw,
+                      const float* knw, float eps, const float* cos_t, const float* sin_t,
+                      _Float16* q16, _Float16* k16, _Float16* vt16, const int2* seg,
+                      hipStream_t s) {
+  dim3 grid((unsigned)(nq + 2 * nkv), (unsigned)(Tp / 16));
+  gemm_i8_qkv_kernel<NB><<<grid, QKV_NW * 64, 0, s>>>(
+      xq, dx, wq, dw, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t, q16, k16,
+      vt16, seg);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 int gemm_i8_route(int64_t M, int64_t Nrows, int64_t K) {
@@ -1093,6 +1356,41 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
       return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
     default:
       return run<64, 64, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+  }
+}
+
+bool gemm_i8_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd) {
+  const int64_t nb = K / QK;
+  return hd == QKV_HD && Tp % 64 == 0 && Tp >= T && T > 0 && Tp <= SMALL_M_MAX &&
+         K % BK == 0 && (nb == 16 || nb == 24 || nb == 32 || nb == 36);
+}
+
+hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* wq,
+                              const float* dw, int64_t T, int64_t Tp, int64_t K, int64_t nq,
+                              int64_t nkv, int64_t hd, const float* qnw, const float* knw,
+                              float eps, const float* cos_t, const float* sin_t, uint16_t* q16,
+                              uint16_t* k16, uint16_t* vt16, const int32_t* seg, hipStream_t s) {
+  if (!gemm_i8_qkv_ok(T, Tp, K, hd) || (nq + 2 * nkv) * hd * K >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  _Float16* q = reinterpret_cast<_Float16*>(q16);
+  _Float16* k = reinterpret_cast<_Float16*>(k16);
+  _Float16* v = reinterpret_cast<_Float16*>(vt16);
+  const int2* sg = reinterpret_cast<const int2*>(seg);
+  switch (K / QK) {
+    case 16:
+      return run_qkv_nb<16>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
+                            sg, s);
+    case 24:
+      return run_qkv_nb<24>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
+                            sg, s);
+    case 32:
+      return run_qkv_nb<32>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
+                            sg, s);
+    case 36:
+      return run_qkv_nb<36>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
+                            sg, s);
+    default:
+      return hipErrorInvalidValue;
   }
 }
 

@@ -364,6 +364,7 @@ struct Rows {
   int64_t t;
   const int32_t* seg;
   int64_t seg_max;
+  const uint32_t* host_ids = nullptr;   // set: the gather reads the ids from the host
 };
 
 // The layers, final norm and pooling with dense bf16 projections (the
@@ -440,10 +441,16 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
 
   // model.rs:507-508: Embedding::forward, then * embed_scale (f64 sqrt(hidden) as f32)
   const float embed_scale = (float)sqrt((double)H);
-  LAUNCH(GLYPR_K_GATHER, s,
-         launch_gather(m->token_embd.w->qs(), m->token_embd.w->dw(), H, m->ids.as<uint32_t>(), t,
-                       embed_scale, h, s),
-         "gather launch");
+  if (rows.host_ids)
+    LAUNCH(GLYPR_K_GATHER, s,
+           launch_gather_host_ids(m->token_embd.w->qs(), m->token_embd.w->dw(), H, rows.host_ids,
+                                  t, embed_scale, h, s),
+           "gather launch");
+  else
+    LAUNCH(GLYPR_K_GATHER, s,
+           launch_gather(m->token_embd.w->qs(), m->token_embd.w->dw(), H, m->ids.as<uint32_t>(),
+                         t, embed_scale, h, s),
+           "gather launch");
   // TextPLE::project_and_norm_per_layer (ple.rs:48-85): per_layer_model_proj of
   // the scaled embeddings, * hidden^-0.5 (f64 powf, applied as candle's f32
   // affine), RMSNorm over ple_dim.  Layer l's input is row t*NL + l of [t*NL][P].
@@ -472,19 +479,36 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     const int64_t hd = L.head_dim, nkv = L.n_kv_heads, qd = nq * hd;
     // ---- attention block (layer.rs:27-34)
     const glypr_q8w* wqkv = L.self_attn.fused_qkv.w;
-    LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, wqkv->qs(), wqkv->dw(), dev_f32(m->qkv), t, wqkv->n, H, wqkv->n,
-                          s),
-           "qkv gemm launch");
     const float* cos_t = dev_f32(L.full_attention ? m->cos_f : m->cos_s);
     const float* sin_t = dev_f32(L.full_attention ? m->sin_f : m->sin_s);
-    RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
-                          L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
-                          L.full_attention ? 0 : c.sliding_window, m->attn_q.as<uint16_t>(),
-                          m->attn_k.as<uint16_t>(), m->attn_vt.as<uint16_t>(),
-                          dev_f32(m->attn_scratch), nullptr,
-                          m->cq.as<int8_t>(), dev_f32(m->dc), s, nullptr, rows.seg,
-                          rows.seg_max));
+    const int64_t window = L.full_attention ? 0 : c.sliding_window;
+    const int64_t tp = attn_padded_len(t);
+    if (gemm_i8_qkv_ok(t, tp, H, hd)) {
+      // the q|k|v GEMM writes the attention operands itself (no f32 q|k|v)
+      LAUNCH(GLYPR_K_GEMM_I8_QKV, s,
+             launch_gemm_i8_qkv(xq, dx, wqkv->qs(), wqkv->dw(), t, tp, H, nq, nkv, hd,
+                                L.self_attn.q_norm.weight, L.self_attn.k_norm.weight, c.eps,
+                                cos_t, sin_t, m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
+                                m->attn_vt.as<uint16_t>(), rows.seg, s),
+             "qkv gemm launch");
+      LAUNCH(GLYPR_K_ATTENTION, s,
+             launch_attention(m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
+                              m->attn_vt.as<uint16_t>(), dev_f32(m->attn_scratch), nullptr,
+                              m->cq.as<int8_t>(), dev_f32(m->dc), t, tp, nq, nkv, hd, window, s,
+                              nullptr, rows.seg, rows.seg_max),
+             "attention launch");
+    } else {
+      LAUNCH(GLYPR_K_GEMM_I8, s,
+             launch_gemm_i8(xq, dx, wqkv->qs(), wqkv->dw(), dev_f32(m->qkv), t, wqkv->n, H,
+                            wqkv->n, s),
+             "qkv gemm launch");
+      RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
+                            L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
+                            window, m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
+                            m->attn_vt.as<uint16_t>(), dev_f32(m->attn_scratch), nullptr,
+                            m->cq.as<int8_t>(), dev_f32(m->dc), s, nullptr, rows.seg,
+                            rows.seg_max));
+    }
     const glypr_q8w* wo = L.self_attn.o.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
            launch_gemm_i8(m->cq.as<int8_t>(), dev_f32(m->dc), wo->qs(), wo->dw(),
@@ -833,10 +857,14 @@ int glypr_hip_model_embed(glypr_model* m, const uint32_t* ids, int64_t t, int64_
   std::lock_guard<std::mutex> lk(ctx->mu);
   // buffers and RoPE tables were sized at finalize
   hipStream_t s = (hipStream_t)stream;
-  GLYPR_TRY_HIP(hipMemcpyAsync(m->ids.p, ids, (size_t)t * 4, hipMemcpyHostToDevice, s),
-                "ids upload");
+  // Up to GATHER_ARG_IDS ids ride in the gather's kernel arguments; longer
+  // sequences are uploaded first.
+  const bool arg_ids = gather_host_ids_ok(c.hidden, t);
+  if (!arg_ids)
+    GLYPR_TRY_HIP(hipMemcpyAsync(m->ids.p, ids, (size_t)t * 4, hipMemcpyHostToDevice, s),
+                  "ids upload");
   float* tokens = nullptr;
-  RET_IF(forward_rows(m, ctx, Rows{t, nullptr, 0}, hidden, &tokens, s));
+  RET_IF(forward_rows(m, ctx, Rows{t, nullptr, 0, arg_ids ? ids : nullptr}, hidden, &tokens, s));
   const int64_t width = c.out_dim > 0 ? c.out_dim : c.hidden;
   LAUNCH(GLYPR_K_POOL, s,
          launch_pool(tokens, nullptr, t, width, trunc, out, dev_f32(m->pooled), s),

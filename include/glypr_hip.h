@@ -421,7 +421,8 @@ typedef enum glypr_kernel_id {
   GLYPR_K_VEC_SEARCH = 17,    /* all-pairs hamming / cosine over encoded vectors */
   GLYPR_K_GEMM_I8_PRO = 18,   /* INT8_EXACT GEMM with the quantize / RMSNorm prologue fused */
   GLYPR_K_GEMM_BF16W = 19,    /* GEMM on dense bf16 weights (+ GeGLU epilogue) */
-  GLYPR_K_COUNT = 20
+  GLYPR_K_GEMM_I8_QKV = 20,   /* INT8_EXACT q|k|v GEMM with the q/k/v norms + RoPE epilogue */
+  GLYPR_K_COUNT = 21
 } glypr_kernel_id;
 
 /* The per-op device timing of forward_profiled (profile.rs:53-56, 63-429),

@@ -351,13 +351,16 @@ def test_concat_views_share_the_fused_buffer(ctx, oracle):
                       "view after fused handle released")
 
 
-def test_gather_bit_exact_and_range(ctx, oracle):
+@pytest.mark.parametrize("n_ids", [1, 512, 768, 769, 3000])
+def test_gather_bit_exact_and_range(ctx, oracle, n_ids):
+    """Up to 768 ids ride in the kernel arguments, more are uploaded first:
+    both routes against the oracle, bit for bit."""
     vocab, d = 50_000, 768
-    say(f"embed gather vocab={vocab} d={d}")
+    say(f"embed gather vocab={vocab} d={d} ids={n_ids}")
     tb = oracle.q8_0_weight(vocab, d, seed=71)
     table = Q8Weight.from_gguf(ctx, tb, vocab, d)
-    ids = oracle.uniform_ids(512, seed=72, vocab=vocab)
-    ids[:4] = [0, vocab - 1, 7, 7]
+    ids = oracle.uniform_ids(n_ids, seed=72, vocab=vocab)
+    ids[:4] = [0, vocab - 1, 7, 7][:n_ids]
     scale = float(np.float32(np.sqrt(768.0)))
     y = host(ops.embed_gather(ctx, table, ids, scale))
     assert_bits_equal(y, oracle.embed_gather(tb, vocab, d, ids, scale), "gather")
