@@ -1086,9 +1086,10 @@ hipError_t run(const int8_t* xq,const float* dx, const int8_t* wq, const float* 
 //   rows that hold no token (past T, or past their sequence in a segment
 //   table) are written as zeros.
 // The f32 q|k|v rows never reach HBM and qkv_post's launch goes away.  Grid:
-// x = head slot (q heads, k heads, v heads), y = 16-row block of the Tp
-// padded rows.  Stage DMA: 2 A units and 32 B units per 128-byte K stage;
-// wave w issues B units 4 w .. 4 w + 3 and waves 0 and 1 one A unit each.
+// (head slot, 16-row block of the Tp padded rows), the slots being the q
+// heads, then the k heads, then the v heads.  Stage DMA: 2 A units and 32 B
+// units per 128-byte K stage; wave w issues B units 4 w .. 4 w + 3 and waves
+// 0 and 1 one A unit each.
 // ---------------------------------------------------------------------------
 constexpr int QKV_HD = 256;
 constexpr int QKV_NW = 8;
@@ -1118,8 +1119,12 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave;
-  const int slot = blockIdx.x;            // head slot
-  const int m0 = blockIdx.y * BM;         // first row (token) of the block
+  // Workgroup i runs on XCD i % 8: each XCD takes a contiguous run of the
+  // slot-major order, so it streams the weight rows of one or two head
+  // slots rather than all of them.
+  int rb, slot;
+  xcd_tile(Tp / BM, nq + 2 * nkv, true, rb, slot);
+  const int m0 = rb * BM;                 // first row (token) of the block
   const int n0 = slot * BN;
   const int M = T;                        // rows with activations
 
@@ -1328,7 +1333,7 @@ hipError_t run_qkv_nb(const int8_t* xq, const float* dx, const int8_t* wq, const
                       const float* knw, float eps, const float* cos_t, const float* sin_t,
                       _Float16* q16, _Float16* k16, _Float16* vt16, const int2* seg,
                       hipStream_t s) {
-  dim3 grid((unsigned)(nq + 2 * nkv), (unsigned)(Tp / 16));
+  const unsigned grid = (unsigned)((nq + 2 * nkv) * (Tp / 16));
   gemm_i8_qkv_kernel<NB><<<grid, QKV_NW * 64, 0, s>>>(
       xq, dx, wq, dw, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t, q16, k16,
       vt16, seg);
