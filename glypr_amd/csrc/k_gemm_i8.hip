@@ -1321,7 +1321,12 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
       const int i = 8 * th + j;
       bool valid;
       (void)seg_row_pos(seg, m0 + i, T, &valid);
-      yh[j] = valid ? (_Float16)(stg[i * QKV_SP + d] * sinv[i]) : (_Float16)0.0f;
+      // the f32 product is rounded first, then converted (qkv_post's two
+      // roundings): left free, the compiler folds multiply and conversion
+      // into one v_fma_mixlo_f16, which rounds once
+      float p = stg[i * QKV_SP + d] * sinv[i];
+      asm volatile("" : "+v"(p));
+      yh[j] = valid ? (_Float16)p : (_Float16)0.0f;
     }
     *reinterpret_cast<h8*>(vt16 + ((int64_t)head * QKV_HD + d) * Tp + m0 + 8 * th) = yh;
   }

@@ -192,6 +192,59 @@ def ctypes_byref(oracle, cfg):
     return ctypes.byref(cfg)
 
 
+@pytest.mark.parametrize("t", [130, 512, 1000])
+def test_model_equals_op_composition_bit_exact(ctx, oracle, t):
+    """The model driver against the same forward composed from the public ops,
+    bit for bit.  The model runs its own launch sequence: ids in the gather's
+    kernel arguments, and the q|k|v GEMM writing the attention operands itself
+    (per-head norms, RoPE, f16) where the composition runs rmsnorm_q8_0_matmul to
+    f32 q|k|v and glypr_hip_attention's separate qkv_post; 6 layers cover the
+    sliding and the full layer kinds (layer.rs:20-50, model.rs:498-578)."""
+    n_layers, vocab, H, eps = 6, 2000, 768, 1e-6
+    say(f"model driver vs op composition layers={n_layers} t={t}: bit-exact token states")
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=60)
+    ids = oracle.uniform_ids(t, seed=t + 3, vocab=vocab)
+    hidden = torch.empty((t, H), dtype=torch.float32, device="cuda")
+    m.embed(ids, trunc=256, hidden=hidden)
+    got = host(hidden)
+    m.close()
+
+    def q8(name, n, k):
+        return ops.Q8Weight.from_gguf(ctx, tensors[name][0], n, k)
+
+    def w(name):
+        return dev(np.ascontiguousarray(tensors[name][0], np.float32).reshape(-1))
+
+    table = q8("token_embd.weight", vocab, H)
+    h = ops.embed_gather(ctx, table, ids, float(np.float32(np.sqrt(768.0))))
+    rope = {th: tuple(dev(a) for a in oracle.rope_tables(256, th, t)) for th in (1e4, 1e6)}
+    weights = [table]
+    for i in range(n_layers):
+        p = f"blk.{i}."
+        parts = [q8(p + "attn_q.weight", 768, H), q8(p + "attn_k.weight", 256, H),
+                 q8(p + "attn_v.weight", 256, H)]
+        wqkv, qkv_views = ops.Q8Weight.concat(ctx, parts)
+        gu = [q8(p + "ffn_gate.weight", 1152, H), q8(p + "ffn_up.weight", 1152, H)]
+        wgu, gu_views = ops.Q8Weight.concat(ctx, gu)
+        wo, wd = q8(p + "attn_output.weight", H, 768), q8(p + "ffn_down.weight", H, 1152)
+        weights += parts + gu + qkv_views + gu_views + [wqkv, wgu, wo, wd]
+        full = (i + 1) % 6 == 0
+        c, s = rope[1e6 if full else 1e4]
+        qkv = ops.rmsnorm_q8_0_matmul(ctx, wqkv, h, w(p + "attn_norm.weight"), eps)
+        ctxv = ops.attention(ctx, qkv, w(p + "attn_q_norm.weight"), w(p + "attn_k_norm.weight"),
+                             eps, c, s, 3, 1, 256, 0 if full else 512)
+        proj = ops.q8_0_matmul(ctx, wo, ctxv)
+        h = h + ops.rmsnorm(ctx, proj, w(p + "post_attention_norm.weight"), eps)
+        mo = ops.rmsnorm_mlp(ctx, wgu, wd, h, w(p + "ffn_norm.weight"), eps)
+        h = h + ops.rmsnorm(ctx, mo, w(p + "post_ffw_norm.weight"), eps)
+    ref = host(ops.rmsnorm(ctx, h, w("output_norm.weight"), eps))
+    for wt in weights:
+        wt.close()
+    diff = int((got.view(np.uint32) != ref.view(np.uint32)).sum())
+    say(f"  token-state values differing from the composition: {diff} of {got.size}")
+    assert diff == 0
+
+
 @pytest.mark.parametrize("n_layers,t", [(3, 130), (2, 512)])
 def test_model_attention_silenced_bit_exact(ctx, oracle, n_layers, t):
     """With every o projection zero (Q8_0 blocks of d = 0), attention adds
