@@ -627,14 +627,22 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
 constexpr int64_t ATTN_BLOCKS = 256;
 // Queries per block: 16 AQS.  HD 512 runs one row of 16 queries (its two
 // 32 KB tile slots and 192 accumulator registers per lane leave no room for
-// more waves).
-inline int attn_qs(int64_t T, int64_t hd) { return hd == 512 ? 1 : (T <= ATTN_SMALL_T ? 1 : 4); }
+// more waves).  HD 256 takes 64-query blocks for long sequences and for many
+// rows (a batch of sequences): from 4096 rows the 64-query blocks' four-fold
+// K/V reuse beats the 16-query blocks' extra workgroups (32 x 512 rows:
+// 64 against 116 us per layer; 16 x 512: 44 against 62 us), below it the
+// 16-query blocks are as fast or faster (4 x 512: 24 against 30 us).
+constexpr int64_t ATTN_QS4_ROWS = 4096;
+inline int attn_qs(int64_t T, int64_t rows, int64_t hd) {
+  if (hd == 512) return 1;
+  return T > ATTN_SMALL_T || rows >= ATTN_QS4_ROWS ? 4 : 1;
+}
 
 // Tseg: the longest sequence (its key range sets the tile count); rows: the
 // padded rows of all sequences (they set the query blocks).
 static int attn_kb_per_part(int64_t Tseg, int64_t rows, int64_t hd, int64_t nq, int64_t nkv,
                             int64_t window, int* kparts) {
-  const int64_t aqb = 16 * attn_qs(Tseg, hd);
+  const int64_t aqb = 16 * attn_qs(Tseg, rows, hd);
   const int64_t nqb = rows / aqb;
   int64_t nkb = (Tseg + AK - 1) / AK;
   if (window > 0 && Tseg > window) {
@@ -674,7 +682,7 @@ static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float*
                                 uint16_t* cb, const int2* seg, int64_t seg_max) {
   const int64_t G = nq / nkv;
   const int64_t Tk = seg ? seg_max : T;   // the longest key range
-  const int aqs = attn_qs(Tk, HD);
+  const int aqs = attn_qs(Tk, Tp, HD);
   int kparts;
   const int per = attn_kb_per_part(Tk, Tp, HD, nq, nkv, window, &kparts);
   if (kparts > 64) return hipErrorInvalidValue;   // the combine holds one partition per lane
