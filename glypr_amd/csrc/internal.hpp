@@ -189,8 +189,9 @@ hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t*
 
 // The q|k|v projection (INT8_EXACT, Q8_0 activations) with qkv_post's work
 // as its epilogue: writes the attention operands q / k / vt (f16, rows padded
-// to Tp, invalid rows zero) straight from the GEMM.  head_dim 256, Tp <= 2048,
-// K in {512, 768, 1024, 1152}.
+// to Tp, invalid rows zero) straight from the GEMM.  head_dim 256, K a
+// multiple of 128; 16-row blocks for Tp <= 2048 with K in {512, 768, 1024,
+// 1152}, 128-row blocks otherwise.
 bool gemm_i8_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd);
 hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* wq,
                               const float* dw, int64_t T, int64_t Tp, int64_t K, int64_t nq,

@@ -1345,6 +1345,282 @@ hipError_t run_qkv_nb(const int8_t* xq, const float* dx, const int8_t* wq, const
   return hipGetLastError();
 }
 
+
+// ---------------------------------------------------------------------------
+// The fused q|k|v projection for many rows (Tp > 2048: long sequences and
+// batches of sequences): the large-M kernel's main loop with the attention
+// prologue as epilogue, as gemm_i8_qkv_kernel does it for few rows.  One
+// workgroup per (128 tokens, head slot of 256 columns), 8 waves: wave w owns
+// rows 32 (w & 3) .. +31 and columns 128 (w >> 2) .. +127 as 4 MFMA tiles of
+// 32 x 32 (the large-M kernel's wave tile and exact epilogue); every 128-byte
+// K stage arrives by LDS DMA into a two-slot ring (A [128][128 B], B
+// [256][128 B], then the A and B scales as [block][row] f32).  After the loop
+// the f32 tile goes through LDS in two halves of 64 rows, each turned into
+// the attention operands exactly as qkv_post_kernel (k_attn.hip) does:
+// RMSNorm over the head in the reference's chain order, q_norm / k_norm,
+// RoPE with both products rounded, f16 (q, k) or transposed f16 (v); rows
+// that hold no token are written as zeros, rows past Tp not at all.
+// ---------------------------------------------------------------------------
+// WMW waves along M (4 or 6: 128 or 192 rows), 2 along N; one workgroup per CU
+// either way (110 or 126 KB of LDS), 2 or 3 waves per SIMD.
+template <int WMW>
+__global__ void __launch_bounds__(WMW * 2 * 64) __attribute__((amdgpu_waves_per_eu(WMW / 2)))
+gemm_i8_qkv_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
+                       const int8_t* __restrict__ B, const float* __restrict__ dB, int K, int T,
+                       int Tp, int nq, int nkv, const float* __restrict__ qnw,
+                       const float* __restrict__ knw, float eps, const float* __restrict__ cos_t,
+                       const float* __restrict__ sin_t, _Float16* __restrict__ q16,
+                       _Float16* __restrict__ k16, _Float16* __restrict__ vt16,
+                       const int2* __restrict__ seg) {
+  constexpr int NW = 2 * WMW, BM = 32 * WMW, BN = QKV_HD, TN = 4;
+  constexpr int UA = BM / 8, UB = BN / 8;                  // 1 KB operand units
+  constexpr int USA = KB * BM / 64, USB = KB * BN / 64;    // 256 B scale units
+  constexpr int NU = UA + UB + USA + USB, UPW = NU / NW;
+  static_assert(NU % NW == 0 && BM % 64 == 0, "stage units split evenly over the waves");
+  constexpr int OFF_SA = (UA + UB) * 1024, OFF_SB = OFF_SA + KB * BM * 4;
+  constexpr int SLOT = OFF_SB + KB * BN * 4;
+  constexpr int HALF = BM / 2;                             // rows per epilogue pass
+  static_assert(WMW == 4 || WMW == 6, "128 or 192 rows");
+  static_assert(HALF * QKV_SP * 4 <= 2 * SLOT, "an epilogue half fits the ring");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * SLOT];
+  __shared__ float sinv[HALF];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WMW, wn = wave / WMW;
+  const int slots = nq + 2 * nkv;
+  // Workgroup i runs on XCD i % 8: each XCD takes a contiguous run of the
+  // (row block, head slot) list, so the slots of a row block share its A rows
+  // in one L2.
+  int mi, slot;
+  xcd_tile((Tp + BM - 1) / BM, slots, false, mi, slot);
+  const int m0 = mi * BM, n0 = slot * BN;
+  const int nb = K / QK, nst = K / BK;
+  auto a_row = [&](int ml) -> int { return m0 + ml < T ? m0 + ml : T - 1; };
+
+  // this wave's DMA units: unit u = NW j + wave (uniform per wave): [0, UA)
+  // A rows, [UA, UA+UB) B rows (8 rows x 128 B, +128 B per stage), then the
+  // A and B scales (64 rows of one block, +16 B per stage)
+  const int rsub = lane >> 3, pch = lane & 7;
+  const int8_t* ubase[UPW];
+  int uvoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; j++) {
+    const int u = j * NW + wave;
+    if (u < UA) {
+      const int row = u * 8 + rsub;
+      ubase[j] = A;
+      uvoff[j] = a_row(row) * K + ((pch ^ big_swz(row)) << 4);
+    } else if (u < UA + UB) {
+      const int row = (u - UA) * 8 + rsub;
+      ubase[j] = B;
+      uvoff[j] = (n0 + row) * K + ((pch ^ big_swz(row)) << 4);
+    } else if (u < UA + UB + USA) {
+      const int v = u - UA - UB, kb = v / (BM / 64);
+      ubase[j] = reinterpret_cast<const int8_t*>(dA);
+      uvoff[j] = (a_row((v % (BM / 64)) * 64 + lane) * nb + kb) * 4;
+    } else {
+      const int v = u - UA - UB - USA, kb = v / (BN / 64);
+      ubase[j] = reinterpret_cast<const int8_t*>(dB);
+      uvoff[j] = ((n0 + (v % (BN / 64)) * 64 + lane) * nb + kb) * 4;
+    }
+  }
+  auto issue = [&](int st, int sl) {
+#pragma unroll
+    for (int j = 0; j < UPW; j++) {
+      const int u = j * NW + wave;
+      if (u < UA + UB)
+        dma16(ubase[j] + st * BK, uvoff[j], lds_u32(ring + sl * SLOT + u * 1024));
+      else
+        dma4(ubase[j] + st * KB * 4, uvoff[j],
+             lds_u32(ring + sl * SLOT + OFF_SA + (u - UA - UB) * 256));
+    }
+  };
+  issue(0, 0);
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int arow = wm * 32 + lrow;
+  int offA[KB], offB[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    const int ch = 2 * kb + lhalf;
+    offA[kb] = arow * BK + ((ch ^ big_swz(arow)) << 4);
+    // B row wn 128 + 32 tn + lrow: its swizzle depends on lrow only
+    offB[kb] = (BM + wn * 128 + lrow) * BK + ((ch ^ big_swz(lrow)) << 4);
+  }
+  const int offX = OFF_SA + (wm * 32 + 4 * lhalf) * 4;
+  const int offW = OFF_SB + (wn * 128 + lrow) * 4;   // tile tn, block kb: + (kb BN + 32 tn) 4
+  v16i magic;
+#pragma unroll
+  for (int i = 0; i < 16; i++) magic[i] = MAGIC;
+  float acc[TN][16];
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[tn][r] = 0.0f;
+
+#pragma unroll 1
+  for (int st = 0; st < nst; st++) {
+    const int r = st & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (st + 1 < nst) issue(st + 1, r ^ 1);
+    const uint8_t* sl = ring + r * SLOT;
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+      const v4i af = *reinterpret_cast<const v4i*>(sl + offA[kb]);
+      v4f xv[4];
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        xv[g] = *reinterpret_cast<const v4f*>(sl + offX + kb * BM * 4 + 32 * g);
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const v4i bf = *reinterpret_cast<const v4i*>(sl + offB[kb] + 32 * BK * tn);
+        const float wd = *reinterpret_cast<const float*>(sl + offW + (kb * BN + 32 * tn) * 4);
+        const float wc = wd * NEG_MAGIC;
+        const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, magic, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+          float t = fmaf(__int_as_float(d[q]), wd, wc);   // round(S * d_w)
+          float u = t * xv[q >> 2][q & 3];                 // round(. * d_x)
+          acc[tn][q] = acc[tn][q] + u;                     // round(acc + .)
+        }
+      }
+    }
+  }
+  __syncthreads();   // every wave is past its last ring read
+
+  float* stg = reinterpret_cast<float*>(ring);
+  const bool is_v = slot >= nq + nkv;
+  const bool is_q = slot < nq;
+  const int head = is_q ? slot : (is_v ? slot - nq - nkv : slot - nq);
+  const float* w = is_q ? qnw : knw;
+  _Float16* outp = is_q ? q16 : k16;
+  const v4f wv = (!is_v && w) ? *reinterpret_cast<const v4f*>(w + 4 * lane) : v4f{1, 1, 1, 1};
+#pragma unroll 1
+  for (int hf = 0; hf < 2; hf++) {
+    const int r0 = m0 + HALF * hf;   // first token of this half
+    // the half's rows: waves wm / (WMW / 2) == hf stage theirs; register q of
+    // tile tn is row 32 wm + 8 (q >> 2) + 4 lhalf + (q & 3), column
+    // 128 wn + 32 tn + lrow
+    if (wm / (WMW / 2) == hf) {
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+        for (int q = 0; q < 16; q++)
+          stg[(32 * (wm % (WMW / 2)) + 8 * (q >> 2) + 4 * lhalf + (q & 3)) * QKV_SP + wn * 128 +
+              32 * tn + lrow] = acc[tn][q];
+    }
+    __syncthreads();
+    // Reference-order 1/rms of staged row 8 wave + l / 8 on lanes 8 c:
+    // lane l runs chain l % 8 of that row, the reads of each half of the
+    // chain ahead of its FMAs (acc of the second half's waves is still live)
+    float inv;
+    {
+      const int i = 8 * wave + (lane >> 3);
+      constexpr int CH = QKV_HD / 8, CB = CH / 2;
+      float a = 0.0f;
+#pragma unroll
+      for (int c0 = 0; c0 < CH; c0 += CB) {
+        float e[CB];
+#pragma unroll
+        for (int c = 0; c < CB; c++) e[c] = stg[i * QKV_SP + 8 * (c0 + c) + (lane & 7)];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int c = 0; c < CB; c++) a = fmaf(e[c], e[c], a);
+      }
+      const float sum = hsum8_avx2(a);
+      inv = 1.0f / sqrtf(sum / (float)QKV_HD + eps);
+    }
+    if (!is_v) {
+      // wave w writes rows 8 w .. 8 w + 7; lane l holds dims 4 l .. 4 l + 3
+#pragma unroll 1
+      for (int k = 0; k < 8; k++) {
+        const int i = 8 * wave + k;
+        const int t = r0 + i;
+        if (t >= Tp) break;   // uniform: rows past the padded length are not stored
+        bool valid;
+        const int pos = seg_row_pos(seg, t, T, &valid);
+        const float iv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), 8 * k));
+        const v4f x = *reinterpret_cast<const v4f*>(stg + i * QKV_SP + 4 * lane);
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (valid) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) y[e] = w ? (x[e] * iv) * wv[e] : x[e] * iv;
+          const v4f cv = *reinterpret_cast<const v4f*>(cos_t + (int64_t)pos * QKV_HD + 4 * lane);
+          const v4f sv = *reinterpret_cast<const v4f*>(sin_t + (int64_t)pos * QKV_HD + 4 * lane);
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            // lanes l and l ^ 32 hold dims d and d +- 128 (rotate_half's pairs)
+            const float ye = y[e];
+            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(ye),
+                                                            __float_as_uint(ye), false, false);
+            const float rt = lane < 32 ? -__uint_as_float(p[1]) : __uint_as_float(p[0]);
+            const float a = ye * cv[e];
+            const float b = rt * sv[e];
+            y[e] = a + b;
+          }
+        }
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        const h4 yh = {(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+        *reinterpret_cast<h4*>(outp + ((int64_t)head * Tp + t) * QKV_HD + 4 * lane) = yh;
+      }
+    } else {
+      // v: the half's HALF 1/rms values through LDS, then thread (dim d,
+      // group g of 8 tokens) writes 8 consecutive tokens of vt row d as one
+      // 16-byte store
+      if ((lane & 7) == 0) sinv[8 * wave + (lane >> 3)] = inv;
+      __syncthreads();
+      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+      constexpr int NG = HALF / 8;   // groups of 8 tokens in the half
+#pragma unroll 1
+      for (int task = tid; task < QKV_HD * NG; task += NW * 64) {
+        const int d = task / NG, g = task % NG;
+        const int t0 = r0 + 8 * g;
+        if (t0 >= Tp) continue;   // Tp is a multiple of 64: whole groups past it
+        h8 yh;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          bool valid;
+          (void)seg_row_pos(seg, t0 + j, T, &valid);
+          // the f32 product is rounded first, then converted (qkv_post's two
+          // roundings; left free the compiler would fold both into one
+          // v_fma_mixlo_f16)
+          float p = stg[(8 * g + j) * QKV_SP + d] * sinv[8 * g + j];
+          asm volatile("" : "+v"(p));
+          yh[j] = valid ? (_Float16)p : (_Float16)0.0f;
+        }
+        *reinterpret_cast<h8*>(vt16 + ((int64_t)head * QKV_HD + d) * Tp + t0) = yh;
+      }
+    }
+    __syncthreads();   // the half is consumed before the next one is staged
+  }
+}
+
+hipError_t run_qkv_big(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                       int64_t K, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
+                       const float* qnw, const float* knw, float eps, const float* cos_t,
+                       const float* sin_t, _Float16* q16, _Float16* k16, _Float16* vt16,
+                       const int2* seg, hipStream_t s) {
+  // one workgroup per CU: pick the row block (128 or 192) whose rounds of 256
+  // workgroups take the fewest rows per CU (8192 rows: 320 blocks of 128 are
+  // two rounds, 215 of 192 one)
+  const int64_t slots = nq + 2 * nkv;
+  auto cost = [&](int64_t bm) { return ((Tp + bm - 1) / bm * slots + 255) / 256 * bm; };
+  if (cost(192) < cost(128)) {
+    const unsigned grid = (unsigned)(slots * ((Tp + 191) / 192));
+    gemm_i8_qkv_big_kernel<6><<<grid, 768, 0, s>>>(xq, dx, wq, dw, (int)K, (int)T, (int)Tp,
+                                                   (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
+                                                   q16, k16, vt16, seg);
+  } else {
+    const unsigned grid = (unsigned)(slots * ((Tp + 127) / 128));
+    gemm_i8_qkv_big_kernel<4><<<grid, 512, 0, s>>>(xq, dx, wq, dw, (int)K, (int)T, (int)Tp,
+                                                   (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
+                                                   q16, k16, vt16, seg);
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 int gemm_i8_route(int64_t M, int64_t Nrows, int64_t K) {
@@ -1369,10 +1645,16 @@ hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, c
   }
 }
 
-bool gemm_i8_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd) {
+// Few rows: the small-M form (16-row blocks); many rows, or a K the small
+// form is not built for: the large-M form (128-row blocks, runtime K).
+static bool qkv_small_ok(int64_t Tp, int64_t K) {
   const int64_t nb = K / QK;
-  return hd == QKV_HD && Tp % 64 == 0 && Tp >= T && T > 0 && Tp <= SMALL_M_MAX &&
-         K % BK == 0 && (nb == 16 || nb == 24 || nb == 32 || nb == 36);
+  return Tp <= SMALL_M_MAX && (nb == 16 || nb == 24 || nb == 32 || nb == 36);
+}
+
+bool gemm_i8_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd) {
+  return hd == QKV_HD && Tp % 64 == 0 && Tp >= T && T > 0 && K > 0 && K % BK == 0 &&
+         (qkv_small_ok(Tp, K) || T * K < (int64_t(1) << 31));
 }
 
 hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* wq,
@@ -1386,6 +1668,9 @@ hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* w
   _Float16* k = reinterpret_cast<_Float16*>(k16);
   _Float16* v = reinterpret_cast<_Float16*>(vt16);
   const int2* sg = reinterpret_cast<const int2*>(seg);
+  if (!qkv_small_ok(Tp, K))
+    return run_qkv_big(xq, dx, wq, dw, K, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v, sg,
+                       s);
   switch (K / QK) {
     case 16:
       return run_qkv_nb<16>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,

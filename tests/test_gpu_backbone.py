@@ -192,14 +192,16 @@ def ctypes_byref(oracle, cfg):
     return ctypes.byref(cfg)
 
 
-@pytest.mark.parametrize("t", [130, 512, 1000])
+@pytest.mark.parametrize("t", [130, 512, 1000, 2100, 6600])
 def test_model_equals_op_composition_bit_exact(ctx, oracle, t):
     """The model driver against the same forward composed from the public ops,
     bit for bit.  The model runs its own launch sequence: ids in the gather's
     kernel arguments, and the q|k|v GEMM writing the attention operands itself
     (per-head norms, RoPE, f16) where the composition runs rmsnorm_q8_0_matmul to
     f32 q|k|v and glypr_hip_attention's separate qkv_post; 6 layers cover the
-    sliding and the full layer kinds (layer.rs:20-50, model.rs:498-578)."""
+    sliding and the full layer kinds (layer.rs:20-50, model.rs:498-578).  The
+    q|k|v GEMM runs in 16-row blocks up to T = 2048, in 128-row blocks at
+    2100 and in 192-row blocks at 6600."""
     n_layers, vocab, H, eps = 6, 2000, 768, 1e-6
     say(f"model driver vs op composition layers={n_layers} t={t}: bit-exact token states")
     m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=60)
