@@ -294,7 +294,9 @@ template <int HD, int G, int AQS>
 __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
     const f16* __restrict__ q16, const f16* __restrict__ kk, const f16* __restrict__ vt,
     float* __restrict__ part_o, float* __restrict__ part_ml, int T, int Tp, int nq, int nkv,
-    int window, int kb_per_part, int kparts, const int2* __restrict__ seg) {
+    int window, int kb_per_part, int kparts, const int2* __restrict__ seg,
+    float* __restrict__ ctx, int8_t* __restrict__ cq, float* __restrict__ dc,
+    uint16_t* __restrict__ cb) {
   static_assert(HD == 256 || HD == 512, "head dims 256 and 512");
   constexpr int NWV = G * AQS;
   constexpr int AQB = 16 * AQS;
@@ -515,6 +517,60 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  if (kparts == 1) {
+    // One partition: the combine's merge is the identity (weight e^0 = 1,
+    // L = l, acc = O), so the context O / l is written here, in the
+    // combine's arithmetic (one division, then per-value products), as f32
+    // and / or the o projection's Q8_0 or bf16 operand; rows past T are not
+    // outputs.  A Q8_0 block (32 dims: t = 2 b, 2 b + 1) spans the lanes
+    // l16 + 16 lq of the query, two permlane swaps give its amax.
+    const float inv = 1.0f / l_run;
+    const bool live = qi < T;
+    const int width = nq * HD;
+    const int64_t rowoff = (int64_t)qi * width + (int64_t)h * HD;
+#pragma unroll
+    for (int t = 0; t < HD / 16; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) o[t][r] = o[t][r] * inv;
+    if (ctx && live)
+#pragma unroll
+      for (int t = 0; t < HD / 16; t++)
+        *reinterpret_cast<v4f_*>(ctx + rowoff + 16 * t + 4 * lq) = o[t];
+    if (cb && live)
+#pragma unroll
+      for (int t = 0; t < HD / 16; t++) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(cb + rowoff + 16 * t + 4 * lq);
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+          dst[e] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)o[t][2 * e]) |
+                   ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)o[t][2 * e + 1]) << 16);
+      }
+    if (cq) {
+#pragma unroll
+      for (int b = 0; b < HD / 32; b++) {
+        float a = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) a = fmaxf(a, fabsf(o[2 * b + tt][r]));
+        a = pair_max32(pair_max16(a));
+        const QScale sc = q8_scale(a);
+        if (live) {
+#pragma unroll
+          for (int tt = 0; tt < 2; tt++) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              packed |= ((uint32_t)(quant_round(o[2 * b + tt][r] * sc.id) & 0xFF)) << (8 * r);
+            *reinterpret_cast<uint32_t*>(cq + rowoff + 16 * (2 * b + tt) + 4 * lq) = packed;
+          }
+          if (lq == 0) dc[(int64_t)qi * (width / QK) + (h * HD) / QK + b] = sc.dq;
+        }
+      }
+    }
+    return;
+  }
+
   // ---- partial results: query qi, dims 16 t + 4 lq .. +3
   const int64_t prow = (int64_t)kp * Tp + qi;
 #pragma unroll
@@ -694,7 +750,7 @@ static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float*
   if (G == GG && aqs == QS)                                                                      \
     attn_partial_kernel<HD, GG, QS><<<grid, GG * QS * 64, 0, s>>>(                               \
         q, k, v, part_o, part_ml, (int)T, (int)Tp, (int)nq, (int)nkv, (int)window, per, kparts, \
-        seg);
+        seg, ctx, cq, dc, cb);
   if constexpr (HD == 256) {
     GLYPR_ATTN_CASE(1, 1) else GLYPR_ATTN_CASE(1, 4)
     else GLYPR_ATTN_CASE(2, 1) else GLYPR_ATTN_CASE(2, 4)
@@ -708,7 +764,7 @@ static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float*
   }
 #undef GLYPR_ATTN_CASE
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || kparts == 1) return e;   // one partition: the partial wrote ctx
   attn_combine_kernel<HD><<<(unsigned)((T * nq + 3) / 4), 256, 0, s>>>(
       part_o, part_ml, (int)T, (int)Tp, (int)nq, kparts, ctx, cq, dc, cb);
   return hipGetLastError();

@@ -60,7 +60,7 @@ def attention_ref(oracle, qkv, qnw, knw, eps, theta, nq, nkv, hd, window, f16_qk
     return oracle.attention(qr, kr, vr, window), c, s
 
 
-@pytest.mark.parametrize("t,window,qk_scale", [(70, 0, 1.0), (512, 0, 0.25), (600, 512, 0.25),
+@pytest.mark.parametrize("t,window,qk_scale", [(40, 0, 1.0), (64, 0, 0.25), (70, 0, 1.0), (512, 0, 0.25), (600, 512, 0.25),
                                                (1100, 256, 1.0), (2048, 512, 0.25),
                                                (4096, 0, 0.25), (8192, 512, 0.25),
                                                (8192, 0, 0.25)])
