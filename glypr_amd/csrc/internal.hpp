@@ -217,6 +217,15 @@ hipError_t launch_gemm_bf16w(const uint16_t* xb, const uint16_t* wb, float* y, i
                              int64_t N, int64_t K, int64_t ldc, hipStream_t s);
 hipError_t launch_gemm_bf16w_geglu(const uint16_t* xb, const uint16_t* wb, uint16_t* hb,
                                    int64_t M, int64_t F, int64_t K, hipStream_t s);
+// The dense-bf16 q|k|v projection with qkv_post's work as its epilogue (f16
+// q / k / vt, rows padded to Tp, invalid rows zero); head_dim 256, K % 64 == 0,
+// Tp >= 2048 (where it beats the two launches).
+bool gemm_bf16w_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd);
+hipError_t launch_gemm_bf16w_qkv(const uint16_t* xb, const uint16_t* wb, int64_t T, int64_t Tp,
+                                 int64_t K, int64_t nq, int64_t nkv, int64_t hd, const float* qnw,
+                                 const float* knw, float eps, const float* cos_t,
+                                 const float* sin_t, uint16_t* q16, uint16_t* k16, uint16_t* vt16,
+                                 const int32_t* seg, hipStream_t s);
 
 // ---- k_vec.hip ----
 hipError_t launch_quantize_binary(const float* x, int64_t n, int64_t dim, uint64_t* out,

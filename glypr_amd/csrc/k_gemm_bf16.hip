@@ -11,6 +11,7 @@
 // the RMSNorm prologue (or a conversion pass).
 #include "device_common.hpp"
 #include "internal.hpp"
+#include "qkv_epilogue.hpp"
 
 namespace glypr {
 
@@ -643,6 +644,153 @@ gemm_bf16w_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
   }
 }
 
+// ---------------------------------------------------------------------------
+// The dense-bf16 q|k|v projection with the attention prologue as epilogue
+// (the bf16-weight model's SelfAttention::forward up to the attention,
+// attention/mod.rs:192-214): the dense kernel's main loop on (64 WMW tokens,
+// head slot of 256 columns) tiles, 4 WMW waves of 64 x 64 (WMW along M, 4
+// along N) over the same two-slot ring of 64-K stages, then the f32 tile
+// through LDS in two halves of 32 WMW rows and qkv_epilogue_rows.
+// The f32 products are those of gemm_bf16w_kernel (same MFMA order), so the
+// operands equal gemm_bf16w + qkv_post bit for bit.  WMW 2 (128 rows, 96 KB)
+// or 3 (192 rows, 112 KB): one workgroup per CU.
+// ---------------------------------------------------------------------------
+template <int WMW>
+__global__ void __launch_bounds__(WMW * 4 * 64) __attribute__((amdgpu_waves_per_eu(WMW)))
+gemm_bf16w_qkv_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, int K,
+                      int T, int Tp, int nq, int nkv, const float* __restrict__ qnw,
+                      const float* __restrict__ knw, float eps, const float* __restrict__ cos_t,
+                      const float* __restrict__ sin_t, _Float16* __restrict__ q16,
+                      _Float16* __restrict__ k16, _Float16* __restrict__ vt16,
+                      const int2* __restrict__ seg) {
+  constexpr int NW = 4 * WMW, TM = 2, TN = 2, BKE = 64;
+  constexpr int BM = 64 * WMW, BN = QKV_HD;
+  constexpr int ROWB = 2 * BKE, CPR = ROWB / 16, RPU = 1024 / ROWB;   // 128 B, 8, 8
+  constexpr int UA = BM / RPU, UB = BN / RPU;                         // 1 KB units
+  constexpr int NU = UA + UB, UPW = (NU + NW - 1) / NW;
+  constexpr int SLOT = NU * 1024;
+  constexpr int NBLK = BKE / 32;
+  constexpr int HALF = BM / 2;
+  static_assert(WMW == 2 || WMW == 3, "128 or 192 rows");
+  static_assert(HALF == 8 * NW && HALF * QKV_SP * 4 <= 2 * SLOT, "epilogue halves");
+  auto swz = [](int r) -> int { return (r >> 1) & 7; };   // 8 chunks per row
+  __shared__ __attribute__((aligned(16))) uint8_t ring[2 * SLOT];
+  __shared__ float sinv[HALF];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  int mi, slot;
+  xcd_tile((Tp + BM - 1) / BM, nq + 2 * nkv, false, mi, slot);
+  const int m0 = mi * BM, n0 = slot * BN;
+  const int nst = K / BKE;
+  auto a_row = [&](int ml) -> int { return m0 + ml < T ? m0 + ml : T - 1; };
+
+  // this wave's DMA units u = NW j + wave (uniform per wave): [0, UA) A rows,
+  // [UA, NU) B rows, RPU rows of 128 B each, + 128 B per stage
+  const int8_t* ubase[UPW];
+  int uvoff[UPW];
+#pragma unroll
+  for (int j = 0; j < UPW; j++) {
+    const int u = j * NW + wave;
+    const int row = (u < UA ? u : u - UA) * RPU + lane / CPR, c = lane % CPR;
+    ubase[j] = reinterpret_cast<const int8_t*>(u < UA ? A : B);
+    uvoff[j] = (u < UA ? a_row(row) : n0 + row) * (2 * K) + ((c ^ swz(row)) << 4);
+  }
+  auto issue = [&](int st, int sl) {
+#pragma unroll
+    for (int j = 0; j < UPW; j++) {
+      const int u = j * NW + wave;
+      if (u < NU)
+        dma16(ubase[j] + st * ROWB, uvoff[j], lds_u32(ring + sl * SLOT + u * 1024));
+    }
+  };
+  issue(0, 0);
+
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  int offA[TM][NBLK][2], offB[TN][NBLK][2];
+#pragma unroll
+  for (int p = 0; p < NBLK; p++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int q = 4 * p + 2 * lhalf + h;
+#pragma unroll
+      for (int tm = 0; tm < TM; tm++) {
+        const int row = 64 * wm + 32 * tm + lrow;
+        offA[tm][p][h] = row * ROWB + ((q ^ swz(row)) << 4);
+      }
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const int row = 64 * wn + 32 * tn + lrow;
+        offB[tn][p][h] = UA * 1024 + row * ROWB + ((q ^ swz(row)) << 4);
+      }
+    }
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
+
+#pragma unroll 1
+  for (int st = 0; st < nst; st++) {
+    const int r = st & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // stage st has landed
+    __syncthreads();   // ... for every wave; the other slot is free
+    if (st + 1 < nst) issue(st + 1, r ^ 1);
+    const uint8_t* sl = ring + r * SLOT;
+#pragma unroll
+    for (int p = 0; p < NBLK; p++) {
+      v8bf a[TM][2], b[TN][2];
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+          a[tm][h] = *reinterpret_cast<const v8bf*>(sl + offA[tm][p][h]);
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++)
+          b[tn][h] = *reinterpret_cast<const v8bf*>(sl + offB[tn][p][h]);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+          for (int tn = 0; tn < TN; tn++)
+            acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[tm][h], b[tn][h],
+                                                                  acc[tm][tn], 0, 0, 0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();   // every wave is past its last ring read
+
+  float* stg = reinterpret_cast<float*>(ring);
+#pragma unroll 1
+  for (int hf = 0; hf < 2; hf++) {
+    // register r of MFMA tile (tm, tn) is row 64 wm + 32 tm + 8 (r >> 2) +
+    // 4 lhalf + (r & 3), column 64 wn + 32 tn + lrow; each 32-row tile lies
+    // in one half
+    const int r0 = m0 + HALF * hf;
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) {
+      const int lr = 64 * wm + 32 * tm - HALF * hf;   // first row of the MFMA tile in the half
+      if (lr >= 0 && lr < HALF) {
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            stg[(lr + 8 * (r >> 2) + 4 * lhalf + (r & 3)) * QKV_SP + 64 * wn + 32 * tn + lrow] =
+                acc[tm][tn][r];
+      }
+    }
+    __syncthreads();
+    qkv_epilogue_rows<NW>(stg, sinv, r0, T, Tp, slot, nq, nkv, qnw, knw, eps, cos_t, sin_t, q16,
+                          k16, vt16, seg);
+    __syncthreads();   // the half is consumed before the next one is staged
+  }
+}
+
 template <bool GEGLU>
 hipError_t run_dense(const uint16_t* xb, const uint16_t* wb, float* y, uint16_t* hb, int64_t M,
                      int64_t Nrows, int64_t K, int64_t ldc, int64_t F, hipStream_t s) {
@@ -702,6 +850,40 @@ hipError_t launch_gemm_bf16w_geglu(const uint16_t* xb, const uint16_t* wb, uint1
   if (M == 0 || F == 0) return hipSuccess;
   if (!gemm_bf16w_ok(M, 2 * F, K) || F % 32 != 0) return hipErrorInvalidValue;
   return run_dense<true>(xb, wb, nullptr, hb, M, 2 * F, K, 0, F, s);
+}
+
+// From 2048 rows the fused launch beats gemm_bf16w + qkv_post (2048: 18.9
+// against 22.9 us; 8192: 32.8 against 46.8 us); below, its 128-row blocks
+// leave most CUs idle (512: 18.0 against 15.3 us).
+bool gemm_bf16w_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd) {
+  return hd == QKV_HD && Tp % 64 == 0 && Tp >= T && T > 0 && Tp >= 2048 && K > 0 &&
+         K % 64 == 0 && 2 * T * K < (int64_t(1) << 31);
+}
+
+hipError_t launch_gemm_bf16w_qkv(const uint16_t* xb, const uint16_t* wb, int64_t T, int64_t Tp,
+                                 int64_t K, int64_t nq, int64_t nkv, int64_t hd, const float* qnw,
+                                 const float* knw, float eps, const float* cos_t,
+                                 const float* sin_t, uint16_t* q16, uint16_t* k16, uint16_t* vt16,
+                                 const int32_t* seg, hipStream_t s) {
+  const int64_t slots = nq + 2 * nkv;
+  if (!gemm_bf16w_qkv_ok(T, Tp, K, hd) || 2 * slots * hd * K >= (int64_t(1) << 31))
+    return hipErrorInvalidValue;
+  _Float16* q = reinterpret_cast<_Float16*>(q16);
+  _Float16* k = reinterpret_cast<_Float16*>(k16);
+  _Float16* v = reinterpret_cast<_Float16*>(vt16);
+  const int2* sg = reinterpret_cast<const int2*>(seg);
+  // one workgroup per CU: the row block (128 or 192) with the fewest rows per
+  // CU over its rounds of 256 workgroups
+  auto cost = [&](int64_t bm) { return ((Tp + bm - 1) / bm * slots + 255) / 256 * bm; };
+  if (cost(192) < cost(128))
+    gemm_bf16w_qkv_kernel<3><<<(unsigned)(slots * ((Tp + 191) / 192)), 768, 0, s>>>(
+        xb, wb, (int)K, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
+        sg);
+  else
+    gemm_bf16w_qkv_kernel<2><<<(unsigned)(slots * ((Tp + 127) / 128)), 512, 0, s>>>(
+        xb, wb, (int)K, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
+        sg);
+  return hipGetLastError();
 }
 
 }  // namespace glypr

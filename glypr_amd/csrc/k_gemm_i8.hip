@@ -23,6 +23,7 @@
 // projection's int8 operand: the f32 h never reaches HBM.
 #include "device_common.hpp"
 #include "internal.hpp"
+#include "qkv_epilogue.hpp"
 
 namespace glypr {
 
@@ -1091,10 +1092,8 @@ hipError_t run(const int8_t* xq,const float* dx, const int8_t* wq, const float* 
 // units per 128-byte K stage; wave w issues B units 4 w .. 4 w + 3 and waves
 // 0 and 1 one A unit each.
 // ---------------------------------------------------------------------------
-constexpr int QKV_HD = 256;
 constexpr int QKV_NW = 8;
 constexpr int QKV_RING = 3;
-constexpr int QKV_SP = QKV_HD + 4;   // staged row stride (floats)
 
 template <int NB>
 __global__ void __launch_bounds__(QKV_NW * 64)
@@ -1491,12 +1490,7 @@ gemm_i8_qkv_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ d
   __syncthreads();   // every wave is past its last ring read
 
   float* stg = reinterpret_cast<float*>(ring);
-  const bool is_v = slot >= nq + nkv;
-  const bool is_q = slot < nq;
-  const int head = is_q ? slot : (is_v ? slot - nq - nkv : slot - nq);
-  const float* w = is_q ? qnw : knw;
-  _Float16* outp = is_q ? q16 : k16;
-  const v4f wv = (!is_v && w) ? *reinterpret_cast<const v4f*>(w + 4 * lane) : v4f{1, 1, 1, 1};
+  static_assert(HALF == 8 * NW, "the epilogue takes 8 rows per wave");
 #pragma unroll 1
   for (int hf = 0; hf < 2; hf++) {
     const int r0 = m0 + HALF * hf;   // first token of this half
@@ -1512,87 +1506,8 @@ gemm_i8_qkv_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ d
               32 * tn + lrow] = acc[tn][q];
     }
     __syncthreads();
-    // Reference-order 1/rms of staged row 8 wave + l / 8 on lanes 8 c:
-    // lane l runs chain l % 8 of that row, the reads of each half of the
-    // chain ahead of its FMAs (acc of the second half's waves is still live)
-    float inv;
-    {
-      const int i = 8 * wave + (lane >> 3);
-      constexpr int CH = QKV_HD / 8, CB = CH / 2;
-      float a = 0.0f;
-#pragma unroll
-      for (int c0 = 0; c0 < CH; c0 += CB) {
-        float e[CB];
-#pragma unroll
-        for (int c = 0; c < CB; c++) e[c] = stg[i * QKV_SP + 8 * (c0 + c) + (lane & 7)];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int c = 0; c < CB; c++) a = fmaf(e[c], e[c], a);
-      }
-      const float sum = hsum8_avx2(a);
-      inv = 1.0f / sqrtf(sum / (float)QKV_HD + eps);
-    }
-    if (!is_v) {
-      // wave w writes rows 8 w .. 8 w + 7; lane l holds dims 4 l .. 4 l + 3
-#pragma unroll 1
-      for (int k = 0; k < 8; k++) {
-        const int i = 8 * wave + k;
-        const int t = r0 + i;
-        if (t >= Tp) break;   // uniform: rows past the padded length are not stored
-        bool valid;
-        const int pos = seg_row_pos(seg, t, T, &valid);
-        const float iv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), 8 * k));
-        const v4f x = *reinterpret_cast<const v4f*>(stg + i * QKV_SP + 4 * lane);
-        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (valid) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) y[e] = w ? (x[e] * iv) * wv[e] : x[e] * iv;
-          const v4f cv = *reinterpret_cast<const v4f*>(cos_t + (int64_t)pos * QKV_HD + 4 * lane);
-          const v4f sv = *reinterpret_cast<const v4f*>(sin_t + (int64_t)pos * QKV_HD + 4 * lane);
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            // lanes l and l ^ 32 hold dims d and d +- 128 (rotate_half's pairs)
-            const float ye = y[e];
-            const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(ye),
-                                                            __float_as_uint(ye), false, false);
-            const float rt = lane < 32 ? -__uint_as_float(p[1]) : __uint_as_float(p[0]);
-            const float a = ye * cv[e];
-            const float b = rt * sv[e];
-            y[e] = a + b;
-          }
-        }
-        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-        const h4 yh = {(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
-        *reinterpret_cast<h4*>(outp + ((int64_t)head * Tp + t) * QKV_HD + 4 * lane) = yh;
-      }
-    } else {
-      // v: the half's HALF 1/rms values through LDS, then thread (dim d,
-      // group g of 8 tokens) writes 8 consecutive tokens of vt row d as one
-      // 16-byte store
-      if ((lane & 7) == 0) sinv[8 * wave + (lane >> 3)] = inv;
-      __syncthreads();
-      typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-      constexpr int NG = HALF / 8;   // groups of 8 tokens in the half
-#pragma unroll 1
-      for (int task = tid; task < QKV_HD * NG; task += NW * 64) {
-        const int d = task / NG, g = task % NG;
-        const int t0 = r0 + 8 * g;
-        if (t0 >= Tp) continue;   // Tp is a multiple of 64: whole groups past it
-        h8 yh;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          bool valid;
-          (void)seg_row_pos(seg, t0 + j, T, &valid);
-          // the f32 product is rounded first, then converted (qkv_post's two
-          // roundings; left free the compiler would fold both into one
-          // v_fma_mixlo_f16)
-          float p = stg[(8 * g + j) * QKV_SP + d] * sinv[8 * g + j];
-          asm volatile("" : "+v"(p));
-          yh[j] = valid ? (_Float16)p : (_Float16)0.0f;
-        }
-        *reinterpret_cast<h8*>(vt16 + ((int64_t)head * QKV_HD + d) * Tp + t0) = yh;
-      }
-    }
+    qkv_epilogue_rows<NW>(stg, sinv, r0, T, Tp, slot, nq, nkv, qnw, knw, eps, cos_t, sin_t, q16,
+                          k16, vt16, seg);
     __syncthreads();   // the half is consumed before the next one is staged
   }
 }

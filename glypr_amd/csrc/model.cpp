@@ -387,17 +387,35 @@ int forward_dense(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* h
     const bool last = li + 1 == m->layers.size();
     const int64_t hd = L.head_dim, nkv = L.n_kv_heads, qd = nq * hd;
     const glypr_bf16w* wqkv = L.self_attn.fused_qkv.wb;
-    LAUNCH(GLYPR_K_GEMM_BF16W, s,
-           launch_gemm_bf16w(xb, wqkv->p, dev_f32(m->qkv), t, wqkv->n, H, wqkv->n, s),
-           "qkv gemm launch");
     const float* cos_t = dev_f32(L.full_attention ? m->cos_f : m->cos_s);
     const float* sin_t = dev_f32(L.full_attention ? m->sin_f : m->sin_s);
-    RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
-                          L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
-                          L.full_attention ? 0 : c.sliding_window, m->attn_q.as<uint16_t>(),
-                          m->attn_k.as<uint16_t>(), m->attn_vt.as<uint16_t>(),
-                          dev_f32(m->attn_scratch), nullptr, nullptr, nullptr, s, xb, rows.seg,
-                          rows.seg_max));
+    const int64_t window = L.full_attention ? 0 : c.sliding_window;
+    const int64_t tp = attn_padded_len(t);
+    if (gemm_bf16w_qkv_ok(t, tp, H, hd)) {
+      // the q|k|v GEMM writes the attention operands itself (no f32 q|k|v);
+      // the attention writes its context as the o projection's bf16 operand
+      LAUNCH(GLYPR_K_GEMM_BF16W, s,
+             launch_gemm_bf16w_qkv(xb, wqkv->p, t, tp, H, nq, nkv, hd, L.self_attn.q_norm.weight,
+                                   L.self_attn.k_norm.weight, c.eps, cos_t, sin_t,
+                                   m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
+                                   m->attn_vt.as<uint16_t>(), rows.seg, s),
+             "qkv gemm launch");
+      LAUNCH(GLYPR_K_ATTENTION, s,
+             launch_attention(m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
+                              m->attn_vt.as<uint16_t>(), dev_f32(m->attn_scratch), nullptr,
+                              nullptr, nullptr, t, tp, nq, nkv, hd, window, s, xb, rows.seg,
+                              rows.seg_max),
+             "attention launch");
+    } else {
+      LAUNCH(GLYPR_K_GEMM_BF16W, s,
+             launch_gemm_bf16w(xb, wqkv->p, dev_f32(m->qkv), t, wqkv->n, H, wqkv->n, s),
+             "qkv gemm launch");
+      RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
+                            L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
+                            window, m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
+                            m->attn_vt.as<uint16_t>(), dev_f32(m->attn_scratch), nullptr,
+                            nullptr, nullptr, s, xb, rows.seg, rows.seg_max));
+    }
     const glypr_bf16w* wo = L.self_attn.o.wb;
     LAUNCH(GLYPR_K_GEMM_BF16W, s,
            launch_gemm_bf16w(xb, wo->p, dev_f32(m->proj), t, H, qd, H, s), "o gemm launch");

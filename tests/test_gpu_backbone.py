@@ -300,7 +300,7 @@ def test_model_forward_vs_oracle(ctx, oracle, n_layers, t, vocab):
     m.close()
 
 
-@pytest.mark.parametrize("n_layers,t,vocab", [(2, 64, 2000), (6, 600, 2000), (1, 4100, 2000)])
+@pytest.mark.parametrize("n_layers,t,vocab", [(2, 64, 2000), (6, 600, 2000), (6, 2100, 2000), (1, 4100, 2000)])
 def test_dense_bf16_model_vs_float64(ctx, oracle, n_layers, t, vocab):
     """The bf16-weight backbone (dense bf16 projections, bf16 activations into
     every GEMM, f32 accumulation) against the float64 statement of the same
