@@ -234,7 +234,8 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 //   are keys 8 lq + 4 kt + r: one contiguous 16-byte chunk of a V^T row is the
 //   matching A operand.  The S^T of tile kb+1 is issued before the softmax of
 //   tile kb so the MFMA pipe and the VALU overlap.  Each partition writes its
-//   running max m, sum l and unnormalised O for its queries.
+//   running max m, sum l and unnormalised O for its queries; with a single
+//   partition the kernel writes the context itself and no combine runs.
 // LDS layouts (16-byte chunks, conflict-free fragment reads):
 //   K slot  [32 keys][256 dims]: chunk c of key row r at c ^ kswz(r);
 //   V^T slot [256 dims][32 keys]: chunk c of dim row r at c ^ vswz(r).
