@@ -247,6 +247,7 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 // ---------------------------------------------------------------------------
 constexpr int AK = 32;            // keys per tile
 constexpr float ATTN_TAU = 8.0f;  // lazy-rescale threshold (natural log): p <= e^8 ~ 2981
+constexpr float ATTN_LOG2E = 1.44269504f;
 static_assert(ATTN_TP_ALIGN % 64 == 0, "query blocks (16 or 64) must tile the padded length");
 // Short sequences use 16-query blocks (more blocks to spread), long ones
 // 64-query blocks (each K/V tile serves 4x the queries; head_dim 256).
@@ -678,6 +679,319 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Short single sequences: one launch, no key partitions, no combine.
+// attn_short: block = (kv group g, 16-query block, DS-dim slice sl of the head
+//   dims), eight waves, two per SIMD.  Each wave owns a contiguous eighth of
+//   the block's keys and walks it in steps of 16 keys: S^T = K Q^T for all G
+//   heads of the group (16 keys x 16 queries per head), the lazy online
+//   softmax of attn_partial, and O^T += V^T P^T for the slice's DS dims with
+//   v_mfma_f32_16x16x16_f16, whose B operand (keys 4 lq .. +3 of query l16)
+//   is exactly the lane's S^T accumulator, so P needs no permutation.  The
+//   eight waves' (m, l, O) merge through LDS in wave order (the combine's
+//   arithmetic), and waves 0..G-1 write head hh's slice of the context:
+//   DS / 32 whole Q8_0 blocks of the o projection's operand.
+//   Every block reads the group's whole K (T x 512 B) but only DS / 256 of
+//   V^T, and repeats the S^T products and the softmax once per slice: the
+//   price of writing no f32 partials and running no second launch.  At
+//   T = 512 with one kv head and 32-dim slices the grid is 32 query blocks x
+//   8 slices = 256 blocks.
+//   Operands reach registers through LDS: read straight from global memory
+//   in the MFMA fragment layouts (neighbouring lanes on different 512-byte
+//   rows) every lane is a cache access of its own, while LDS DMA moves 1 KB
+//   of contiguous rows per instruction.  Each wave owns a two-slot ring
+//   (16 keys of K, 8 KB, and of the slice's V^T) that only it fills and
+//   reads, so the ring needs vmcnt waits but no barriers; the next step's
+//   DMA is issued before the current step's fragments are read, and the
+//   other wave of the SIMD runs while one waits.  The group's Q
+//   (G x 16 rows x 512 B) is staged once in the first waves' second slots.
+//   LDS rows of K and Q (512 B) hold 16-byte chunk c at c ^ (row % 16), so
+//   the 16 rows a fragment read touches fall on distinct bank groups.
+// ---------------------------------------------------------------------------
+constexpr int ASH_WAVES = 8;
+constexpr int ASH_KS = 16;                  // keys per step
+constexpr int ASH_DS = 32;                  // head dims per slice (one Q8_0 block)
+constexpr int64_t ATTN_SHORT_TP = 1024;     // padded lengths it runs up to
+constexpr int ASH_KU = 8;                   // 1 KB K units per step (2 key rows each)
+constexpr int ASH_SLOT_K = ASH_KS * 256 * 2;
+
+typedef _Float16 v4h_ __attribute__((ext_vector_type(4)));
+
+template <int G, int DS>
+__global__ void __launch_bounds__(ASH_WAVES * 64) attn_short_kernel(
+    const f16* __restrict__ q16, const f16* __restrict__ kk, const f16* __restrict__ vt, int T,
+    int Tp, int nq, int nkv, int window, float* __restrict__ ctx, int8_t* __restrict__ cq,
+    float* __restrict__ dc, uint16_t* __restrict__ cb) {
+  constexpr int HD = 256;
+  constexpr int NW = ASH_WAVES;
+  constexpr int NSL = HD / DS;          // slices per head
+  constexpr int NT = DS / 16;           // O^T tiles (16 dims) per slice
+  constexpr int VU = DS / 32;           // 1 KB V^T units per step (32 dim rows of 32 B)
+  constexpr int SLOT_V = DS * ASH_KS * 2;
+  static_assert(G <= NW / 2, "the first G waves stage one head's Q each (in their second slot)");
+  static_assert(DS % 32 == 0 && HD % DS == 0, "slices are whole Q8_0 blocks");
+  // K ring [NW][2][8 KB], V^T ring [NW][2][DS x 32 B]; after the key loop
+  // the K ring holds the merge buffers.
+  __shared__ __attribute__((aligned(16))) char lds[NW * 2 * (ASH_SLOT_K + SLOT_V)];
+  static_assert(NW * G * NT * 64 * 16 + 2 * NW * G * 16 * 4 <= NW * 2 * ASH_SLOT_K,
+                "merge buffers fit the K ring");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lq = lane >> 4;
+  // one contiguous run of work items per XCD (block id % 8): neighbouring
+  // query blocks and their slices, whose K/V ranges overlap, share an L2
+  const int nqb = Tp / 16;
+  const int W = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+  if (W >= nkv * nqb * NSL) return;   // grid padding (whole block)
+  const int g = W / (nqb * NSL);
+  const int q0 = ((W / NSL) % nqb) * 16;
+  const int sl = W % NSL;
+  const int qi = q0 + l16;   // this lane's query
+  const bool banded = window > 0 && T > window;
+  int kb_lo = 0, kb_hi = (T + ASH_KS - 1) / ASH_KS;
+  if (banded) {
+    const int lo_key = q0 - window, hi_key = q0 + 15 + window;
+    kb_lo = (lo_key > 0 ? lo_key : 0) / ASH_KS;
+    kb_hi = (hi_key < T - 1 ? hi_key : T - 1) / ASH_KS + 1;
+  }
+  const int per = (kb_hi - kb_lo + NW - 1) / NW;
+  const int kw0 = kb_lo + w * per;
+  const int kw1 = kw0 + per < kb_hi ? kw0 + per : kb_hi;
+
+  char* kring = lds + w * 2 * ASH_SLOT_K;
+  char* vring = lds + NW * 2 * ASH_SLOT_K + w * 2 * SLOT_V;
+  // DMA lane offsets.  K (and Q) unit u = rows 2u, 2u + 1 (lane: row
+  // 2u + krow, 16-byte chunk kpc of the LDS row, fetched from global chunk
+  // kpc ^ (row % 16) = (kpc ^ krow) ^ 2u): byte offset 1024 u (the unit's
+  // base) + (kl ^ (2u << 4)).  V^T unit u = dim rows 32u .. 32u + 31 of the
+  // slice, 16 keys (32 B) each (lane: row 32u + lane / 2, chunk lane % 2).
+  const int krow = lane >> 5, kpc = lane & 31;
+  const int kl = 512 * krow + ((kpc ^ krow) << 4);
+  const int vl = (lane >> 1) * Tp * 2 + ((lane & 1) << 4);
+  const f16* kbase = kk + (int64_t)g * Tp * HD;
+  const f16* vbase = vt + ((int64_t)g * HD + DS * sl) * Tp;
+  auto issue = [&](int kb, int slot) {
+    const int8_t* kb_base = reinterpret_cast<const int8_t*>(kbase + (int64_t)kb * ASH_KS * HD);
+    const int8_t* vb_base = reinterpret_cast<const int8_t*>(vbase + (int64_t)kb * ASH_KS);
+#pragma unroll
+    for (int u = 0; u < ASH_KU; u++)
+      dma16(kb_base + 1024 * u, kl ^ (u << 5), lds_u32(kring + slot * ASH_SLOT_K + u * 1024));
+#pragma unroll
+    for (int u = 0; u < VU; u++)
+      dma16(vb_base + (int64_t)64 * u * Tp, vl, lds_u32(vring + slot * SLOT_V + u * 1024));
+  };
+
+  // ---- Q of head w (w < G): 16 rows x 512 B into this wave's second K slot
+  if (w < G) {
+    const int8_t* qb_base =
+        reinterpret_cast<const int8_t*>(q16 + ((int64_t)(g * G + w) * Tp + q0) * HD);
+#pragma unroll
+    for (int u = 0; u < ASH_KU; u++)
+      dma16(qb_base + 1024 * u, kl ^ (u << 5), lds_u32(kring + ASH_SLOT_K + u * 1024));
+  }
+  if (kw0 < kw1) {
+    issue(kw0, 0);
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(ASH_KU + VU) : "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __syncthreads();   // every head's Q has landed
+  // Q fragments (B operand of S^T = K Q^T): query qi of head g G + hh,
+  // dims 32 s + 8 lq .. +7
+  v8h qf[G][HD / 32];
+#pragma unroll
+  for (int hh = 0; hh < G; hh++) {
+    const char* qs = lds + hh * 2 * ASH_SLOT_K + ASH_SLOT_K + l16 * 512;
+#pragma unroll
+    for (int s = 0; s < HD / 32; s++)
+      qf[hh][s] = *reinterpret_cast<const v8h*>(qs + (((4 * s + lq) ^ l16) << 4));
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): Q is in registers
+  __syncthreads();                      // ... in every wave: the second slots are free
+
+  float m_run[G], l_run[G], thr[G], mlog[G];
+  v4f_ o[G][NT];   // O^T: dims DS sl + 16 t + 4 lq + r of query qi
+#pragma unroll
+  for (int hh = 0; hh < G; hh++) {
+    m_run[hh] = -INFINITY;
+    thr[hh] = -INFINITY;
+    mlog[hh] = 0.0f;
+    l_run[hh] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; t++) o[hh][t] = v4f_{0, 0, 0, 0};
+  }
+  for (int kb = kw0, slot = 0; kb < kw1; kb++, slot ^= 1) {
+    if (kb + 1 < kw1) {
+      // the other slot's fragments were read (and used) in the previous step
+      issue(kb + 1, slot ^ 1);
+      asm volatile("s_waitcnt vmcnt(%0)" :: "n"(ASH_KU + VU) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const char* ks = kring + slot * ASH_SLOT_K + l16 * 512;
+    const char* vs = vring + slot * SLOT_V;
+    // K fragments (A operand): key k0 + l16, dims 32 s + 8 lq .. +7
+    v8h kf[HD / 32];
+#pragma unroll
+    for (int s = 0; s < HD / 32; s++)
+      kf[s] = *reinterpret_cast<const v8h*>(ks + (((4 * s + lq) ^ l16) << 4));
+    // V^T fragments (A operand of the 16x16x16 PV): dim rows 16 t + l16 of
+    // the slice, keys 4 lq .. +3 of the step
+    v4h_ vf[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+      vf[t] = *reinterpret_cast<const v4h_*>(vs + (16 * t + l16) * 32 + 8 * lq);
+    // S^T: sacc[hh][r] = S[qi][k0 + 4 lq + r]
+    v4f_ sacc[G];
+#pragma unroll
+    for (int hh = 0; hh < G; hh++) sacc[hh] = v4f_{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < HD / 32; s++)
+#pragma unroll
+      for (int hh = 0; hh < G; hh++)
+        sacc[hh] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[s], qf[hh][s], sacc[hh], 0, 0, 0);
+    const int k0 = kb * ASH_KS;
+    const bool edge = k0 + ASH_KS > T ||
+                      (banded && (k0 < q0 + 15 - window || k0 + ASH_KS - 1 > q0 + window));
+    if (edge) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = k0 + 4 * lq + r;
+        bool ok = key < T;
+        if (banded) {
+          const int d = qi - key;
+          ok = ok && d <= window && -d <= window;
+        }
+#pragma unroll
+        for (int hh = 0; hh < G; hh++)
+          if (!ok) sacc[hh][r] = -INFINITY;
+      }
+    }
+    // Online softmax for query qi of every head with attn_partial's lazy
+    // rescale, made lane-local in the common case: m_run (the same in the
+    // four lanes of a query) moves only when some S exceeds it by more than
+    // ATTN_TAU, which a wave vote on each lane's own four values detects;
+    // only then are the lanes' maxima reduced and O and l rescaled.  l is
+    // kept per lane (the lane's own keys) and summed over the query's four
+    // lanes after the loop.  P = 2^(S log2 e - m log2 e).
+#pragma unroll
+    for (int hh = 0; hh < G; hh++) {
+      const float mloc = fmaxf(fmaxf(sacc[hh][0], sacc[hh][1]), fmaxf(sacc[hh][2], sacc[hh][3]));
+      if (__any(mloc > thr[hh])) {
+        const float mx = pair_max32(pair_max16(mloc));
+        const float m_new = mx > thr[hh] ? mx : m_run[hh];
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __expf(m_run[hh] - m_use);
+        l_run[hh] *= alpha;
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) o[hh][t][r] *= alpha;
+        m_run[hh] = m_new;
+        thr[hh] = m_new + ATTN_TAU;
+        mlog[hh] = m_use * ATTN_LOG2E;
+      }
+      v4h_ pf;   // P^T B operand: k-slot r = key 4 lq + r
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[hh][r], ATTN_LOG2E, -mlog[hh]));
+        l_run[hh] += pv;
+        pf[r] = (f16)pv;
+      }
+#pragma unroll
+      for (int t = 0; t < NT; t++)
+        o[hh][t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[t], pf, o[hh][t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int hh = 0; hh < G; hh++) l_run[hh] = pair_sum32(pair_sum16(l_run[hh]));
+
+  // ---- merge the eight waves' partial results (wave order), write the slice
+  v4f_(*lo)[G][NT][64] = reinterpret_cast<v4f_(*)[G][NT][64]>(lds);
+  float(*lm)[G][16] = reinterpret_cast<float(*)[G][16]>(lds + NW * G * NT * 64 * 16);
+  float(*ll)[G][16] = lm + NW;
+  __syncthreads();   // every wave is done with its ring
+#pragma unroll
+  for (int hh = 0; hh < G; hh++) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) lo[w][hh][t][lane] = o[hh][t];
+    if (lq == 0) {
+      lm[w][hh][l16] = m_run[hh];
+      ll[w][hh][l16] = l_run[hh];
+    }
+  }
+  __syncthreads();
+  if (w >= G) return;
+  const int hh = w;
+  float mw[NW];
+  float M = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < NW; v++) {
+    mw[v] = lm[v][hh][l16];
+    M = fmaxf(M, mw[v]);
+  }
+  float L = 0.0f;
+  v4f_ acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; t++) acc[t] = v4f_{0, 0, 0, 0};
+#pragma unroll
+  for (int v = 0; v < NW; v++) {
+    const float wgt = mw[v] == -INFINITY ? 0.0f : __expf(mw[v] - M);
+    L += wgt * ll[v][hh][l16];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const v4f_ ov = lo[v][hh][t][lane];
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[t][r] += wgt * ov[r];
+    }
+  }
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = acc[t][r] * inv;
+  const bool live = qi < T;
+  const int h = g * G + hh;
+  const int width = nq * HD;
+  const int64_t off = (int64_t)qi * width + (int64_t)h * HD + DS * sl + 4 * lq;
+  if (ctx && live)
+#pragma unroll
+    for (int t = 0; t < NT; t++) *reinterpret_cast<v4f_*>(ctx + off + 16 * t) = acc[t];
+  if (cb && live)
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(cb + off + 16 * t);
+#pragma unroll
+      for (int e = 0; e < 2; e++)
+        dst[e] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)acc[t][2 * e]) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)acc[t][2 * e + 1]) << 16);
+    }
+  if (cq) {
+    // Q8_0 block b of the slice = tiles t = 2b, 2b + 1: lanes l16 + 16 lq
+#pragma unroll
+    for (int b = 0; b < NT / 2; b++) {
+      float a = 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) a = fmaxf(a, fabsf(acc[2 * b + tt][r]));
+      a = pair_max32(pair_max16(a));
+      const QScale sc = q8_scale(a);
+      if (live) {
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+          uint32_t packed = 0;
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            packed |= ((uint32_t)(quant_round(acc[2 * b + tt][r] * sc.id) & 0xFF)) << (8 * r);
+          *reinterpret_cast<uint32_t*>(cq + off + 16 * (2 * b + tt)) = packed;
+        }
+        if (lq == 0) dc[(int64_t)qi * (width / QK) + (h * HD + DS * sl) / QK + b] = sc.dq;
+      }
+    }
+  }
+}
+
 // Key partitions: enough (query block, partition) items for one round of
 // workgroups (256 CUs), at most half the key tiles per partition and at most
 // 64 partitions (the combine holds one partition per lane).
@@ -738,6 +1052,18 @@ static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float*
                                 int64_t nq, int64_t nkv, int64_t window, hipStream_t s,
                                 uint16_t* cb, const int2* seg, int64_t seg_max) {
   const int64_t G = nq / nkv;
+  if (HD == 256 && !seg && Tp <= ATTN_SHORT_TP && G <= 3) {
+    // one short sequence: the single-launch slice kernel
+    const int64_t items = nkv * (Tp / 16) * (HD / ASH_DS);
+    const unsigned grid = (unsigned)((items + 7) / 8 * 8);
+#define GLYPR_ASH_CASE(GG)                                                                      \
+  if (G == GG)                                                                                  \
+    attn_short_kernel<GG, ASH_DS><<<grid, ASH_WAVES * 64, 0, s>>>(                              \
+        q, k, v, (int)T, (int)Tp, (int)nq, (int)nkv, (int)window, ctx, cq, dc, cb);
+    GLYPR_ASH_CASE(1) else GLYPR_ASH_CASE(2) else GLYPR_ASH_CASE(3)
+#undef GLYPR_ASH_CASE
+    return hipGetLastError();
+  }
   const int64_t Tk = seg ? seg_max : T;   // the longest key range
   const int aqs = attn_qs(Tk, Tp, HD);
   int kparts;

@@ -85,6 +85,32 @@ def test_attention_core_vs_oracle(ctx, oracle, t, window, qk_scale):
     assert np.abs(got - ref).max() <= bound * scale, np.abs(got - ref).max() / scale
 
 
+@pytest.mark.parametrize("t,window,nq,nkv", [(1, 0, 3, 1), (33, 0, 1, 1), (200, 0, 2, 1),
+                                             (512, 0, 4, 2), (512, 100, 3, 1), (512, 0, 4, 1),
+                                             (777, 0, 6, 2), (1000, 256, 3, 1),
+                                             (1024, 512, 2, 2), (1025, 512, 3, 1)])
+def test_attention_core_geometries(ctx, oracle, t, window, nq, nkv):
+    """Single sequences of up to 1024 padded rows run one launch per layer
+    (query block x 32-dim slice, no key partitions); group sizes 1-3, several
+    kv heads, bands narrower than the sequence, and the neighbours that take
+    the partitioned kernels (4 q heads per kv head, 1025 tokens)."""
+    hd, eps = 256, 1e-6
+    say(f"attention core geometry t={t} window={window} nq={nq} nkv={nkv}")
+    qkv = oracle.normal(t * (nq + 2 * nkv) * hd, seed=t + 11).reshape(t, -1) * np.float32(0.7)
+    qnw = (1 + 0.1 * oracle.normal(hd, seed=5)) * QK_NORM_SCALE
+    knw = (1 + 0.1 * oracle.normal(hd, seed=6)) * QK_NORM_SCALE
+    ref16, c, s = attention_ref(oracle, qkv, qnw, knw, eps, 10000.0, nq, nkv, hd, window, True)
+    ref, _, _ = attention_ref(oracle, qkv, qnw, knw, eps, 10000.0, nq, nkv, hd, window)
+    got = host(ops.attention(ctx, dev(qkv), dev(qnw), dev(knw), eps, dev(c), dev(s), nq, nkv, hd,
+                             window)).astype(np.float64)
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref16).max() <= 5e-4 * scale, np.abs(got - ref16).max() / scale
+    assert np.abs(got - ref).max() <= 1e-3 * scale, np.abs(got - ref).max() / scale
+    again = host(ops.attention(ctx, dev(qkv), dev(qnw), dev(knw), eps, dev(c), dev(s), nq, nkv,
+                               hd, window)).astype(np.float64)
+    assert np.array_equal(got, again)
+
+
 # q_norm / k_norm weights are 0.25 * (1 + 0.1 N(0,1)): glypr's attention has no
 # 1/sqrt(head_dim) scale (attention/metal_flash.rs:331), so trained models fold
 # it into these norms.  With unit norms the random network is chaotic: logits
