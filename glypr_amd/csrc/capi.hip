@@ -507,6 +507,12 @@ int glypr_hip_q8_0_matmul_noalloc(glypr_hip_ctx* ctx, const glypr_q8w* w, const 
   GLYPR_CHECK(m >= 0, GLYPR_ERR_SHAPE, "m = %lld is negative", (long long)m);
   RET_IF(check_variant(variant));
   GLYPR_CHECK(w != nullptr, GLYPR_ERR_INVALID_ARG, "w is NULL");
+  // every operand form takes at least m * k bytes: bound m before the byte
+  // count is formed, so that it cannot wrap
+  GLYPR_CHECK(m <= (int64_t)(GLYPR_NOALLOC_SCRATCH_BYTES / (size_t)w->k), GLYPR_ERR_SHAPE,
+              "m = %lld, k = %lld exceeds the no-allocation matmul's %zu bytes of activation "
+              "scratch",
+              (long long)m, (long long)w->k, (size_t)GLYPR_NOALLOC_SCRATCH_BYTES);
   const size_t need = matmul_ws_bytes(m, w->n, w->k, false, variant);
   GLYPR_CHECK(need <= GLYPR_NOALLOC_SCRATCH_BYTES, GLYPR_ERR_SHAPE,
               "m = %lld, k = %lld needs %zu bytes of activation scratch; the no-allocation "

@@ -120,11 +120,12 @@ hipError_t launch_pool(const float* tok, const uint8_t* mask, int64_t t, int64_t
                        float* out, float* scratch, hipStream_t s);
 // Several sequences at 64-aligned row offsets of tok [rows][d] (rows % 64 ==
 // 0): seg is the per-row segment table (launch_qkv_post), seqs {offset,
-// length} per sequence; out [n_seqs][trunc or d].
+// length} per sequence; out [n_seqs][trunc or d].  mixed: the lengths differ,
+// so each mean divides by its count (the reference's masked batch pooling).
 size_t pool_segments_scratch_floats(int64_t rows, int64_t n_seqs, int64_t d);
 hipError_t launch_pool_segments(const float* tok, int64_t rows, const int32_t* seg,
                                 const int32_t* seqs, int64_t n_seqs, int64_t d, int64_t trunc,
-                                float* out, float* scratch, hipStream_t s);
+                                float* out, float* scratch, hipStream_t s, bool mixed);
 
 // h = h + rmsnorm(x; w_post); if xq: (xq, dx) = Q8_0(rmsnorm(h; w_next)).  dim % 32 == 0.
 // scalar (device, nullable): h = (h + RMSNorm(x)) * scalar.  plain_q: xq/dx
@@ -141,9 +142,28 @@ hipError_t launch_affine(float* x, int64_t n, float mul, hipStream_t s);
 hipError_t launch_geglu_quant(const float* g, const float* u, int64_t u_stride, int64_t rows,
                               int64_t dim, int8_t* hq, float* dh, hipStream_t s);
 
-// ---- k_attn.hip ----
+// ---- k_attn.hip, attn_plan.cpp ----
 // Attention operands are padded to Tp = attn_padded_len(T) tokens.
 constexpr int64_t ATTN_TP_ALIGN = 64;
+// The partitioned kernels: keys per K/V tile; sequences up to ATTN_SMALL_T
+// use 16-query blocks (more blocks to spread), longer ones 64-query blocks
+// (each K/V tile serves 4x the queries; head_dim 256).
+constexpr int ATTN_AK = 32;
+constexpr int64_t ATTN_SMALL_T = 1024;
+// Key partitions: enough (query block, partition) items for one round of
+// workgroups (256 CUs), at most half the key tiles per partition and at most
+// 64 partitions (the combine holds one partition per lane).
+constexpr int64_t ATTN_BLOCKS = 256;
+// From this many padded rows (a batch of sequences) head_dim 256 takes
+// 64-query blocks.
+constexpr int64_t ATTN_QS4_ROWS = 4096;
+// Queries per block / 16 for the longest sequence T over `rows` padded rows.
+int attn_qs(int64_t T, int64_t rows, int64_t hd);
+// Key tiles per partition (returned) and the partition count (*kparts) for
+// the longest sequence Tseg (its key range sets the tile count) over `rows`
+// padded rows (they set the query blocks).
+int attn_kb_per_part(int64_t Tseg, int64_t rows, int64_t hd, int64_t nq, int64_t nkv,
+                     int64_t window, int* kparts);
 inline int64_t attn_padded_len(int64_t t) { return (t + ATTN_TP_ALIGN - 1) / ATTN_TP_ALIGN * ATTN_TP_ALIGN; }
 // q16 [nq][Tp][hd], k16 [nkv][Tp][hd], vt16 [nkv][hd][Tp] (f16).  hd == 256.
 // seg (nullable, device int32 pairs [Tp][2]): row t holds position t - seg[t][0]
@@ -158,9 +178,18 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 // sequences share the buffers (0: attn_padded_len(T)).
 size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
                                 int64_t rows = 0);
-// Whether launch_attention runs this geometry: head_dim 256, nq / nkv in
-// 1..4, at most 64 key partitions at T (T <= 0: any length).
+// The largest attention_scratch_floats over every longest-sequence length
+// up to max_t (multiples of 32, and max_t) and every padded row count from
+// attn_padded_len of it up to cap_rows (a multiple of 64).
+size_t attention_scratch_bound(int64_t max_t, int64_t cap_rows, int64_t nq, int64_t nkv,
+                               int64_t hd, int64_t window);
+// Whether launch_attention runs this geometry: head_dim 256 or 512, nq / nkv
+// in 1..4, at most 64 key partitions at T and attention_rows_ok (T <= 0: any
+// length).
 bool attention_supported(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window);
+// Whether `rows` padded rows of head dim hd keep every per-lane byte offset
+// of the attention kernels (2 hd Tp) below 2^31.
+bool attention_rows_ok(int64_t rows, int64_t hd);
 // ctx (f32 [T][nq*hd]), (cq, dc) (Q8_0 planar) and cb (bf16 [T][nq*hd]) may
 // each be null.
 // seg / seg_max: the segment table of launch_qkv_post and the longest sequence;

@@ -245,13 +245,10 @@ hipError_t launch_qkv_post(const float* qkv, int64_t T, int64_t Tp, int64_t nq, 
 // MFMA 16x16x32 layouts: A (16 x 32): lane l holds row l%16, k = 8(l/16)..+7;
 // B (32 x 16): column l%16, same k; D (16 x 16): column l%16, rows 4(l/16)+r.
 // ---------------------------------------------------------------------------
-constexpr int AK = 32;            // keys per tile
+constexpr int AK = ATTN_AK;       // keys per tile
 constexpr float ATTN_TAU = 8.0f;  // lazy-rescale threshold (natural log): p <= e^8 ~ 2981
 constexpr float ATTN_LOG2E = 1.44269504f;
 static_assert(ATTN_TP_ALIGN % 64 == 0, "query blocks (16 or 64) must tile the padded length");
-// Short sequences use 16-query blocks (more blocks to spread), long ones
-// 64-query blocks (each K/V tile serves 4x the queries; head_dim 256).
-constexpr int64_t ATTN_SMALL_T = 1024;
 
 typedef float v4f_ __attribute__((ext_vector_type(4)));
 
@@ -992,60 +989,6 @@ __global__ void __launch_bounds__(ASH_WAVES * 64) attn_short_kernel(
   }
 }
 
-// Key partitions: enough (query block, partition) items for one round of
-// workgroups (256 CUs), at most half the key tiles per partition and at most
-// 64 partitions (the combine holds one partition per lane).
-constexpr int64_t ATTN_BLOCKS = 256;
-// Queries per block: 16 AQS.  HD 512 runs one row of 16 queries (its two
-// 32 KB tile slots and 192 accumulator registers per lane leave no room for
-// more waves).  HD 256 takes 64-query blocks for long sequences and for many
-// rows (a batch of sequences): from 4096 rows the 64-query blocks' four-fold
-// K/V reuse beats the 16-query blocks' extra workgroups (32 x 512 rows:
-// 64 against 116 us per layer; 16 x 512: 44 against 62 us), below it the
-// 16-query blocks are as fast or faster (4 x 512: 24 against 30 us).
-constexpr int64_t ATTN_QS4_ROWS = 4096;
-inline int attn_qs(int64_t T, int64_t rows, int64_t hd) {
-  if (hd == 512) return 1;
-  return T > ATTN_SMALL_T || rows >= ATTN_QS4_ROWS ? 4 : 1;
-}
-
-// Tseg: the longest sequence (its key range sets the tile count); rows: the
-// padded rows of all sequences (they set the query blocks).
-static int attn_kb_per_part(int64_t Tseg, int64_t rows, int64_t hd, int64_t nq, int64_t nkv,
-                            int64_t window, int* kparts) {
-  const int64_t aqb = 16 * attn_qs(Tseg, rows, hd);
-  const int64_t nqb = rows / aqb;
-  int64_t nkb = (Tseg + AK - 1) / AK;
-  if (window > 0 && Tseg > window) {
-    int64_t band = (2 * window + aqb + AK - 1) / AK + 1;
-    if (band < nkb) nkb = band;
-  }
-  int64_t want = (ATTN_BLOCKS + nqb * nkv - 1) / (nqb * nkv);
-  if (want > (nkb + 1) / 2) want = (nkb + 1) / 2;
-  if (want < (nkb + 63) / 64) want = (nkb + 63) / 64;
-  if (want < 1) want = 1;
-  const int64_t per = (nkb + want - 1) / want;
-  *kparts = (int)((nkb + per - 1) / per);
-  return (int)per;
-}
-
-bool attention_supported(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window) {
-  if ((hd != 256 && hd != 512) || nq <= 0 || nkv <= 0 || nq % nkv != 0 || nq / nkv > 4)
-    return false;
-  if (T <= 0) return true;
-  int kparts;
-  attn_kb_per_part(T, attn_padded_len(T), hd, nq, nkv, window, &kparts);
-  return kparts <= 64;   // the combine holds one partition per lane
-}
-
-size_t attention_scratch_floats(int64_t T, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
-                                int64_t rows) {
-  const int64_t tp = rows > 0 ? rows : attn_padded_len(T);
-  int kp;
-  attn_kb_per_part(T, tp, hd, nq, nkv, window, &kp);
-  return (size_t)(kp * tp * nq * (hd + 2));
-}
-
 template <int HD>
 static hipError_t run_attention(const f16* q, const f16* k, const f16* v, float* scratch,
                                 float* ctx, int8_t* cq, float* dc, int64_t T, int64_t Tp,
@@ -1102,6 +1045,9 @@ hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint
                             int64_t Tp, int64_t nq, int64_t nkv, int64_t hd, int64_t window,
                             hipStream_t s, uint16_t* cb, const int32_t* seg, int64_t seg_max) {
   if (Tp % ATTN_TP_ALIGN != 0 || Tp < T || nq % nkv != 0) return hipErrorInvalidValue;
+  // the kernels' per-lane DMA offsets into V^T (row Tp + column, in bytes,
+  // rows < hd) are 32-bit
+  if (!attention_rows_ok(Tp, hd)) return hipErrorInvalidValue;
   if (seg && (seg_max <= 0 || seg_max > Tp)) return hipErrorInvalidValue;
   const f16* q = reinterpret_cast<const f16*>(q16);
   const f16* k = reinterpret_cast<const f16*>(k16);

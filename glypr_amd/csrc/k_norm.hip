@@ -580,12 +580,16 @@ __device__ __forceinline__ float block_sum_1024(float v, float* red) {
 
 // seqs (nullable): {row offset, length} per sequence; block b then pools
 // sequence b from its own chunks into out[b][td] (pooled: d floats per block).
+// count_div: divide the sum by the token count, as the reference's masked
+// mean does for a batch of mixed lengths (model.rs:671-680, lib.rs:902-941);
+// otherwise multiply by 1/t as its mean (a homogeneous batch, one sequence).
 __global__ void __launch_bounds__(1024) pool_finalize_kernel(const float* __restrict__ partial,
                                                              const uint8_t* __restrict__ mask,
                                                              int64_t t, int64_t d, int64_t trunc,
                                                              float* __restrict__ out,
                                                              float* __restrict__ pooled,
-                                                             const int32_t* __restrict__ seqs) {
+                                                             const int32_t* __restrict__ seqs,
+                                                             bool count_div = false) {
   __shared__ float red[16];
   const int64_t td_out = (trunc > 0 && trunc < d) ? trunc : d;
   if (seqs) {
@@ -610,7 +614,7 @@ __global__ void __launch_bounds__(1024) pool_finalize_kernel(const float* __rest
   for (int64_t i = threadIdx.x; i < d; i += blockDim.x) {
     float s = 0.0f;
     for (int64_t c = 0; c < nchunk; c++) s += partial[c * d + i];
-    const float v = mask ? s / cnt : s * inv_t + 0.0f;
+    const float v = mask ? s / cnt : count_div ? s / (float)t : s * inv_t + 0.0f;
     pooled[i] = v;
     ss += v * v;
   }
@@ -654,7 +658,7 @@ size_t pool_segments_scratch_floats(int64_t rows, int64_t n_seqs, int64_t d) {
 
 hipError_t launch_pool_segments(const float* tok, int64_t rows, const int32_t* seg,
                                 const int32_t* seqs, int64_t n_seqs, int64_t d, int64_t trunc,
-                                float* out, float* scratch, hipStream_t s) {
+                                float* out, float* scratch, hipStream_t s, bool mixed) {
   if (rows % POOL_CHUNK != 0) return hipErrorInvalidValue;
   const int64_t nchunk = rows / POOL_CHUNK;
   float* partial = scratch;
@@ -663,7 +667,7 @@ hipError_t launch_pool_segments(const float* tok, int64_t rows, const int32_t* s
   pool_partial_kernel<<<g1, 256, 0, s>>>(tok, nullptr, rows, d, partial,
                                          reinterpret_cast<const int2*>(seg));
   pool_finalize_kernel<<<(unsigned)n_seqs, 1024, 0, s>>>(partial, nullptr, rows, d, trunc, out,
-                                                          pooled, seqs);
+                                                          pooled, seqs, mixed);
   return hipGetLastError();
 }
 

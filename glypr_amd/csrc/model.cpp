@@ -187,8 +187,7 @@ int ensure_rope(glypr_model* m, int64_t t) {
 
 // Attention scratch for the largest case the model can meet: any (longest)
 // sequence length up to max_seq_len with any padded row count up to the
-// capacity (key partitions shrink as rows grow, so the product is checked at
-// every 64-row step), for each layer's geometry.
+// capacity, for each layer geometry (attention_scratch_bound).
 size_t model_attention_scratch(const glypr_model* m, int64_t cap) {
   const glypr_model_config& c = m->cfg;
   size_t best = 0;
@@ -196,14 +195,8 @@ size_t model_attention_scratch(const glypr_model* m, int64_t cap) {
     const int64_t hd = full ? c.full_head_dim : c.head_dim;
     const int64_t nkv = full ? c.full_n_kv_heads : c.n_kv_heads;
     const int64_t w = full ? 0 : c.sliding_window;
-    for (int64_t tk = 32;; tk += 32) {
-      if (tk > c.max_seq_len) tk = c.max_seq_len;
-      for (int64_t rows = attn_padded_len(tk); rows <= cap; rows += 64) {
-        const size_t sc = attention_scratch_floats(tk, c.n_heads, nkv, hd, w, rows);
-        best = sc > best ? sc : best;
-      }
-      if (tk == c.max_seq_len) break;
-    }
+    const size_t sc = attention_scratch_bound(c.max_seq_len, cap, c.n_heads, nkv, hd, w);
+    best = sc > best ? sc : best;
   }
   return best;
 }
@@ -676,6 +669,15 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
   GLYPR_CHECK(c.max_batch_tokens >= 0 && c.max_batch_tokens <= (int64_t(1) << 24),
               GLYPR_ERR_SHAPE, "max_batch_tokens %lld outside [0, 2^24]",
               (long long)c.max_batch_tokens);
+  {
+    // the attention operands hold max(max_seq_len, max_batch_tokens) rows
+    const int64_t rows = c.max_seq_len > c.max_batch_tokens ? c.max_seq_len : c.max_batch_tokens;
+    const int64_t hd = c.head_dim > c.full_head_dim ? c.head_dim : c.full_head_dim;
+    GLYPR_CHECK(attention_rows_ok(rows, hd), GLYPR_ERR_SHAPE,
+                "%lld rows of head_dim %lld exceed the attention kernels' 32-bit offsets "
+                "(2 * head_dim * padded rows must stay below 2^31)",
+                (long long)rows, (long long)hd);
+  }
   // the attention kernels' geometry, checked for both layer types at the
   // longest sequence (shorter ones use fewer key partitions)
   GLYPR_CHECK(attention_supported(c.max_seq_len, c.n_heads, c.n_kv_heads, c.head_dim,
@@ -954,9 +956,13 @@ int glypr_hip_model_embed_batch(glypr_model* m, const uint32_t* ids, const int64
   float* tokens = nullptr;
   RET_IF(forward_rows(m, ctx, Rows{rows, m->seg.as<int32_t>(), longest}, nullptr, &tokens, s));
   const int64_t width = c.out_dim > 0 ? c.out_dim : c.hidden;
+  // lib.rs:902-941: a batch of equal lengths pools by the plain mean, a mixed
+  // one by the masked sum over the token count
+  bool mixed = false;
+  for (int64_t i = 1; i < n_seqs; i++) mixed = mixed || lens[i] != lens[0];
   LAUNCH(GLYPR_K_POOL, s,
          launch_pool_segments(tokens, rows, m->seg.as<int32_t>(), m->seqs.as<int32_t>(), n_seqs,
-                              width, trunc, out, dev_f32(m->pooled), s),
+                              width, trunc, out, dev_f32(m->pooled), s, mixed),
          "pool launch");
   return GLYPR_OK;
 }

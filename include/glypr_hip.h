@@ -346,9 +346,13 @@ int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, in
 
 /* embed_batch_inner (lib.rs:752-952) for text: n_seqs sequences of lens[i]
  * tokens (ids concatenated, host memory) in one forward pass.  Each sequence's
- * embedding equals the one the reference computes from its padded batch (pad
+ * embedding is the one the reference computes from its padded batch (pad
  * keys masked out of attention, pads left out of the mean, model.rs:580-705),
- * which is the sequence's own single-sequence embedding.  The sequences sit at
+ * which is the sequence's own single-sequence embedding: pooled by the mean
+ * (sum times 1/len) when all lengths are equal and by the masked sum divided
+ * by the token count when they differ, as the reference (lib.rs:902-941); the
+ * pooling sum runs in chunks, so it matches the reference's to rounding
+ * (float64 bound 1e-6 of the largest value), not bit for bit.  The sequences sit at
  * 64-aligned row offsets, so every projection runs once over all of their rows
  * and attention and pooling stay within each sequence.  out [n_seqs][trunc,
  * or the embedding width].  Each len must be in [1, max_seq_len] (the

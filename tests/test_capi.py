@@ -223,6 +223,22 @@ def test_attention_geometry_validation():
                                     ctypes.byref(out)) == _lib.GLYPR_ERR_UNSUPPORTED
     assert L.glypr_hip_model_create(NULL, ctypes.byref(_cfg(max_seq_len=-1)),
                                     ctypes.byref(out)) == _lib.GLYPR_ERR_SHAPE
+    # row capacities at which the attention kernels' 32-bit per-lane byte
+    # offsets (2 head_dim padded_rows) would reach 2^31 are refused: 2^22 rows
+    # of head_dim 256, 2^21 of 512 (the released full layers), as batch
+    # capacity or as sequence length; a batch capacity one 64-row step below
+    # passes validation
+    for cap, geometry in (((1 << 22), _cfg()), ((1 << 21), real)):
+        for field in ("max_batch_tokens", "max_seq_len"):
+            setattr(geometry, field, cap)
+            assert L.glypr_hip_model_create(NULL, ctypes.byref(geometry),
+                                            ctypes.byref(out)) == _lib.GLYPR_ERR_SHAPE
+            assert "2^31" in _lib.last_error()
+            setattr(geometry, field, 0)
+        geometry.max_batch_tokens = cap - 64
+        assert L.glypr_hip_model_create(NULL, ctypes.byref(geometry),
+                                        ctypes.byref(out)) == _lib.GLYPR_ERR_INVALID_ARG
+        geometry.max_batch_tokens = 0
     # glypr_hip_attention: the same geometry rule, checked before the pointers
     args = lambda nq, nkv, hd: (NULL, FAKE, FAKE, FAKE, 1e-6, FAKE, FAKE, 512, nq, nkv, hd, 0,
                                 FAKE, NULL)
@@ -231,6 +247,9 @@ def test_attention_geometry_validation():
     assert L.glypr_hip_attention(*args(3, 2, 256)) == _lib.GLYPR_ERR_SHAPE
     assert L.glypr_hip_attention(*args(4, 1, 256)) == _lib.GLYPR_ERR_INVALID_ARG   # ctx NULL
     assert L.glypr_hip_attention(*args(4, 1, 512)) == _lib.GLYPR_ERR_INVALID_ARG
+    big = lambda t, hd: (NULL, FAKE, FAKE, FAKE, 1e-6, FAKE, FAKE, t, 3, 1, hd, 0, FAKE, NULL)
+    assert L.glypr_hip_attention(*big(1 << 22, 256)) == _lib.GLYPR_ERR_UNSUPPORTED
+    assert L.glypr_hip_attention(*big(1 << 21, 512)) == _lib.GLYPR_ERR_UNSUPPORTED
 
 
 def test_gemm_routing():

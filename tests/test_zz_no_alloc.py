@@ -73,6 +73,13 @@ def test_noalloc_matmul_rejects_oversized():
     rc = L.glypr_hip_q8_0_matmul_noalloc(ctx.handle, w.handle, ops._ptr(x), ops._ptr(y),
                                          m_ok + 1, BF16_DEQUANT, ctx.stream)
     assert rc == _lib.GLYPR_ERR_SHAPE and "scratch" in _lib.last_error()
+    # row counts whose byte count m k would wrap 64 bits are refused the same
+    # way (the bound on m comes before the product); x and y are not touched
+    for m_huge in (1 << 55, (1 << 63) - 1):
+        for variant in (INT8_EXACT, BF16_DEQUANT):
+            rc = L.glypr_hip_q8_0_matmul_noalloc(ctx.handle, w.handle, ops._ptr(x), ops._ptr(y),
+                                                 ctypes.c_int64(m_huge), variant, ctx.stream)
+            assert rc == _lib.GLYPR_ERR_SHAPE and "scratch" in _lib.last_error()
     rc = L.glypr_hip_q8_0_matmul_noalloc(ctx.handle, w.handle, ops._ptr(x), ops._ptr(y), m_ok,
                                          BF16_DEQUANT, ctx.stream)
     assert rc == _lib.GLYPR_OK
