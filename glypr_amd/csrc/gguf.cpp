@@ -27,6 +27,7 @@
 #include <new>
 #include <string>
 #include <vector>
+#include <vector>
 
 #include "host_common.hpp"
 #include "internal.hpp"
@@ -95,6 +96,37 @@ void ggml_type_size(uint32_t t, int64_t* blk, int64_t* bytes) {
   } else if (t == 27 || t == 28) {   // I64, F64
     *blk = 1; *bytes = 8;
   }
+}
+
+// IEEE binary16 -> binary32, exact (normals, subnormals, infinities, NaNs).
+float half_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+  uint32_t exp = (h >> 10) & 0x1F, man = h & 0x3FF, bits;
+  if (exp == 0x1F) {
+    bits = sign | 0x7F800000u | (man << 13);
+  } else if (exp != 0) {
+    bits = sign | ((exp + 112) << 23) | (man << 13);
+  } else if (man == 0) {
+    bits = sign;
+  } else {   // subnormal: normalise
+    int e = 113;
+    while ((man & 0x400) == 0) {
+      man <<= 1;
+      e--;
+    }
+    bits = sign | ((uint32_t)e << 23) | ((man & 0x3FF) << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+// binary32 -> bfloat16, round to nearest even; NaNs stay (quiet) NaNs.
+uint16_t float_to_bf16_rne(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
 struct Cursor {
@@ -520,23 +552,33 @@ static int model_load_gguf_impl(glypr_hip_ctx* ctx, const char* path, glypr_mode
   if (kv_arr && kv_len > 0) RET_IF(glypr_gguf_get_array_u64(g, kvk.c_str(), 0, &kv_heads));
   clear_error();
 
-  // layer pattern: the backend runs the default 5 sliding + 1 full layout
+  // layer_types (config.rs:117-140): sliding_window_pattern, an array of
+  // bools (true = sliding), when the file has one; else layer i is full iff
+  // (i+1) % 6 == 0.  The pattern must cover every block.
+  GLYPR_CHECK(layers > 0 && layers < (1u << 20), GLYPR_ERR_SHAPE, "block_count %llu",
+              (unsigned long long)layers);
+  std::vector<uint8_t> layer_full((size_t)layers);
+  int pat_et = 0;
   int64_t pat_len = 0;
   const std::string patk = key("attention.sliding_window_pattern");
-  const bool has_pat = glypr_gguf_get_array(g, patk.c_str(), &et, &pat_len) == GLYPR_OK;
+  const bool has_pat = glypr_gguf_get_array(g, patk.c_str(), &pat_et, &pat_len) == GLYPR_OK;
   clear_error();
+  if (has_pat) {
+    GLYPR_CHECK(pat_et == T_BOOL, GLYPR_ERR_UNSUPPORTED,
+                "Invalid boolean in sliding_window_pattern (element type %d)", pat_et);
+    GLYPR_CHECK(pat_len >= (int64_t)layers, GLYPR_ERR_SHAPE,
+                "sliding_window_pattern has %lld entries for %llu blocks", (long long)pat_len,
+                (unsigned long long)layers);
+  }
   uint64_t full_kv = 0;   // the full layers' kv heads (0: no full layer)
   for (uint64_t i = 0; i < layers; i++) {
-    const bool full = (i + 1) % 6 == 0;
+    bool full = (i + 1) % 6 == 0;
     if (has_pat) {
       uint64_t sliding = 0;
-      GLYPR_CHECK((int64_t)i < pat_len &&
-                      glypr_gguf_get_array_u64(g, patk.c_str(), (int64_t)i, &sliding) == GLYPR_OK,
-                  GLYPR_ERR_UNSUPPORTED, "sliding_window_pattern is shorter than block_count");
-      GLYPR_CHECK((sliding != 0) == !full, GLYPR_ERR_UNSUPPORTED,
-                  "layer %llu: only the 5-sliding / 1-full layer pattern is supported",
-                  (unsigned long long)i);
+      RET_IF(glypr_gguf_get_array_u64(g, patk.c_str(), (int64_t)i, &sliding));
+      full = sliding == 0;
     }
+    layer_full[(size_t)i] = full ? 1 : 0;
     if (!full) continue;
     uint64_t kvi = 1;
     if (kv_arr && kv_len > (int64_t)i) RET_IF(glypr_gguf_get_array_u64(g, kvk.c_str(), (int64_t)i, &kvi));
@@ -567,6 +609,7 @@ static int model_load_gguf_impl(glypr_hip_ctx* ctx, const char* path, glypr_mode
   cfg.eps = (float)opt_f("attention.layer_norm_rms_epsilon", 1e-6);
   cfg.rope_theta_sliding = opt_f("rope.freq_base_swa", 10000.0);
   cfg.rope_theta_full = opt_f("rope.freq_base", 1000000.0);
+  cfg.layer_types = layer_full.data();
   clear_error();
   // TextPLE (model.rs:257-275) and the embedding projection (model.rs:472-473)
   // when the file has them
@@ -574,12 +617,9 @@ static int model_load_gguf_impl(glypr_hip_ctx* ctx, const char* path, glypr_mode
   const bool has_ple = glypr_gguf_find_tensor(g, "per_layer_model_proj.weight", &pi) == GLYPR_OK;
   const bool has_out = glypr_gguf_find_tensor(g, "output.weight", &oi) == GLYPR_OK;
   clear_error();
-  cfg.ple_dim = 0;
-  if (has_ple) {
-    uint64_t pd = 0;
-    RET_IF(req_u("embedding_length_per_layer_input", &pd));
-    cfg.ple_dim = (int64_t)pd;
-  }
+  // hidden_size_per_layer_input, 512 without the key (config.rs:100-102)
+  cfg.ple_dim = has_ple ? (int64_t)opt_u("embedding_length_per_layer_input", 512) : 0;
+  clear_error();
   cfg.out_dim = has_out ? g->tensors[(size_t)oi].ne[1] : 0;
 
   glypr_model* m = nullptr;
@@ -590,37 +630,58 @@ static int model_load_gguf_impl(glypr_hip_ctx* ctx, const char* path, glypr_mode
       if (*m) glypr_hip_model_destroy(*m);
     }
   } dropper{&m};
-  auto load = [&](const std::string& name) -> int {
+  // LinearOp::from_gguf_tensor (linear.rs:36-78): a layer projection stored as
+  // F32, F16 or BF16 becomes a dense Linear; here the dense bf16 arm, its rows
+  // rounded to bf16 (nearest even; exact for BF16, narrower than the
+  // reference's f32 Linear for F32 and F16).  Norms and scalars are F32, the
+  // token table, PLE and output projections Q8_0.
+  std::vector<uint16_t> bf;
+  auto load = [&](const std::string& name, bool projection) -> int {
     int64_t idx;
     RET_IF(glypr_gguf_find_tensor(g, name.c_str(), &idx));
     const GgufTensor& t = g->tensors[(size_t)idx];
-    GLYPR_CHECK(t.type == 0 || t.type == 8, GLYPR_ERR_UNSUPPORTED,
-                "tensor '%s' has ggml type %u (F32 and Q8_0 are supported)", name.c_str(),
-                t.type);
     GLYPR_CHECK(t.n_dims <= 2, GLYPR_ERR_SHAPE, "tensor '%s' has %u dimensions", name.c_str(),
                 t.n_dims);
-    return glypr_hip_model_set_tensor(m, name.c_str(), t.data, t.ne[1], t.ne[0],
-                                      t.type == 8 ? 1 : 0);
+    if (t.type == 8 || (t.type == 0 && !projection))
+      return glypr_hip_model_set_tensor(m, name.c_str(), t.data, t.ne[1], t.ne[0],
+                                        t.type == 8 ? 1 : 0);
+    GLYPR_CHECK(projection && (t.type == 0 || t.type == 1 || t.type == 30),
+                GLYPR_ERR_UNSUPPORTED,
+                "tensor '%s' has ggml type %u (Q8_0, and F32 / F16 / BF16 layer projections, "
+                "are supported)", name.c_str(), t.type);
+    const int64_t n = t.ne[0] * t.ne[1];
+    bf.resize((size_t)n);
+    for (int64_t i = 0; i < n; i++) {
+      if (t.type == 30) {
+        bf[(size_t)i] = reinterpret_cast<const uint16_t*>(t.data)[i];
+        continue;
+      }
+      float f;
+      if (t.type == 0) memcpy(&f, t.data + 4 * i, 4);
+      else f = half_to_float(reinterpret_cast<const uint16_t*>(t.data)[i]);
+      bf[(size_t)i] = float_to_bf16_rne(f);
+    }
+    return glypr_hip_model_set_tensor(m, name.c_str(), bf.data(), t.ne[1], t.ne[0], 2);
   };
-  int rc = load("token_embd.weight");
-  if (rc == GLYPR_OK) rc = load("output_norm.weight");
+  int rc = load("token_embd.weight", false);
+  if (rc == GLYPR_OK) rc = load("output_norm.weight", false);
   static const char* kLayer[] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate",
                                  "ffn_up", "ffn_down", "attn_norm", "post_attention_norm",
                                  "ffn_norm", "post_ffw_norm", "attn_q_norm", "attn_k_norm"};
   static const char* kPle[] = {"inp_gate", "proj", "post_norm", "layer_output_scale"};
   for (uint64_t i = 0; rc == GLYPR_OK && i < layers; i++) {
-    for (const char* nm : kLayer) {
-      rc = load("blk." + std::to_string(i) + "." + nm + ".weight");
+    for (int j = 0; j < (int)(sizeof(kLayer) / sizeof(kLayer[0])); j++) {
+      rc = load("blk." + std::to_string(i) + "." + kLayer[j] + ".weight", j < 7);
       if (rc != GLYPR_OK) break;
     }
     for (const char* nm : kPle) {
       if (rc != GLYPR_OK || !has_ple) break;
-      rc = load("blk." + std::to_string(i) + "." + nm + ".weight");
+      rc = load("blk." + std::to_string(i) + "." + nm + ".weight", false);
     }
   }
-  if (rc == GLYPR_OK && has_ple) rc = load("per_layer_model_proj.weight");
-  if (rc == GLYPR_OK && has_ple) rc = load("per_layer_proj_norm.weight");
-  if (rc == GLYPR_OK && has_out) rc = load("output.weight");
+  if (rc == GLYPR_OK && has_ple) rc = load("per_layer_model_proj.weight", false);
+  if (rc == GLYPR_OK && has_ple) rc = load("per_layer_proj_norm.weight", false);
+  if (rc == GLYPR_OK && has_out) rc = load("output.weight", false);
   if (rc == GLYPR_OK) rc = glypr_hip_model_finalize(m);
   if (rc != GLYPR_OK) {
     std::string msg = glypr_hip_last_error();

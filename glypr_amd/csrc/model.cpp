@@ -663,6 +663,7 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
               "ple_dim (%lld) must be a non-negative multiple of 32, out_dim (%lld) >= 0",
               (long long)cfg->ple_dim, (long long)cfg->out_dim);
   glypr_model_config c = *cfg;
+  c.layer_types = nullptr;   // read below, not kept
   if (c.full_head_dim == 0) c.full_head_dim = c.head_dim;
   if (c.full_n_kv_heads == 0) c.full_n_kv_heads = c.n_kv_heads;
   if (c.max_seq_len == 0) c.max_seq_len = 8320;   // DEFAULT_MAX_SEQ_LEN, lib.rs:47
@@ -698,7 +699,9 @@ int glypr_hip_model_create(glypr_hip_ctx* ctx, const glypr_model_config* cfg,
   m->layers.resize((size_t)c.n_layers);
   for (int64_t i = 0; i < c.n_layers; i++) {
     EncoderLayer& L = m->layers[(size_t)i];
-    L.full_attention = ((i + 1) % 6) == 0;  // config.rs:131-140
+    // layer_types from sliding_window_pattern, or the default 5 sliding +
+    // 1 full pattern (config.rs:117-140)
+    L.full_attention = cfg->layer_types ? cfg->layer_types[i] != 0 : ((i + 1) % 6) == 0;
     L.head_dim = L.full_attention ? c.full_head_dim : c.head_dim;
     L.n_kv_heads = L.full_attention ? c.full_n_kv_heads : c.n_kv_heads;
   }

@@ -385,7 +385,8 @@ class ModelConfig(ctypes.Structure):
                 ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double),
                 ("ple_dim", ctypes.c_int64), ("out_dim", ctypes.c_int64),
                 ("full_head_dim", ctypes.c_int64), ("full_n_kv_heads", ctypes.c_int64),
-                ("max_seq_len", ctypes.c_int64), ("max_batch_tokens", ctypes.c_int64)]
+                ("max_seq_len", ctypes.c_int64), ("max_batch_tokens", ctypes.c_int64),
+                ("layer_types", ctypes.c_void_p)]
 
 
 class Gguf:
@@ -489,7 +490,10 @@ class Model:
         m.handle = h
         return m
 
-    def __init__(self, ctx: Context, **cfg):
+    def __init__(self, ctx: Context, layer_types=None, **cfg):
+        """layer_types: n_layers values, nonzero = a full-attention layer
+        (sliding_window_pattern, config.rs:117-140); None = the default
+        5 sliding + 1 full pattern."""
         defaults = dict(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256, n_layers=24,
                         vocab=262144, sliding_window=512, eps=1e-6, rope_theta_sliding=10000.0,
                         rope_theta_full=1e6, ple_dim=0, out_dim=0, full_head_dim=0,
@@ -498,6 +502,11 @@ class Model:
         self.cfg = defaults
         self.ctx = ctx
         c = ModelConfig(**defaults)
+        if layer_types is not None:
+            lt = np.ascontiguousarray(np.asarray(layer_types) != 0, dtype=np.uint8)
+            if lt.size != defaults["n_layers"]:
+                raise ValueError("layer_types needs one entry per layer")
+            c.layer_types = lt.ctypes.data   # read by glypr_hip_model_create only
         h = ctypes.c_void_p()
         check(lib().glypr_hip_model_create(ctx.handle, ctypes.byref(c), ctypes.byref(h)))
         self.handle = h

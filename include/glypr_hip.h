@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define GLYPR_HIP_ABI_VERSION 5
+#define GLYPR_HIP_ABI_VERSION 6
 
 typedef enum glypr_status {
   GLYPR_OK = 0,
@@ -300,13 +300,20 @@ typedef struct glypr_model_config {
   int64_t max_batch_tokens;    /* padded rows one glypr_hip_model_embed_batch
                                 * call may take (each sequence rounded up to 64);
                                 * buffers are sized for max(max_seq_len, this) */
+  const uint8_t* layer_types;  /* nullable: n_layers entries, nonzero = a
+                                * full-attention layer, 0 = sliding (the
+                                * layer_types TextConfig builds from
+                                * sliding_window_pattern, config.rs:117-140);
+                                * read at create, not kept.  NULL = the default
+                                * pattern, layer i full iff (i+1) % 6 == 0 */
 } glypr_model_config;
 
 typedef struct glypr_model glypr_model;
 
 /* EmbeddingGemma2Model::from_gguf_content (model.rs:244-488): an empty model
  * whose tensors arrive through glypr_hip_model_set_tensor.  Layer i is full
- * attention iff (i+1) % 6 == 0 (config.rs:131-140), sliding otherwise.  With
+ * attention as cfg->layer_types says, or iff (i+1) % 6 == 0 without it
+ * (config.rs:117-140), sliding otherwise.  With
  * ple_dim > 0 (a multiple of 32) every layer ends with the TextPLEBlock and its
  * layer scalar (layer.rs:45-49); with out_dim > 0 the final norm feeds the
  * embedding projection. */

@@ -642,7 +642,7 @@ static void orc_linear(const uint8_t* w, int64_t n, int64_t k, const float* x, i
 
 void orc_encoder_layer(const orc_model_config* cfg, const orc_layer_weights* w, int64_t layer_idx,
                        float* hidden, const float* per_layer_input, int64_t t, int threads) {
-  int full = orc_layer_is_full(layer_idx);
+  int full = cfg->layer_types ? cfg->layer_types[layer_idx] != 0 : orc_layer_is_full(layer_idx);
   /* per-layer geometry: full-attention layers take their own head_dim and kv
    * head count (TextConfig::get_head_dim / get_num_kv_heads, config.rs:142-169,
    * 208-230; model.rs:286-287), the RoPE table of their head_dim */

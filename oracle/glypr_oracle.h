@@ -150,6 +150,9 @@ typedef struct {
   int64_t out_dim;      /* rows of output.weight; 0 = no embedding projection */
   int64_t full_head_dim;   /* full-attention layers' head_dim (config.rs:149-166); 0 = head_dim */
   int64_t full_n_kv_heads; /* full-attention layers' kv heads (config.rs:151-157); 0 = n_kv_heads */
+  const uint8_t* layer_types; /* n_layers entries, nonzero = full attention (the
+                               * sliding_window_pattern of config.rs:117-140);
+                               * NULL = orc_layer_is_full's default pattern */
 } orc_model_config;
 
 /* Per-layer weights, host memory.  Q8_0 tensors are GGUF blocks. */
@@ -176,7 +179,8 @@ typedef struct {
   const float* layer_scalar;   /* layer_output_scale [1] */
 } orc_layer_weights;
 
-/* layer_types: 0 = sliding, 1 = full (config.rs:131-140). */
+/* The default layer_types without a sliding_window_pattern: 0 = sliding,
+ * 1 = full, layer i full iff (i+1) % 6 == 0 (config.rs:131-140). */
 int orc_layer_is_full(int64_t layer_idx);
 /* RoPE tables (rope.rs:14-87): cos/sin f32 [t][head_dim]. */
 void orc_rope_tables(int64_t head_dim, double theta, int64_t t, float* cos_t, float* sin_t);

@@ -47,7 +47,7 @@ class ModelConfig(ctypes.Structure):
                 ("sliding_window", _i64), ("eps", ctypes.c_float),
                 ("rope_theta_sliding", ctypes.c_double), ("rope_theta_full", ctypes.c_double),
                 ("ple_dim", _i64), ("out_dim", _i64), ("full_head_dim", _i64),
-                ("full_n_kv_heads", _i64)]
+                ("full_n_kv_heads", _i64), ("layer_types", ctypes.c_void_p)]
 
 
 class LayerWeights(ctypes.Structure):
@@ -391,12 +391,14 @@ def model_forward(tensors: dict, ids: np.ndarray, trunc: int, *, hidden: int, ff
                   n_heads: int, n_kv_heads: int, head_dim: int, n_layers: int, vocab: int,
                   sliding_window: int = 512, eps: float = 1e-6, theta_sliding: float = 1e4,
                   theta_full: float = 1e6, full_head_dim: int = 0, full_n_kv_heads: int = 0,
-                  threads: int = 0):
+                  threads: int = 0, layer_types=None):
     """orc_model_forward over GGUF-named tensors {name: array} (Q8_0 tensors as
     block bytes, norms as f32).  The PLE block runs when
     `per_layer_model_proj.weight` is present (ple_dim = its rows / n_layers),
-    the embedding projection when `output.weight` is.  Returns (pooled
-    [trunc or out dim], unpooled token embeddings [t, out dim])."""
+    the embedding projection when `output.weight` is.  layer_types (n_layers
+    values, nonzero = full attention) replaces the default 5 sliding + 1 full
+    pattern.  Returns (pooled [trunc or out dim], unpooled token embeddings
+    [t, out dim])."""
     ple_dim = 0
     if "per_layer_model_proj.weight" in tensors:
         ple_dim = tensors["per_layer_model_proj.weight"].shape[0] // n_layers
@@ -407,6 +409,11 @@ def model_forward(tensors: dict, ids: np.ndarray, trunc: int, *, hidden: int, ff
                       rope_theta_full=theta_full, ple_dim=ple_dim, out_dim=out_dim,
                       full_head_dim=full_head_dim, full_n_kv_heads=full_n_kv_heads)
     keep = []
+    if layer_types is not None:
+        lt = np.ascontiguousarray(np.asarray(layer_types) != 0, dtype=np.uint8)
+        assert lt.size == n_layers
+        keep.append(lt)
+        cfg.layer_types = lt.ctypes.data
 
     def arr(name, dt, ptype):
         if name not in tensors:

@@ -6,7 +6,7 @@ import struct
 import numpy as np
 
 U8, I8, U16, I16, U32, I32, F32, BOOL, STR, ARR, U64, I64, F64 = range(13)
-GGML_F32, GGML_F16, GGML_Q8_0 = 0, 1, 8
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
 
 _SCALAR = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f",
            BOOL: "<?", U64: "<Q", I64: "<q", F64: "<d"}
@@ -51,8 +51,13 @@ def write_gguf(path, metadata, tensors, alignment=32, version=3):
 
 
 def model_gguf(path, tensors_by_name, n_layers, hidden, ffn, n_heads, n_kv_heads, head_dim,
-               extra_meta=()):
-    """Write a gemma-embedding2 GGUF from {name: (array, rows, cols, is_q8)}."""
+               extra_meta=(), pattern=None, types=None):
+    """Write a gemma-embedding2 GGUF from {name: (array, rows, cols, is_q8)}.
+    pattern: the sliding_window_pattern bools (True = sliding; default 5
+    sliding + 1 full); types: {name: (ggml type, raw array)} overrides, for
+    tensors stored in another type."""
+    if pattern is None:
+        pattern = [(i + 1) % 6 != 0 for i in range(n_layers)]
     meta = [("general.architecture", STR, "gemma-embedding2"),
             ("gemma-embedding2.block_count", U32, n_layers),
             ("gemma-embedding2.embedding_length", U32, hidden),
@@ -65,10 +70,13 @@ def model_gguf(path, tensors_by_name, n_layers, hidden, ffn, n_heads, n_kv_heads
             ("gemma-embedding2.rope.freq_base", F32, 1000000.0),
             ("gemma-embedding2.rope.freq_base_swa", F32, 10000.0),
             ("gemma-embedding2.attention.sliding_window_pattern", ARR,
-             (BOOL, [(i + 1) % 6 != 0 for i in range(n_layers)]))] + list(extra_meta)
+             (BOOL, [bool(p) for p in pattern]))] + list(extra_meta)
     tens = []
     for name, (arr, rows, cols, q8) in tensors_by_name.items():
+        gtype = GGML_Q8_0 if q8 else GGML_F32
+        if types and name in types:
+            gtype, arr = types[name]
         a = np.ascontiguousarray(arr)
-        tens.append((name, GGML_Q8_0 if q8 else GGML_F32, (cols, rows) if rows > 1 else (cols,),
+        tens.append((name, gtype, (cols, rows) if rows > 1 else (cols,),
                      a.view(np.uint8).tobytes()))
     return write_gguf(path, meta, tens)

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_symbols():
         assert hasattr(L, name), name
-    assert L.glypr_hip_abi_version() == 5
+    assert L.glypr_hip_abi_version() == 6
 
 
 def _has_gpu():
@@ -285,7 +285,7 @@ def test_gemm_routing():
 
 # ---- the model-config struct: C header, ctypes mirror and the Rust binding ----
 
-_C_FIELDS = re.compile(r"^\s*(int64_t|float|double)\s+(\w+);", re.M)
+_C_FIELDS = re.compile(r"^\s*(int64_t|float|double|const uint8_t\*)\s+(\w+);", re.M)
 
 
 def _header_struct_fields():
@@ -329,6 +329,7 @@ def test_integration_rust_struct_matches_header():
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     body = text[text.index("pub struct glypr_model_config {"):]
     body = body[len("pub struct glypr_model_config {"):body.index("}")]
-    rust = re.findall(r"pub\s+(\w+)\s*:\s*(\w+)", body)
-    rmap = {"int64_t": "i64", "float": "f32", "double": "f64"}
+    rust = [(n, " ".join(t.split())) for n, t in
+            re.findall(r"pub\s+(\w+)\s*:\s*(\*const\s+\w+|\w+)", body)]
+    rmap = {"int64_t": "i64", "float": "f32", "double": "f64", "const uint8_t*": "*const u8"}
     assert [(n, t) for n, t in rust] == [(n, rmap[t]) for t, n in _header_struct_fields()]

@@ -120,7 +120,8 @@ def test_attention_core_geometries(ctx, oracle, t, window, nq, nkv):
 QK_NORM_SCALE = np.float32(0.25)
 
 
-def make_model(ctx, oracle, n_layers, vocab, seed=0, ple_dim=0, out_dim=0, dense=False):
+def make_model(ctx, oracle, n_layers, vocab, seed=0, ple_dim=0, out_dim=0, dense=False,
+               layer_types=None):
     """The BASELINE backbone; ple_dim / out_dim > 0 add the real model's
     Per-Layer-Embedding path (ple.rs) and embedding projection (output.weight).
     dense: the layer projections are dense bf16 weights, the Q8_0 values rounded
@@ -167,18 +168,23 @@ def make_model(ctx, oracle, n_layers, vocab, seed=0, ple_dim=0, out_dim=0, dense
     if out_dim:
         tensors["output.weight"] = (oracle.q8_0_weight(out_dim, H, seed=rng_seed + 5, sigma=0.05),
                                     out_dim, H, True)
-    m = Model(ctx, n_layers=n_layers, vocab=vocab, ple_dim=ple_dim, out_dim=out_dim)
+    m = Model(ctx, n_layers=n_layers, vocab=vocab, ple_dim=ple_dim, out_dim=out_dim,
+              layer_types=layer_types)
     for name, (data, r, c, q8) in tensors.items():
         m.set_tensor(name, data, r, c, q8)
     m.finalize()
     return m, tensors
 
 
-def oracle_forward(oracle, tensors, n_layers, vocab, ids, trunc):
+def oracle_forward(oracle, tensors, n_layers, vocab, ids, trunc, layer_types=None):
     cfg = oracle.ModelConfig(hidden=768, ffn=1152, n_heads=3, n_kv_heads=1, head_dim=256,
                              n_layers=n_layers, vocab=vocab, sliding_window=512, eps=1e-6,
                              rope_theta_sliding=10000.0, rope_theta_full=1e6)
     keep = []
+    if layer_types is not None:
+        lt = np.ascontiguousarray(np.asarray(layer_types) != 0, dtype=np.uint8)
+        keep.append(lt)
+        cfg.layer_types = lt.ctypes.data
 
     def u8(name):
         a = np.ascontiguousarray(tensors[name][0], dtype=np.uint8)
@@ -638,6 +644,144 @@ def test_real_geometry_gguf_load(ctx, oracle, tmp_path):
     m.close()
 
 
+# ------------------------------- GGUF loader: the TextConfig / LinearOp rules --
+
+@pytest.mark.parametrize("pattern", [[0, 1, 0, 1], [1, 1, 0, 0, 0]])
+def test_gguf_sliding_window_pattern(ctx, oracle, tmp_path, pattern):
+    """TextConfig::from_gguf_metadata (config.rs:117-140) takes layer_types
+    from sliding_window_pattern (true = sliding): a file with a pattern other
+    than the default loads bit-identically to set_tensor with the same
+    layer_types, meets the oracle run with that pattern, and not the oracle
+    run with the default one (the full layers' RoPE table has theta 1e6).  A
+    pattern of non-booleans or shorter than block_count is refused."""
+    import gguf_util as gu
+    n_layers, vocab, t = len(pattern), 2000, 300
+    say(f"GGUF sliding_window_pattern, layer_types {pattern}")
+    m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=71, layer_types=pattern)
+    path = tmp_path / "pattern.gguf"
+    gu.model_gguf(path, tensors, n_layers, 768, 1152, 3, 1, 256,
+                  pattern=[not f for f in pattern])
+    g = Model.from_gguf(ctx, str(path))
+    ids = oracle.uniform_ids(t, seed=72, vocab=vocab)
+    a = host(m.embed(ids, trunc=256))
+    b = host(g.embed(ids, trunc=256))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    ref, _ = oracle_forward(oracle, tensors, n_layers, vocab, ids, 256, layer_types=pattern)
+    ref_default, _ = oracle_forward(oracle, tensors, n_layers, vocab, ids, 256)
+    c, c_default = _cos(a, ref), _cos(a, ref_default)
+    say(f"  cos vs oracle with the pattern {c:.8f}, with the default pattern {c_default:.8f}")
+    assert c >= 0.9999 and c_default < 0.9999
+    g.close()
+    m.close()
+    from glypr_amd._lib import GlyprError
+    bad = [("u8", gu.ARR, (gu.U8, [int(not f) for f in pattern]), _lib.GLYPR_ERR_UNSUPPORTED),
+           ("short", gu.ARR, (gu.BOOL, [True] * (n_layers - 1)), _lib.GLYPR_ERR_SHAPE)]
+    gu_tensors = [(name, gu.GGML_Q8_0 if q8 else gu.GGML_F32, (c, r) if r > 1 else (c,),
+                   np.ascontiguousarray(arr).view(np.uint8).tobytes())
+                  for name, (arr, r, c, q8) in tensors.items()]
+    for tag, vt, val, code in bad:
+        bad_path = tmp_path / f"bad_{tag}.gguf"
+        meta = _model_meta(gu, n_layers) + [
+            ("gemma-embedding2.attention.sliding_window_pattern", vt, val)]
+        gu.write_gguf(bad_path, meta, gu_tensors)
+        with pytest.raises(GlyprError) as e:
+            Model.from_gguf(ctx, str(bad_path))
+        assert e.value.code == code, (tag, e.value)
+
+
+def _model_meta(gu, n_layers):
+    """The BASELINE geometry's metadata without a sliding_window_pattern."""
+    return [("general.architecture", gu.STR, "gemma-embedding2"),
+            ("gemma-embedding2.block_count", gu.U32, n_layers),
+            ("gemma-embedding2.embedding_length", gu.U32, 768),
+            ("gemma-embedding2.feed_forward_length", gu.U32, 1152),
+            ("gemma-embedding2.attention.head_count", gu.U32, 3),
+            ("gemma-embedding2.attention.head_count_kv", gu.ARR, (gu.U32, [1] * n_layers)),
+            ("gemma-embedding2.attention.key_length_swa", gu.U32, 256),
+            ("gemma-embedding2.attention.key_length", gu.U32, 256),
+            ("gemma-embedding2.attention.layer_norm_rms_epsilon", gu.F32, 1e-6),
+            ("gemma-embedding2.rope.freq_base", gu.F32, 1000000.0),
+            ("gemma-embedding2.rope.freq_base_swa", gu.F32, 10000.0)]
+
+
+def test_gguf_dense_projections(ctx, oracle, tmp_path):
+    """LinearOp::from_gguf_tensor (linear.rs:48-54): layer projections stored
+    as BF16, F16 or F32 load into the dense arm, each value rounded to bf16
+    (nearest even): bit-identical to set_tensor with those bf16 patterns.  One
+    layer of each type, 6 layers."""
+    import gguf_util as gu
+    n_layers, vocab, t = 6, 2000, 300
+    say("GGUF dense projections: BF16, F16 and F32 tensors")
+    _, tensors = make_model(ctx, oracle, n_layers, vocab, seed=73, dense=True)
+    tensors = dict(tensors)
+    types = {}
+    kinds = [gu.GGML_BF16, gu.GGML_F16, gu.GGML_F32]
+    for i in range(n_layers):
+        kind = kinds[i % 3]
+        for nm in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"):
+            name = f"blk.{i}.{nm}.weight"
+            bits, r, c, _ = tensors[name]
+            vals = (bits.astype(np.uint32) << 16).view(np.float32)   # the bf16 values
+            if kind == gu.GGML_F16:
+                # stored as f16 of a perturbed value: the loader rounds f16 -> bf16
+                src = (vals * np.float32(1.0 + 2.0 ** -10)).astype(np.float16)
+                tensors[name] = (ops.f32_to_bf16_bits(src.astype(np.float32)), r, c, False)
+            elif kind == gu.GGML_F32:
+                src = vals * np.float32(1.0 + 2.0 ** -12)
+                tensors[name] = (ops.f32_to_bf16_bits(src), r, c, False)
+            else:
+                src = bits
+            types[name] = (kind, src)
+    m = Model(ctx, n_layers=n_layers, vocab=vocab)
+    for name, (data, r, c, q8) in tensors.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    path = tmp_path / "dense.gguf"
+    gu.model_gguf(path, tensors, n_layers, 768, 1152, 3, 1, 256, types=types)
+    g = Model.from_gguf(ctx, str(path))
+    ids = oracle.uniform_ids(t, seed=74, vocab=vocab)
+    a = host(m.embed(ids, trunc=256))
+    b = host(g.embed(ids, trunc=256))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    g.close()
+    m.close()
+
+
+def test_gguf_ple_dim_default(ctx, oracle, tmp_path):
+    """embedding_length_per_layer_input defaults to 512 (config.rs:100-102): a
+    released-geometry file with 512-wide PLE tensors and no such key loads
+    bit-identically to set_tensor with ple_dim 512."""
+    import gguf_util as gu
+    n_layers, vocab, t, P, D = 6, 2000, 200, 512, 768
+    say("GGUF without embedding_length_per_layer_input (PLE 512)")
+    raw, shaped = real_geometry_tensors(oracle, n_layers, vocab, P, D, seed=75)
+    m = Model(ctx, n_layers=n_layers, vocab=vocab, ple_dim=P, out_dim=D, **REAL)
+    for name, (data, r, c, q8) in shaped.items():
+        m.set_tensor(name, data, r, c, q8)
+    m.finalize()
+    meta = [("general.architecture", gu.STR, "gemma-embedding2"),
+            ("gemma-embedding2.block_count", gu.U32, n_layers),
+            ("gemma-embedding2.embedding_length", gu.U32, 512),
+            ("gemma-embedding2.feed_forward_length", gu.U32, 2048),
+            ("gemma-embedding2.attention.head_count", gu.U32, 4),
+            ("gemma-embedding2.attention.head_count_kv", gu.ARR,
+             (gu.U32, [1 if (i + 1) % 6 == 0 else 2 for i in range(n_layers)]))]
+    tens = []
+    for name, (a, rows, cols, q8) in shaped.items():
+        arr = np.ascontiguousarray(a)
+        tens.append((name, gu.GGML_Q8_0 if q8 else gu.GGML_F32,
+                     (cols, rows) if rows > 1 else (cols,), arr.view(np.uint8).tobytes()))
+    path = tmp_path / "ple512.gguf"
+    gu.write_gguf(path, meta, tens)
+    g = Model.from_gguf(ctx, str(path))
+    ids = oracle.uniform_ids(t, seed=76, vocab=vocab)
+    a = host(m.embed(ids, trunc=256))
+    b = host(g.embed(ids, trunc=256))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    g.close()
+    m.close()
+
+
 # ------------------------------------------------ several sequences at once --
 
 def _cos(a, b):
@@ -670,8 +814,14 @@ def test_embed_batch_vs_single_and_oracle(ctx, oracle, lens):
         # BASELINE's 0.9999 is a bar on pooled embeddings; a sequence of a few
         # tokens pools (almost) nothing, so it is held to the token-state bound
         # of test_model_forward_vs_oracle (the f16 attention operands' rounding
-        # reaches each token through the o projection's Q8_0 input)
-        assert c1 >= 0.99999 and c2 >= (0.9999 if lens[i] >= 64 else 0.999)
+        # reaches each token through the o projection's Q8_0 input).  A single
+        # sequence of up to 1024 tokens runs the single-launch attention, the
+        # batch the partitioned kernels: their probabilities are rounded to f16
+        # against different running maxima (~2^-12 each), which sequences of
+        # fewer than a few hundred tokens do not average out in the pooled mean
+        # (64 tokens: 1.2e-5 of cosine apart, each 2e-5 from the oracle)
+        assert c1 >= (0.99999 if lens[i] >= 256 else 0.9999)
+        assert c2 >= (0.9999 if lens[i] >= 64 else 0.999)
         assert abs(np.linalg.norm(got[i].astype(np.float64)) - 1) < 1e-5
     # a batch of one is the single-sequence embedding
     one = host(m.embed_batch([seqs[2]], trunc=256))

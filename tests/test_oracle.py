@@ -409,7 +409,7 @@ def test_rope_tables_closed_form(oracle, hd, theta):
 # -------------------------------------------------------- whole forward ----
 
 def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, window, eps=1e-6,
-                 full_hd=0, full_nkv=0):
+                 full_hd=0, full_nkv=0, layer_types=None):
     """Independent float64 statement of forward_embeds (model.rs:498-578) over the
     layer order of layer.rs:20-50: the same Q8_0 quantization of every GEMM input
     (oracle quantizer, pinned above), everything else in float64.  With
@@ -419,7 +419,8 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
     given as a uint16 [n, k] array is a dense bf16 weight (linear.rs:48-54): its
     exact values, and no quantization of its input.  full_hd / full_nkv (0: the
     sliding values) give the full-attention layers their own head_dim and kv
-    head count (config.rs:142-169)."""
+    head count (config.rs:142-169); layer_types (nonzero = full) replaces the
+    default 5 sliding + 1 full pattern (config.rs:117-140)."""
     def deq(name, n, k):
         w = tensors[name]
         if w.dtype == np.uint16:
@@ -459,7 +460,7 @@ def _forward_f64(oracle, tensors, ids, trunc, H, F, nh, nkv, hd, n_layers, windo
     sliding_hd, sliding_nkv = hd, nkv
     for l in range(n_layers):
         p = f"blk.{l}."
-        full = (l + 1) % 6 == 0
+        full = bool(layer_types[l]) if layer_types is not None else (l + 1) % 6 == 0
         hd = (full_hd or sliding_hd) if full else sliding_hd
         nkv = (full_nkv or sliding_nkv) if full else sliding_nkv
         theta = 1e6 if full else 1e4
@@ -569,6 +570,29 @@ def test_model_forward_with_ple_vs_float64_statement(oracle):
     no_out = {k: v for k, v in tensors.items() if k != "output.weight"}
     _, s4 = oracle.model_forward(no_out, ids, 32, **kw)
     assert float(o2 @ out) < 0.9999 and float(o3 @ out) < 0.9999 and s4.shape == (t, H)
+
+
+def test_model_forward_layer_types_vs_float64_statement(oracle):
+    """A layer_types pattern other than the default (full layers first, third
+    and sixth; sliding_window_pattern, config.rs:117-140): the oracle against
+    the float64 statement with the same pattern, and far from the statement
+    with the default pattern (a full layer takes no band and the 1e6 RoPE
+    table), so an ignored pattern fails."""
+    H, F, nh, nkv, hd, L, vocab, t, W = 128, 192, 2, 1, 64, 6, 1000, 40, 8
+    rng = np.random.default_rng(13)
+    tensors = _small_model(oracle, H, F, nh, nkv, hd, L, vocab, rng)
+    ids = rng.integers(0, vocab, t).astype(np.uint32)
+    pattern = [1, 0, 1, 0, 0, 1]
+    out, states = oracle.model_forward(tensors, ids, 32, hidden=H, ffn=F, n_heads=nh,
+                                       n_kv_heads=nkv, head_dim=hd, n_layers=L, vocab=vocab,
+                                       sliding_window=W, layer_types=pattern)
+    ref_out, ref_states = _forward_f64(oracle, tensors, ids, 32, H, F, nh, nkv, hd, L, W,
+                                       layer_types=pattern)
+    dflt_out, _ = _forward_f64(oracle, tensors, ids, 32, H, F, nh, nkv, hd, L, W)
+    row_cos = (states * ref_states).sum(1) / np.linalg.norm(states, axis=1) / \
+        np.linalg.norm(ref_states, axis=1)
+    assert row_cos.min() > 0.9995 and float(out @ ref_out) > 0.99999
+    assert float(out @ dflt_out) < 0.999
 
 
 def test_model_forward_vs_float64_statement(oracle):
