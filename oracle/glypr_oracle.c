@@ -331,6 +331,14 @@ float orc_geglu_scalar_libm(float g, float u) {
   return act * u;
 }
 
+/* orc_geglu with the platform tanhf: glypr's CPU numerics where libm's tanhf
+ * is glibc's (the reference's Rust f32::tanh). */
+void orc_geglu_libm(const float* gate, const float* up, float* out, int64_t n, int threads) {
+  int nt = orc_threads(threads);
+#pragma omp parallel for num_threads(nt) schedule(static, 1024)
+  for (int64_t i = 0; i < n; i++) out[i] = orc_geglu_scalar_libm(gate[i], up[i]);
+}
+
 /* CpuGeGLUOp::cpu_fwd (cpu_simd/geglu.rs:27-113): chunks of 1024 in parallel. */
 void orc_geglu(const float* gate, const float* up, float* out, int64_t n, int threads) {
   int nt = orc_threads(threads);

@@ -102,6 +102,7 @@ float orc_geglu_scalar(float g, float u);
 void orc_geglu(const float* gate, const float* up, float* out, int64_t n, int threads);
 /* Same with the platform libm tanhf (glibc), for the tanh-substitution study. */
 float orc_geglu_scalar_libm(float g, float u);
+void orc_geglu_libm(const float* gate, const float* up, float* out, int64_t n, int threads);
 
 /* ---- Token embedding gather (model.rs:252-255, 507-508) ---- */
 /* out[t,:] = dequant(table[ids[t],:]) * scale.  Returns 0, or -1 if an id >= vocab. */

@@ -82,6 +82,7 @@ def lib():
             "orc_tanhf": (ctypes.c_float, [ctypes.c_float]),
             "orc_geglu_scalar": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
             "orc_geglu_scalar_libm": (ctypes.c_float, [ctypes.c_float, ctypes.c_float]),
+            "orc_geglu_libm": (None, [_f32p, _f32p, _f32p, _i64, ctypes.c_int]),
             "orc_geglu": (None, [_f32p, _f32p, _f32p, _i64, ctypes.c_int]),
             "orc_embed_gather": (ctypes.c_int, [_u8p, _i64, _i64, _u32p, _i64, ctypes.c_float,
                                                 _f32p]),
@@ -239,6 +240,16 @@ def geglu(gate: np.ndarray, up: np.ndarray, threads: int = 0) -> np.ndarray:
     assert g.shape == u.shape
     out = np.empty_like(g)
     lib().orc_geglu(_p(g, _f32p), _p(u, _f32p), _p(out, _f32p), g.size, threads)
+    return out
+
+
+def geglu_libm(gate: np.ndarray, up: np.ndarray, threads: int = 0) -> np.ndarray:
+    """geglu with the platform tanhf (glypr's own CPU numerics on glibc)."""
+    g = np.ascontiguousarray(gate, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float32)
+    assert g.shape == u.shape
+    out = np.empty_like(g)
+    lib().orc_geglu_libm(_p(g, _f32p), _p(u, _f32p), _p(out, _f32p), g.size, threads)
     return out
 
 

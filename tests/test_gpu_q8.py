@@ -555,3 +555,70 @@ def test_c3_bf16_dequant_qkv_and_mlp(ctx, oracle):
     c8 = (z[rows] * z8).sum(1) / np.linalg.norm(z[rows], axis=1) / np.linalg.norm(z8, axis=1)
     say(f"  mlp cosine to the INT8_EXACT oracle: min {c8.min():.7f} mean {c8.mean():.7f}")
     assert c8.min() > 0.998
+
+
+# ------------------------------------- against glypr's platform-tanh numerics --
+# glypr's CPU GeGLU calls the platform tanhf (cpu_simd/geglu.rs:6-18).  This
+# library and its oracle share their own tanh instead, a few ulp from glibc's
+# (test_geglu_tanh_substitution_is_ulp_level).  Where such an ulp moves an h
+# value across a rounding boundary of its Q8_0 block, one int8 of the down
+# projection's input changes by 1: these tests hold the GPU path to an oracle
+# built on glibc's tanhf (geglu_libm), at BASELINE's tolerance, and report how
+# many bytes of Q8_0(h) the substitution changed.
+
+def _mlp_ref_libm(oracle, xn, gb, ub, db, H, F):
+    gate, up = oracle.matmul(xn, gb, F), oracle.matmul(xn, ub, F)
+    h_ours, h_libm = oracle.geglu(gate, up), oracle.geglu_libm(gate, up)
+    flips = int(np.count_nonzero(oracle.quantize_rows(h_ours) != oracle.quantize_rows(h_libm)))
+    return oracle.matmul(h_libm, db, H), flips
+
+
+@pytest.mark.parametrize("m", [512, C3_M])
+def test_mlp_vs_platform_tanh(ctx, oracle, m):
+    """The INT8_EXACT RMSNorm -> gate/up GeGLU -> down MLP at C2's M = 512 (every
+    row) and C3's M = 16384 (256 sampled rows) against the glibc-tanhf oracle."""
+    H, F = 768, 1152
+    say(f"INT8_EXACT rmsnorm_mlp m={m} vs the platform-tanh oracle")
+    x = oracle.normal(m * H, seed=611).reshape(m, H)
+    nw = 1 + 0.1 * oracle.normal(H, seed=612)
+    gb, ub, db = (oracle.q8_0_weight(F, H, seed=613), oracle.q8_0_weight(F, H, seed=614),
+                  oracle.q8_0_weight(H, F, seed=615))
+    g, u = Q8Weight.from_gguf(ctx, gb, F, H), Q8Weight.from_gguf(ctx, ub, F, H)
+    d = Q8Weight.from_gguf(ctx, db, H, F)
+    gu, _ = Q8Weight.concat(ctx, [g, u])
+    y = host(ops.rmsnorm_mlp(ctx, gu, d, dev(x), dev(nw), 1e-6, INT8_EXACT))
+    rows = np.arange(m) if m <= 512 else np.sort(np.random.default_rng(7).choice(m, 256, False))
+    ref, flips = _mlp_ref_libm(oracle, oracle.rmsnorm(x[rows], nw, 1e-6), gb, ub, db, H, F)
+    err = np.abs(y[rows].astype(np.float64) - ref)
+    rel = err / np.maximum(np.abs(ref), 1e-4)
+    say(f"  bytes of Q8_0(h) changed by the tanh substitution: {flips} of {len(rows) * F}; "
+        f"max |d| {err.max():.3g}, max relative (1e-4 floor) {rel.max():.3g}")
+    baseline_tolerance(y[rows], ref.astype(np.float64))
+
+
+def test_c2_layer_vs_platform_tanh(ctx, oracle):
+    """C2, one layer's seven projections at T = 512 (RMSNorm -> q|k|v, o,
+    RMSNorm -> gate/up GeGLU -> down), against the glibc-tanhf oracle: the
+    projections without a GeGLU stay bit-exact, the MLP meets BASELINE's
+    tolerance."""
+    m, H, F = 512, 768, 1152
+    say("C2 layer projections vs the platform-tanh oracle")
+    x = oracle.normal(m * H, seed=621).reshape(m, H)
+    ctxv = oracle.normal(m * H, seed=622).reshape(m, H)
+    n1, n2 = 1 + 0.1 * oracle.normal(H, seed=623), 1 + 0.1 * oracle.normal(H, seed=624)
+    qkvb = oracle.q8_0_weight(1280, H, seed=625)
+    ob = oracle.q8_0_weight(H, H, seed=626)
+    gb, ub, db = (oracle.q8_0_weight(F, H, seed=627), oracle.q8_0_weight(F, H, seed=628),
+                  oracle.q8_0_weight(H, F, seed=629))
+    wqkv, wo = Q8Weight.from_gguf(ctx, qkvb, 1280, H), Q8Weight.from_gguf(ctx, ob, H, H)
+    g, u = Q8Weight.from_gguf(ctx, gb, F, H), Q8Weight.from_gguf(ctx, ub, F, H)
+    d = Q8Weight.from_gguf(ctx, db, H, F)
+    gu, _ = Q8Weight.concat(ctx, [g, u])
+    qkv = host(ops.rmsnorm_q8_0_matmul(ctx, wqkv, dev(x), dev(n1), 1e-6, INT8_EXACT))
+    o = host(ops.q8_0_matmul(ctx, wo, dev(ctxv), INT8_EXACT))
+    y = host(ops.rmsnorm_mlp(ctx, gu, d, dev(x), dev(n2), 1e-6, INT8_EXACT))
+    assert_bits_equal(qkv, oracle.matmul(oracle.rmsnorm(x, n1, 1e-6), qkvb, 1280), "qkv")
+    assert_bits_equal(o, oracle.matmul(ctxv, ob, H), "o")
+    ref, flips = _mlp_ref_libm(oracle, oracle.rmsnorm(x, n2, 1e-6), gb, ub, db, H, F)
+    say(f"  bytes of Q8_0(h) changed by the tanh substitution: {flips} of {m * F}")
+    baseline_tolerance(y, ref.astype(np.float64))

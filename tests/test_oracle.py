@@ -245,6 +245,8 @@ def test_geglu_tanh_substitution_is_ulp_level(oracle):
     ours = oracle.geglu(g, u)
     libm = np.array([oracle.lib().orc_geglu_scalar_libm(float(a), float(b))
                      for a, b in zip(g, u)], np.float32)
+    # the array form runs the same scalar function on every element
+    assert np.array_equal(oracle.geglu_libm(g, u).view(np.uint32), libm.view(np.uint32))
     diff = np.abs(ours.astype(np.float64) - libm)
     assert np.all(diff <= 0.5 * np.abs(g * u) * 4 * 2.0 ** -24 + 4e-6 * np.abs(libm))
     ok = g > -1
@@ -712,6 +714,7 @@ PINS = {
     "orc_geglu_scalar": ["test_geglu_kat_and_formula"],
     "orc_geglu": ["test_geglu_kat_and_formula"],
     "orc_geglu_scalar_libm": ["test_geglu_tanh_substitution_is_ulp_level"],
+    "orc_geglu_libm": ["test_geglu_tanh_substitution_is_ulp_level"],
     "orc_embed_gather": ["test_gather_equals_dequant_rows"],
     "orc_pool_normalize": ["test_pool_kat", "test_pool_long_context_vs_f64"],
     "orc_l2_normalize": ["test_l2_normalize_kat_and_sequential_sum"],
