@@ -9,8 +9,9 @@ A step is one embedding (glypr_hip_model_embed); value = embeddings/s.
 
 Also reported (in "extra"): C2 (one layer's 7 projections at T = 512, the
 previous headline, with its own roofline), C1 (one 512 x 768 x 1152 linear),
-C3 (M = 16384 through the 7 projections, TOPS and % of MFMA peak, both
-variants, BF16_DEQUANT's per-row cosine to INT8_EXACT), C5 (T = 8192, Q8_0 and
+C3 (M = 16384 through the 7 projections, TOPS and % of MFMA peak, all three
+variants, BF16_DEQUANT's per-row cosine and INT8_FMA's error relative to
+BASELINE's tolerance, both against INT8_EXACT), C5 (T = 8192, Q8_0 and
 bf16 weights, GEMM vs attention split), the Q8_0 gather on its own at 1M ids,
 the output-vector codecs, and hipBLASLt on the C3 shapes for reference.
 
@@ -818,7 +819,7 @@ def main():
 
     import torch
     from glypr_amd import ops
-    from glypr_amd.ops import BF16_DEQUANT, INT8_EXACT
+    from glypr_amd.ops import BF16_DEQUANT, INT8_EXACT, INT8_FMA
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     variant = INT8_EXACT if args.variant == "int8" else BF16_DEQUANT
@@ -861,11 +862,11 @@ def main():
     if "c3" in todo:
         import torch
         keep = {}
-        for vname, v in (("int8", INT8_EXACT), ("bf16", BF16_DEQUANT)):
+        for vname, v in (("int8", INT8_EXACT), ("bf16", BF16_DEQUANT), ("int8_fma", INT8_FMA)):
             Lx, msx, kx = run_workload(ctx, 16384, v, max(50, args.steps), max(3, args.warmup),
                                        prewarm_s=0.5)
             t = Lx.ops_per_step() / (msx / 1e3) / 1e12
-            pk = INT8_PEAK_TOPS if v == INT8_EXACT else BF16_PEAK_TFLOPS
+            pk = BF16_PEAK_TFLOPS if v == BF16_DEQUANT else INT8_PEAK_TOPS
             extra[f"c3_{vname}"] = {
                 "tops": round(t, 2), "ms_per_step": round(msx, 4),
                 "pct_mfma_peak": round(100 * t / pk, 2),
@@ -885,6 +886,18 @@ def main():
             c = (a * b).sum(1) / a.norm(dim=1) / b.norm(dim=1)
             cos[out_name[2:]] = {"min": round(float(c.min()), 7), "mean": round(float(c.mean()), 7)}
         extra["c3_bf16"]["cosine_to_int8_exact_per_row"] = cos
+        # INT8_FMA against INT8_EXACT on the same inputs: BASELINE's 1e-3 relative
+        # error (1e-4 absolute floor), and how many outputs differ at all
+        dif = {}
+        for out_name in ("y_qkv", "y_o", "y_mlp"):
+            a = getattr(keep["int8_fma"], out_name)
+            b = getattr(keep["int8"], out_name)
+            err = (a.double() - b.double()).abs()
+            lim = torch.clamp(1e-3 * b.double().abs(), min=1e-4)
+            dif[out_name[2:]] = {"max_err_over_tolerance": round(float((err / lim).max()), 5),
+                                 "frac_outputs_differing": round(float((a != b).double().mean()),
+                                                                 4)}
+        extra["c3_int8_fma"]["vs_int8_exact"] = dif
         del keep
         torch.cuda.synchronize()
     if "vendor" in todo:
@@ -895,7 +908,8 @@ def main():
     if "c3" in todo:
         # the same C3 step's GEMM launches only (no norm / quantize launches)
         for vname, gk, geglu in (("int8", "gemm_i8", "gemm_i8_geglu"),
-                                 ("bf16", "gemm_bf16", "gemm_bf16_geglu")):
+                                 ("bf16", "gemm_bf16", "gemm_bf16_geglu"),
+                                 ("int8_fma", "gemm_i8", "gemm_i8_geglu")):
             ku = extra[f"c3_{vname}"]["kernels_us"]
             if gk in ku and geglu in ku:
                 us = 3 * ku[gk] + ku[geglu]

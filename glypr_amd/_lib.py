@@ -24,6 +24,7 @@ GLYPR_ERR_NOT_FOUND = 9
 
 INT8_EXACT = 0
 BF16_DEQUANT = 1
+INT8_FMA = 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64

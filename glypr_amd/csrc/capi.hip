@@ -42,7 +42,7 @@ namespace {
 // Workspace bytes matmul_impl needs for [m, k] activations in `variant`
 // (0 when the prologue-fused GEMM runs and needs none).
 size_t matmul_ws_bytes(int64_t m, int64_t n, int64_t k, bool norm, int variant) {
-  if (variant == GLYPR_Q8_INT8_EXACT)
+  if (variant != GLYPR_Q8_BF16_DEQUANT)
     return gemm_i8_pro_ok(m, n, k, norm) ? 0 : q8_act_bytes(m, k);
   return align_up((size_t)(m * k) * 2, 256);
 }
@@ -53,10 +53,11 @@ int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const fl
                 float eps, bool norm, float* y, int64_t m, int variant, void* ws,
                 hipStream_t s) {
   const int64_t n = w->n, k = w->k;
-  if (variant == GLYPR_Q8_INT8_EXACT) {
+  if (variant != GLYPR_Q8_BF16_DEQUANT) {
+    const bool fma2 = variant == GLYPR_Q8_INT8_FMA;
     if (gemm_i8_pro_ok(m, n, k, norm)) {
       LAUNCH(GLYPR_K_GEMM_I8_PRO, s,
-             launch_gemm_i8_pro(x, norm_w, eps, norm, w->qs(), w->dw(), y, m, n, k, n, s),
+             launch_gemm_i8_pro(x, norm_w, eps, norm, w->qs(), w->dw(), y, m, n, k, n, s, fma2),
              "gemm_i8_pro launch");
       return GLYPR_OK;
     }
@@ -68,7 +69,7 @@ int matmul_impl(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x, const fl
              "rmsnorm_quant launch");
     else
       LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(x, m, k, xq, dx, s), "quantize launch");
-    LAUNCH(GLYPR_K_GEMM_I8, s, launch_gemm_i8(xq, dx, w->qs(), w->dw(), y, m, n, k, n, s),
+    LAUNCH(GLYPR_K_GEMM_I8, s, launch_gemm_i8(xq, dx, w->qs(), w->dw(), y, m, n, k, n, s, fma2),
            "gemm_i8 launch");
     return GLYPR_OK;
   }
@@ -96,7 +97,8 @@ int mlp_impl(glypr_hip_ctx* ctx, const glypr_q8w* gu, const glypr_q8w* down, con
              const float* norm_w, float eps, bool norm, float* y, int64_t m, int variant,
              hipStream_t s) {
   const int64_t H = gu->k, F = down->k;
-  if (variant == GLYPR_Q8_INT8_EXACT) {
+  if (variant != GLYPR_Q8_BF16_DEQUANT) {
+    const bool fma2 = variant == GLYPR_Q8_INT8_FMA;
     RET_IF(ensure_ws(ctx, q8_act_bytes(m, H) + q8_act_bytes(m, F)));
     Carve c(ctx->ws);
     int8_t* xq = c.take<int8_t>((size_t)(m * H));
@@ -109,9 +111,10 @@ int mlp_impl(glypr_hip_ctx* ctx, const glypr_q8w* gu, const glypr_q8w* down, con
     else
       LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(x, m, H, xq, dx, s), "quantize launch");
     LAUNCH(GLYPR_K_GEMM_I8_GEGLU, s,
-           launch_gemm_i8_geglu(xq, dx, gu->qs(), gu->dw(), hq, dh, m, F, H, s),
+           launch_gemm_i8_geglu(xq, dx, gu->qs(), gu->dw(), hq, dh, m, F, H, s, fma2),
            "gate/up GeGLU launch");
-    LAUNCH(GLYPR_K_GEMM_I8, s, launch_gemm_i8(hq, dh, down->qs(), down->dw(), y, m, H, F, H, s),
+    LAUNCH(GLYPR_K_GEMM_I8, s,
+           launch_gemm_i8(hq, dh, down->qs(), down->dw(), y, m, H, F, H, s, fma2),
            "down launch");
     return GLYPR_OK;
   }

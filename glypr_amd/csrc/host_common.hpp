@@ -132,7 +132,8 @@ inline int check_weight_device(const glypr_hip_ctx* ctx, const glypr_q8w* w, con
 }
 
 inline int check_variant(int variant) {
-  GLYPR_CHECK(variant == GLYPR_Q8_INT8_EXACT || variant == GLYPR_Q8_BF16_DEQUANT,
+  GLYPR_CHECK(variant == GLYPR_Q8_INT8_EXACT || variant == GLYPR_Q8_BF16_DEQUANT ||
+                  variant == GLYPR_Q8_INT8_FMA,
               GLYPR_ERR_UNSUPPORTED, "unknown Q8_0 variant %d", variant);
   return GLYPR_OK;
 }

@@ -207,14 +207,16 @@ hipError_t launch_attention(const uint16_t* q16, const uint16_t* k16, const uint
 enum { GEMM_ROUTE_SMALL = 0, GEMM_ROUTE_BIG = 1, GEMM_ROUTE_REG128 = 2, GEMM_ROUTE_REG64 = 3 };
 int gemm_i8_route(int64_t M, int64_t Nrows, int64_t K);
 // y[m,n] = sum_b ((float)S_b * dw[n,b]) * dx[m,b], sequential over b (exact).
+// fma2 (GLYPR_Q8_INT8_FMA): each block's term is added as
+// fma(round(S_b * dw[n,b]), dx[m,b], acc), one rounding fewer per block.
 hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                           float* y, int64_t M, int64_t N, int64_t K, int64_t ldc,
-                          hipStream_t s);
+                          hipStream_t s, bool fma2 = false);
 // Gate/up GEMM ([gate; up] rows, 2F x K) with GeGLU + Q8_0 quantization epilogue:
 // hq int8 [M][F], dh f32 [M][F/32].
 hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t* wq,
                                 const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
-                                int64_t K, hipStream_t s);
+                                int64_t K, hipStream_t s, bool fma2 = false);
 
 // The q|k|v projection (INT8_EXACT, Q8_0 activations) with qkv_post's work
 // as its epilogue: writes the attention operands q / k / vt (f16, rows padded
@@ -236,7 +238,7 @@ hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* w
 bool gemm_i8_pro_ok(int64_t M, int64_t N, int64_t K, bool norm);
 hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
                               const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
-                              int64_t K, int64_t ldc, hipStream_t s);
+                              int64_t K, int64_t ldc, hipStream_t s, bool fma2 = false);
 
 // ---- k_gemm_bf16.hip, dense bf16 weights ----
 // y = xb . wb^T (xb bf16 [M][K], wb bf16 [N][K]), f32 out; the GeGLU form takes

@@ -34,7 +34,21 @@ constexpr int KB = BK / QK;    // Q8_0 blocks per stage
 constexpr int MAGIC = 0x4B400000;
 constexpr float NEG_MAGIC = -12582912.0f;  // -(1.5 * 2^23)
 
-template <int BM, int BN, int WM, int WN, bool GEGLU>
+// One Q8_0 block's term added to an output.  `sb` is the MFMA accumulator
+// word MAGIC + S (S the block's integer dot product), wc = wd * NEG_MAGIC, so
+// the first FMA is round(S * d_w) exactly.  EXACT (F2 = false) then rounds
+// the product by d_x and the sum separately, the reference's vec_dot order;
+// F2 fuses the last two into one FMA (GLYPR_Q8_INT8_FMA: 2 VALU ops per
+// output and block instead of 3, one rounding fewer).
+template <bool F2>
+__device__ __forceinline__ float q8_term(float acc, int sb, float wd, float wc, float xd) {
+  const float t = fmaf(__int_as_float(sb), wd, wc);  // round(S * d_w)
+  if constexpr (F2) return fmaf(t, xd, acc);         // round(acc + . * d_x)
+  const float u = t * xd;                            // round(. * d_x)
+  return acc + u;                                    // round(acc + .)
+}
+
+template <int BM, int BN, int WM, int WN, bool GEGLU, bool F2>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
                const int8_t* __restrict__ B, const float* __restrict__ dB,
@@ -201,11 +215,9 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
           for (int tn = 0; tn < TN; tn++) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-              float t = fmaf(__int_as_float(d[tm][tn][r]), wd[tn], wc[tn]);  // round(S * d_w)
-              float u = t * xd[r >> 2][r & 3];                               // round(. * d_x)
-              acc[tm][tn][r] = acc[tm][tn][r] + u;                           // round(acc + .)
-            }
+            for (int r = 0; r < 16; r++)
+              acc[tm][tn][r] =
+                  q8_term<F2>(acc[tm][tn][r], d[tm][tn][r], wd[tn], wc[tn], xd[r >> 2][r & 3]);
           }
         }
       }
@@ -312,7 +324,7 @@ constexpr int SMALL_NB_MAX = 64;   // K <= 2048
 // a stage are 16 contiguous bytes of a row: per stage a lane reads its four
 // row scales and its TNW column scales with 4 + TNW ds_read_b128.  The stage
 // loop is unrolled by RING so ring slots are compile-time LDS offsets.
-template <int WM, int WN, int TNW, bool GEGLU, int RING, int NB>
+template <int WM, int WN, int TNW, bool GEGLU, bool F2, int RING, int NB>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
                      const int8_t* __restrict__ B, const float* __restrict__ dB,
@@ -453,11 +465,8 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
             const float wd = wq[t][kb];
             const float wc = wd * NEG_MAGIC;
 #pragma unroll
-            for (int rr = 0; rr < 4; rr++) {
-              float tt = fmaf(__int_as_float(d[kb][t][rr]), wd, wc);  // round(S * d_w)
-              float u = tt * xq[rr][kb];                              // round(. * d_x)
-              acc[t][rr] = acc[t][rr] + u;                            // round(acc + .)
-            }
+            for (int rr = 0; rr < 4; rr++)
+              acc[t][rr] = q8_term<F2>(acc[t][rr], d[kb][t][rr], wd, wc, xq[rr][kb]);
           }
       }
     }
@@ -503,13 +512,13 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   }
 }
 
-template <int WM, int WN, int TNW, bool GEGLU, int RING, int NB>
+template <int WM, int WN, int TNW, bool GEGLU, bool F2, int RING, int NB>
 hipError_t run_small_nb(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                         float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t ldc,
                         int64_t F, hipStream_t s) {
   constexpr int BM = WM * 16, BN = WN * 16 * TNW;
   dim3 grid((unsigned)((Nrows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  gemm_i8_small_kernel<WM, WN, TNW, GEGLU, RING, NB><<<grid, WM * WN * 64, 0, s>>>(
+  gemm_i8_small_kernel<WM, WN, TNW, GEGLU, F2, RING, NB><<<grid, WM * WN * 64, 0, s>>>(
       xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)ldc, (int)F);
   return hipGetLastError();
 }
@@ -517,14 +526,14 @@ hipError_t run_small_nb(const int8_t* xq, const float* dx, const int8_t* wq, con
 // K is a multiple of 128 and <= 2048 (small_ok): the BASELINE widths (768,
 // 1152) and the released EmbeddingGemma-2's (512; 2048 for its down and
 // full-layer o projections).
-template <int WM, int WN, int TNW, bool GEGLU, int RING>
+template <int WM, int WN, int TNW, bool GEGLU, bool F2, int RING>
 hipError_t run_small(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                      float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K,
                      int64_t ldc, int64_t F, hipStream_t s) {
 #define GLYPR_SMALL_NB(nb)                                                                 \
   case nb:                                                                                 \
-    return run_small_nb<WM, WN, TNW, GEGLU, RING, nb>(xq, dx, wq, dw, y, hq, dh, M, Nrows, \
-                                                      ldc, F, s);
+    return run_small_nb<WM, WN, TNW, GEGLU, F2, RING, nb>(xq, dx, wq, dw, y, hq, dh, M,     \
+                                                          Nrows, ldc, F, s);
   switch (K / QK) {
     GLYPR_SMALL_NB(4)
     GLYPR_SMALL_NB(8)
@@ -582,7 +591,7 @@ inline bool small_ok(int64_t M, int64_t Nrows, int64_t K) {
 // ---------------------------------------------------------------------------
 enum { PRO_QUANT = 1, PRO_NORM = 2 };
 
-template <int PRO, int WN, int TNW, int RING, int NB>
+template <int PRO, bool F2, int WN, int TNW, int RING, int NB>
 __global__ void __launch_bounds__(WN * 64)
 gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, float eps,
                    const int8_t* __restrict__ B, const float* __restrict__ dB,
@@ -773,11 +782,8 @@ gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, fl
             const float wd = wq[t][kb];
             const float wc = wd * NEG_MAGIC;
 #pragma unroll
-            for (int rr = 0; rr < 4; rr++) {
-              float tt = fmaf(__int_as_float(d[kb][t][rr]), wd, wc);  // round(S * d_w)
-              float u = tt * xq[rr][kb];                              // round(. * d_x)
-              acc[t][rr] = acc[t][rr] + u;                            // round(acc + .)
-            }
+            for (int rr = 0; rr < 4; rr++)
+              acc[t][rr] = q8_term<F2>(acc[t][rr], d[kb][t][rr], wd, wc, xq[rr][kb]);
           }
       }
     }
@@ -794,7 +800,7 @@ gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, fl
   }
 }
 
-template <int PRO, int WN, int TNW, int RING>
+template <int PRO, bool F2, int WN, int TNW, int RING>
 hipError_t run_pro(const float* x, const float* nw, float eps, const int8_t* wq, const float* dw,
                    float* y, int64_t M, int64_t N, int64_t K, int64_t ldc, hipStream_t s) {
   constexpr int BN = WN * 16 * TNW;
@@ -804,7 +810,7 @@ hipError_t run_pro(const float* x, const float* nw, float eps, const int8_t* wq,
   const int nmajor = 4 * M * 8 < 9 * N ? 1 : 0;
 #define GLYPR_PRO_NB(nb)                                                                  \
   case nb:                                                                                \
-    gemm_i8_pro_kernel<PRO, WN, TNW, RING, nb><<<grid, WN * 64, 0, s>>>(                  \
+    gemm_i8_pro_kernel<PRO, F2, WN, TNW, RING, nb><<<grid, WN * 64, 0, s>>>(              \
         x, nw, eps, wq, dw, y, (int)M, (int)N, (int)ldc, nmajor);                         \
     break;
   switch (K / QK) {
@@ -854,7 +860,7 @@ constexpr int BIG_BM = 128, BIG_BN = 128;
 
 __device__ __forceinline__ int big_swz(int row) { return (row >> 1) & 7; }
 
-template <bool GEGLU>
+template <bool GEGLU, bool F2>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_i8_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
                    const int8_t* __restrict__ B, const float* __restrict__ dB,
@@ -971,11 +977,8 @@ gemm_i8_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
         const float wc = wd * NEG_MAGIC;
         const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, magic, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          float t = fmaf(__int_as_float(d[r]), wd, wc);   // round(S * d_w)
-          float u = t * xv[r >> 2][r & 3];                 // round(. * d_x)
-          acc[tn][r] = acc[tn][r] + u;                     // round(acc + .)
-        }
+        for (int r = 0; r < 16; r++)
+          acc[tn][r] = q8_term<F2>(acc[tn][r], d[r], wd, wc, xv[r >> 2][r & 3]);
       }
     }
   };
@@ -1047,13 +1050,13 @@ gemm_i8_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   }
 }
 
-template <bool GEGLU>
+template <bool GEGLU, bool F2>
 hipError_t run_big(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                    float* y, int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K,
                    int64_t ldc, int64_t F, hipStream_t s) {
   const int64_t tiles_n = (Nrows + BIG_BN - 1) / BIG_BN;
   const int64_t tiles = ((M + BIG_BM - 1) / BIG_BM) * tiles_n;
-  gemm_i8_big_kernel<GEGLU><<<dim3((unsigned)tiles), 256, 0, s>>>(
+  gemm_i8_big_kernel<GEGLU, F2><<<dim3((unsigned)tiles), 256, 0, s>>>(
       xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F, (int)tiles_n);
   return hipGetLastError();
 }
@@ -1063,12 +1066,12 @@ inline bool big_ok(int64_t M, int64_t Nrows, int64_t K) {
   return K % BK == 0 && M * K < (int64_t(1) << 31) && Nrows * K < (int64_t(1) << 31);
 }
 
-template <int BM, int BN, int WM, int WN, bool GEGLU>
+template <int BM, int BN, int WM, int WN, bool GEGLU, bool F2>
 hipError_t run(const int8_t* xq,const float* dx, const int8_t* wq, const float* dw, float* y,
                int8_t* hq, float* dh, int64_t M, int64_t Nrows, int64_t K, int64_t ldc,
                int64_t F, hipStream_t s) {
   dim3 grid((unsigned)((Nrows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  gemm_i8_kernel<BM, BN, WM, WN, GEGLU><<<grid, WM * WN * 64, 0, s>>>(
+  gemm_i8_kernel<BM, BN, WM, WN, GEGLU, F2><<<grid, WM * WN * 64, 0, s>>>(
       xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)K, (int)ldc, (int)F);
   return hipGetLastError();
 }
@@ -1228,11 +1231,8 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
             const float wd = wq[t][kb];
             const float wc = wd * NEG_MAGIC;
 #pragma unroll
-            for (int rr = 0; rr < 4; rr++) {
-              float tt = fmaf(__int_as_float(d[kb][t][rr]), wd, wc);  // round(S * d_w)
-              float u = tt * xq[rr][kb];                              // round(. * d_x)
-              acc[t][rr] = acc[t][rr] + u;                            // round(acc + .)
-            }
+            for (int rr = 0; rr < 4; rr++)
+              acc[t][rr] = q8_term<false>(acc[t][rr], d[kb][t][rr], wd, wc, xq[rr][kb]);
           }
       }
     }
@@ -1479,11 +1479,8 @@ gemm_i8_qkv_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ d
         const float wc = wd * NEG_MAGIC;
         const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, magic, 0, 0, 0);
 #pragma unroll
-        for (int q = 0; q < 16; q++) {
-          float t = fmaf(__int_as_float(d[q]), wd, wc);   // round(S * d_w)
-          float u = t * xv[q >> 2][q & 3];                 // round(. * d_x)
-          acc[tn][q] = acc[tn][q] + u;                     // round(acc + .)
-        }
+        for (int q = 0; q < 16; q++)
+          acc[tn][q] = q8_term<false>(acc[tn][q], d[q], wd, wc, xv[q >> 2][q & 3]);
       }
     }
   }
@@ -1544,20 +1541,51 @@ int gemm_i8_route(int64_t M, int64_t Nrows, int64_t K) {
   return ((M + 127) / 128) * ((Nrows + 127) / 128) >= 512 ? GEMM_ROUTE_REG128 : GEMM_ROUTE_REG64;
 }
 
-hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+namespace {
+
+template <bool F2>
+hipError_t gemm_i8_routed(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                           float* y, int64_t M, int64_t N, int64_t K, int64_t ldc,
                           hipStream_t s) {
-  if (M == 0 || N == 0) return hipSuccess;
   switch (gemm_i8_route(M, N, K)) {
     case GEMM_ROUTE_SMALL:
-      return run_small<1, 2, 1, false, 3>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+      return run_small<1, 2, 1, false, F2, 3>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc,
+                                              0, s);
     case GEMM_ROUTE_BIG:
-      return run_big<false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+      return run_big<false, F2>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
     case GEMM_ROUTE_REG128:
-      return run<128, 128, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+      return run<128, 128, 2, 2, false, F2>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0,
+                                            s);
     default:
-      return run<64, 64, 2, 2, false>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
+      return run<64, 64, 2, 2, false, F2>(xq, dx, wq, dw, y, nullptr, nullptr, M, N, K, ldc, 0, s);
   }
+}
+
+template <bool F2>
+hipError_t geglu_i8_routed(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                           int8_t* hq, float* dh, int64_t M, int64_t F, int64_t K,
+                           hipStream_t s) {
+  switch (gemm_i8_route(M, 2 * F, K)) {
+    case GEMM_ROUTE_SMALL:
+      return run_small<2, 2, 2, true, F2, 3>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F,
+                                             s);
+    case GEMM_ROUTE_BIG:
+      return run_big<true, F2>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+    case GEMM_ROUTE_REG128:
+      return run<128, 128, 2, 2, true, F2>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+    default:
+      return run<64, 128, 2, 2, true, F2>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_i8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                          float* y, int64_t M, int64_t N, int64_t K, int64_t ldc, hipStream_t s,
+                          bool fma2) {
+  if (M == 0 || N == 0) return hipSuccess;
+  return fma2 ? gemm_i8_routed<true>(xq, dx, wq, dw, y, M, N, K, ldc, s)
+              : gemm_i8_routed<false>(xq, dx, wq, dw, y, M, N, K, ldc, s);
 }
 
 // Few rows: the small-M form (16-row blocks); many rows, or a K the small
@@ -1613,27 +1641,23 @@ bool gemm_i8_pro_ok(int64_t M, int64_t N, int64_t K, bool norm) {
 
 hipError_t launch_gemm_i8_pro(const float* x, const float* nw, float eps, bool norm,
                               const int8_t* wq, const float* dw, float* y, int64_t M, int64_t N,
-                              int64_t K, int64_t ldc, hipStream_t s) {
+                              int64_t K, int64_t ldc, hipStream_t s, bool fma2) {
   if (M == 0 || N == 0) return hipSuccess;
   if (!gemm_i8_pro_ok(M, N, K, norm)) return hipErrorInvalidValue;
-  if (norm) return run_pro<PRO_NORM, 4, 2, 3>(x, nw, eps, wq, dw, y, M, N, K, ldc, s);
-  return run_pro<PRO_QUANT, 4, 2, 3>(x, nullptr, 0.0f, wq, dw, y, M, N, K, ldc, s);
+  if (fma2) {
+    if (norm) return run_pro<PRO_NORM, true, 4, 2, 3>(x, nw, eps, wq, dw, y, M, N, K, ldc, s);
+    return run_pro<PRO_QUANT, true, 4, 2, 3>(x, nullptr, 0.0f, wq, dw, y, M, N, K, ldc, s);
+  }
+  if (norm) return run_pro<PRO_NORM, false, 4, 2, 3>(x, nw, eps, wq, dw, y, M, N, K, ldc, s);
+  return run_pro<PRO_QUANT, false, 4, 2, 3>(x, nullptr, 0.0f, wq, dw, y, M, N, K, ldc, s);
 }
 
 hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t* wq,
                                 const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
-                                int64_t K, hipStream_t s) {
+                                int64_t K, hipStream_t s, bool fma2) {
   if (M == 0 || F == 0) return hipSuccess;
-  switch (gemm_i8_route(M, 2 * F, K)) {
-    case GEMM_ROUTE_SMALL:
-      return run_small<2, 2, 2, true, 3>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
-    case GEMM_ROUTE_BIG:
-      return run_big<true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
-    case GEMM_ROUTE_REG128:
-      return run<128, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
-    default:
-      return run<64, 128, 2, 2, true>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F, s);
-  }
+  return fma2 ? geglu_i8_routed<true>(xq, dx, wq, dw, hq, dh, M, F, K, s)
+              : geglu_i8_routed<false>(xq, dx, wq, dw, hq, dh, M, F, K, s);
 }
 
 }  // namespace glypr

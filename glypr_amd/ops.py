@@ -13,10 +13,11 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from ._lib import BF16_DEQUANT, GLYPR_ERR_UNSUPPORTED, INT8_EXACT, GlyprError, check, lib
+from ._lib import (BF16_DEQUANT, GLYPR_ERR_UNSUPPORTED, INT8_EXACT, INT8_FMA, GlyprError, check,
+                   lib)
 
-__all__ = ["Context", "Q8Weight", "BF16Weight", "INT8_EXACT", "BF16_DEQUANT", "q8_0_matmul",
-           "bf16_matmul", "f32_to_bf16_bits",
+__all__ = ["Context", "Q8Weight", "BF16Weight", "INT8_EXACT", "BF16_DEQUANT", "INT8_FMA",
+           "q8_0_matmul", "bf16_matmul", "f32_to_bf16_bits",
            "rmsnorm_q8_0_matmul", "rmsnorm", "geglu", "mlp", "rmsnorm_mlp", "dequantize",
            "quantize", "embed_gather", "pool_normalize"]
 

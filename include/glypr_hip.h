@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define GLYPR_HIP_ABI_VERSION 6
+#define GLYPR_HIP_ABI_VERSION 7
 
 typedef enum glypr_status {
   GLYPR_OK = 0,
@@ -59,10 +59,17 @@ typedef enum glypr_status {
  *   is bit-identical to glypr's CPU QMatMul path on x86-64.
  * BF16_DEQUANT: weights dequantized in registers to bf16(q*d), activations
  *   rounded to bf16, bf16 MFMA with f32 accumulation (the semantics of
- *   glypr's Metal kernels / CANDLE_DEQUANTIZE_ALL, at bf16 precision). */
+ *   glypr's Metal kernels / CANDLE_DEQUANTIZE_ALL, at bf16 precision).
+ * INT8_FMA (ABI >= 7): INT8_EXACT's operands and block sums, with each
+ *   block's term added as sum = fma((float)isum * d_w, d_x, sum): one
+ *   rounding fewer per block than the vec_dot sequence, so not bit-identical
+ *   to it (within 1e-3 relative / 1e-4 absolute; measured to ~1e-6 relative),
+ *   and 2 instead of 3 vector ops per output and block, the bound of the
+ *   int8 GEMM at large M.  The model driver always uses INT8_EXACT. */
 typedef enum glypr_q8_variant {
   GLYPR_Q8_INT8_EXACT = 0,
-  GLYPR_Q8_BF16_DEQUANT = 1
+  GLYPR_Q8_BF16_DEQUANT = 1,
+  GLYPR_Q8_INT8_FMA = 2
 } glypr_q8_variant;
 
 typedef struct glypr_hip_ctx glypr_hip_ctx; /* per-device context + workspace */

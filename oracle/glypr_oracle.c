@@ -197,6 +197,38 @@ void orc_q8_0_matmul(const float* x, int64_t m, int64_t k, const uint8_t* w, int
   free(xq);
 }
 
+/* The INT8_FMA variant (no counterpart in the reference): vec_dot_unopt's
+ * operands and block order, with the last two roundings of each block fused,
+ * sumf = fmaf((float)isum * d_w, d_x, sumf).  fmaf is the C99 correctly
+ * rounded fused multiply-add. */
+float orc_q8_0_vec_dot_fma(int64_t k, const uint8_t* wblocks, const uint8_t* xblocks) {
+  int64_t nb = k / ORC_QK8_0;
+  float sumf = 0.0f;
+  for (int64_t b = 0; b < nb; b++) {
+    const uint8_t* wb = wblocks + b * ORC_BLOCK_BYTES;
+    const uint8_t* xb = xblocks + b * ORC_BLOCK_BYTES;
+    const int8_t* wq = blk_qs(wb);
+    const int8_t* xq = blk_qs(xb);
+    int32_t isum = 0;
+    for (int j = 0; j < ORC_QK8_0; j++) isum += (int32_t)wq[j] * (int32_t)xq[j];
+    const float t = (float)isum * orc_f16_to_f32(blk_d(wb));
+    sumf = fmaf(t, orc_f16_to_f32(blk_d(xb)), sumf);
+  }
+  return sumf;
+}
+
+void orc_q8_0_matmul_fma(const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t n,
+                         float* y, int threads) {
+  int64_t rb = (k / ORC_QK8_0) * ORC_BLOCK_BYTES;
+  uint8_t* xq = (uint8_t*)malloc((size_t)(m * rb > 0 ? m * rb : 1));
+  orc_q8_0_quantize_rows(x, m, k, xq);
+  int nt = orc_threads(threads);
+#pragma omp parallel for num_threads(nt) schedule(static)
+  for (int64_t i = 0; i < m; i++)
+    for (int64_t c = 0; c < n; c++) y[i * n + c] = orc_q8_0_vec_dot_fma(k, w + c * rb, xq + i * rb);
+  free(xq);
+}
+
 void orc_q8_0_matmul_f64(const uint8_t* xq, int64_t m, int64_t k, const uint8_t* w, int64_t n,
                          double* y) {
   int64_t nb = k / ORC_QK8_0;

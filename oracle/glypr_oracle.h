@@ -23,6 +23,9 @@
  *    (tests/golden/q8_0_kat.json), float64 restatement of the definition,
  *    lossless case (GEMM == numpy float64 X @ W^T exactly).
  *  - matmul / matmul_preq: float64 brute force over the same quantized operands.
+ *  - vec_dot_fma / matmul_fma: exact rational brute force of every fused
+ *    rounding on small inputs, vec_dot itself for one block (k = 32), and the
+ *    float64 brute force within the fused form's error bound.
  *  - rmsnorm: constant-row KAT, float64 formula, 2^k scale invariance.
  *  - tanhf / geglu: double-precision tanh (<= 3 ulp), exact special points.
  *  - embed_gather, pool_normalize: dequantized rows; closed-form KAT and the
@@ -73,6 +76,10 @@ void orc_q8_0_dequantize_rows(const uint8_t* blocks, int64_t rows, int64_t k, fl
 
 /* BlockQ8_0::vec_dot_unopt: sum_b ((float)isum_b * f32(d_w)) * f32(d_x), f32 sequential. */
 float orc_q8_0_vec_dot(int64_t k, const uint8_t* wblocks, const uint8_t* xblocks);
+/* INT8_FMA (this backend's third variant): sum = fmaf((float)isum_b * d_w, d_x, sum). */
+float orc_q8_0_vec_dot_fma(int64_t k, const uint8_t* wblocks, const uint8_t* xblocks);
+void orc_q8_0_matmul_fma(const float* x, int64_t m, int64_t k, const uint8_t* w, int64_t n,
+                         float* y, int threads);
 
 /* k_quants::matmul::<BlockQ8_0> as reached from LinearOp::forward (Quantized arm):
  * x f32 [m,k], w Q8_0 [n][k/32], y f32 [m,n].  threads <= 0 -> all cores. */

@@ -74,6 +74,8 @@ def lib():
             "orc_q8_0_vec_dot": (ctypes.c_float, [_i64, _u8p, _u8p]),
             "orc_q8_0_matmul": (None, [_f32p, _i64, _i64, _u8p, _i64, _f32p, ctypes.c_int]),
             "orc_q8_0_matmul_preq": (None, [_u8p, _i64, _i64, _u8p, _i64, _f32p, ctypes.c_int]),
+            "orc_q8_0_vec_dot_fma": (ctypes.c_float, [_i64, _u8p, _u8p]),
+            "orc_q8_0_matmul_fma": (None, [_f32p, _i64, _i64, _u8p, _i64, _f32p, ctypes.c_int]),
             "orc_q8_0_matmul_f64": (None, [_u8p, _i64, _i64, _u8p, _i64, _f64p]),
             "orc_q8_0_matmul_dequant_f64": (None, [_f32p, _i64, _i64, _u8p, _i64, _f64p,
                                                    ctypes.c_int]),
@@ -188,6 +190,23 @@ def matmul(x: np.ndarray, w_blocks: np.ndarray, n: int, threads: int = 0) -> np.
     w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
     lib().orc_q8_0_matmul(_p(x, _f32p), m, k, _p(w, _u8p), n, _p(y, _f32p), threads)
     return y
+
+
+def matmul_fma(x: np.ndarray, w_blocks: np.ndarray, n: int, threads: int = 0) -> np.ndarray:
+    """The INT8_FMA variant: matmul's operands, each block's term added with
+    one fused multiply-add (orc_q8_0_vec_dot_fma)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    m, k = x.shape
+    y = np.empty((m, n), np.float32)
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    lib().orc_q8_0_matmul_fma(_p(x, _f32p), m, k, _p(w, _u8p), n, _p(y, _f32p), threads)
+    return y
+
+
+def vec_dot_fma(k: int, w_blocks: np.ndarray, x_blocks: np.ndarray) -> float:
+    w = np.ascontiguousarray(w_blocks, dtype=np.uint8)
+    xb = np.ascontiguousarray(x_blocks, dtype=np.uint8)
+    return float(lib().orc_q8_0_vec_dot_fma(k, _p(w, _u8p), _p(xb, _u8p)))
 
 
 def matmul_preq(xq: np.ndarray, m: int, k: int, w_blocks: np.ndarray, n: int,

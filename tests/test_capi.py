@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_symbols():
         assert hasattr(L, name), name
-    assert L.glypr_hip_abi_version() == 6
+    assert L.glypr_hip_abi_version() == 7
 
 
 def _has_gpu():
@@ -89,6 +89,17 @@ def test_matmul_validation_order():
         _lib.GLYPR_ERR_INVALID_ARG
     assert L.glypr_hip_rmsnorm_mlp(NULL, FAKE, FAKE, MISALIGNED, NULL, 1e-6, FAKE, 4, 1,
                                    NULL) == _lib.GLYPR_ERR_ALIGNMENT
+    # the three variants pass the variant check (and fail later, on the NULL
+    # weight); the next value does not
+    for v in (_lib.INT8_EXACT, _lib.BF16_DEQUANT, _lib.INT8_FMA):
+        assert L.glypr_hip_q8_0_matmul(NULL, NULL, FAKE, FAKE, 4, v, NULL) == \
+            _lib.GLYPR_ERR_INVALID_ARG
+        assert L.glypr_hip_mlp(NULL, NULL, FAKE, FAKE, FAKE, 4, v, NULL) == \
+            _lib.GLYPR_ERR_INVALID_ARG
+    assert L.glypr_hip_q8_0_matmul(NULL, NULL, FAKE, FAKE, 4, 3, NULL) == \
+        _lib.GLYPR_ERR_UNSUPPORTED
+    assert L.glypr_hip_mlp(NULL, FAKE, FAKE, FAKE, FAKE, 4, 3, NULL) == \
+        _lib.GLYPR_ERR_UNSUPPORTED
 
 
 def test_noalloc_matmul_validation():

@@ -147,6 +147,97 @@ def test_matmul_lossless_equals_numpy(oracle):
     assert np.all(np.abs(y - ref) <= 1e-6 * scale + 1e-30)
 
 
+# ------------------------------------------- the INT8_FMA variant's oracle --
+
+def _f32_round(q):
+    """Round a Fraction to the nearest binary32 value, ties to even (normal
+    range), exactly: the IEEE definition of one rounding."""
+    from fractions import Fraction
+    if q == 0:
+        return Fraction(0)
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    assert -126 <= e <= 127
+    ulp = Fraction(2) ** (e - 23)
+    n, r = divmod(a, ulp)
+    if r > ulp / 2 or (r == ulp / 2 and n % 2 == 1):
+        n += 1
+    return (n * ulp) if q > 0 else -(n * ulp)
+
+
+def _block_terms(oracle, xq, w, k):
+    """Per output and block: the integer block sum S and the two f16 scales,
+    exactly (as Fractions)."""
+    from fractions import Fraction
+    dw, qw = oracle.split_blocks(w, k)
+    dx, qx = oracle.split_blocks(xq, k)
+    fdw = oracle.f16_bits_to_f32(dw).astype(np.float64)
+    fdx = oracle.f16_bits_to_f32(dx).astype(np.float64)
+    s = np.stack([qx[:, b * 32:(b + 1) * 32].astype(np.int64)
+                  @ qw[:, b * 32:(b + 1) * 32].astype(np.int64).T for b in range(k // 32)])
+    return s, fdw, fdx, Fraction
+
+
+def test_matmul_fma_exact_rational_bruteforce(oracle):
+    """Every rounding of both accumulation orders stated with exact rationals:
+    the 2-op form t = round(S d_w), acc = round(acc + t d_x) must match
+    matmul_fma bit for bit, the 3-op form acc = round(acc + round(t d_x)) must
+    match matmul, and on these inputs the two orders differ somewhere (so the
+    check tells them apart)."""
+    m, k, n = 8, 256, 16
+    x = oracle.normal(m * k, seed=71).reshape(m, k)
+    w = oracle.q8_0_weight(n, k, seed=72)
+    xq = oracle.quantize_rows(x)
+    s, fdw, fdx, Fraction = _block_terms(oracle, xq, w, k)
+    fma_ref = np.empty((m, n), np.float32)
+    seq_ref = np.empty((m, n), np.float32)
+    for i in range(m):
+        for c in range(n):
+            a2 = a3 = Fraction(0)
+            for b in range(k // 32):
+                t = _f32_round(Fraction(int(s[b, i, c])) * Fraction(fdw[c, b]))
+                a2 = _f32_round(a2 + t * Fraction(fdx[i, b]))
+                a3 = _f32_round(a3 + _f32_round(t * Fraction(fdx[i, b])))
+            fma_ref[i, c], seq_ref[i, c] = float(a2), float(a3)
+    assert np.array_equal(f32_to_bits(oracle.matmul_fma(x, w, n)), f32_to_bits(fma_ref))
+    assert np.array_equal(f32_to_bits(oracle.matmul(x, w, n)), f32_to_bits(seq_ref))
+    assert np.count_nonzero(f32_to_bits(fma_ref) != f32_to_bits(seq_ref)) > 0
+    assert np.array_equal(oracle.matmul_fma(x, w, n, threads=1), oracle.matmul_fma(x, w, n))
+    rb = (k // 32) * 34
+    for i, c in ((0, 0), (m - 1, n - 1), (3, 11)):
+        got = oracle.vec_dot_fma(k, w[c].reshape(-1)[:rb], xq[i].reshape(-1)[:rb])
+        assert f32_to_bits(np.float32(got)) == f32_to_bits(fma_ref[i, c])
+
+
+def test_matmul_fma_one_block_is_vec_dot(oracle):
+    """k = 32: fma(t, d_x, 0) = round(t d_x) = vec_dot's single term."""
+    m, n = 40, 50
+    x = oracle.normal(m * 32, seed=73).reshape(m, 32) * np.float32(5.0)
+    w = oracle.q8_0_weight(n, 32, seed=74, sigma=0.3)
+    assert np.array_equal(f32_to_bits(oracle.matmul_fma(x, w, n)),
+                          f32_to_bits(oracle.matmul(x, w, n)))
+
+
+@pytest.mark.parametrize("m,k,n", [(19, 256, 128), (64, 768, 96), (7, 1152, 33)])
+def test_matmul_fma_vs_f64_bruteforce(oracle, m, k, n):
+    """The fused form's error against the float64 sum: nb roundings of t and
+    nb of the accumulate, bounded by (2 nb + 2) 2^-24 sum |terms|; and within
+    BASELINE's 1e-3 relative / 1e-4 absolute of the INT8_EXACT oracle."""
+    x = oracle.normal(m * k, seed=91 + m).reshape(m, k)
+    w = oracle.q8_0_weight(n, k, seed=92 + n)
+    xq = oracle.quantize_rows(x)
+    y = oracle.matmul_fma(x, w, n).astype(np.float64)
+    y64 = oracle.matmul_f64(xq, m, k, w, n)
+    s, fdw, fdx, _ = _block_terms(oracle, xq, w, k)
+    absterm = np.einsum("bmn,nb,mb->mn", np.abs(s).astype(np.float64), np.abs(fdw), np.abs(fdx))
+    nb = k // 32
+    assert np.all(np.abs(y - y64) <= (2 * nb + 2) * 2.0 ** -24 * absterm + 1e-30)
+    exact = oracle.matmul(x, w, n).astype(np.float64)
+    assert np.all(np.abs(y - exact) <= np.maximum(1e-3 * np.abs(exact), 1e-4))
+
+
 def test_reference_metal_case_activation_error_bound(oracle):
     """glypr's Q8_0 unit-test inputs (metal_kernels/mod.rs:1924-1979): w =
     sin(0.031 i)*1.5 quantized to Q8_0 [128 x 256], x = cos(0.059 i)*3 via bf16,
@@ -706,6 +797,10 @@ PINS = {
     "orc_q8_0_vec_dot": ["test_vec_dot_kat"],
     "orc_q8_0_matmul": ["test_matmul_vs_f64_bruteforce", "test_matmul_lossless_equals_numpy"],
     "orc_q8_0_matmul_preq": ["test_matmul_vs_f64_bruteforce"],
+    "orc_q8_0_vec_dot_fma": ["test_matmul_fma_exact_rational_bruteforce"],
+    "orc_q8_0_matmul_fma": ["test_matmul_fma_exact_rational_bruteforce",
+                            "test_matmul_fma_one_block_is_vec_dot",
+                            "test_matmul_fma_vs_f64_bruteforce"],
     "orc_q8_0_matmul_f64": ["test_matmul_lossless_equals_numpy"],
     "orc_q8_0_matmul_dequant_f64": ["test_reference_metal_case_activation_error_bound"],
     "orc_rmsnorm_row": ["test_rmsnorm_kat", "test_rmsnorm_vs_f64_and_invariants"],
