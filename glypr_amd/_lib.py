@@ -21,6 +21,7 @@ GLYPR_ERR_OOM = 6
 GLYPR_ERR_RANGE = 7
 GLYPR_ERR_UNSUPPORTED = 8
 GLYPR_ERR_NOT_FOUND = 9
+GLYPR_ERR_BUSY = 10
 
 INT8_EXACT = 0
 BF16_DEQUANT = 1

@@ -178,7 +178,9 @@ int glypr_hip_ctx_create(int device, glypr_hip_ctx** out) {
   // this device's no-allocation scratch array (scratch.hip), with the device
   // current; if it cannot be resolved only glypr_hip_q8_0_matmul_noalloc fails
   void* scratch_ptr = nullptr;
-  const hipError_t se = resolve_scratch(&scratch_ptr);
+  hipError_t se = resolve_scratch(&scratch_ptr);
+  if (se == hipSuccess) se = scratch_guard_init(device);
+  if (se != hipSuccess) scratch_ptr = nullptr;
   glypr_hip_ctx* ctx = new (std::nothrow) glypr_hip_ctx();
   GLYPR_CHECK(ctx != nullptr, GLYPR_ERR_OOM, "host allocation failed");
   ctx->device = device;
@@ -532,11 +534,34 @@ int glypr_hip_q8_0_matmul_noalloc(glypr_hip_ctx* ctx, const glypr_q8w* w, const 
   if (m == 0) return GLYPR_OK;
   DeviceScope ds(ctx->device);
   if (ds.err != hipSuccess) return hip_error(ds.err, "hipSetDevice");
+  ScratchGuard* g = scratch_guard(ctx->device);
+  GLYPR_CHECK(g != nullptr, GLYPR_ERR_DEVICE, "no scratch guard for device %d", ctx->device);
+  const hipStream_t s = (hipStream_t)stream;
+  std::lock_guard<std::mutex> gl(g->mu);
+  // a stream under graph capture runs later, at replay: nothing to check now
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  const bool eager = hipStreamIsCapturing(s, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone;
+  if (!eager) (void)hipGetLastError();
+  if (eager && g->armed && g->last != s) {
+    const hipError_t q = hipEventQuery(g->done);
+    if (q == hipErrorNotReady) {
+      (void)hipGetLastError();
+      return set_error(GLYPR_ERR_BUSY,
+                       "the no-allocation scratch of device %d is in use by a pending call on "
+                       "another stream",
+                       ctx->device);
+    }
+    if (q != hipSuccess) return hip_error(q, "hipEventQuery (scratch guard)");
+  }
   std::lock_guard<std::mutex> lk(ctx->mu);
   ctx->no_events = true;
-  const int rc = matmul_impl(ctx, w, x, nullptr, 0.0f, false, y, m, variant, ctx->scratch,
-                             (hipStream_t)stream);
+  const int rc = matmul_impl(ctx, w, x, nullptr, 0.0f, false, y, m, variant, ctx->scratch, s);
   ctx->no_events = false;
+  if (rc == GLYPR_OK && eager) {
+    GLYPR_TRY_HIP(hipEventRecord(g->done, s), "hipEventRecord (scratch guard)");
+    g->last = s;
+    g->armed = true;
+  }
   return rc;
 }
 

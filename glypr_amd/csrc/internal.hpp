@@ -80,6 +80,17 @@ namespace glypr {
 // This device's address of the no-allocation scratch array (the device must be
 // current); on failure *ptr is NULL and the HIP error is returned.
 hipError_t resolve_scratch(void** ptr);
+// The device's record of its last no-allocation call: the stream it ran on
+// and an event recorded after it (created by scratch_guard_init, with the
+// device current, when the first context on the device is made).
+struct ScratchGuard {
+  std::mutex mu;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool armed = false;   // done holds a recorded call
+};
+hipError_t scratch_guard_init(int device);
+ScratchGuard* scratch_guard(int device);   // null before scratch_guard_init
 
 // error.cpp-style helpers (defined in capi.hip)
 int set_error(int code, const char* fmt, ...);

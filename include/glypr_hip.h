@@ -49,7 +49,9 @@ typedef enum glypr_status {
   GLYPR_ERR_OOM = 6,         /* device allocation failed */
   GLYPR_ERR_RANGE = 7,       /* token id >= vocab */
   GLYPR_ERR_UNSUPPORTED = 8, /* unknown variant or flag, unsupported file layout */
-  GLYPR_ERR_NOT_FOUND = 9    /* GGUF metadata key or tensor absent */
+  GLYPR_ERR_NOT_FOUND = 9,   /* GGUF metadata key or tensor absent */
+  GLYPR_ERR_BUSY = 10        /* (ABI >= 7) the no-allocation scratch is in use by a
+                                pending call on another stream */
 } glypr_status;
 
 /* Numerics of the Q8_0 GEMM.
@@ -171,8 +173,14 @@ int glypr_hip_q8_0_matmul(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x
  * each device holds until the process ends; the call allocates nothing.
  * Calls whose operand needs more (INT8_EXACT: m*k + 4*m*k/32 bytes, rounded
  * up to 256 each; BF16_DEQUANT: 2*m*k) fail with GLYPR_ERR_SHAPE.  Every call
- * on a device shares that device's array, across contexts: calls that overlap
- * on one device (other streams, other threads) race. */
+ * on a device shares that device's array, across contexts: calls on one
+ * stream are ordered, but calls that overlap on one device (other streams,
+ * other threads) would race.  (ABI >= 7) The library records an event after
+ * each call on a device; a call on another stream while the previous call's
+ * event is still pending fails with GLYPR_ERR_BUSY and launches nothing (wait
+ * for the earlier stream, or order the streams, and call again).  Calls on a
+ * stream under HIP graph capture are not checked and not recorded: their
+ * replays must not overlap other calls on the device. */
 #define GLYPR_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int glypr_hip_q8_0_matmul_noalloc(glypr_hip_ctx* ctx, const glypr_q8w* w, const float* x,
                                   float* y, int64_t m, int variant, glypr_stream stream);

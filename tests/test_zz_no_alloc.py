@@ -3,7 +3,9 @@ through the C ABI, its output equals glypr_hip_q8_0_matmul's bit for bit (both
 variants), on two calls in a row with the second input smaller (the shared
 per-device scratch keeps the first call's contents), on a second context of the
 same device (which shares the array) and with profiling on; sizes beyond the
-scratch are refused with GLYPR_ERR_SHAPE before anything runs."""
+scratch are refused with GLYPR_ERR_SHAPE before anything runs; a call on a
+second stream while the first stream's call is still pending is refused with
+GLYPR_ERR_BUSY, and accepted once that call has finished."""
 import ctypes
 
 import numpy as np
@@ -84,5 +86,49 @@ def test_noalloc_matmul_rejects_oversized():
                                          BF16_DEQUANT, ctx.stream)
     assert rc == _lib.GLYPR_OK
     torch.cuda.synchronize()
+    w.close()
+    ctx.close()
+
+
+def test_noalloc_matmul_rejects_overlap_on_another_stream():
+    """Stream A is held by a bounded spin kernel (torch.cuda._sleep), so the
+    no-allocation call queued behind it is pending when stream B calls: B's
+    call must fail with GLYPR_ERR_BUSY and launch nothing.  Calls on A itself
+    stay accepted (one stream orders them), and after A has finished B's call
+    runs and gives the matmul's bits."""
+    from oracle import pyoracle as po
+    ctx = ops.Context(0)
+    n, k, m = 1152, 768, 512
+    wb = po.q8_0_weight(n, k, seed=81)
+    w = Q8Weight.from_gguf(ctx, wb, n, k)
+    x = torch.from_numpy(po.normal(m * k, seed=82).reshape(m, k)).cuda()
+    ref = ops.q8_0_matmul(ctx, w, x, INT8_EXACT)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    ya = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    yb = torch.full((m, n), -1.0, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    L = _lib.lib()
+    fn = L.glypr_hip_q8_0_matmul_noalloc
+
+    def call(y, stream):
+        return fn(ctx.handle, w.handle, ctypes.c_void_p(x.data_ptr()),
+                  ctypes.c_void_p(y.data_ptr()), m, INT8_EXACT,
+                  ctypes.c_void_p(stream.cuda_stream))
+
+    say("no-alloc overlap: stream A held by a spin kernel, then a call on A and one on B")
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(100_000_000)      # bounded: ~50 ms of GPU clocks
+    assert call(ya, sa) == _lib.GLYPR_OK
+    assert call(ya, sa) == _lib.GLYPR_OK    # the same stream: ordered, accepted
+    rc = call(yb, sb)
+    assert rc == _lib.GLYPR_ERR_BUSY, (rc, _lib.last_error())
+    assert "another stream" in _lib.last_error()
+    sa.synchronize()
+    sb.synchronize()
+    assert np.all(yb.cpu().numpy() == -1.0)  # the refused call launched nothing
+    assert call(yb, sb) == _lib.GLYPR_OK     # A has finished: accepted
+    assert np.array_equal(bits(ya), bits(ref))
+    assert np.array_equal(bits(yb), bits(ref))
     w.close()
     ctx.close()
