@@ -50,7 +50,15 @@ static hipError_t launch_rmsnorm_generic(const float* x, const float* w, float e
 // layout), and also written to LDS so that lanes 0..7 can run the reference's
 // eight sequential FMA chains (lane j: elements j, j+8, j+16, ...) from LDS.
 // The chains are the only serial part; quantization then uses all 64 lanes.
-constexpr int NORM_WAVES = 4;  // rows per 256-thread block
+// A block holds 1, 2 or 4 row waves: about one block per CU when rows are few
+// (512 rows: 256 blocks of 2 waves, measured ahead of 128 blocks of 4 and
+// 512 blocks of 1), 4 per block for long row counts.
+constexpr int NORM_WAVES_MAX = 4;
+inline int norm_waves(int64_t rows) { return rows <= 256 ? 1 : rows <= 512 ? 2 : 4; }
+// Few rows: each chain lane reads its whole chain from LDS before the first
+// FMA (one LDS round trip, 32 NV registers); many rows: in batches of 12
+// chunks, which keeps the occupancy that hides the loads of other rows.
+inline bool norm_full_reads(int64_t rows) { return rows <= 2048; }
 
 enum NormOut { OUT_F32 = 0, OUT_Q8 = 1, OUT_BF16 = 2 };
 
@@ -78,11 +86,11 @@ __device__ __forceinline__ void stage_chains(float* lrow, int S, int c4, const v
 // the chain issued before its first FMA: chunks past dim / 32 are read
 // clamped and replaced by zeros.  The horizontal sum runs through DPP and
 // lane 0's total is broadcast with readlane.
-template <int NV>
+template <int NV, bool FULL>
 __device__ __forceinline__ float chain_row_inv(const float* lrow, int dim, int lane, float eps) {
-  // reads in batches of up to 12 chunks (48 registers): the row-per-wave
-  // kernels also stream large row counts, where occupancy hides latency
-  constexpr int NC = 8 * NV, BATCH = NC < 12 ? NC : 12;
+  // FULL: every chunk of the chain in one batch; else batches of up to 12
+  // chunks (48 registers)
+  constexpr int NC = 8 * NV, BATCH = FULL ? NC : (NC < 12 ? NC : 12);
   float sum = 0.0f;
   if (lane < 8) {
     const v4f* src = reinterpret_cast<const v4f*>(lrow + lane * chain_stride(dim));
@@ -126,15 +134,15 @@ __device__ __forceinline__ float chain_row_inv(const float* lrow, int dim, int l
 }
 
 // NV = float4s per lane = ceil(dim / 256).  dim % 4 == 0 (dim % 32 == 0 for Q8).
-template <int NV, int MODE, bool CHAIN>
-__global__ void __launch_bounds__(64 * NORM_WAVES)
+template <int NV, int MODE, bool CHAIN, bool FULL>
+__global__ void __launch_bounds__(64 * NORM_WAVES_MAX)
 rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64_t rows, int dim,
                    float* y, int8_t* __restrict__ xq, float* __restrict__ dx,
                    uint16_t* __restrict__ xb) {
   extern __shared__ float lds_rows[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t row = (int64_t)blockIdx.x * NORM_WAVES + wave;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
   if (row >= rows) return;  // whole wave exits together
   float* lrow = lds_rows + wave * (dim + 32);
   const float* xr = x + row * dim;
@@ -158,7 +166,7 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
-    inv = chain_row_inv<NV>(lrow, dim, lane, eps);
+    inv = chain_row_inv<NV, FULL>(lrow, dim, lane, eps);
   } else {
 #pragma unroll
     for (int i = 0; i < NV; i++) {
@@ -241,18 +249,22 @@ template <int MODE>
 static hipError_t launch_norm(const float* x, const float* w, float eps, int64_t rows, int64_t dim,
                               float* y, int8_t* xq, float* dx, uint16_t* xb, hipStream_t s) {
   if (rows == 0) return hipSuccess;
-  const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
-  const size_t lds = (size_t)NORM_WAVES * (dim + 32) * sizeof(float);
+  const int nw = norm_waves(rows);
+  const unsigned grid = (unsigned)((rows + nw - 1) / nw);
+  const size_t lds = (size_t)nw * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
-  const bool chain = dim % 32 == 0;
+  const bool chain = dim % 32 == 0, full = norm_full_reads(rows);
   switch (nv) {
 #define NORM_CASE(N, NK)                                                                      \
   case N:                                                                                     \
-    if (chain)                                                                                \
-      rmsnorm_row_kernel<NK, MODE, true><<<grid, 64 * NORM_WAVES, lds, s>>>(                  \
+    if (chain && full)                                                                        \
+      rmsnorm_row_kernel<NK, MODE, true, true><<<grid, 64 * nw, lds, s>>>(                    \
+          x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
+    else if (chain)                                                                           \
+      rmsnorm_row_kernel<NK, MODE, true, false><<<grid, 64 * nw, lds, s>>>(                   \
           x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
     else                                                                                      \
-      rmsnorm_row_kernel<NK, MODE, false><<<grid, 64 * NORM_WAVES, lds, s>>>(                 \
+      rmsnorm_row_kernel<NK, MODE, false, false><<<grid, 64 * nw, lds, s>>>(                  \
           x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
     break;
     NORM_CASE(1, 1)
@@ -298,8 +310,8 @@ hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_
 // itself (the input of a projection that has no norm in front); 3 = bf16 of
 // RMSNorm(h; w_next) (dense-bf16 weights).  scalar (device, nullable):
 // forward_residual_add's layer_scalar, h = (h + n) * s.
-template <int NV, int NEXT>
-__global__ void __launch_bounds__(64 * NORM_WAVES)
+template <int NV, int NEXT, bool FULL>
+__global__ void __launch_bounds__(64 * NORM_WAVES_MAX)
 residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_post,
                      float* __restrict__ h, const float* __restrict__ w_next,
                      const float* __restrict__ scalar, float eps, int64_t rows, int dim,
@@ -309,7 +321,7 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   extern __shared__ float lds_rows[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t row = (int64_t)blockIdx.x * NORM_WAVES + wave;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
   if (row >= rows) return;
   float* lrow = lds_rows + wave * (dim + 32);
   const int n4 = dim >> 2;
@@ -333,7 +345,7 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  const float inv = chain_row_inv<NV>(lrow, dim, lane, eps);
+  const float inv = chain_row_inv<NV, FULL>(lrow, dim, lane, eps);
   __builtin_amdgcn_wave_barrier();
   const float sv = scalar ? *scalar : 1.0f;
 #pragma unroll
@@ -355,7 +367,7 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
       // the staging writes must land; the h stores need not
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_wave_barrier();
-      inv2 = chain_row_inv<NV>(lrow, dim, lane, eps);
+      inv2 = chain_row_inv<NV, FULL>(lrow, dim, lane, eps);
     }
     // all NV chunks' scales first (independent chains the scheduler can
     // interleave), then the stores
@@ -410,14 +422,21 @@ hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, c
                                 hipStream_t s, const float* scalar, bool plain_q, uint16_t* xb) {
   if (rows == 0) return hipSuccess;
   if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
-  const unsigned grid = (unsigned)((rows + NORM_WAVES - 1) / NORM_WAVES);
-  const size_t lds = (size_t)NORM_WAVES * (dim + 32) * sizeof(float);
+  const int nw = norm_waves(rows);
+  const unsigned grid = (unsigned)((rows + nw - 1) / nw);
+  const size_t lds = (size_t)nw * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
   const int mode = xb != nullptr ? 3 : xq == nullptr ? 0 : (plain_q ? 2 : 1);
+  const bool full = norm_full_reads(rows);
 #define RES_LAUNCH(N, MODE)                                                                    \
-  residual_norm_kernel<N, MODE><<<grid, 64 * NORM_WAVES, lds, s>>>(x, w_post, h, w_next,       \
-                                                                   scalar, eps, rows,          \
-                                                                   (int)dim, xq, dx, xb)
+  do {                                                                                         \
+    if (full)                                                                                  \
+      residual_norm_kernel<N, MODE, true><<<grid, 64 * nw, lds, s>>>(                          \
+          x, w_post, h, w_next, scalar, eps, rows, (int)dim, xq, dx, xb);                      \
+    else                                                                                       \
+      residual_norm_kernel<N, MODE, false><<<grid, 64 * nw, lds, s>>>(                         \
+          x, w_post, h, w_next, scalar, eps, rows, (int)dim, xq, dx, xb);                      \
+  } while (0)
 #define RES_CASE(N)                                                                            \
   case N:                                                                                      \
     if (mode == 0) RES_LAUNCH(N, 0);                                                           \
