@@ -417,11 +417,120 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   }
 }
 
+// The same layer boundary for few rows: one row per block of NV waves, wave
+// v holding float4 64 v + lane of the row (one per lane, where
+// residual_norm_kernel's single wave holds NV).  The chain lanes 0..7 of
+// every wave run the row's two reference-order chains from the block's
+// shared LDS copy (each wave gets inv itself, so no broadcast), and the
+// elementwise work, the quantization and the stores are split NV ways: at
+// 512 x 768 the row's waves fill 1536 SIMD slots instead of 512.  Each
+// chain reads its own staging buffer, so the second staging needs no
+// barrier in front of it.  Same arithmetic per element as
+// residual_norm_kernel, so the outputs are bit-identical.
+template <int NV, int NEXT>
+__global__ void __launch_bounds__(256)
+residual_norm_split_kernel(const float* __restrict__ x, const float* __restrict__ w_post,
+                           float* __restrict__ h, const float* __restrict__ w_next,
+                           const float* __restrict__ scalar, float eps, int dim,
+                           int8_t* __restrict__ xq, float* __restrict__ dx,
+                           uint16_t* __restrict__ xb) {
+  constexpr bool QNEXT = NEXT != 0;
+  constexpr bool CHAIN2 = NEXT == 1 || NEXT == 3;
+  // chain-major staging reaches index 7 S + dim / 8 = dim + 28
+  __shared__ __attribute__((aligned(16))) float lrow[CHAIN2 ? 2 : 1][NV * 256 + 32];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int n4 = dim >> 2;
+  const int S = chain_stride(dim);
+  const int c4 = lane + 64 * wv;
+  const bool ok = c4 < n4;
+  const v4f v = ok ? *reinterpret_cast<const v4f*>(x + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
+  const v4f hv = ok ? *reinterpret_cast<const v4f*>(h + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
+  const v4f wp = ok ? *reinterpret_cast<const v4f*>(w_post + 4 * c4) : v4f{0, 0, 0, 0};
+  const v4f wn = (QNEXT && w_next && ok) ? *reinterpret_cast<const v4f*>(w_next + 4 * c4)
+                                         : v4f{1, 1, 1, 1};
+  if (ok) stage_chains(lrow[0], S, c4, v);
+  __syncthreads();
+  const float inv = chain_row_inv<NV, true>(lrow[0], dim, lane, eps);
+  const float sv = scalar ? *scalar : 1.0f;
+  v4f nh;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float sum = hv[e] + (v[e] * inv) * wp[e];
+    nh[e] = scalar ? sum * sv : sum;
+  }
+  if (ok) {
+    *reinterpret_cast<v4f*>(h + row * dim + 4 * c4) = nh;
+    if (CHAIN2) stage_chains(lrow[CHAIN2 ? 1 : 0], S, c4, nh);
+  }
+  if constexpr (QNEXT) {
+    float inv2 = 1.0f;
+    if constexpr (CHAIN2) {
+      __syncthreads();
+      inv2 = chain_row_inv<NV, true>(lrow[1], dim, lane, eps);
+    }
+    v4f yv;
+    float am = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      if (NEXT == 2) yv[e] = nh[e];
+      else yv[e] = w_next ? (nh[e] * inv2) * wn[e] : nh[e] * inv2;
+      am = fmaxf(am, fabsf(yv[e]));
+    }
+    if constexpr (NEXT == 3) {
+      if (ok) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
+        dst[0] = bf16_rne(yv[0]) | (bf16_rne(yv[1]) << 16);
+        dst[1] = bf16_rne(yv[2]) | (bf16_rne(yv[3]) << 16);
+      }
+    } else {
+      const QScale sc = q8_scale(max8(am));
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
+      if (ok) {
+        *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed;
+        if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc.dq;
+      }
+    }
+  }
+}
+
+// Rows up to which the layer boundary runs one row per block of NV waves.
+inline bool residual_split(int64_t rows) { return rows <= 2048; }
+
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
                                 hipStream_t s, const float* scalar, bool plain_q, uint16_t* xb) {
   if (rows == 0) return hipSuccess;
   if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
+  if (residual_split(rows)) {
+    const int nv = (int)((dim + 255) / 256);
+    const int mode = xb != nullptr ? 3 : xq == nullptr ? 0 : (plain_q ? 2 : 1);
+#define RES_SPLIT(N, MODE)                                                                     \
+  residual_norm_split_kernel<N, MODE><<<(unsigned)rows, 64 * N, 0, s>>>(                       \
+      x, w_post, h, w_next, scalar, eps, (int)dim, xq, dx, xb)
+#define RES_SPLIT_CASE(N)                                                                      \
+  case N:                                                                                      \
+    if (mode == 0) RES_SPLIT(N, 0);                                                            \
+    else if (mode == 1) RES_SPLIT(N, 1);                                                       \
+    else if (mode == 2) RES_SPLIT(N, 2);                                                       \
+    else RES_SPLIT(N, 3);                                                                      \
+    break;
+    switch (nv) {
+      RES_SPLIT_CASE(1)
+      RES_SPLIT_CASE(2)
+      RES_SPLIT_CASE(3)
+      RES_SPLIT_CASE(4)
+      default:
+        return hipErrorInvalidValue;
+    }
+#undef RES_SPLIT_CASE
+#undef RES_SPLIT
+    return hipGetLastError();
+  }
   const int nw = norm_waves(rows);
   const unsigned grid = (unsigned)((rows + nw - 1) / nw);
   const size_t lds = (size_t)nw * (dim + 32) * sizeof(float);
