@@ -245,10 +245,79 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
   }
 }
 
+// Few rows (dim % 32 == 0, dim <= 1024): one row per block of NV waves,
+// wave v holding float4 64 v + lane, as residual_norm_split_kernel (below);
+// every wave's chain lanes run the row's chains from the block's LDS copy.
+// Same arithmetic per element as rmsnorm_row_kernel.  x may equal y.
+template <int NV, int MODE>
+__global__ void __launch_bounds__(256)
+rmsnorm_split_kernel(const float* x, const float* __restrict__ w, float eps, int dim, float* y,
+                     int8_t* __restrict__ xq, float* __restrict__ dx, uint16_t* __restrict__ xb) {
+  __shared__ __attribute__((aligned(16))) float lrow[NV * 256 + 32];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int n4 = dim >> 2;
+  const int c4 = lane + 64 * wv;
+  const bool ok = c4 < n4;
+  const v4f v = ok ? *reinterpret_cast<const v4f*>(x + row * dim + 4 * c4) : v4f{0, 0, 0, 0};
+  const v4f ww = (w && ok) ? *reinterpret_cast<const v4f*>(w + 4 * c4) : v4f{1, 1, 1, 1};
+  if (ok) stage_chains(lrow, chain_stride(dim), c4, v);
+  __syncthreads();
+  const float inv = chain_row_inv<NV, true>(lrow, dim, lane, eps);
+  v4f yv;
+#pragma unroll
+  for (int e = 0; e < 4; e++) yv[e] = w ? (v[e] * inv) * ww[e] : v[e] * inv;
+  if constexpr (MODE == OUT_F32) {
+    if (ok) *reinterpret_cast<v4f*>(y + row * dim + 4 * c4) = yv;
+  } else if constexpr (MODE == OUT_BF16) {
+    if (ok) {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
+      dst[0] = bf16_rne(yv[0]) | (bf16_rne(yv[1]) << 16);
+      dst[1] = bf16_rne(yv[2]) | (bf16_rne(yv[3]) << 16);
+    }
+  } else {
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) a = fmaxf(a, fabsf(yv[e]));
+    const QScale sc = q8_scale(max8(a));
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
+    if (ok) {
+      *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed;
+      if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc.dq;
+    }
+  }
+}
+
+// Rows up to which the row norms run one row per block of NV waves.
+inline bool norm_split(int64_t rows, int64_t dim) {
+  return rows <= 2048 && dim % 32 == 0 && dim <= 1024;
+}
+
 template <int MODE>
 static hipError_t launch_norm(const float* x, const float* w, float eps, int64_t rows, int64_t dim,
                               float* y, int8_t* xq, float* dx, uint16_t* xb, hipStream_t s) {
   if (rows == 0) return hipSuccess;
+  if (norm_split(rows, dim)) {
+    switch ((dim + 255) / 256) {
+#define NORM_SPLIT_CASE(N)                                                                    \
+  case N:                                                                                     \
+    rmsnorm_split_kernel<N, MODE><<<(unsigned)rows, 64 * N, 0, s>>>(x, w, eps, (int)dim, y,   \
+                                                                     xq, dx, xb);             \
+    break;
+      NORM_SPLIT_CASE(1)
+      NORM_SPLIT_CASE(2)
+      NORM_SPLIT_CASE(3)
+      NORM_SPLIT_CASE(4)
+#undef NORM_SPLIT_CASE
+      default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const int nw = norm_waves(rows);
   const unsigned grid = (unsigned)((rows + nw - 1) / nw);
   const size_t lds = (size_t)nw * (dim + 32) * sizeof(float);
@@ -498,15 +567,13 @@ residual_norm_split_kernel(const float* __restrict__ x, const float* __restrict_
   }
 }
 
-// Rows up to which the layer boundary runs one row per block of NV waves.
-inline bool residual_split(int64_t rows) { return rows <= 2048; }
 
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
                                 hipStream_t s, const float* scalar, bool plain_q, uint16_t* xb) {
   if (rows == 0) return hipSuccess;
   if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
-  if (residual_split(rows)) {
+  if (norm_split(rows, dim)) {
     const int nv = (int)((dim + 255) / 256);
     const int mode = xb != nullptr ? 3 : xq == nullptr ? 0 : (plain_q ? 2 : 1);
 #define RES_SPLIT(N, MODE)                                                                     \
