@@ -50,15 +50,12 @@ static hipError_t launch_rmsnorm_generic(const float* x, const float* w, float e
 // layout), and also written to LDS so that lanes 0..7 can run the reference's
 // eight sequential FMA chains (lane j: elements j, j+8, j+16, ...) from LDS.
 // The chains are the only serial part; quantization then uses all 64 lanes.
-// A block holds 1, 2 or 4 row waves: about one block per CU when rows are few
-// (512 rows: 256 blocks of 2 waves, measured ahead of 128 blocks of 4 and
-// 512 blocks of 1), 4 per block for long row counts.
+// A block holds 1, 2 or 4 row waves: about one block per CU when rows are few,
+// 4 per block for long row counts.  Up to 2048 rows of at most 1024 values
+// (dim % 32 == 0) the split kernels below take the row over NV waves
+// instead.
 constexpr int NORM_WAVES_MAX = 4;
 inline int norm_waves(int64_t rows) { return rows <= 256 ? 1 : rows <= 512 ? 2 : 4; }
-// Few rows: each chain lane reads its whole chain from LDS before the first
-// FMA (one LDS round trip, 32 NV registers); many rows: in batches of 12
-// chunks, which keeps the occupancy that hides the loads of other rows.
-inline bool norm_full_reads(int64_t rows) { return rows <= 2048; }
 
 enum NormOut { OUT_F32 = 0, OUT_Q8 = 1, OUT_BF16 = 2 };
 
@@ -134,7 +131,7 @@ __device__ __forceinline__ float chain_row_inv(const float* lrow, int dim, int l
 }
 
 // NV = float4s per lane = ceil(dim / 256).  dim % 4 == 0 (dim % 32 == 0 for Q8).
-template <int NV, int MODE, bool CHAIN, bool FULL>
+template <int NV, int MODE, bool CHAIN>
 __global__ void __launch_bounds__(64 * NORM_WAVES_MAX)
 rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64_t rows, int dim,
                    float* y, int8_t* __restrict__ xq, float* __restrict__ dx,
@@ -166,7 +163,7 @@ rmsnorm_row_kernel(const float* x, const float* __restrict__ w, float eps, int64
     }
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
-    inv = chain_row_inv<NV, FULL>(lrow, dim, lane, eps);
+    inv = chain_row_inv<NV, false>(lrow, dim, lane, eps);
   } else {
 #pragma unroll
     for (int i = 0; i < NV; i++) {
@@ -322,18 +319,15 @@ static hipError_t launch_norm(const float* x, const float* w, float eps, int64_t
   const unsigned grid = (unsigned)((rows + nw - 1) / nw);
   const size_t lds = (size_t)nw * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
-  const bool chain = dim % 32 == 0, full = norm_full_reads(rows);
+  const bool chain = dim % 32 == 0;
   switch (nv) {
 #define NORM_CASE(N, NK)                                                                      \
   case N:                                                                                     \
-    if (chain && full)                                                                        \
-      rmsnorm_row_kernel<NK, MODE, true, true><<<grid, 64 * nw, lds, s>>>(                    \
-          x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
-    else if (chain)                                                                           \
-      rmsnorm_row_kernel<NK, MODE, true, false><<<grid, 64 * nw, lds, s>>>(                   \
+    if (chain)                                                                                \
+      rmsnorm_row_kernel<NK, MODE, true><<<grid, 64 * nw, lds, s>>>(                          \
           x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
     else                                                                                      \
-      rmsnorm_row_kernel<NK, MODE, false, false><<<grid, 64 * nw, lds, s>>>(                  \
+      rmsnorm_row_kernel<NK, MODE, false><<<grid, 64 * nw, lds, s>>>(                         \
           x, w, eps, rows, (int)dim, y, xq, dx, xb);                                          \
     break;
     NORM_CASE(1, 1)
@@ -379,7 +373,7 @@ hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_
 // itself (the input of a projection that has no norm in front); 3 = bf16 of
 // RMSNorm(h; w_next) (dense-bf16 weights).  scalar (device, nullable):
 // forward_residual_add's layer_scalar, h = (h + n) * s.
-template <int NV, int NEXT, bool FULL>
+template <int NV, int NEXT>
 __global__ void __launch_bounds__(64 * NORM_WAVES_MAX)
 residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_post,
                      float* __restrict__ h, const float* __restrict__ w_next,
@@ -414,7 +408,7 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
-  const float inv = chain_row_inv<NV, FULL>(lrow, dim, lane, eps);
+  const float inv = chain_row_inv<NV, false>(lrow, dim, lane, eps);
   __builtin_amdgcn_wave_barrier();
   const float sv = scalar ? *scalar : 1.0f;
 #pragma unroll
@@ -436,7 +430,7 @@ residual_norm_kernel(const float* __restrict__ x, const float* __restrict__ w_po
       // the staging writes must land; the h stores need not
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       __builtin_amdgcn_wave_barrier();
-      inv2 = chain_row_inv<NV, FULL>(lrow, dim, lane, eps);
+      inv2 = chain_row_inv<NV, false>(lrow, dim, lane, eps);
     }
     // all NV chunks' scales first (independent chains the scheduler can
     // interleave), then the stores
@@ -603,16 +597,9 @@ hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, c
   const size_t lds = (size_t)nw * (dim + 32) * sizeof(float);
   const int nv = (int)((dim + 255) / 256);
   const int mode = xb != nullptr ? 3 : xq == nullptr ? 0 : (plain_q ? 2 : 1);
-  const bool full = norm_full_reads(rows);
 #define RES_LAUNCH(N, MODE)                                                                    \
-  do {                                                                                         \
-    if (full)                                                                                  \
-      residual_norm_kernel<N, MODE, true><<<grid, 64 * nw, lds, s>>>(                          \
-          x, w_post, h, w_next, scalar, eps, rows, (int)dim, xq, dx, xb);                      \
-    else                                                                                       \
-      residual_norm_kernel<N, MODE, false><<<grid, 64 * nw, lds, s>>>(                         \
-          x, w_post, h, w_next, scalar, eps, rows, (int)dim, xq, dx, xb);                      \
-  } while (0)
+  residual_norm_kernel<N, MODE><<<grid, 64 * nw, lds, s>>>(x, w_post, h, w_next, scalar, eps,  \
+                                                          rows, (int)dim, xq, dx, xb)
 #define RES_CASE(N)                                                                            \
   case N:                                                                                      \
     if (mode == 0) RES_LAUNCH(N, 0);                                                           \
