@@ -564,6 +564,209 @@ inline bool small_ok(int64_t M, int64_t Nrows, int64_t K) {
 }
 
 // ---------------------------------------------------------------------------
+// GeGLU gate/up for few rows, one 16-column MFMA tile per wave whose columns
+// are 8 gate rows of W and the 8 matching up rows: a wave owns 16 rows x 8 h
+// columns and a workgroup of four waves one whole Q8_0 block of h (16 rows x
+// 32 h columns).  The exact epilogue's VALU work binds these launches, so
+// what matters is the work of the busiest SIMD: at M = 512, F = 1152 this is
+// 4608 waves on 1024 SIMDs (at most 5 where the mean is 4.5), where 16 h
+// columns per wave (gemm_i8_small_kernel's GeGLU tile) give 2304 waves (at
+// most 3 where the mean is 2.25).
+//   Gate and up of one h column meet in lanes j and j + 8 of a 16-lane row;
+// one DPP row rotation by 8 trades them so that lane j < 8 holds rows
+// 4 lq, 4 lq + 1 and lane j + 8 rows 4 lq + 2, 4 lq + 3 of that column, and
+// every lane evaluates two h values.  A row's 32-wide amax is 8 lanes of
+// each of the four waves, merged through LDS after one barrier.
+//   Ring and scales as gemm_i8_small_kernel: A rows (16) then B rows (64) per
+// 128-byte K stage, ten 1 KB DMA units per stage, three for waves 0 and 1
+// and two for waves 2 and 3.  Same arithmetic per output, so Q8_0(h) is
+// bit-identical to gemm_i8_small_kernel's GeGLU route.
+// ---------------------------------------------------------------------------
+template <bool F2, int RING, int NB>
+__global__ void __launch_bounds__(256)
+gemm_i8_geglu8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
+                      const int8_t* __restrict__ B, const float* __restrict__ dB,
+                      int8_t* __restrict__ Hq, float* __restrict__ dH, int M, int F) {
+  constexpr int K = NB * QK, NST = NB / KB;
+  constexpr int NW = 4, BM = 16, BN = 64;
+  constexpr int UA = BM / 8, UB = BN / 8, UN = UA + UB;   // 2 + 8 DMA units per stage
+  constexpr int SA = NB * BM, SB = NB * BN;
+  static_assert(NB % KB == 0 && NB <= SMALL_NB_MAX, "K must be a multiple of 128, <= 2048");
+  static_assert(RING >= 2, "ring needs >= 2 slots");
+  constexpr int SLOT = (BM + BN) * BK;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING * SLOT];
+  __shared__ __attribute__((aligned(16))) float sc[SA + SB + 256];
+  __shared__ float amax_w[NW][BM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hb = blockIdx.x;            // Q8_0 block of h: columns 32 hb ..
+  const int m0 = blockIdx.y * BM;
+  const int hc0 = hb * QK;
+  // B row of tile-local row nl: wave nl / 16, gate (nl % 16 < 8) or up
+  auto b_row = [&](int nl) -> int {
+    const int c = hc0 + 8 * (nl >> 4) + (nl & 7);
+    return (nl & 8) ? F + c : c;
+  };
+
+  constexpr int NQ = NB / 4;
+  constexpr int SCH = (SA + SB) / 4;
+  for (int c0 = wave * 64; c0 < SCH; c0 += NW * 64) {
+    const int c = c0 + lane < SCH ? c0 + lane : SCH - 1;
+    const float* src;
+    if (c < SA / 4) {
+      const int r = c / NQ, q = c - r * NQ;
+      const int gm = m0 + r < M ? m0 + r : M - 1;
+      src = dA + (int64_t)gm * NB + 4 * q;
+    } else {
+      const int f = c - SA / 4, r = f / NQ, q = f - r * NQ;
+      src = dB + (int64_t)b_row(r) * NB + 4 * q;
+    }
+    dma16_flat(src, lds_u32(sc + 4 * c0));
+  }
+  // DMA units u = wave, wave + 4, wave + 8 (< UN): three for waves 0, 1
+  const int rsub = lane >> 3, pch = lane & 7;
+  const bool three = wave + 8 < UN;
+  const int8_t* ubase[3];
+  int uvoff[3];
+#pragma unroll
+  for (int j = 0; j < 3; j++) {
+    const int u = j * NW + wave < UN ? j * NW + wave : UN - 1;
+    const int row = (u < UA ? u : u - UA) * 8 + rsub;
+    const int grow = u < UA ? (m0 + row < M ? m0 + row : M - 1) : b_row(row);
+    ubase[j] = u < UA ? A : B;
+    uvoff[j] = grow * K + ((pch ^ (row & 7)) << 4);
+  }
+  auto issue = [&](int st, int slot) {
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+      if (j < 2 || three)
+        dma16(ubase[j] + st * BK, uvoff[j],
+              lds_u32(ring + slot * SLOT + (j * NW + wave) * 1024));
+  };
+#pragma unroll
+  for (int st = 0; st < RING - 1; st++)
+    if (st < NST) issue(st, st);
+
+  const int l16 = lane & 15, lq = lane >> 4;
+  int offA[KB], offB[KB];
+#pragma unroll
+  for (int kb = 0; kb < KB; kb++) {
+    const int ch = 2 * kb + (lq >> 1);
+    offA[kb] = l16 * BK + ((ch ^ (l16 & 7)) << 4) + ((lq & 1) << 3);
+    const int brow = wave * 16 + l16;
+    offB[kb] = (BM + brow) * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+  }
+  const float* xrow = sc + (4 * lq) * NB;
+  const float* wrow = sc + SA + (wave * 16 + l16) * NB;
+  const v4i magic = {MAGIC, MAGIC, MAGIC, MAGIC};
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll 1
+  for (int g = 0; g < NST; g += RING) {
+#pragma unroll
+    for (int r = 0; r < RING; r++) {
+      const int st = g + r;
+      if (st < NST) {
+        const int later = (st + RING - 2 < NST - 1 ? st + RING - 2 : NST - 1) - st;
+        if (three)
+          vm_wait_units<3, RING - 2>(later);
+        else
+          vm_wait_units<2, RING - 2>(later);
+        __syncthreads();
+        if (st + RING - 1 < NST) issue(st + RING - 1, (r + RING - 1) % RING);
+        const uint8_t* slot = ring + r * SLOT;
+        v4i d[KB];
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+          const v1l af = *reinterpret_cast<const v1l*>(slot + offA[kb]);
+          const v1l bf = *reinterpret_cast<const v1l*>(slot + offB[kb]);
+          d[kb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(af, bf, magic, 0, 0, 0);
+        }
+        v4f xq[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++)
+          xq[rr] = *reinterpret_cast<const v4f*>(xrow + rr * NB + st * KB);
+        const v4f wq = *reinterpret_cast<const v4f*>(wrow + st * KB);
+#pragma unroll
+        for (int kb = 0; kb < KB; kb++) {
+          const float wd = wq[kb];
+          const float wc = wd * NEG_MAGIC;
+#pragma unroll
+          for (int rr = 0; rr < 4; rr++)
+            acc[rr] = q8_term<F2>(acc[rr], d[kb][rr], wd, wc, xq[rr][kb]);
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // lane j < 8: gate rows 4 lq .. 4 lq + 3 of column j; lane j + 8: up rows
+  const bool hi = (l16 & 8) != 0;
+  const float s0 = hi ? acc[0] : acc[2];
+  const float s1 = hi ? acc[1] : acc[3];
+  const float r0 = dpp_mov<0x128>(s0, s0);   // row_ror:8 (lane j <-> j ^ 8)
+  const float r1 = dpp_mov<0x128>(s1, s1);
+  const float g0 = hi ? r0 : acc[0], g1 = hi ? r1 : acc[1];
+  const float u0 = hi ? acc[2] : r0, u1 = hi ? acc[3] : r1;
+  float h[2];
+  h[0] = geglu_scalar(g0, u0);
+  h[1] = geglu_scalar(g1, u1);
+  // rows of h[e]: 4 lq + 2 hi + e; their 8 columns of this wave are one
+  // aligned group of 8 lanes
+  const int rbase = 4 * lq + (hi ? 2 : 0);
+#pragma unroll
+  for (int e = 0; e < 2; e++) {
+    const float v = max8_nonneg(fmaxf(0.0f, fabsf(h[e])));
+    if ((l16 & 7) == 0) amax_w[wave][rbase + e] = v;
+  }
+  __syncthreads();
+  // lane 8 k + e' of a group derives the scale of row rbase + (e' & 1)
+  const int rs = rbase + (l16 & 1);
+  const QScale q =
+      q8_scale(fmaxf(fmaxf(amax_w[0][rs], amax_w[1][rs]), fmaxf(amax_w[2][rs], amax_w[3][rs])));
+  const float id0 = bcast8<0>(q.id), id1 = bcast8<1>(q.id);
+  const int hc = hc0 + 8 * wave + (l16 & 7);
+  const int nbh = F / QK;
+  if (m0 + rbase < M) Hq[(int64_t)(m0 + rbase) * F + hc] = (int8_t)quant_round(h[0] * id0);
+  if (m0 + rbase + 1 < M) Hq[(int64_t)(m0 + rbase + 1) * F + hc] = (int8_t)quant_round(h[1] * id1);
+  if (wave == 0 && (l16 & 7) < 2 && m0 + rs < M) dH[(int64_t)(m0 + rs) * nbh + hb] = q.dq;
+}
+
+template <bool F2, int RING, int NB>
+hipError_t run_geglu8_nb(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                         int8_t* hq, float* dh, int64_t M, int64_t F, hipStream_t s) {
+  dim3 grid((unsigned)(F / QK), (unsigned)((M + 15) / 16));
+  gemm_i8_geglu8_kernel<F2, RING, NB><<<grid, 256, 0, s>>>(xq, dx, wq, dw, hq, dh, (int)M,
+                                                            (int)F);
+  return hipGetLastError();
+}
+
+template <bool F2, int RING>
+hipError_t run_geglu8(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                      int8_t* hq, float* dh, int64_t M, int64_t F, int64_t K, hipStream_t s) {
+#define GLYPR_GEGLU8_NB(nb) \
+  case nb:                  \
+    return run_geglu8_nb<F2, RING, nb>(xq, dx, wq, dw, hq, dh, M, F, s);
+  switch (K / QK) {
+    GLYPR_GEGLU8_NB(4)
+    GLYPR_GEGLU8_NB(8)
+    GLYPR_GEGLU8_NB(12)
+    GLYPR_GEGLU8_NB(16)
+    GLYPR_GEGLU8_NB(20)
+    GLYPR_GEGLU8_NB(24)
+    GLYPR_GEGLU8_NB(28)
+    GLYPR_GEGLU8_NB(32)
+    GLYPR_GEGLU8_NB(36)
+    GLYPR_GEGLU8_NB(48)
+    GLYPR_GEGLU8_NB(64)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef GLYPR_GEGLU8_NB
+}
+
+// ---------------------------------------------------------------------------
 // Small-M GEMM with the activation prologue fused (one launch per op): the
 // workgroup reads its 16 rows of f32 x and builds their Q8_0 operand in LDS
 // itself, while the weight stages stream in by LDS DMA.
@@ -1567,6 +1770,7 @@ hipError_t geglu_i8_routed(const int8_t* xq, const float* dx, const int8_t* wq, 
                            hipStream_t s) {
   switch (gemm_i8_route(M, 2 * F, K)) {
     case GEMM_ROUTE_SMALL:
+      if (F % QK == 0) return run_geglu8<F2, 2>(xq, dx, wq, dw, hq, dh, M, F, K, s);
       return run_small<2, 2, 2, true, F2, 3>(xq, dx, wq, dw, nullptr, hq, dh, M, 2 * F, K, 0, F,
                                              s);
     case GEMM_ROUTE_BIG:
