@@ -107,6 +107,13 @@ hipError_t launch_gather(const int8_t* qs, const float* dw, int64_t k, const uin
 // the kernel arguments, so the ids need no device copy): rows of width k with
 // k % 32 == 0 and k <= 1024, at most GATHER_ARG_IDS ids.
 constexpr int GATHER_ARG_IDS = 768;
+// Ids carried by value in the kernel arguments (up to GATHER_ARG_IDS of
+// them, 3 KB): the launch needs no device copy of the ids, so the caller's
+// host array is read when the launch is enqueued and nothing waits on it.
+struct GatherIds {
+  uint32_t v[GATHER_ARG_IDS];
+  __device__ uint32_t operator[](int64_t i) const { return v[i]; }
+};
 bool gather_host_ids_ok(int64_t k, int64_t n_ids);
 hipError_t launch_gather_host_ids(const int8_t* qs, const float* dw, int64_t k,
                                   const uint32_t* host_ids, int64_t n_ids, float scale, float* out,
@@ -122,6 +129,16 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float eps, float* y, i
                           int64_t dim, hipStream_t s);
 hipError_t launch_rmsnorm_quant(const float* x, const float* w, float eps, int64_t rows,
                                 int64_t dim, int8_t* xq, float* dx, hipStream_t s);
+// The token gather x scale (launch_gather's arithmetic) and the first input
+// RMSNorm + Q8_0 (launch_rmsnorm_quant's) in one launch: writes the gathered
+// rows to h and their normalised Q8_0 to xq / dx.  Ids from host memory
+// (host_ids, at most GATHER_ARG_IDS) or device memory (dev_ids).  Only for
+// gather_norm_ok shapes.
+bool gather_norm_ok(int64_t rows, int64_t dim);
+hipError_t launch_gather_norm(const int8_t* qs, const float* dw, int64_t dim,
+                              const uint32_t* host_ids, const uint32_t* dev_ids, int64_t rows,
+                              float scale, const float* w, float eps, float* h, int8_t* xq,
+                              float* dx, hipStream_t s);
 hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_t rows,
                                int64_t dim, uint16_t* xb, hipStream_t s);
 hipError_t launch_geglu(const float* g, const float* u, float* out, int64_t n, hipStream_t s);
@@ -142,11 +159,13 @@ hipError_t launch_pool_segments(const float* tok, int64_t rows, const int32_t* s
 // scalar (device, nullable): h = (h + RMSNorm(x)) * scalar.  plain_q: xq/dx
 // receive Q8_0 of h itself instead of Q8_0 of RMSNorm(h; w_next).
 // xb (nullable, instead of xq): bf16 of RMSNorm(h; w_next), the next dense-bf16
-// GEMM's operand.
+// GEMM's operand.  yf (nullable, instead of xq and xb): f32 RMSNorm(h; w_next),
+// the model's final norm.
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
                                 hipStream_t s, const float* scalar = nullptr,
-                                bool plain_q = false, uint16_t* xb = nullptr);
+                                bool plain_q = false, uint16_t* xb = nullptr,
+                                float* yf = nullptr);
 // x = x * mul + 0 (f32), in place
 hipError_t launch_affine(float* x, int64_t n, float mul, hipStream_t s);
 // Q8_0 of geglu(g, u): g [rows][dim], u row r at u + r * u_stride

@@ -115,14 +115,6 @@ hipError_t launch_dequant(const int8_t* qs, const float* dw, int64_t rows, int64
 // ---------------------------------------------------------------------------
 constexpr int GATHER_ROWS = 8;
 
-// Ids carried by value in the kernel arguments (up to GATHER_ARG_IDS of
-// them, 3 KB): the launch needs no device copy of the ids, so the caller's
-// host array is read when the launch is enqueued and nothing waits on it.
-struct GatherIds {
-  uint32_t v[GATHER_ARG_IDS];
-  __device__ uint32_t operator[](int64_t i) const { return v[i]; }
-};
-
 template <class Ids>
 __global__ void __launch_bounds__(256) gather_rows_kernel(const int8_t* __restrict__ qs,
                                                           const float* __restrict__ dw, int k,

@@ -11,6 +11,8 @@
 #include "device_common.hpp"
 #include "internal.hpp"
 
+#include <cstring>
+
 namespace glypr {
 
 // Fallback for dims that are not a multiple of 4 or exceed 2048: eight lanes
@@ -361,6 +363,91 @@ hipError_t launch_rmsnorm_bf16(const float* x, const float* w, float eps, int64_
   return launch_norm<OUT_BF16>(x, w, eps, rows, dim, nullptr, nullptr, nullptr, xb, s);
 }
 
+// The model's first boundary for few rows: Embedding::forward x embed_scale
+// (model.rs:254-255, 507-508) and layer 0's input RMSNorm + Q8_0 in one
+// launch, one row per block of NV waves as rmsnorm_split_kernel.  Lane
+// (wave v, lane l) dequantizes float4 64 v + l of table row ids[row] with
+// gather_rows_kernel's arithmetic ((float)q * d, then * scale + 0), writes it
+// to h and stages it for the reference-order chains; the rest is
+// rmsnorm_split_kernel<NV, OUT_Q8>.  Bit-identical to the two launches.
+template <int NV, class Ids>
+__global__ void __launch_bounds__(256)
+gather_norm_split_kernel(const int8_t* __restrict__ qs, const float* __restrict__ dw, Ids ids,
+                         float scale, const float* __restrict__ w, float eps, int dim,
+                         float* __restrict__ h, int8_t* __restrict__ xq, float* __restrict__ dx) {
+  __shared__ __attribute__((aligned(16))) float lrow[NV * 256 + 32];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;
+  const int n4 = dim >> 2;
+  const int c4 = lane + 64 * wv;
+  const bool ok = c4 < n4;
+  const int64_t src = (int64_t)ids[row];
+  const int q = ok ? *reinterpret_cast<const int*>(qs + src * dim + 4 * c4) : 0;
+  const float d = ok ? dw[src * (dim / QK) + (c4 >> 3)] : 0.0f;
+  const v4f ww = (w && ok) ? *reinterpret_cast<const v4f*>(w + 4 * c4) : v4f{1, 1, 1, 1};
+  v4f v;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float y = (float)(int8_t)((q >> (8 * e)) & 0xFF) * d;
+    v[e] = y * scale + 0.0f;
+  }
+  if (ok) {
+    *reinterpret_cast<v4f*>(h + row * dim + 4 * c4) = v;
+    stage_chains(lrow, chain_stride(dim), c4, v);
+  }
+  __syncthreads();
+  const float inv = chain_row_inv<NV, true>(lrow, dim, lane, eps);
+  v4f yv;
+  float a = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    yv[e] = w ? (v[e] * inv) * ww[e] : v[e] * inv;
+    a = fmaxf(a, fabsf(yv[e]));
+  }
+  const QScale sc = q8_scale(max8(a));
+  uint32_t packed = 0;
+#pragma unroll
+  for (int e = 0; e < 4; e++)
+    packed |= ((uint32_t)(quant_round(yv[e] * sc.id) & 0xFF)) << (8 * e);
+  if (ok) {
+    *reinterpret_cast<uint32_t*>(xq + row * dim + 4 * c4) = packed;
+    if ((lane & 7) == 0) dx[row * (dim / QK) + (c4 >> 3)] = sc.dq;
+  }
+}
+
+bool gather_norm_ok(int64_t rows, int64_t dim) { return rows > 0 && norm_split(rows, dim); }
+
+hipError_t launch_gather_norm(const int8_t* qs, const float* dw, int64_t dim,
+                              const uint32_t* host_ids, const uint32_t* dev_ids, int64_t rows,
+                              float scale, const float* w, float eps, float* h, int8_t* xq,
+                              float* dx, hipStream_t s) {
+  if (!gather_norm_ok(rows, dim) || (host_ids && rows > GATHER_ARG_IDS) ||
+      (!host_ids && !dev_ids))
+    return hipErrorInvalidValue;
+  GatherIds arg;
+  if (host_ids) memcpy(arg.v, host_ids, (size_t)rows * 4);
+  switch ((dim + 255) / 256) {
+#define GATHER_NORM_CASE(N)                                                                    \
+  case N:                                                                                      \
+    if (host_ids)                                                                              \
+      gather_norm_split_kernel<N, GatherIds><<<(unsigned)rows, 64 * N, 0, s>>>(                \
+          qs, dw, arg, scale, w, eps, (int)dim, h, xq, dx);                                    \
+    else                                                                                       \
+      gather_norm_split_kernel<N, const uint32_t*><<<(unsigned)rows, 64 * N, 0, s>>>(          \
+          qs, dw, dev_ids, scale, w, eps, (int)dim, h, xq, dx);                                \
+    break;
+    GATHER_NORM_CASE(1)
+    GATHER_NORM_CASE(2)
+    GATHER_NORM_CASE(3)
+    GATHER_NORM_CASE(4)
+#undef GATHER_NORM_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Layer boundary: RMSNorm::forward_residual_add (norm.rs:65-95),
 //   h = h + rmsnorm(x; w_post),
@@ -496,9 +583,9 @@ residual_norm_split_kernel(const float* __restrict__ x, const float* __restrict_
                            float* __restrict__ h, const float* __restrict__ w_next,
                            const float* __restrict__ scalar, float eps, int dim,
                            int8_t* __restrict__ xq, float* __restrict__ dx,
-                           uint16_t* __restrict__ xb) {
+                           uint16_t* __restrict__ xb, float* __restrict__ yf) {
   constexpr bool QNEXT = NEXT != 0;
-  constexpr bool CHAIN2 = NEXT == 1 || NEXT == 3;
+  constexpr bool CHAIN2 = NEXT == 1 || NEXT == 3 || NEXT == 4;
   // chain-major staging reaches index 7 S + dim / 8 = dim + 28
   __shared__ __attribute__((aligned(16))) float lrow[CHAIN2 ? 2 : 1][NV * 256 + 32];
   const int lane = threadIdx.x & 63;
@@ -541,7 +628,9 @@ residual_norm_split_kernel(const float* __restrict__ x, const float* __restrict_
       else yv[e] = w_next ? (nh[e] * inv2) * wn[e] : nh[e] * inv2;
       am = fmaxf(am, fabsf(yv[e]));
     }
-    if constexpr (NEXT == 3) {
+    if constexpr (NEXT == 4) {
+      if (ok) *reinterpret_cast<v4f*>(yf + row * dim + 4 * c4) = yv;
+    } else if constexpr (NEXT == 3) {
       if (ok) {
         uint32_t* dst = reinterpret_cast<uint32_t*>(xb + row * dim + 4 * c4);
         dst[0] = bf16_rne(yv[0]) | (bf16_rne(yv[1]) << 16);
@@ -564,21 +653,30 @@ residual_norm_split_kernel(const float* __restrict__ x, const float* __restrict_
 
 hipError_t launch_residual_norm(const float* x, const float* w_post, float* h, const float* w_next,
                                 float eps, int64_t rows, int64_t dim, int8_t* xq, float* dx,
-                                hipStream_t s, const float* scalar, bool plain_q, uint16_t* xb) {
+                                hipStream_t s, const float* scalar, bool plain_q, uint16_t* xb,
+                                float* yf) {
   if (rows == 0) return hipSuccess;
   if (dim % 32 != 0 || dim > 1024) return hipErrorInvalidValue;
+  if (yf && !norm_split(rows, dim)) {
+    // the final norm as its own launch
+    const hipError_t e = launch_residual_norm(x, w_post, h, nullptr, eps, rows, dim, nullptr,
+                                              nullptr, s, scalar);
+    return e != hipSuccess ? e : launch_rmsnorm(h, w_next, eps, yf, rows, dim, s);
+  }
   if (norm_split(rows, dim)) {
     const int nv = (int)((dim + 255) / 256);
-    const int mode = xb != nullptr ? 3 : xq == nullptr ? 0 : (plain_q ? 2 : 1);
+    const int mode =
+        yf != nullptr ? 4 : xb != nullptr ? 3 : xq == nullptr ? 0 : (plain_q ? 2 : 1);
 #define RES_SPLIT(N, MODE)                                                                     \
   residual_norm_split_kernel<N, MODE><<<(unsigned)rows, 64 * N, 0, s>>>(                       \
-      x, w_post, h, w_next, scalar, eps, (int)dim, xq, dx, xb)
+      x, w_post, h, w_next, scalar, eps, (int)dim, xq, dx, xb, yf)
 #define RES_SPLIT_CASE(N)                                                                      \
   case N:                                                                                      \
     if (mode == 0) RES_SPLIT(N, 0);                                                            \
     else if (mode == 1) RES_SPLIT(N, 1);                                                       \
     else if (mode == 2) RES_SPLIT(N, 2);                                                       \
-    else RES_SPLIT(N, 3);                                                                      \
+    else if (mode == 3) RES_SPLIT(N, 3);                                                       \
+    else RES_SPLIT(N, 4);                                                                      \
     break;
     switch (nv) {
       RES_SPLIT_CASE(1)

@@ -452,7 +452,17 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
 
   // model.rs:507-508: Embedding::forward, then * embed_scale (f64 sqrt(hidden) as f32)
   const float embed_scale = (float)sqrt((double)H);
-  if (rows.host_ids)
+  const int64_t P = c.ple_dim, NL = c.n_layers;
+  // Without PLE the gather and layer 0's input norm run as one launch (the
+  // PLE projection would need xq for its own operand in between).
+  const bool gather_norm = P == 0 && !m->dense && gather_norm_ok(t, H);
+  if (gather_norm)
+    LAUNCH(GLYPR_K_GATHER, s,
+           launch_gather_norm(m->token_embd.w->qs(), m->token_embd.w->dw(), H, rows.host_ids,
+                              rows.host_ids ? nullptr : m->ids.as<uint32_t>(), t, embed_scale,
+                              m->layers[0].input_layernorm.weight, c.eps, h, xq, dx, s),
+           "gather + input norm launch");
+  else if (rows.host_ids)
     LAUNCH(GLYPR_K_GATHER, s,
            launch_gather_host_ids(m->token_embd.w->qs(), m->token_embd.w->dw(), H, rows.host_ids,
                                   t, embed_scale, h, s),
@@ -465,7 +475,6 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
   // TextPLE::project_and_norm_per_layer (ple.rs:48-85): per_layer_model_proj of
   // the scaled embeddings, * hidden^-0.5 (f64 powf, applied as candle's f32
   // affine), RMSNorm over ple_dim.  Layer l's input is row t*NL + l of [t*NL][P].
-  const int64_t P = c.ple_dim, NL = c.n_layers;
   float* ple = dev_f32(m->ple);
   if (P > 0) {
     LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(h, t, H, xq, dx, s), "quantize launch");
@@ -480,9 +489,15 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
   }
   if (m->dense) return forward_dense(m, ctx, rows, hidden, tokens_out, s);
   // layer 0 input_layernorm as the qkv GEMM's prologue
-  LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
-         launch_rmsnorm_quant(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xq, dx, s),
-         "rmsnorm_quant launch");
+  if (!gather_norm)
+    LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
+           launch_rmsnorm_quant(h, m->layers[0].input_layernorm.weight, c.eps, t, H, xq, dx, s),
+           "rmsnorm_quant launch");
+  // model.rs:576-577: the final norm rides on the last layer's residual launch:
+  // into xq / dx for the embedding projection, else as f32 token rows
+  float* tokens = hidden;
+  if (!tokens) tokens = dev_f32(c.out_dim > 0 ? m->tokens : m->normed);
+  float* final_f32 = c.out_dim > 0 ? nullptr : tokens;
 
   for (size_t li = 0; li < m->layers.size(); li++) {
     EncoderLayer& L = m->layers[li];
@@ -541,13 +556,17 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
            launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wd->qs(), wd->dw(),
                           dev_f32(m->proj), t, H, F, H, s),
            "down gemm launch");
-    const float* w_next = last ? nullptr : m->layers[li + 1].input_layernorm.weight;
+    // next layer's input norm, or after the last layer the final norm
+    const float* w_next = last ? m->norm.weight : m->layers[li + 1].input_layernorm.weight;
+    int8_t* q_next = last && final_f32 ? nullptr : xq;
+    float* d_next = last && final_f32 ? nullptr : dx;
+    float* y_next = last ? final_f32 : nullptr;
     if (P == 0) {
       // post_feedforward_layernorm.forward_residual_add + next layer's input norm
       LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
              launch_residual_norm(dev_f32(m->proj), L.post_feedforward_layernorm.weight, h,
-                                  w_next, c.eps, t, H, last ? nullptr : xq, last ? nullptr : dx,
-                                  s),
+                                  w_next, c.eps, t, H, q_next, d_next, s, nullptr, false, nullptr,
+                                  y_next),
              "residual_norm launch");
       continue;
     }
@@ -574,25 +593,16 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     // post_norm.forward_residual_add(.., layer_scalar) + next layer's input norm
     LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
            launch_residual_norm(dev_f32(m->proj), L.ple_block.norm.weight, h, w_next, c.eps, t, H,
-                                last ? nullptr : xq, last ? nullptr : dx, s,
-                                L.ple_block.layer_scalar, false),
+                                q_next, d_next, s, L.ple_block.layer_scalar, false, nullptr,
+                                y_next),
            "residual_norm launch");
   }
-  // model.rs:576-577: final norm, then the embedding projection when present
-  float* tokens = hidden;
+  // then the embedding projection when present
   if (c.out_dim > 0) {
-    if (!tokens) tokens = dev_f32(m->tokens);
-    LAUNCH(GLYPR_K_RMSNORM_QUANT, s,
-           launch_rmsnorm_quant(h, m->norm.weight, c.eps, t, H, xq, dx, s),
-           "rmsnorm_quant launch");
     const glypr_q8w* we = m->embedding_projection.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
            launch_gemm_i8(xq, dx, we->qs(), we->dw(), tokens, t, c.out_dim, H, c.out_dim, s),
            "embedding projection launch");
-  } else {
-    if (!tokens) tokens = dev_f32(m->normed);
-    LAUNCH(GLYPR_K_RMSNORM, s, launch_rmsnorm(h, m->norm.weight, c.eps, tokens, t, H, s),
-           "final rmsnorm launch");
   }
   *tokens_out = tokens;
   return GLYPR_OK;
