@@ -1396,6 +1396,25 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
     for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
 
+  // q / k epilogue operands of this wave's rows 2 w, 2 w + 1 (dims 4 l ..):
+  // the norm weight and the RoPE rows, loaded now so that their latency
+  // passes under the K loop
+  const bool qk_slot = slot < nq + nkv;
+  v4f ep_w = {1.0f, 1.0f, 1.0f, 1.0f}, ep_cos[2], ep_sin[2];
+  bool ep_valid[2];
+  if (qk_slot) {
+    const float* w = slot < nq ? qnw : knw;
+    if (w) ep_w = *reinterpret_cast<const v4f*>(w + 4 * lane);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const int pos = seg_row_pos(seg, m0 + 2 * wave + k, T, &ep_valid[k]);
+      ep_cos[k] = ep_valid[k] ? *reinterpret_cast<const v4f*>(cos_t + (int64_t)pos * QKV_HD + 4 * lane)
+                              : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      ep_sin[k] = ep_valid[k] ? *reinterpret_cast<const v4f*>(sin_t + (int64_t)pos * QKV_HD + 4 * lane)
+                              : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+
 #pragma unroll 1
   for (int g = 0; g < NST; g += QKV_RING) {
 #pragma unroll
@@ -1466,7 +1485,7 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     return 1.0f / sqrtf(sum / (float)QKV_HD + eps);   // valid on lanes 8 c
   };
 
-  if (slot < nq + nkv) {
+  if (qk_slot) {
     // q / k: wave w handles rows 2 w and 2 w + 1; lane l holds dims 4 l .. 4 l + 3
     const bool is_q = slot < nq;
     const int head = is_q ? slot : slot - nq;
@@ -1476,21 +1495,20 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     const float invp = row_inv(2 * wave + ((lane >> 3) & 1));
     const float inv0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(invp), 0));
     const float inv1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(invp), 8));
-    const v4f wv = w ? *reinterpret_cast<const v4f*>(w + 4 * lane) : v4f{1, 1, 1, 1};
+    const v4f wv = ep_w;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
       const int i = 2 * wave + k;
       const int t = m0 + i;
-      bool valid;
-      const int pos = seg_row_pos(seg, t, T, &valid);
+      const bool valid = ep_valid[k];
       const float inv = k == 0 ? inv0 : inv1;
       const v4f x = *reinterpret_cast<const v4f*>(stg + i * QKV_SP + 4 * lane);
       float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (valid) {
 #pragma unroll
         for (int e = 0; e < 4; e++) y[e] = w ? (x[e] * inv) * wv[e] : x[e] * inv;
-        const v4f cv = *reinterpret_cast<const v4f*>(cos_t + (int64_t)pos * QKV_HD + 4 * lane);
-        const v4f sv = *reinterpret_cast<const v4f*>(sin_t + (int64_t)pos * QKV_HD + 4 * lane);
+        const v4f cv = ep_cos[k];
+        const v4f sv = ep_sin[k];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           // lanes l and l ^ 32 hold dims d and d +- 128 (rotate_half's pairs)
