@@ -116,12 +116,24 @@ def test_noalloc_matmul_rejects_overlap_on_another_stream():
                   ctypes.c_void_p(y.data_ptr()), m, INT8_EXACT,
                   ctypes.c_void_p(stream.cuda_stream))
 
-    say("no-alloc overlap: stream A held by a spin kernel, then a call on A and one on B")
+    # the spin kernel counts GPU clock ticks: time a short spin first, so the
+    # hold below lasts ~300 ms of wall time whatever the clock runs at
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(sa):
-        torch.cuda._sleep(100_000_000)      # bounded: ~50 ms of GPU clocks
+        e0.record()
+        torch.cuda._sleep(10_000_000)
+        e1.record()
+    e1.synchronize()
+    ticks_per_ms = 10_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    hold = int(min(max(300 * ticks_per_ms, 1e7), 4e9))
+    say(f"no-alloc overlap: stream A held by a {hold}-tick spin (~300 ms), then a call on A "
+        "and one on B")
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(hold)
     assert call(ya, sa) == _lib.GLYPR_OK
     assert call(ya, sa) == _lib.GLYPR_OK    # the same stream: ordered, accepted
     rc = call(yb, sb)
+    assert not sa.query(), "stream A finished before B's call: the hold did not cover it"
     assert rc == _lib.GLYPR_ERR_BUSY, (rc, _lib.last_error())
     assert "another stream" in _lib.last_error()
     sa.synchronize()
