@@ -203,8 +203,11 @@ __device__ __forceinline__ void dma4(const int8_t* base, int voff, uint32_t lds_
 // N tiles (an XCD reads its slice of B once and all of A: 8*A + B bytes from
 // memory), otherwise whole rows of M tiles (A + 8*B).  The caller picks the
 // order that re-reads the smaller operand.
+// The grid is exactly tm x tn blocks (every caller launches that): the block
+// count comes from the arguments, not from gridDim, which is a hidden kernel
+// argument in memory while the explicit leading ones arrive preloaded in SGPRs.
 __device__ __forceinline__ void xcd_tile(int tm, int tn, bool nmajor, int& mi, int& ni) {
-  const int nblk = gridDim.x, id = blockIdx.x;
+  const int nblk = tm * tn, id = blockIdx.x;
   const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
   const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
   if (nmajor) {

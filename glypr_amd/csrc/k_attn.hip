@@ -317,7 +317,9 @@ __global__ void __launch_bounds__(G * AQS * 64) attn_partial_kernel(
   // K/V range one XCD streams (one partition, or the band of neighbouring
   // query blocks) stays in its L2.
   const int nqb = Tp / AQB;
-  const int W = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+  // the grid is the work items rounded up to a multiple of 8 (run_attention)
+  const int n8 = (nkv * kparts * nqb + 7) / 8;
+  const int W = (int)(blockIdx.x % 8) * n8 + (int)(blockIdx.x / 8);
   if (W >= nkv * kparts * nqb) return;   // grid padding (whole block)
   const int g = W / (kparts * nqb);
   const int kp = (W / nqb) % kparts;
@@ -738,7 +740,9 @@ __global__ void __launch_bounds__(ASH_WAVES * 64) attn_short_kernel(
   // one contiguous run of work items per XCD (block id % 8): neighbouring
   // query blocks and their slices, whose K/V ranges overlap, share an L2
   const int nqb = Tp / 16;
-  const int W = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+  // the grid is the work items rounded up to a multiple of 8 (run_attention)
+  const int n8 = (nkv * nqb * NSL + 7) / 8;
+  const int W = (int)(blockIdx.x % 8) * n8 + (int)(blockIdx.x / 8);
   if (W >= nkv * nqb * NSL) return;   // grid padding (whole block)
   const int g = W / (nqb * NSL);
   const int q0 = ((W / NSL) % nqb) * 16;

@@ -324,12 +324,15 @@ constexpr int SMALL_NB_MAX = 64;   // K <= 2048
 // a stage are 16 contiguous bytes of a row: per stage a lane reads its four
 // row scales and its TNW column scales with 4 + TNW ds_read_b128.  The stage
 // loop is unrolled by RING so ring slots are compile-time LDS offsets.
+// Argument order: everything the first DMAs need (operands, scales, M, N)
+// comes first, so that it lies within the 14 argument dwords the hardware
+// preloads into SGPRs; the outputs, used at the end, follow.
 template <int WM, int WN, int TNW, bool GEGLU, bool F2, int RING, int NB>
 __global__ void __launch_bounds__(WM * WN * 64)
 gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
-                     const int8_t* __restrict__ B, const float* __restrict__ dB,
-                     float* __restrict__ C, int8_t* __restrict__ Hq, float* __restrict__ dH,
-                     int M, int N, int ldc, int F) {
+                     const int8_t* __restrict__ B, const float* __restrict__ dB, int M, int N,
+                     int ldc, int F, float* __restrict__ C, int8_t* __restrict__ Hq,
+                     float* __restrict__ dH) {
   constexpr int K = NB * QK, NST = NB / KB;
   constexpr int NW = WM * WN;
   constexpr int BM = WM * 16;
@@ -519,7 +522,7 @@ hipError_t run_small_nb(const int8_t* xq, const float* dx, const int8_t* wq, con
   constexpr int BM = WM * 16, BN = WN * 16 * TNW;
   dim3 grid((unsigned)((Nrows + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
   gemm_i8_small_kernel<WM, WN, TNW, GEGLU, F2, RING, NB><<<grid, WM * WN * 64, 0, s>>>(
-      xq, dx, wq, dw, y, hq, dh, (int)M, (int)Nrows, (int)ldc, (int)F);
+      xq, dx, wq, dw, (int)M, (int)Nrows, (int)ldc, (int)F, y, hq, dh);
   return hipGetLastError();
 }
 
