@@ -268,8 +268,9 @@ gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave;
-  // XCD-aware tile id: workgroup i runs on XCD i % 8.
-  const int nblk = gridDim.x, id = blockIdx.x;
+  // XCD-aware tile id: workgroup i runs on XCD i % 8 (the grid is exactly
+  // the tile count, taken from the arguments rather than gridDim)
+  const int nblk = ((M + BFB_BM - 1) / BFB_BM) * tiles_n, id = blockIdx.x;
   const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
   const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
   const int tmi = W / tiles_n;
@@ -487,7 +488,8 @@ gemm_bf16w_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int nblk = gridDim.x, id = blockIdx.x;
+  // the grid is exactly the tile count (from the arguments, not gridDim)
+  const int nblk = ((M + BFW_BM - 1) / BFW_BM) * tiles_n, id = blockIdx.x;
   const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
   const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
   const int tmi = W / tiles_n;

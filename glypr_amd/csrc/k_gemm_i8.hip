@@ -1085,8 +1085,9 @@ gemm_i8_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // XCD-aware tile id: workgroup i runs on XCD i % 8.
-  const int nblk = gridDim.x, id = blockIdx.x;
+  // XCD-aware tile id: workgroup i runs on XCD i % 8 (the grid is exactly
+  // the tile count, taken from the arguments rather than gridDim)
+  const int nblk = ((M + BIG_BM - 1) / BIG_BM) * tiles_n, id = blockIdx.x;
   const int xq8 = nblk >> 3, xr8 = nblk & 7, xcd = id & 7;
   const int W = xcd * xq8 + (xcd < xr8 ? xcd : xr8) + (id >> 3);
   const int tmi = W / tiles_n;
