@@ -445,10 +445,13 @@ def clock_warmup(fn, seconds):
     return n
 
 
-def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1, prewarm_s=0.0):
+def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1, prewarm_s=0.0,
+                 q8_variant=None):
     """Embeddings/s of the full backbone for one t-token sequence (config 4/5), plus
     the per-op split from a second pass of the same steps with per-kernel events.
-    prewarm_s: seconds of untimed embeddings before the `warmup` steps."""
+    prewarm_s: seconds of untimed embeddings before the `warmup` steps.
+    q8_variant: glypr_hip_model_set_variant's variant (None: the default,
+    INT8_EXACT)."""
     import torch
     from glypr_amd import _lib
     from glypr_amd.ops import Model
@@ -456,6 +459,8 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1, prewar
     for name, (data, r, c, q8) in tensors.items():
         m.set_tensor(name, data, r, c, q8)
     m.finalize()
+    if q8_variant is not None:
+        m.set_variant(q8_variant)
     ids = np.random.default_rng(seed).integers(0, vocab, size=t).astype(np.uint32)
     out = torch.empty(256, dtype=torch.float32, device="cuda")
     # The embeddings run on a stream of their own (default priority, not the
@@ -497,6 +502,7 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1, prewar
     launches = sum(v["launches"] for v in kern.values()) / steps
     gemm = sum(v for k, v in split.items() if k.startswith("gemm"))
     att = split.get("attention", 0.0) + split.get("qkv_post", 0.0)
+    emb = out.cpu().numpy().astype(np.float64)
     m.close()
     return {"ms_per_embedding": round(ms, 4), "embeddings_per_s": round(1000.0 / ms, 2),
             "tokens_per_s": round(t * 1000.0 / ms, 1),
@@ -506,7 +512,7 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1, prewar
             "launches_per_embedding": int(round(launches)),
             "event_cost_us_per_launch": round(1000.0 * (ms_prof - ms) / max(1.0, launches), 3),
             "steps": steps, "warmup_steps": warmup, "clock_warmup_embeddings": n_pre,
-            "_kernels": kern, "_steps": steps}
+            "_kernels": kern, "_steps": steps, "_embedding": emb}
 
 
 # Projections of one backbone layer as the model driver launches them (all
@@ -805,9 +811,9 @@ def main():
                     help="Q8_0 variant of the C2 / cold-C2 extra lines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C3/C4/C5 extra lines")
-    ap.add_argument("--extras", default="c2,c1,cold,c3,vendor,c5,c3model,gather,vec",
+    ap.add_argument("--extras", default="c4fma,c2,c1,cold,c3,vendor,c5,c3model,gather,vec",
                     help="comma list of the extra workloads to run "
-                         "(c2, c1, cold, c3, vendor, c5, c3model, gather, vec)")
+                         "(c4fma, c2, c1, cold, c3, vendor, c5, c3model, gather, vec)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one plain device copy of MIB MiB (calibrates rocprof "
                          "FETCH_SIZE / WRITE_SIZE against known bytes)")
@@ -843,6 +849,20 @@ def main():
                                             for k, v in c4["_kernels"].items()}
 
     todo = set() if args.no_extra else {e.strip() for e in args.extras.split(",") if e.strip()}
+    if "c4fma" in todo:
+        # the same backbone and ids with every Q8_0 projection on INT8_FMA
+        # (glypr_hip_model_set_variant): the cost of vec_dot bit-identity
+        fma = run_backbone(ctx, tensors, n_layers, vocab, t_c4, args.steps, args.warmup,
+                           prewarm_s=0.25, q8_variant=INT8_FMA)
+        a, b = c4["_embedding"], fma["_embedding"]
+        extra["c4_int8_fma"] = {
+            **{k: v for k, v in fma.items() if not k.startswith("_")},
+            "kernels_us_per_launch": {k: round(v["us_per_launch"], 3)
+                                      for k, v in fma["_kernels"].items()},
+            "cosine_to_int8_exact": round(float(a @ b / np.linalg.norm(a) / np.linalg.norm(b)),
+                                          9),
+            "numerics": "INT8_FMA: one rounding fewer per Q8_0 block than vec_dot, within "
+                        "1e-3 relative / 1e-4 absolute; not the default"}
     if "c2" in todo:
         m = 512
         L, ms, kern = run_workload(ctx, m, variant, args.steps, args.warmup)

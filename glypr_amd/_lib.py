@@ -73,6 +73,7 @@ SIGNATURES = {
     "glypr_hip_model_finalize": (_int, [_vp]),
     "glypr_hip_model_embed": (_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "glypr_hip_model_embed_batch": (_int, [_vp, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "glypr_hip_model_set_variant": (_int, [_vp, _int]),
     "glypr_hip_model_destroy": (_int, [_vp]),
     "glypr_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "glypr_gguf_close": (_int, [_vp]),

@@ -248,8 +248,8 @@ hipError_t launch_gemm_i8_geglu(const int8_t* xq, const float* dx, const int8_t*
                                 const float* dw, int8_t* hq, float* dh, int64_t M, int64_t F,
                                 int64_t K, hipStream_t s, bool fma2 = false);
 
-// The q|k|v projection (INT8_EXACT, Q8_0 activations) with qkv_post's work
-// as its epilogue: writes the attention operands q / k / vt (f16, rows padded
+// The q|k|v projection (INT8_EXACT, or INT8_FMA with fma2; Q8_0 activations)
+// with qkv_post's work as its epilogue: writes the attention operands q / k / vt (f16, rows padded
 // to Tp, invalid rows zero) straight from the GEMM.  head_dim 256, K a
 // multiple of 128; 16-row blocks for Tp <= 2048 with K in {512, 768, 1024,
 // 1152}, 128-row blocks otherwise.
@@ -258,7 +258,8 @@ hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* w
                               const float* dw, int64_t T, int64_t Tp, int64_t K, int64_t nq,
                               int64_t nkv, int64_t hd, const float* qnw, const float* knw,
                               float eps, const float* cos_t, const float* sin_t, uint16_t* q16,
-                              uint16_t* k16, uint16_t* vt16, const int32_t* seg, hipStream_t s);
+                              uint16_t* k16, uint16_t* vt16, const int32_t* seg, hipStream_t s,
+                              bool fma2 = false);
 
 // The int8 GEMM with the activation prologue fused: x is f32 [M][K],
 // quantized to Q8_0 inside the GEMM (norm: of RMSNorm(x; nw, eps), nw

@@ -1305,7 +1305,7 @@ hipError_t run(const int8_t* xq,const float* dx, const int8_t* wq, const float* 
 constexpr int QKV_NW = 8;
 constexpr int QKV_RING = 3;
 
-template <int NB>
+template <bool F2, int NB>
 __global__ void __launch_bounds__(QKV_NW * 64)
 gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
                    const int8_t* __restrict__ B, const float* __restrict__ dB, int T, int Tp,
@@ -1458,7 +1458,7 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
             const float wc = wd * NEG_MAGIC;
 #pragma unroll
             for (int rr = 0; rr < 4; rr++)
-              acc[t][rr] = q8_term<false>(acc[t][rr], d[kb][t][rr], wd, wc, xq[rr][kb]);
+              acc[t][rr] = q8_term<F2>(acc[t][rr], d[kb][t][rr], wd, wc, xq[rr][kb]);
           }
       }
     }
@@ -1556,14 +1556,14 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
   }
 }
 
-template <int NB>
+template <bool F2, int NB>
 hipError_t run_qkv_nb(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                       int64_t T, int64_t Tp, int64_t nq, int64_t nkv, const float* qnw,
                       const float* knw, float eps, const float* cos_t, const float* sin_t,
                       _Float16* q16, _Float16* k16, _Float16* vt16, const int2* seg,
                       hipStream_t s) {
   const unsigned grid = (unsigned)((nq + 2 * nkv) * (Tp / 16));
-  gemm_i8_qkv_kernel<NB><<<grid, QKV_NW * 64, 0, s>>>(
+  gemm_i8_qkv_kernel<F2, NB><<<grid, QKV_NW * 64, 0, s>>>(
       xq, dx, wq, dw, (int)T, (int)Tp, (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t, q16, k16,
       vt16, seg);
   return hipGetLastError();
@@ -1587,7 +1587,7 @@ hipError_t run_qkv_nb(const int8_t* xq, const float* dx, const int8_t* wq, const
 // ---------------------------------------------------------------------------
 // WMW waves along M (4 or 6: 128 or 192 rows), 2 along N; one workgroup per CU
 // either way (110 or 126 KB of LDS), 2 or 3 waves per SIMD.
-template <int WMW>
+template <int WMW, bool F2>
 __global__ void __launch_bounds__(WMW * 2 * 64) __attribute__((amdgpu_waves_per_eu(WMW / 2)))
 gemm_i8_qkv_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
                        const int8_t* __restrict__ B, const float* __restrict__ dB, int K, int T,
@@ -1705,7 +1705,7 @@ gemm_i8_qkv_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ d
         const v16i d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, magic, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < 16; q++)
-          acc[tn][q] = q8_term<false>(acc[tn][q], d[q], wd, wc, xv[q >> 2][q & 3]);
+          acc[tn][q] = q8_term<F2>(acc[tn][q], d[q], wd, wc, xv[q >> 2][q & 3]);
       }
     }
   }
@@ -1734,6 +1734,7 @@ gemm_i8_qkv_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ d
   }
 }
 
+template <bool F2>
 hipError_t run_qkv_big(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
                        int64_t K, int64_t T, int64_t Tp, int64_t nq, int64_t nkv,
                        const float* qnw, const float* knw, float eps, const float* cos_t,
@@ -1746,12 +1747,12 @@ hipError_t run_qkv_big(const int8_t* xq, const float* dx, const int8_t* wq, cons
   auto cost = [&](int64_t bm) { return ((Tp + bm - 1) / bm * slots + 255) / 256 * bm; };
   if (cost(192) < cost(128)) {
     const unsigned grid = (unsigned)(slots * ((Tp + 191) / 192));
-    gemm_i8_qkv_big_kernel<6><<<grid, 768, 0, s>>>(xq, dx, wq, dw, (int)K, (int)T, (int)Tp,
+    gemm_i8_qkv_big_kernel<6, F2><<<grid, 768, 0, s>>>(xq, dx, wq, dw, (int)K, (int)T, (int)Tp,
                                                    (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
                                                    q16, k16, vt16, seg);
   } else {
     const unsigned grid = (unsigned)(slots * ((Tp + 127) / 128));
-    gemm_i8_qkv_big_kernel<4><<<grid, 512, 0, s>>>(xq, dx, wq, dw, (int)K, (int)T, (int)Tp,
+    gemm_i8_qkv_big_kernel<4, F2><<<grid, 512, 0, s>>>(xq, dx, wq, dw, (int)K, (int)T, (int)Tp,
                                                    (int)nq, (int)nkv, qnw, knw, eps, cos_t, sin_t,
                                                    q16, k16, vt16, seg);
   }
@@ -1826,36 +1827,52 @@ bool gemm_i8_qkv_ok(int64_t T, int64_t Tp, int64_t K, int64_t hd) {
          (qkv_small_ok(Tp, K) || T * K < (int64_t(1) << 31));
 }
 
+namespace {
+
+template <bool F2>
+hipError_t qkv_routed(const int8_t* xq, const float* dx, const int8_t* wq, const float* dw,
+                      int64_t T, int64_t Tp, int64_t K, int64_t nq, int64_t nkv, const float* qnw,
+                      const float* knw, float eps, const float* cos_t, const float* sin_t,
+                      _Float16* q, _Float16* k, _Float16* v, const int2* sg, hipStream_t s) {
+  if (!qkv_small_ok(Tp, K))
+    return run_qkv_big<F2>(xq, dx, wq, dw, K, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k,
+                           v, sg, s);
+  switch (K / QK) {
+    case 16:
+      return run_qkv_nb<F2, 16>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k,
+                                v, sg, s);
+    case 24:
+      return run_qkv_nb<F2, 24>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k,
+                                v, sg, s);
+    case 32:
+      return run_qkv_nb<F2, 32>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k,
+                                v, sg, s);
+    case 36:
+      return run_qkv_nb<F2, 36>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k,
+                                v, sg, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
 hipError_t launch_gemm_i8_qkv(const int8_t* xq, const float* dx, const int8_t* wq,
                               const float* dw, int64_t T, int64_t Tp, int64_t K, int64_t nq,
                               int64_t nkv, int64_t hd, const float* qnw, const float* knw,
                               float eps, const float* cos_t, const float* sin_t, uint16_t* q16,
-                              uint16_t* k16, uint16_t* vt16, const int32_t* seg, hipStream_t s) {
+                              uint16_t* k16, uint16_t* vt16, const int32_t* seg, hipStream_t s,
+                              bool fma2) {
   if (!gemm_i8_qkv_ok(T, Tp, K, hd) || (nq + 2 * nkv) * hd * K >= (int64_t(1) << 31))
     return hipErrorInvalidValue;
   _Float16* q = reinterpret_cast<_Float16*>(q16);
   _Float16* k = reinterpret_cast<_Float16*>(k16);
   _Float16* v = reinterpret_cast<_Float16*>(vt16);
   const int2* sg = reinterpret_cast<const int2*>(seg);
-  if (!qkv_small_ok(Tp, K))
-    return run_qkv_big(xq, dx, wq, dw, K, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v, sg,
-                       s);
-  switch (K / QK) {
-    case 16:
-      return run_qkv_nb<16>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
-                            sg, s);
-    case 24:
-      return run_qkv_nb<24>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
-                            sg, s);
-    case 32:
-      return run_qkv_nb<32>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
-                            sg, s);
-    case 36:
-      return run_qkv_nb<36>(xq, dx, wq, dw, T, Tp, nq, nkv, qnw, knw, eps, cos_t, sin_t, q, k, v,
-                            sg, s);
-    default:
-      return hipErrorInvalidValue;
-  }
+  return fma2 ? qkv_routed<true>(xq, dx, wq, dw, T, Tp, K, nq, nkv, qnw, knw, eps, cos_t, sin_t,
+                                 q, k, v, sg, s)
+              : qkv_routed<false>(xq, dx, wq, dw, T, Tp, K, nq, nkv, qnw, knw, eps, cos_t, sin_t,
+                                  q, k, v, sg, s);
 }
 
 // The prologue is repeated by every workgroup along N, so fusing pays only

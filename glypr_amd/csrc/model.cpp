@@ -120,6 +120,9 @@ struct glypr_model {
   LinearOp embedding_projection;  // output.weight
   bool finalized = false;
   bool dense = false;  // projections are dense bf16 weights (activations run in bf16)
+  // the Q8_0 projections' block epilogue: false = INT8_EXACT (vec_dot's
+  // three roundings per block), true = INT8_FMA (glypr_hip_model_set_variant)
+  bool fma2 = false;
   // RoPE tables [max_seq_len][head_dim] of the sliding and full layer types
   // (rope_sliding / rope_full, model.rs:278-279).
   DevBuf cos_s, sin_s, cos_f, sin_f;
@@ -480,7 +483,7 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     LAUNCH(GLYPR_K_QUANTIZE, s, launch_quantize_planar(h, t, H, xq, dx, s), "quantize launch");
     const glypr_q8w* wpl = m->ple_projection.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, wpl->qs(), wpl->dw(), ple, t, NL * P, H, NL * P, s),
+           launch_gemm_i8(xq, dx, wpl->qs(), wpl->dw(), ple, t, NL * P, H, NL * P, s, m->fma2),
            "per-layer projection launch");
     LAUNCH(GLYPR_K_RMSNORM, s, launch_affine(ple, t * NL * P, (float)pow((double)H, -0.5), s),
            "per-layer scale launch");
@@ -515,7 +518,7 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
              launch_gemm_i8_qkv(xq, dx, wqkv->qs(), wqkv->dw(), t, tp, H, nq, nkv, hd,
                                 L.self_attn.q_norm.weight, L.self_attn.k_norm.weight, c.eps,
                                 cos_t, sin_t, m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
-                                m->attn_vt.as<uint16_t>(), rows.seg, s),
+                                m->attn_vt.as<uint16_t>(), rows.seg, s, m->fma2),
              "qkv gemm launch");
       LAUNCH(GLYPR_K_ATTENTION, s,
              launch_attention(m->attn_q.as<uint16_t>(), m->attn_k.as<uint16_t>(),
@@ -526,7 +529,7 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     } else {
       LAUNCH(GLYPR_K_GEMM_I8, s,
              launch_gemm_i8(xq, dx, wqkv->qs(), wqkv->dw(), dev_f32(m->qkv), t, wqkv->n, H,
-                            wqkv->n, s),
+                            wqkv->n, s, m->fma2),
              "qkv gemm launch");
       RET_IF(attention_core(ctx, dev_f32(m->qkv), L.self_attn.q_norm.weight,
                             L.self_attn.k_norm.weight, c.eps, cos_t, sin_t, t, nq, nkv, hd,
@@ -538,7 +541,7 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     const glypr_q8w* wo = L.self_attn.o.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
            launch_gemm_i8(m->cq.as<int8_t>(), dev_f32(m->dc), wo->qs(), wo->dw(),
-                          dev_f32(m->proj), t, H, qd, H, s),
+                          dev_f32(m->proj), t, H, qd, H, s, m->fma2),
            "o gemm launch");
     // post_attention_layernorm.forward_residual_add + pre_feedforward_layernorm prologue
     LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
@@ -549,12 +552,12 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     const glypr_q8w* wgu = L.mlp.fused_gate_up.w;
     LAUNCH(GLYPR_K_GEMM_I8_GEGLU, s,
            launch_gemm_i8_geglu(xq, dx, wgu->qs(), wgu->dw(), m->hq.as<int8_t>(), dev_f32(m->dh),
-                                t, F, H, s),
+                                t, F, H, s, m->fma2),
            "gate/up GeGLU launch");
     const glypr_q8w* wd = L.mlp.down.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
            launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wd->qs(), wd->dw(),
-                          dev_f32(m->proj), t, H, F, H, s),
+                          dev_f32(m->proj), t, H, F, H, s, m->fma2),
            "down gemm launch");
     // next layer's input norm, or after the last layer the final norm
     const float* w_next = last ? m->norm.weight : m->layers[li + 1].input_layernorm.weight;
@@ -579,7 +582,7 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     // ---- TextPLEBlock::forward_with_scalar (ple.rs:118-145)
     const glypr_q8w* wg = L.ple_block.gate.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, wg->qs(), wg->dw(), dev_f32(m->ple_gate), t, P, H, P, s),
+           launch_gemm_i8(xq, dx, wg->qs(), wg->dw(), dev_f32(m->ple_gate), t, P, H, P, s, m->fma2),
            "per-layer gate launch");
     LAUNCH(GLYPR_K_GEGLU, s,
            launch_geglu_quant(dev_f32(m->ple_gate), ple + (int64_t)li * P, NL * P, t, P,
@@ -588,7 +591,7 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
     const glypr_q8w* wpj = L.ple_block.projection.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
            launch_gemm_i8(m->hq.as<int8_t>(), dev_f32(m->dh), wpj->qs(), wpj->dw(),
-                          dev_f32(m->proj), t, H, P, H, s),
+                          dev_f32(m->proj), t, H, P, H, s, m->fma2),
            "per-layer proj launch");
     // post_norm.forward_residual_add(.., layer_scalar) + next layer's input norm
     LAUNCH(GLYPR_K_RESIDUAL_NORM, s,
@@ -601,7 +604,8 @@ int forward_rows(glypr_model* m, glypr_hip_ctx* ctx, const Rows& rows, float* hi
   if (c.out_dim > 0) {
     const glypr_q8w* we = m->embedding_projection.w;
     LAUNCH(GLYPR_K_GEMM_I8, s,
-           launch_gemm_i8(xq, dx, we->qs(), we->dw(), tokens, t, c.out_dim, H, c.out_dim, s),
+           launch_gemm_i8(xq, dx, we->qs(), we->dw(), tokens, t, c.out_dim, H, c.out_dim, s,
+                          m->fma2),
            "embedding projection launch");
   }
   *tokens_out = tokens;
@@ -977,6 +981,17 @@ int glypr_hip_model_embed_batch(glypr_model* m, const uint32_t* ids, const int64
          launch_pool_segments(tokens, rows, m->seg.as<int32_t>(), m->seqs.as<int32_t>(), n_seqs,
                               width, trunc, out, dev_f32(m->pooled), s, mixed),
          "pool launch");
+  return GLYPR_OK;
+}
+
+int glypr_hip_model_set_variant(glypr_model* m, int variant) {
+  clear_error();
+  GLYPR_CHECK(m != nullptr, GLYPR_ERR_INVALID_ARG, "model is NULL");
+  GLYPR_CHECK(variant == GLYPR_Q8_INT8_EXACT || variant == GLYPR_Q8_INT8_FMA,
+              GLYPR_ERR_UNSUPPORTED,
+              "the model runs its Q8_0 projections as INT8_EXACT or INT8_FMA, not variant %d",
+              variant);
+  m->fma2 = variant == GLYPR_Q8_INT8_FMA;
   return GLYPR_OK;
 }
 

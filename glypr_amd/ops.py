@@ -526,6 +526,11 @@ class Model:
     def finalize(self):
         check(lib().glypr_hip_model_finalize(self.handle))
 
+    def set_variant(self, variant: int):
+        """glypr_hip_model_set_variant: INT8_EXACT (default) or INT8_FMA for
+        every Q8_0 projection of the later embed calls."""
+        check(lib().glypr_hip_model_set_variant(self.handle, variant))
+
     def embed(self, ids, trunc: int = 0, hidden: Optional[torch.Tensor] = None,
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
         ids = np.ascontiguousarray(ids, dtype=np.uint32)

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define GLYPR_HIP_ABI_VERSION 7
+#define GLYPR_HIP_ABI_VERSION 8
 
 typedef enum glypr_status {
   GLYPR_OK = 0,
@@ -67,7 +67,8 @@ typedef enum glypr_status {
  *   rounding fewer per block than the vec_dot sequence, so not bit-identical
  *   to it (within 1e-3 relative / 1e-4 absolute; measured to ~1e-6 relative),
  *   and 2 instead of 3 vector ops per output and block, the bound of the
- *   int8 GEMM at large M.  The model driver always uses INT8_EXACT. */
+ *   int8 GEMM at large M.  The model driver uses INT8_EXACT unless
+ *   glypr_hip_model_set_variant (ABI >= 8) selects INT8_FMA. */
 typedef enum glypr_q8_variant {
   GLYPR_Q8_INT8_EXACT = 0,
   GLYPR_Q8_BF16_DEQUANT = 1,
@@ -361,8 +362,9 @@ int glypr_hip_model_finalize(glypr_model* model);
  * width when trunc is 0 or wider] on the device.  hidden (nullable, device
  * [t][width]) receives the unpooled token embeddings: the projection's output,
  * or the final-normed states without one.  The embedding width is out_dim
- * when set, else hidden.  Q8_0 projections run as INT8_EXACT; dense bf16 ones
- * take bf16 activations (nearest even) with f32 accumulation. */
+ * when set, else hidden.  Q8_0 projections run as INT8_EXACT (or INT8_FMA,
+ * see glypr_hip_model_set_variant); dense bf16 ones take bf16 activations
+ * (nearest even) with f32 accumulation. */
 int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, int64_t trunc,
                           float* out, float* hidden, glypr_stream stream);
 
@@ -382,6 +384,16 @@ int glypr_hip_model_embed(glypr_model* model, const uint32_t* ids, int64_t t, in
  * max_batch_tokens) (GLYPR_ERR_SHAPE otherwise). */
 int glypr_hip_model_embed_batch(glypr_model* model, const uint32_t* ids, const int64_t* lens,
                                 int64_t n_seqs, int64_t trunc, float* out, glypr_stream stream);
+
+/* (ABI >= 8) No counterpart in the reference, whose CPU path has one
+ * numerics (vec_dot, linear.rs:153-162): the block epilogue of every Q8_0
+ * projection of the model's later embed calls, GLYPR_Q8_INT8_EXACT (the
+ * default, bit-identical to vec_dot) or GLYPR_Q8_INT8_FMA (one rounding fewer
+ * per block, within 1e-3 relative / 1e-4 absolute of it, and 2 instead of 3
+ * vector ops per output and block).  For callers that trade bit-identity for
+ * throughput within the reference's stated tolerance.  Dense bf16 projections
+ * are unaffected.  Any other variant -> GLYPR_ERR_UNSUPPORTED. */
+int glypr_hip_model_set_variant(glypr_model* model, int variant);
 
 int glypr_hip_model_destroy(glypr_model* model);
 

@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_symbols():
         assert hasattr(L, name), name
-    assert L.glypr_hip_abi_version() == 7
+    assert L.glypr_hip_abi_version() == 8
 
 
 def _has_gpu():

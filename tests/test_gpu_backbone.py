@@ -224,8 +224,11 @@ def ctypes_byref(oracle, cfg):
     return ctypes.byref(cfg)
 
 
-@pytest.mark.parametrize("t", [130, 512, 1000, 2100, 6600])
-def test_model_equals_op_composition_bit_exact(ctx, oracle, t):
+@pytest.mark.parametrize("t,variant", [(130, ops.INT8_EXACT), (512, ops.INT8_EXACT),
+                                       (1000, ops.INT8_EXACT), (2100, ops.INT8_EXACT),
+                                       (6600, ops.INT8_EXACT), (512, ops.INT8_FMA),
+                                       (2100, ops.INT8_FMA)])
+def test_model_equals_op_composition_bit_exact(ctx, oracle, t, variant):
     """The model driver against the same forward composed from the public ops,
     bit for bit.  The model runs its own launch sequence: ids in the gather's
     kernel arguments, and the q|k|v GEMM writing the attention operands itself
@@ -233,10 +236,13 @@ def test_model_equals_op_composition_bit_exact(ctx, oracle, t):
     f32 q|k|v and glypr_hip_attention's separate qkv_post; 6 layers cover the
     sliding and the full layer kinds (layer.rs:20-50, model.rs:498-578).  The
     q|k|v GEMM runs in 16-row blocks up to T = 2048, in 128-row blocks at
-    2100 and in 192-row blocks at 6600."""
+    2100 and in 192-row blocks at 6600.  With INT8_FMA set on the model and
+    passed to every public op, the two sides still agree bit for bit."""
     n_layers, vocab, H, eps = 6, 2000, 768, 1e-6
-    say(f"model driver vs op composition layers={n_layers} t={t}: bit-exact token states")
+    say(f"model driver vs op composition layers={n_layers} t={t} variant={variant}: "
+        "bit-exact token states")
     m, tensors = make_model(ctx, oracle, n_layers, vocab, seed=60)
+    m.set_variant(variant)
     ids = oracle.uniform_ids(t, seed=t + 3, vocab=vocab)
     hidden = torch.empty((t, H), dtype=torch.float32, device="cuda")
     m.embed(ids, trunc=256, hidden=hidden)
@@ -264,12 +270,12 @@ def test_model_equals_op_composition_bit_exact(ctx, oracle, t):
         weights += parts + gu + qkv_views + gu_views + [wqkv, wgu, wo, wd]
         full = (i + 1) % 6 == 0
         c, s = rope[1e6 if full else 1e4]
-        qkv = ops.rmsnorm_q8_0_matmul(ctx, wqkv, h, w(p + "attn_norm.weight"), eps)
+        qkv = ops.rmsnorm_q8_0_matmul(ctx, wqkv, h, w(p + "attn_norm.weight"), eps, variant)
         ctxv = ops.attention(ctx, qkv, w(p + "attn_q_norm.weight"), w(p + "attn_k_norm.weight"),
                              eps, c, s, 3, 1, 256, 0 if full else 512)
-        proj = ops.q8_0_matmul(ctx, wo, ctxv)
+        proj = ops.q8_0_matmul(ctx, wo, ctxv, variant)
         h = h + ops.rmsnorm(ctx, proj, w(p + "post_attention_norm.weight"), eps)
-        mo = ops.rmsnorm_mlp(ctx, wgu, wd, h, w(p + "ffn_norm.weight"), eps)
+        mo = ops.rmsnorm_mlp(ctx, wgu, wd, h, w(p + "ffn_norm.weight"), eps, variant)
         h = h + ops.rmsnorm(ctx, mo, w(p + "post_ffw_norm.weight"), eps)
     ref = host(ops.rmsnorm(ctx, h, w("output_norm.weight"), eps))
     for wt in weights:
@@ -329,6 +335,27 @@ def test_model_forward_vs_oracle(ctx, oracle, n_layers, t, vocab):
     # determinism: a second call gives identical bits
     again = host(m.embed(ids, trunc=256))
     assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+    # INT8_FMA projections (glypr_hip_model_set_variant): one rounding fewer
+    # per Q8_0 block than vec_dot, held to the same bars against the oracle
+    m.set_variant(ops.INT8_FMA)
+    fh = torch.empty((t, 768), dtype=torch.float32, device="cuda")
+    fma = host(m.embed(ids, trunc=256, hidden=fh))
+    fcos = float(fma @ ref / np.linalg.norm(fma) / np.linalg.norm(ref))
+    fg = host(fh)
+    frow = (fg * ref_hidden).sum(1) / np.linalg.norm(fg, axis=1) / \
+        np.linalg.norm(ref_hidden, axis=1)
+    say(f"  INT8_FMA: embedding cosine vs oracle {fcos:.8f}, token-state cosine min "
+        f"{frow.min():.8f}, values differing from INT8_EXACT's "
+        f"{int((fg.view(np.uint32) != gh.view(np.uint32)).sum())} of {fg.size}")
+    assert fcos >= 0.9999 and frow.min() >= 0.999
+    assert not np.array_equal(fg.view(np.uint32), gh.view(np.uint32))   # the variant is live
+    # back to INT8_EXACT: the first call's bits again; other variants refused
+    m.set_variant(ops.INT8_EXACT)
+    assert np.array_equal(host(m.embed(ids, trunc=256)).view(np.uint32), got.view(np.uint32))
+    for v in (ops.BF16_DEQUANT, 7, -1):
+        with pytest.raises(_lib.GlyprError) as e:
+            m.set_variant(v)
+        assert e.value.code == _lib.GLYPR_ERR_UNSUPPORTED
     m.close()
 
 
@@ -400,6 +427,17 @@ def test_model_with_ple_and_projection_vs_oracle(ctx, oracle):
     other = host(m2.embed(ids, trunc=256))
     assert float(other @ got / np.linalg.norm(other) / np.linalg.norm(got)) < 0.999
     m2.close()
+    # INT8_FMA reaches the PLE projections and the embedding projection too
+    m.set_variant(ops.INT8_FMA)
+    ft = torch.empty((t, D), dtype=torch.float32, device="cuda")
+    fma = host(m.embed(ids, trunc=256, hidden=ft))
+    fcos = float(fma @ ref / np.linalg.norm(fma) / np.linalg.norm(ref))
+    fg = host(ft)
+    frow = (fg * ref_tokens).sum(1) / np.linalg.norm(fg, axis=1) / \
+        np.linalg.norm(ref_tokens, axis=1)
+    say(f"  INT8_FMA: final embedding cosine {fcos:.8f}, token cosine min {frow.min():.8f}")
+    assert fcos >= 0.9999 and frow.min() >= 0.999
+    assert not np.array_equal(fg.view(np.uint32), gt.view(np.uint32))
     m.close()
 
 
