@@ -11,15 +11,17 @@
 // on synthetic Q8_0 weights (BASELINE's N(0, 0.02) quantized as
 // BlockQ8_0::from_float does: d = amax / 127 as f16) and N(0, 1) activations.
 //
-//   capi_bench [--m 16384] [--variant int8|bf16] [--steps 20] [--warmup 3]
+//   capi_bench [--m 16384] [--variant int8|fma|bf16] [--steps 20] [--warmup 3]
 //              [--copy-probe MB]
-//   capi_bench --model [--t 512] [--steps 20] [--warmup 3] [--copy-probe MB]
+//   capi_bench --model [--t 512] [--variant int8|fma] [--steps 20] [--warmup 3]
+//              [--copy-probe MB]
 //
 // Prints one JSON line: ms per step and TOPS (2 * m * 7-projection MACs).
 // --model instead runs config 4: glypr_hip_model_embed of one t-token
 // sequence through the 24-layer backbone (hidden 768, 3 q / 1 kv heads of
 // 256, FFN 1152, the 262144 x 768 Q8_0 token table, MRL-256), synthetic
-// weights as above and norm weights 1 + N(0, 0.1) (q/k norms x 0.25).
+// weights as above and norm weights 1 + N(0, 0.1) (q/k norms x 0.25); its
+// --variant (INT8_EXACT unless given) goes to glypr_hip_model_set_variant.
 // --copy-probe MB ends the run with one device-to-device copy of MB MiB: the
 // known-size launch that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE.
 #include <hip/hip_runtime.h>
@@ -106,7 +108,7 @@ std::vector<float> host_normal(std::mt19937_64& rng, int64_t n, float mean, floa
 }
 
 // Config 4 through glypr_hip_model_*: ms per embedding.
-int run_model(int64_t t, int steps, int warmup) {
+int run_model(int64_t t, int steps, int warmup, int variant) {
   constexpr int64_t L = 24, V = 262144, HD = 256;
   glypr_hip_ctx* ctx = nullptr;
   CK(glypr_hip_ctx_create(0, &ctx));
@@ -153,6 +155,7 @@ int run_model(int64_t t, int steps, int warmup) {
     }
   }
   CK(glypr_hip_model_finalize(m));
+  CK(glypr_hip_model_set_variant(m, variant));
   std::vector<uint32_t> ids((size_t)t);
   std::uniform_int_distribution<uint32_t> ud(0, (uint32_t)V - 1);
   for (auto& v : ids) v = ud(rng);
@@ -176,10 +179,12 @@ int run_model(int64_t t, int steps, int warmup) {
   HK(hipEventSynchronize(e1));
   float ms = 0.0f;
   HK(hipEventElapsedTime(&ms, e0, e1));
-  printf("{\"workload\": \"c4-embed\", \"t\": %lld, \"layers\": %lld, \"steps\": %d, "
+  printf("{\"workload\": \"c4-embed\", \"variant\": %d, \"t\": %lld, \"layers\": %lld, "
+         "\"steps\": %d, "
          "\"ms_per_embedding\": %.4f, \"embeddings_per_s\": %.2f, "
          "\"host_enqueue_ms_per_embedding\": %.4f}\n",
-         (long long)t, (long long)L, steps, ms / steps, 1000.0 * steps / ms, host_ms / steps);
+         variant, (long long)t, (long long)L, steps, ms / steps, 1000.0 * steps / ms,
+         host_ms / steps);
   fflush(stdout);
   HK(hipFree(out));
   HK(hipStreamDestroy(s));
@@ -216,7 +221,7 @@ float* device_normal(std::mt19937_64& rng, int64_t n, float mean, float sigma) {
 
 int main(int argc, char** argv) {
   int64_t m = 16384;
-  int variant = GLYPR_Q8_BF16_DEQUANT, steps = 20, warmup = 3;
+  int variant = -1, steps = 20, warmup = 3;
   int64_t probe_mb = 0, t = 512;
   bool model = false;
   for (int i = 1; i < argc; i++) {
@@ -225,15 +230,18 @@ int main(int argc, char** argv) {
     else if (!strcmp(argv[i], "--t") && i + 1 < argc) t = atoll(argv[++i]);
     else if (!strcmp(argv[i], "--variant") && i + 1 < argc) {
       ++i;
-      variant = !strcmp(argv[i], "int8") ? GLYPR_Q8_INT8_EXACT : GLYPR_Q8_BF16_DEQUANT;
+      variant = !strcmp(argv[i], "int8")   ? GLYPR_Q8_INT8_EXACT
+                : !strcmp(argv[i], "fma")  ? GLYPR_Q8_INT8_FMA
+                : !strcmp(argv[i], "bf16") ? GLYPR_Q8_BF16_DEQUANT
+                                           : -2;
     } else if (!strcmp(argv[i], "--steps") && i + 1 < argc) steps = atoi(argv[++i]);
     else if (!strcmp(argv[i], "--warmup") && i + 1 < argc) warmup = atoi(argv[++i]);
     else if (!strcmp(argv[i], "--copy-probe") && i + 1 < argc) probe_mb = atoll(argv[++i]);
     else {
       fprintf(stderr,
-              "usage: %s [--m M] [--variant int8|bf16] [--steps K] [--warmup W] "
-              "[--copy-probe MB]\n       %s --model [--t T] [--steps K] [--warmup W] "
-              "[--copy-probe MB]\n", argv[0], argv[0]);
+              "usage: %s [--m M] [--variant int8|fma|bf16] [--steps K] [--warmup W] "
+              "[--copy-probe MB]\n       %s --model [--t T] [--variant int8|fma] [--steps K] "
+              "[--warmup W] [--copy-probe MB]\n", argv[0], argv[0]);
       return 2;
     }
   }
@@ -243,11 +251,16 @@ int main(int argc, char** argv) {
                     "[0, 4096]\n");
     return 2;
   }
+  if (variant == -2 || (model && variant == GLYPR_Q8_BF16_DEQUANT)) {
+    fprintf(stderr, "--variant: int8, fma or (without --model) bf16\n");
+    return 2;
+  }
   if (model) {
-    const int rc = run_model(t, steps, warmup);
+    const int rc = run_model(t, steps, warmup, variant < 0 ? GLYPR_Q8_INT8_EXACT : variant);
     copy_probe(probe_mb);
     return rc;
   }
+  if (variant < 0) variant = GLYPR_Q8_BF16_DEQUANT;
   glypr_hip_ctx* ctx = nullptr;
   CK(glypr_hip_ctx_create(0, &ctx));
   CK(glypr_hip_ctx_reserve(ctx, m));
@@ -295,7 +308,9 @@ int main(int argc, char** argv) {
   const double macs = (double)m * (double)(H * (NQ + 2 * NKV) + NQ * H + H * 2 * F + F * H);
   printf("{\"workload\": \"c3-layer-projections\", \"m\": %lld, \"variant\": \"%s\", "
          "\"steps\": %d, \"ms_per_step\": %.4f, \"tops\": %.2f}\n",
-         (long long)m, variant == GLYPR_Q8_INT8_EXACT ? "int8" : "bf16", steps, per,
+         (long long)m,
+         variant == GLYPR_Q8_INT8_EXACT ? "int8" : variant == GLYPR_Q8_INT8_FMA ? "fma" : "bf16",
+         steps, per,
          2.0 * macs / (per / 1e3) / 1e12);
   fflush(stdout);
   copy_probe(probe_mb);
