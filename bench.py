@@ -515,8 +515,8 @@ def run_backbone(ctx, tensors, n_layers, vocab, t, steps, warmup, seed=1, prewar
             "_kernels": kern, "_steps": steps, "_embedding": emb}
 
 
-# Projections of one backbone layer as the model driver launches them (all
-# INT8_EXACT, Q8_0 operands from the fused prologues): (kernel, N, K).
+# Projections of one backbone layer as the model driver launches them (INT8_EXACT
+# by default, Q8_0 operands from the fused prologues): (kernel, N, K).
 MODEL_GEMMS = [("gemm_i8_qkv", NQ + 2 * NKV, H), ("gemm_i8", H, NQ), ("gemm_i8_geglu", 2 * F, H),
                ("gemm_i8", H, F)]
 

@@ -9,8 +9,9 @@
 //   TextPLE/TextPLEBlock ple.rs:20-145
 //   EmbeddingGemma2Model model.rs:244-705      (gather, PLE inputs, layers, final norm,
 //                                               embedding projection, pooling)
-// The forward pass runs every projection as an INT8_EXACT Q8_0 GEMM and fuses
-// what the reference computes in separate ops:
+// The forward pass runs every projection as an INT8_EXACT Q8_0 GEMM (INT8_FMA
+// after glypr_hip_model_set_variant) and fuses what the reference computes in
+// separate ops:
 //   - each RMSNorm that feeds a projection is the GEMM's quantizing prologue;
 //   - forward_residual_add of one sublayer and the next sublayer's input
 //     RMSNorm are one kernel (residual_norm);
@@ -19,8 +20,8 @@
 //   - the PLE block's geglu(gate, per-layer input) is fused with the Q8_0
 //     quantization of the proj GEMM's operand, and its forward_residual_add
 //     with the layer scalar feeds the next layer's input norm.
-// The GEMMs, norms, GeGLU and residual adds are bit-exact with the CPU path;
-// attention (f16 MFMA with split operands, see k_attn.hip) and the chunked
+// The GEMMs (INT8_EXACT), norms, GeGLU and residual adds are bit-exact with
+// the CPU path; attention (f16 MFMA with split operands, see k_attn.hip) and the chunked
 // pooling sum differ from it at f32-rounding level.
 #include <math.h>
 #include <stdio.h>
