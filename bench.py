@@ -949,6 +949,11 @@ def main():
                        if not k.startswith("_")}
         extra["c5"]["attention_layers"] = ("4 full + 20 sliding (window 512) layers, "
                                            "1.341 TFLOP per embedding")
+        extra["c5_int8_fma"] = {
+            k: v for k, v in run_backbone(ctx, tensors, n_layers, vocab, 8192, 50, 5,
+                                          prewarm_s=0.25, q8_variant=INT8_FMA).items()
+            if k in ("ms_per_embedding", "embeddings_per_s", "tokens_per_s", "gemm_ms",
+                     "attention_ms", "split_ms_profiled")}
     if "c3model" in todo:
         extra["c3_model_batch"] = run_backbone_batch(ctx, tensors, n_layers, vocab, 32, 512, 5, 1)
     cpu = None

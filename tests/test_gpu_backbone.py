@@ -908,7 +908,7 @@ def test_embed_batch_real_geometry_and_dense(ctx, oracle):
 def test_embed_batch_c3_regime(ctx, oracle):
     """C3's batch, 32 sequences x 512 tokens (M = 16384 through every
     projection), on 2 layers with max_batch_tokens 16384: sampled sequences
-    against their single-sequence embeddings."""
+    against their single-sequence embeddings, on INT8_EXACT and on INT8_FMA."""
     vocab = 5000
     say("embed_batch 32 x 512 (M = 16384)")
     m = Model(ctx, n_layers=2, vocab=vocab, max_batch_tokens=16384)
@@ -925,5 +925,15 @@ def test_embed_batch_c3_regime(ctx, oracle):
         ref, _ = oracle_forward(oracle, tensors, 2, vocab, seqs[i], 256)
         c2 = _cos(got[i], ref)
         say(f"  seq {i}: cos vs single {c1:.9f}, vs oracle {c2:.8f}")
+        assert c1 >= 0.99999 and c2 >= 0.9999, (i, c1, c2)
+    # INT8_FMA through the large-M routes (128/192-row q|k|v, large-M GEMM and
+    # GeGLU kernels): the batch again, against INT8_EXACT's and the oracle
+    m.set_variant(ops.INT8_FMA)
+    fma = host(m.embed_batch(seqs, trunc=256))
+    assert not np.array_equal(fma.view(np.uint32), got.view(np.uint32))
+    for i in (0, 13, 31):
+        ref, _ = oracle_forward(oracle, tensors, 2, vocab, seqs[i], 256)
+        c1, c2 = _cos(fma[i], got[i]), _cos(fma[i], ref)
+        say(f"  INT8_FMA seq {i}: cos vs INT8_EXACT {c1:.9f}, vs oracle {c2:.8f}")
         assert c1 >= 0.99999 and c2 >= 0.9999, (i, c1, c2)
     m.close()
