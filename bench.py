@@ -272,8 +272,9 @@ def c1_linear(ctx, steps):
 def vendor_ref(steps):
     """hipBLASLt (through torch) on the C3 projection shapes, as a reference for
     what the platform's own GEMM library reaches there: bf16 x bf16 -> bf16
-    (torch.matmul) and int8 x int8 -> int32 (torch._int_mm).  Plain GEMMs: no
-    Q8_0 block scales, no activation quantization, half-width (bf16) outputs."""
+    (torch.matmul), bf16 x bf16 -> f32 (torch.mm with out_dtype, the output
+    width of glypr_hip_q8_0_matmul) and int8 x int8 -> int32 (torch._int_mm).
+    Plain GEMMs: no Q8_0 block scales, no activation quantization."""
     import torch
     out = {}
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -290,12 +291,22 @@ def vendor_ref(steps):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / steps * 1e3   # us
 
-    step_bf16 = step_i8 = 0.0
+    step_bf16 = step_i8 = step_f32 = 0.0
+    f32_err = None
     m = 16384
     for name, n, k in PROJ:
         a = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
         b = torch.randn(n, k, device="cuda", generator=gen).to(torch.bfloat16)
         us_bf = timed(lambda: a @ b.t())
+        us_f32 = None
+        if f32_err is None:
+            bt = b.t().contiguous()
+            try:
+                us_f32 = timed(lambda: torch.mm(a, bt, out_dtype=torch.float32))
+                step_f32 += us_f32
+            except Exception as e:   # an op this torch build does not provide
+                f32_err = f"{type(e).__name__}: {e}"[:160]
+            del bt
         ai = torch.randint(-127, 128, (m, k), device="cuda", dtype=torch.int8, generator=gen)
         bi = torch.randint(-127, 128, (k, n), device="cuda", dtype=torch.int8, generator=gen)
         us_i8 = timed(lambda: torch._int_mm(ai, bi))
@@ -303,6 +314,9 @@ def vendor_ref(steps):
         out[name] = {"M": m, "N": n, "K": k,
                      "bf16_us": round(us_bf, 2), "bf16_tflops": round(ops_ / us_bf / 1e6, 1),
                      "int8_us": round(us_i8, 2), "int8_tops": round(ops_ / us_i8 / 1e6, 1)}
+        if us_f32 is not None:
+            out[name]["bf16_f32out_us"] = round(us_f32, 2)
+            out[name]["bf16_f32out_tflops"] = round(ops_ / us_f32 / 1e6, 1)
         step_bf16 += us_bf
         step_i8 += us_i8
         del a, b, ai, bi
@@ -311,6 +325,11 @@ def vendor_ref(steps):
                       "bf16_tflops": round(total / step_bf16 / 1e6, 1),
                       "int8_ms": round(step_i8 / 1e3, 4),
                       "int8_tops": round(total / step_i8 / 1e6, 1)}
+    if f32_err is None:
+        out["c3_step"]["bf16_f32out_ms"] = round(step_f32 / 1e3, 4)
+        out["c3_step"]["bf16_f32out_tflops"] = round(total / step_f32 / 1e6, 1)
+    else:
+        out["bf16_f32out_error"] = f32_err
     out["library"] = "hipBLASLt via torch " + torch.__version__
     return out
 
@@ -623,16 +642,19 @@ def gather_line(ctx, steps, n_ids=1 << 20, vocab=262144, d=768):
             "note": "per call also uploads the 4 MB of host ids (PCIe) before the kernel"}
 
 
-def run_backbone_batch(ctx, tensors, n_layers, vocab, n_seqs, t, steps, warmup, seed=2):
+def run_backbone_batch(ctx, tensors, n_layers, vocab, n_seqs, t, steps, warmup, seed=2,
+                       q8_variant=None):
     """Embeddings/s of the full backbone on a batch of n_seqs t-token sequences in
     one glypr_hip_model_embed_batch call (C3's 32 x 512 regime through the whole
-    model: every projection at M = n_seqs * t)."""
+    model: every projection at M = n_seqs * t).  q8_variant: as run_backbone."""
     import torch
     from glypr_amd.ops import Model
     m = Model(ctx, n_layers=n_layers, vocab=vocab, max_batch_tokens=n_seqs * t)
     for name, (data, r, c, q8) in tensors.items():
         m.set_tensor(name, data, r, c, q8)
     m.finalize()
+    if q8_variant is not None:
+        m.set_variant(q8_variant)
     rng = np.random.default_rng(seed)
     seqs = [rng.integers(0, vocab, size=t).astype(np.uint32) for _ in range(n_seqs)]
     out = torch.empty((n_seqs, 256), dtype=torch.float32, device="cuda")
@@ -956,6 +978,8 @@ def main():
                      "attention_ms", "split_ms_profiled")}
     if "c3model" in todo:
         extra["c3_model_batch"] = run_backbone_batch(ctx, tensors, n_layers, vocab, 32, 512, 5, 1)
+        extra["c3_model_batch_int8_fma"] = run_backbone_batch(ctx, tensors, n_layers, vocab, 32,
+                                                              512, 5, 1, q8_variant=INT8_FMA)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_backbone_baseline(tensors, n_layers, vocab, t_c4)
