@@ -383,14 +383,15 @@ gemm_bf16_big_kernel(const uint16_t* __restrict__ A, const int8_t* __restrict__ 
       for (int tm = 0; tm < TM; tm++)
 #pragma unroll
         for (int r = 0; r < 16; r++)
-          crow[(int64_t)(32 * tm + 8 * (r >> 2) + (r & 3)) * ldc] = acc[tm][r];
+          st_nt(&crow[(int64_t)(32 * tm + 8 * (r >> 2) + (r & 3)) * ldc], (float)acc[tm][r]);
     } else {
 #pragma unroll
       for (int tm = 0; tm < TM; tm++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int gm = m0 + 32 * tm + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-          if (gm < M && gn < N) crow[(int64_t)(32 * tm + 8 * (r >> 2) + (r & 3)) * ldc] = acc[tm][r];
+          if (gm < M && gn < N)
+            st_nt(&crow[(int64_t)(32 * tm + 8 * (r >> 2) + (r & 3)) * ldc], (float)acc[tm][r]);
         }
     }
   } else {

@@ -1208,7 +1208,7 @@ gemm_i8_big_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int gm = row0 + 8 * (r >> 2) + (r & 3);
-        if (gm < M && gn < N) C[(int64_t)gm * ldc + gn] = acc[tn][r];
+        if (gm < M && gn < N) st_nt(&C[(int64_t)gm * ldc + gn], (float)acc[tn][r]);
       }
     }
   } else {
