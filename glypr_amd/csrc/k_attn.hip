@@ -278,13 +278,17 @@ __device__ __forceinline__ float pair_sum32(float v) {
   return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
-// LDS swizzles (16-byte chunk c of row r is stored at chunk c ^ swz(r)); both
-// keep any 8 consecutive lanes of a fragment read on distinct 16-byte bank
-// groups of a 128-byte line and any 16 on distinct groups of 256 bytes.
+// LDS swizzles (16-byte chunk c of row r is stored at chunk c ^ swz(r)),
+// chosen by measurement: with them the fragment reads show no
+// SQ_LDS_BANK_CONFLICT cycles.
 // K rows are 512 B; the S^T tiles read rows 8 (l16 / 4) + 4 kt + l16 % 4.
 __device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
-// V^T rows are 64 B (4 chunks); the O^T tiles read rows 16 t + l16.
-__device__ __forceinline__ int vswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// V^T rows are 64 B (4 chunks); the O^T tiles read rows 16 t + l16.  Of the
+// row functions measured for these ds_read_b128 fragments (SQ_LDS_BANK_CONFLICT
+// per read, rows 16 t + l16 for every t), (r >> 1) & 3 is the one with no
+// conflict cycles; (r >> 1 ^ r >> 3) & 3, r & 3, (r >> 2) & 3 and no swizzle
+// all cost ~4 cycles per read.
+__device__ __forceinline__ int vswz(int r) { return (r >> 1) & 3; }
 
 // HD = 512: the K and V^T tiles are 32 KB each, so the ring has two slots
 // (128 KB) and each block is one 16-query row of waves (AQS = 1): the next
