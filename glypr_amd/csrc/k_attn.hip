@@ -772,7 +772,11 @@ __global__ void __launch_bounds__(ASH_WAVES * 64) attn_short_kernel(
   // slice, 16 keys (32 B) each (lane: row 32u + lane / 2, chunk lane % 2).
   const int krow = lane >> 5, kpc = lane & 31;
   const int kl = 512 * krow + ((kpc ^ krow) << 4);
-  const int vl = (lane >> 1) * Tp * 2 + ((lane & 1) << 4);
+  // V^T row r of a unit keeps its two 16-byte chunks swapped when bit 3 of r
+  // is set (row 32 u + lane / 2: bit 3 is bit 4 of the lane), which keeps the
+  // PV fragment reads below free of LDS bank-conflict cycles (measured; the
+  // unswizzled rows cost ~2 cycles per ds_read_b64)
+  const int vl = (lane >> 1) * Tp * 2 + (((lane & 1) ^ ((lane >> 4) & 1)) << 4);
   const f16* kbase = kk + (int64_t)g * Tp * HD;
   const f16* vbase = vt + ((int64_t)g * HD + DS * sl) * Tp;
   auto issue = [&](int kb, int slot) {
@@ -845,7 +849,8 @@ __global__ void __launch_bounds__(ASH_WAVES * 64) attn_short_kernel(
     v4h_ vf[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++)
-      vf[t] = *reinterpret_cast<const v4h_*>(vs + (16 * t + l16) * 32 + 8 * lq);
+      vf[t] = *reinterpret_cast<const v4h_*>(vs + (16 * t + l16) * 32 +
+                                             ((((lq >> 1) ^ (l16 >> 3)) << 4) | ((lq & 1) << 3)));
     // S^T: sacc[hh][r] = S[qi][k0 + 4 lq + r]
     v4f_ sacc[G];
 #pragma unroll
