@@ -308,12 +308,17 @@ gemm_i8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 //  - stages the per-block scales once, coalesced, in their natural [row][b]
 //    layout (dA rows of the tile, then dB rows).
 // LDS layout of a ring slot: A rows then B rows, each [row][128 B] with the
-// 16-byte chunk c of row r stored at chunk c ^ (r & 7).  One DMA writes 1 KB
+// 16-byte chunk c of row r stored at chunk c ^ sm_swz(r).  One DMA writes 1 KB
 // linearly (lane i -> row i/8, physical chunk i%8), so lane i reads global
-// chunk (i%8) ^ (row & 7).  Rows past M/N are clamped to a valid row (their
+// chunk (i%8) ^ sm_swz(row).  Rows past M/N are clamped to a valid row (their
 // outputs are never stored).
 // ---------------------------------------------------------------------------
 constexpr int SMALL_NB_MAX = 64;   // K <= 2048
+// Row swizzle of the small-M kernels' 128-byte LDS rows.  The fragment reads
+// (ds_read_b64: rows l16 of a 16-row tile, chunk 2 kb + (lq >> 1), half lq & 1)
+// measured 2 SQ_LDS_BANK_CONFLICT cycles per read with r & 7 and none with
+// (r >> 1) & 7.
+__device__ __forceinline__ int sm_swz(int r) { return (r >> 1) & 7; }
 
 // WM x WN waves; wave (wm, wn) owns rows 16 wm.. and TNW 16-row B tiles.
 // GEGLU: TNW == 2 (gate tile, up tile of the same 16 h columns) and WN == 2:
@@ -396,7 +401,7 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
     const int row = (u < UA ? u : u - UA) * 8 + rsub;
     const int grow = u < UA ? (m0 + row < M ? m0 + row : M - 1) : b_row(row);
     ubase[j] = u < UA ? A : B;
-    uvoff[j] = grow * K + ((pch ^ (row & 7)) << 4);
+    uvoff[j] = grow * K + ((pch ^ sm_swz(row)) << 4);
   }
   // stage st into ring slot `slot`
   auto issue = [&](int st, int slot) {
@@ -414,11 +419,11 @@ gemm_i8_small_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
   for (int kb = 0; kb < KB; kb++) {
     const int ch = 2 * kb + (lq >> 1);
-    offA[kb] = arow * BK + ((ch ^ (arow & 7)) << 4) + ((lq & 1) << 3);
+    offA[kb] = arow * BK + ((ch ^ sm_swz(arow)) << 4) + ((lq & 1) << 3);
 #pragma unroll
     for (int t = 0; t < TNW; t++) {
       const int brow = wn * 16 * TNW + t * 16 + l16;
-      offB[t][kb] = (BM + brow) * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+      offB[t][kb] = (BM + brow) * BK + ((ch ^ sm_swz(brow)) << 4) + ((lq & 1) << 3);
     }
   }
   const float* xrow = sc + (wm * 16 + 4 * lq) * NB;   // row 4 lq + r at xrow + r * NB
@@ -638,7 +643,7 @@ gemm_i8_geglu8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA
     const int row = (u < UA ? u : u - UA) * 8 + rsub;
     const int grow = u < UA ? (m0 + row < M ? m0 + row : M - 1) : b_row(row);
     ubase[j] = u < UA ? A : B;
-    uvoff[j] = grow * K + ((pch ^ (row & 7)) << 4);
+    uvoff[j] = grow * K + ((pch ^ sm_swz(row)) << 4);
   }
   auto issue = [&](int st, int slot) {
 #pragma unroll
@@ -656,9 +661,9 @@ gemm_i8_geglu8_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA
 #pragma unroll
   for (int kb = 0; kb < KB; kb++) {
     const int ch = 2 * kb + (lq >> 1);
-    offA[kb] = l16 * BK + ((ch ^ (l16 & 7)) << 4) + ((lq & 1) << 3);
+    offA[kb] = l16 * BK + ((ch ^ sm_swz(l16)) << 4) + ((lq & 1) << 3);
     const int brow = wave * 16 + l16;
-    offB[kb] = (BM + brow) * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+    offB[kb] = (BM + brow) * BK + ((ch ^ sm_swz(brow)) << 4) + ((lq & 1) << 3);
   }
   const float* xrow = sc + (4 * lq) * NB;
   const float* wrow = sc + SA + (wave * 16 + l16) * NB;
@@ -843,7 +848,7 @@ gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, fl
 #pragma unroll
   for (int j = 0; j < UPW; j++) {
     const int row = (j * NW + wave) * 8 + rsub;
-    uvoff[j] = b_row(row) * K + ((pch ^ (row & 7)) << 4);
+    uvoff[j] = b_row(row) * K + ((pch ^ sm_swz(row)) << 4);
   }
   auto issue = [&](int st, int slot) {
 #pragma unroll
@@ -923,7 +928,7 @@ gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, fl
         const int col = QK * (part * BPP + g0 + i) + 4 * pj;
         const int st = col >> 7, qb = col & (BK - 1);
         *reinterpret_cast<uint32_t*>(ares + st * (BM * BK) + pr * BK +
-                                     (((qb >> 4) ^ (pr & 7)) << 4) + (qb & 15)) = packed;
+                                     (((qb >> 4) ^ sm_swz(pr)) << 4) + (qb & 15)) = packed;
       }
     }
   }
@@ -933,11 +938,11 @@ gemm_i8_pro_kernel(const float* __restrict__ X, const float* __restrict__ nw, fl
 #pragma unroll
   for (int kb = 0; kb < KB; kb++) {
     const int ch = 2 * kb + (lq >> 1);
-    offA[kb] = l16 * BK + ((ch ^ (l16 & 7)) << 4) + ((lq & 1) << 3);
+    offA[kb] = l16 * BK + ((ch ^ sm_swz(l16)) << 4) + ((lq & 1) << 3);
 #pragma unroll
     for (int t = 0; t < TNW; t++) {
       const int brow = wn * 16 * TNW + t * 16 + l16;
-      offB[t][kb] = brow * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+      offB[t][kb] = brow * BK + ((ch ^ sm_swz(brow)) << 4) + ((lq & 1) << 3);
     }
   }
   const float* xrow = sc + (4 * lq) * NB;                    // row 4 lq + r at xrow + r NB
@@ -1359,14 +1364,14 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
   for (int j = 0; j < UBW; j++) {
     const int row = (UBW * wave + j) * 8 + rsub;
-    boff[j] = (n0 + row) * K + ((pch ^ (row & 7)) << 4);
+    boff[j] = (n0 + row) * K + ((pch ^ sm_swz(row)) << 4);
   }
   const bool has_a = wave < UA;
   int aoff;
   {
     const int row = (has_a ? wave : 0) * 8 + rsub;
     const int gm = m0 + row < M ? m0 + row : M - 1;
-    aoff = gm * K + ((pch ^ (row & 7)) << 4);
+    aoff = gm * K + ((pch ^ sm_swz(row)) << 4);
   }
   auto issue = [&](int st, int sl) {
     uint8_t* base = ring + sl * SLOT;
@@ -1384,11 +1389,11 @@ gemm_i8_qkv_kernel(const int8_t* __restrict__ A, const float* __restrict__ dA,
 #pragma unroll
   for (int kb = 0; kb < KB; kb++) {
     const int ch = 2 * kb + (lq >> 1);
-    offA[kb] = l16 * BK + ((ch ^ (l16 & 7)) << 4) + ((lq & 1) << 3);
+    offA[kb] = l16 * BK + ((ch ^ sm_swz(l16)) << 4) + ((lq & 1) << 3);
 #pragma unroll
     for (int t = 0; t < TNW; t++) {
       const int brow = wn * 16 * TNW + t * 16 + l16;
-      offB[t][kb] = (BM + brow) * BK + ((ch ^ (brow & 7)) << 4) + ((lq & 1) << 3);
+      offB[t][kb] = (BM + brow) * BK + ((ch ^ sm_swz(brow)) << 4) + ((lq & 1) << 3);
     }
   }
   const float* xrow = sc + (4 * lq) * NB;
