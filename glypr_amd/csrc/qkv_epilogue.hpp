@@ -12,7 +12,10 @@
 namespace glypr {
 
 constexpr int QKV_HD = 256;
-constexpr int QKV_SP = QKV_HD + 4;   // staged row stride (floats)
+// staged row stride (floats): 8 banks of shift per row, so the chain reads of
+// two neighbouring rows (lanes 0-7 and 8-15) and the accumulator writes of
+// rows 4 apart fall on distinct LDS banks
+constexpr int QKV_SP = QKV_HD + 8;
 
 // Rows 0 .. 8 NW - 1 of stg (tokens r0 ..) of head slot `slot`, NW waves of
 // the calling workgroup, all of which call this (it holds a barrier); sinv
